@@ -1,0 +1,196 @@
+#!/usr/bin/env python3
+"""Decode/prefill benchmark of the HIP StableLM forwarder on one MI355X.
+
+Workload (one "step"): StableLM-3B shapes (32 layers, hidden 2560, 32 x 80
+heads, 25% rotary, SiLU MLP 6912, vocab 65536) with seeded synthetic GGUF
+Q8_0 weights, fp32 KV; a 512-token uniform-random prompt is prefilled, then
+256 greedy tokens are chosen (255 one-token decode forwards, the logits of
+each copied to the host and argmax'd there, as the Go host does).
+
+Prints one JSON line: value = decode tokens/s over the timed steps, plus the
+prefill seconds, the roofline fraction of the dominant decode kernel
+(HIP-event durations on the library's stream) and the CPU oracle timed on
+the host cores.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
+
+
+def q8_bytes(rows, cols):
+    return rows * cols // 32 * 34
+
+
+def decode_in_bytes(c):
+    """Algorithmic HBM bytes of one decode_in launch: the layer's q, k, v,
+    gate and up rows once, plus its activations (x, LayerNorm w/b, q, k, v, m)."""
+    d, I = c["hidden_size"], c["intermediate_size"]
+    kv = d // c["num_attention_heads"] * c["num_key_value_heads"]
+    weights = q8_bytes(d, d) + 2 * q8_bytes(kv, d) + 2 * q8_bytes(I, d)
+    acts = 4 * (d + 2 * d + d + 2 * kv + I)
+    return weights + acts
+
+
+def token_bytes(c, pos, kv_bytes=4):
+    """Algorithmic bytes of one decode forward at position pos: every weight
+    once (layers + head), one embedding row, the KV read and write."""
+    d, I, L, V = c["hidden_size"], c["intermediate_size"], c["num_hidden_layers"], c["vocab_size"]
+    kv = d // c["num_attention_heads"] * c["num_key_value_heads"]
+    layer = 2 * q8_bytes(d, d) + 2 * q8_bytes(kv, d) + 3 * q8_bytes(I, d)
+    return L * layer + q8_bytes(V, d) + d // 32 * 34 + L * 2 * kv * kv_bytes * (pos + 2)
+
+
+def cpu_baseline(config, tensors, threads, prompt_len):
+    """The oracle (C restatement of the Go scalar engine) on the host cores:
+    a 128-token batched prefill chunk (prefillBatch) and 2 decode forwards
+    at positions prompt_len, prompt_len + 1 on a zero-initialised KV."""
+    import numpy as np
+    from oracle import pyoracle
+    pyoracle.set_threads(threads)
+    m = pyoracle.StableLM(config, tensors, capacity=1024)
+    rng = np.random.default_rng(5)
+    ids = rng.integers(0, config["vocab_size"], 128).astype(np.int32)
+    t0 = time.perf_counter()
+    m.prefill(ids, 0)
+    prefill_tok_s = 128 / (time.perf_counter() - t0)
+    t0 = time.perf_counter()
+    for i in range(2):
+        m.forward(int(ids[i]), prompt_len + i)
+    decode_tok_s = 2 / (time.perf_counter() - t0)
+    m.close()
+    return {"value": round(decode_tok_s, 4), "unit": "tok/s", "cores": threads, "kind": "port",
+            "prefill_tok_s": round(prefill_tok_s, 3),
+            "prefill_s_extrapolated": round(prompt_len / prefill_tok_s, 2),
+            "sample": f"oracle (C restatement of tinyoai's Go scalar-float64 engine, -ffp-contract=off, "
+                      f"{threads} OpenMP threads): one 128-token batched prefill chunk and 2 decode forwards "
+                      f"at positions {prompt_len}-{prompt_len + 1} with zero-initialised fp32 KV, same weights"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--prompt", type=int, default=512)
+    ap.add_argument("--generate", type=int, default=256)
+    ap.add_argument("--layers", type=int, default=32)
+    ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--seed", type=int, default=1234)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the path would shard by "
+              f"attention head / MLP column with one all-reduce per layer; see DESIGN.md).", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    from tinyoai_amd import hip, weights as W
+
+    torch.cuda.set_device(0)
+    config = W.validate_stablelm_config(dict(W.STABLELM_3B, num_hidden_layers=args.layers))
+    t0 = time.perf_counter()
+    tensors = W.synthetic_stablelm(config, W.Q8_0, seed=args.seed)
+    gen_s = time.perf_counter() - t0
+    print(f"[bench] synthetic weights in {gen_s:.1f}s", file=sys.stderr, flush=True)
+    fwd = hip.StableLMForwarder(config, tensors)
+    print("[bench] weights resident in HBM", file=sys.stderr, flush=True)
+    rng = np.random.default_rng(args.seed + 1)
+    prompt = rng.integers(0, config["vocab_size"], args.prompt).astype(np.int32)
+
+    def step():
+        t_a = time.perf_counter()
+        logits = fwd.forward(0, prompt)
+        t_b = time.perf_counter()
+        resident, toks = args.prompt, []
+        for n in range(args.generate):
+            tok = int(np.argmax(logits))
+            toks.append(tok)
+            if n + 1 < args.generate:
+                logits = fwd.forward(resident, [tok])
+                resident += 1
+        t_c = time.perf_counter()
+        return t_b - t_a, t_c - t_b, toks
+
+    for _ in range(args.warmup):
+        step()
+        print("[bench] warmup step done", file=sys.stderr, flush=True)
+    fwd.profile(True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    prefill_s, decode_s, streams = [], [], []
+    for i in range(args.steps):
+        p, d, toks = step()
+        prefill_s.append(p)
+        decode_s.append(d)
+        streams.append(toks)
+        print(f"[bench] step {i}: prefill {p * 1e3:.1f} ms, decode {d * 1e3:.1f} ms", file=sys.stderr, flush=True)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    prof = fwd.profile_read()
+    fwd.profile(False)
+    decode_forwards = (args.generate - 1) * args.steps
+    decode_tok_s = decode_forwards / sum(decode_s)
+    mean_prefill = sum(prefill_s) / len(prefill_s)
+
+    ms, count = prof["decode_in"]
+    avg_s = ms / 1e3 / max(count, 1)
+    nbytes = decode_in_bytes(config)
+    achieved = nbytes / avg_s / 1e9
+    mean_pos = args.prompt + (args.generate - 2) / 2
+    roof_tok_s = 1.0 / (token_bytes(config, mean_pos) / (HBM_PEAK_GBS * 1e9))
+    kernels = {k: {"avg_us": round(v[0] * 1e3 / v[1], 2) if v[1] else None, "launches": v[1]}
+               for k, v in prof.items()}
+
+    out = {
+        "metric": "decode tok/s + prefill s, 3B StableLM Q8_0 512+256; % of HBM/MFMA roofline",
+        "value": round(decode_tok_s, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall / args.steps * 1e3, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": f"StableLM-3B-shape GGUF Q8_0, {args.prompt}-token prompt + {args.generate} greedy "
+                               f"tokens, fp32 KV", "layers": config["num_hidden_layers"],
+                   "hidden": config["hidden_size"], "heads": config["num_attention_heads"], "head_dim": 80,
+                   "intermediate": config["intermediate_size"], "vocab": config["vocab_size"],
+                   "prompt_tokens": args.prompt, "generated_tokens": args.generate, "kv": "f32",
+                   "weights_seed": args.seed},
+        "prefill_s": round(mean_prefill, 4),
+        "prefill_tok_s": round(args.prompt / mean_prefill, 1),
+        "decode_roofline_tok_s": round(roof_tok_s, 1),
+        "decode_frac_of_hbm_roofline": round(decode_tok_s / roof_tok_s, 4),
+        "greedy_stream_stable": all(s == streams[0] for s in streams),
+        "roofline": {"kernel": "decode_in (LayerNorm + Q8_0 q/k/v/gate/up matvec + RoPE + KV append + SiLU-gate)",
+                     "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "algorithmic_bytes_per_launch": nbytes, "avg_launch_us": round(avg_s * 1e6, 2),
+                     "launches": count},
+        "kernels": kernels,
+    }
+    fwd.close()
+    if not args.no_cpu:
+        print("[bench] timing the CPU oracle", file=sys.stderr, flush=True)
+        out["cpu_baseline"] = cpu_baseline(config, tensors, args.cpu_threads, args.prompt)
+    else:
+        out["cpu_baseline"] = None
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,161 @@
+/*
+ * tinyoai_hip.h -- C ABI of the MI355X (gfx950) forward-pass backend.
+ *
+ * The entry points are what tinyoai's GPU forwarder contract binds
+ * (mlx.go:45-51, mlx_llama.go:27-35, mlx_kv.go:78-91, mlx_native.go:231-244),
+ * plus the weightTensor operations the kernel-level benchmarks and tests use
+ * (safetensors.go:268-280, matmul.go:12-95). Plain pointers and sizes only.
+ *
+ * Conventions
+ *  - Every call returns 0 on success or a negative TINYOAI_E* code; the
+ *    message is then available from tinyoai_last_error() on the same thread.
+ *  - Host buffers stay owned by the caller; the library copies what it keeps.
+ *  - A handle is used by one thread at a time (the caller holds the model
+ *    gate, stablelm.go:478-484 / mlx.go:291-296). Different handles are
+ *    independent and run on their own HIP streams.
+ *  - Cancellation stays with the caller, checked between calls; an admitted
+ *    forward always completes (mlx_native.go:491-494).
+ */
+#ifndef TINYOAI_HIP_H
+#define TINYOAI_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TINYOAI_OK 0
+#define TINYOAI_EINVAL (-1)   /* invalid argument or unsupported configuration */
+#define TINYOAI_EDEVICE (-2)  /* HIP runtime or kernel launch failure */
+#define TINYOAI_ENOMEM (-3)   /* device or host allocation failure */
+
+/* GGUF tensor type codes (gguf.go:183-214). Q4_K (12) is accepted although
+ * the reference rejects it (gguf.go:203-204). */
+#define TINYOAI_F32 0
+#define TINYOAI_F16 1
+#define TINYOAI_Q5_1 7
+#define TINYOAI_Q8_0 8
+#define TINYOAI_Q4_K 12
+#define TINYOAI_Q5_K 13
+#define TINYOAI_Q6_K 14
+#define TINYOAI_BF16 30
+
+typedef struct tinyoai_model tinyoai_model;
+typedef struct tinyoai_weight tinyoai_weight;
+
+/* One tensor in its on-disk encoding, row-major [rows, cols] (vectors:
+ * rows = 1), named as in the Hugging Face checkpoint
+ * (stablelm.go:180-191); weightTensor, safetensors.go:193-197. */
+typedef struct {
+  const char *name;
+  int32_t dtype;
+  int64_t rows, cols;
+  const void *data;
+  uint64_t nbytes;
+} tinyoai_tensor;
+
+/* StableLMConfig after validate() (stablelm.go:18-111). */
+typedef struct {
+  int32_t vocab_size, hidden_size, intermediate_size, num_hidden_layers;
+  int32_t num_attention_heads, num_key_value_heads, max_position_embeddings;
+  int32_t bos_token_id, eos_token_id;
+  double layer_norm_eps, rope_theta, partial_rotary_factor;
+} tinyoai_stablelm_config;
+
+/* llama2.c Config header (model.go:29-37). */
+typedef struct {
+  int32_t dim, hidden_dim, n_layers, n_heads, n_kv_heads, vocab_size, seq_len;
+} tinyoai_llama_config;
+
+/* The calling thread's message for its last failed call. */
+const char *tinyoai_last_error(void);
+
+/* ---------------- StableLM forwarder (mlxForwarder, mlx.go:45-51) ---------------- */
+
+/* Uploads every tensor named by loadStableWeights (stablelm.go:178-191) to
+ * HBM and prepares fp32 KV storage (StableLMOptions{KVCache: "f32"}). */
+int tinyoai_stablelm_load(const tinyoai_stablelm_config *config, const tinyoai_tensor *tensors,
+                          int32_t n_tensors, tinyoai_model **out);
+
+/* Forward (mlx.go:47-48; nativeMLX.Forward, mlx_native.go:292-297):
+ * replaces the resident suffix after `prefix` (0 <= prefix <= offset) with
+ * `tokens`, writes their KV, and when want_logits is nonzero writes the last
+ * position's fp32 logits [vocab_size] to the caller's `logits`. On success
+ * the resident offset becomes prefix + n. On failure the KV is reset
+ * (mlx_native.go:487-490) and the offset is 0. */
+int tinyoai_stablelm_forward(tinyoai_model *m, int32_t prefix, const int32_t *tokens, int32_t n,
+                             int32_t want_logits, float *logits);
+
+/* SetKVBits (mlx_kv.go:78-91): 32 = fp32 KV, 16 = fp16 KV rounded with
+ * floatHalf (kv_cache.go:27-65). A change discards the resident prefix and
+ * sets *cleared = 1. */
+int tinyoai_stablelm_set_kv_bits(tinyoai_model *m, int32_t bits, int32_t *cleared);
+
+/* LimitCache (mlx_native.go:231-244): reserves `limit` KV positions; a
+ * larger retained cache is discarded and *cleared = 1. */
+int tinyoai_stablelm_limit_cache(tinyoai_model *m, int32_t limit, int32_t *cleared);
+
+/* Discards KV, keeping weights resident (nativeMLX.reset, mlx_native.go:216-224). */
+int tinyoai_stablelm_reset(tinyoai_model *m);
+
+/* Resident prefix length (nativeMLX.offset), or a negative code. */
+int tinyoai_stablelm_offset(const tinyoai_model *m);
+
+/* Releases weights, KV and the stream (mlx_native.go:247-259). */
+int tinyoai_stablelm_close(tinyoai_model *m);
+
+/* Debug hooks for parity checks: copy KV head `kv_head` of `layer` for
+ * positions [0, n) as fp32 [n][head_dim] (stableState keys/values,
+ * kv_cache.go:91-96); record the residual stream after every layer for the
+ * final token of each forward (the stage boundaries of stableProfile,
+ * stablelm.go:339-384) and read it back as [layers][hidden]. */
+int tinyoai_stablelm_read_kv(tinyoai_model *m, int32_t layer, int32_t kv_head, int32_t n, float *keys,
+                             float *values);
+int tinyoai_stablelm_trace(tinyoai_model *m, int32_t enable);
+int tinyoai_stablelm_trace_read(tinyoai_model *m, float *residual);
+
+/* Stage timings (stableProfile, stablelm.go:227-250): when enabled, each
+ * kernel is bracketed by hipEvents on the handle's stream and its duration
+ * is added to its stage: 0 embedding, 1 decode_in (layer_norm +
+ * projections + rotary + kv_write + SiLU-gate), 2 attention, 3 decode_out
+ * (output_projection + down + residual), 4 lm_head, 5 prefill layer_norm,
+ * 6 prefill projections, 7 prefill rotary + kv_write, 8 prefill attention,
+ * 9 prefill SiLU-gate and residual. Enabling clears the totals.
+ * profile_read fills ms[] and counts[] (n_stages >= 10) and returns the
+ * number of stages. */
+int tinyoai_stablelm_profile(tinyoai_model *m, int32_t enable);
+int tinyoai_stablelm_profile_read(tinyoai_model *m, double *ms, int64_t *counts, int32_t n_stages);
+
+/* ---------------- legacy Llama forwarder (llamaMLXForwarder, mlx_llama.go:27-35) ---------------- */
+
+/* `weights` is the float32 payload after the 7-int32 header, in
+ * readWeights order (model.go:129-166). */
+int tinyoai_llama_load(const tinyoai_llama_config *config, const float *weights, uint64_t n_floats,
+                       tinyoai_model **out);
+/* Forward (mlx_llama.go:30-31): evaluates `tokens` after `prefix`; writes
+ * all n rows of logits ([n][vocab]) when all_logits is nonzero, else only
+ * the last row. */
+int tinyoai_llama_forward(tinyoai_model *m, int32_t prefix, const int32_t *tokens, int32_t n,
+                          int32_t all_logits, float *logits);
+int tinyoai_llama_reset(tinyoai_model *m);  /* Reset (mlx_llama.go:32-33) */
+int tinyoai_llama_close(tinyoai_model *m);  /* Close (mlx_llama.go:34) */
+
+/* ---------------- single weight matrices (weightTensor, safetensors.go:193-280) ---------------- */
+
+int tinyoai_weight_upload(int32_t dtype, int64_t rows, int64_t cols, const void *data, uint64_t nbytes,
+                          tinyoai_weight **out);
+/* readValues (matmul.go:12-50): n values from flat element `offset`, bit-exact. */
+int tinyoai_weight_read_values(tinyoai_weight *w, int64_t offset, int64_t n, float *out);
+/* mulScratch (n == 1, safetensors.go:275-280) or mulBatch (n > 1,
+ * matmul.go:55-95): out[n][rows] = x[n][cols] * W^T, host buffers. */
+int tinyoai_weight_mul(tinyoai_weight *w, const float *x, int32_t n, float *out);
+/* The same product on device-resident buffers, enqueued on `stream`
+ * (a hipStream_t; NULL = the weight's own stream) without synchronizing. */
+int tinyoai_weight_mul_device(tinyoai_weight *w, const float *x_dev, int32_t n, float *out_dev, void *stream);
+int tinyoai_weight_free(tinyoai_weight *w);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

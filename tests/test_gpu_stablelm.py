@@ -1,0 +1,173 @@
+"""End-to-end StableLM parity of the HIP forwarder against the reference's
+fixtures and the CPU oracle.
+
+Mirrors TestStableLMReference (stablelm_test.go:50-82), TestBatchedPrefill
+(prefill_test.go:217-277), TestHalfKVPrefixReuse (kv_cache_test.go:45-80)
+and the forwarder semantics of nativeMLX.Forward (mlx_native.go:292-495).
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+from tinyoai_amd import weights as W
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+HELLO_ABC = [2, 340, 328, 331]  # see test_oracle.HELLO_ABC
+
+
+@pytest.fixture(scope="module")
+def hip():
+    from tinyoai_amd import hip as H
+    H.lib()
+    return H
+
+
+@pytest.fixture(scope="module")
+def expected():
+    with open(os.path.join(GOLDEN, "stablelm", "expected.json")) as f:
+        return json.load(f)
+
+
+def greedy(fwd, ids, max_tokens, eos):
+    """MLX.generate's greedy path over the forwarder (mlx.go:342-468)."""
+    logits = fwd.forward(0, ids, True)
+    out, resident = [], len(ids)
+    for n in range(max_tokens):
+        tok = int(np.argmax(logits))
+        out.append(tok)
+        if tok == eos:
+            break
+        if n + 1 < max_tokens:
+            logits = fwd.forward(resident, [tok], True)
+            resident += 1
+    return out
+
+
+def test_reference_logits_sequential(hip, tiny_stablelm, expected):
+    """Seven one-token forwards against Transformers fp32 within 3e-5."""
+    config, tensors = tiny_stablelm
+    f = hip.StableLMForwarder(config, tensors)
+    for pos, tok in enumerate(expected["input_ids"]):
+        got = f.forward(pos, [tok])
+        assert np.max(np.abs(got - np.array(expected["logits"][pos], np.float32))) <= 3e-5, pos
+    assert f.offset == len(expected["input_ids"])
+
+
+def test_reference_logits_batched(hip, tiny_stablelm, expected):
+    """One batched prefill forward; last-row logits within 3e-5."""
+    config, tensors = tiny_stablelm
+    f = hip.StableLMForwarder(config, tensors)
+    ids = expected["input_ids"]
+    got = f.forward(0, ids)
+    assert np.max(np.abs(got - np.array(expected["logits"][-1], np.float32))) <= 3e-5
+
+
+@pytest.mark.parametrize("kv_bits", [32, 16])
+def test_reference_greedy(hip, tiny_stablelm, expected, kv_bits):
+    config, tensors = tiny_stablelm
+    f = hip.StableLMForwarder(config, tensors)
+    f.set_kv_bits(kv_bits)
+    assert greedy(f, HELLO_ABC, 8, config["eos_token_id"]) == expected["generation"]["ids"]
+
+
+@pytest.mark.parametrize("n", [2, 17, 63, 64, 65, 129, 257])
+def test_batched_prefill_against_oracle(hip, oracle, tiny_stablelm, n):
+    """TestBatchedPrefill: a 7-token prefix, then a batched suffix; logits and
+    KV against the oracle's sequential forwards within 3e-5, then one decode."""
+    config, tensors = tiny_stablelm
+    config = dict(config, max_position_embeddings=384)
+    ids = [32 + (i * 13) % 250 for i in range(n + 7)]
+    seq = oracle.StableLM(config, tensors, capacity=384)
+    for i, tok in enumerate(ids):
+        want = seq.forward(tok, i)
+    f = hip.StableLMForwarder(config, tensors)
+    f.forward(0, ids[:7], False)
+    got = f.forward(7, ids[7:])
+    assert np.max(np.abs(got - want)) <= 3e-5
+    for layer in range(config["num_hidden_layers"]):
+        k1, v1 = seq.read_kv(layer, 0, len(ids))
+        k2, v2 = f.read_kv(layer, 0, len(ids))
+        assert np.max(np.abs(k1 - k2)) <= 3e-5 and np.max(np.abs(v1 - v2)) <= 3e-5
+    assert np.max(np.abs(seq.forward(123, len(ids)) - f.forward(len(ids), [123]))) <= 3e-5
+
+
+def test_prefix_rewind_and_errors(hip, tiny_stablelm):
+    """Forward replaces the suffix after `prefix` (rewind allowed); invalid
+    requests fail, and a failed forward leaves no resident prefix."""
+    config, tensors = tiny_stablelm
+    f = hip.StableLMForwarder(config, tensors)
+    ids = [5, 9, 13, 17, 21, 25]
+    full = f.forward(0, ids)
+    f.forward(0, [5, 9, 100, 101])
+    assert f.offset == 4
+    rewound = f.forward(2, ids[2:])
+    assert np.max(np.abs(rewound - full)) <= 1e-6
+    with pytest.raises(hip.TinyoaiError):
+        f.forward(f.offset + 1, [1])  # prefix beyond the resident tokens
+    with pytest.raises(hip.TinyoaiError):
+        f.forward(0, [config["vocab_size"]])
+    with pytest.raises(hip.TinyoaiError):
+        f.forward(0, list(range(config["max_position_embeddings"] + 1)))
+    assert f.offset == 6  # validation failures happen before any work
+    assert f.set_kv_bits(16) is True and f.offset == 0
+    assert f.set_kv_bits(16) is False
+    assert f.limit_cache(32) is False or f.offset == 0
+
+
+def test_half_kv_prefix_reuse(hip, tiny_stablelm):
+    """TestHalfKVPrefixReuse: warm, extended and replaced prompts on an fp16
+    KV cache match cold forwards."""
+    config, tensors = tiny_stablelm
+    config = dict(config, max_position_embeddings=384)
+    warm = hip.StableLMForwarder(config, tensors)
+    warm.set_kv_bits(16)
+    resident = []
+    for prompt in ([2, 40, 41], [2, 40, 41], [2, 40, 41] + [7] * 140, [2, 40, 41] + [7] * 155, [2, 99]):
+        prefix = 0
+        while prefix < min(len(resident), len(prompt) - 1) and resident[prefix] == prompt[prefix]:
+            prefix += 1  # reusablePrefix (generation_policy.go:26-32)
+        got = warm.forward(prefix, prompt[prefix:])
+        resident = list(prompt)
+        cold = hip.StableLMForwarder(config, tensors)
+        cold.set_kv_bits(16)
+        want = cold.forward(0, prompt)
+        assert np.max(np.abs(got - want)) <= 1e-5
+        cold.close()
+
+
+def test_three_b_shapes_two_layers(hip, oracle):
+    """StableLM-3B layer shapes (hidden 2560, 32 x 80 heads, 25% rotary,
+    MLP 6912, vocab 65536, Q8_0) cut to two layers: per-layer residuals and
+    logits against the oracle within 1e-3 relative to their range, and greedy
+    agreement over 24 tokens after a 64-token prompt."""
+    config = W.validate_stablelm_config(dict(W.STABLELM_3B, num_hidden_layers=2, max_position_embeddings=256))
+    tensors = W.synthetic_stablelm(config, W.Q8_0, seed=7)
+    rng = np.random.default_rng(11)
+    prompt = rng.integers(0, 65536, 64).astype(np.int32)
+    oracle.set_threads(8)
+    ref = oracle.StableLM(config, tensors, capacity=256)
+    ref.trace(True)
+    f = hip.StableLMForwarder(config, tensors)
+    f.trace(True)
+    want = ref.prefill(prompt, 0)
+    got = f.forward(0, prompt)
+    span = float(want.max() - want.min())
+    assert np.max(np.abs(got - want)) <= 1e-3 * span
+    rt, gt = ref.trace_data(), f.trace_read()
+    for layer in range(2):
+        assert np.max(np.abs(rt[layer] - gt[layer])) <= 1e-3 * float(np.ptp(rt[layer]))
+    toks_ref, toks_gpu = [], []
+    lr, lg = want, got
+    for step in range(24):
+        tr, tg = int(np.argmax(lr)), int(np.argmax(lg))
+        toks_ref.append(tr)
+        toks_gpu.append(tg)
+        if tr != tg:
+            break
+        lr = ref.forward(tr, 64 + step)
+        lg = f.forward(64 + step, [tg])
+        assert np.max(np.abs(lg - lr)) <= 1e-3 * float(np.ptp(lr))
+    assert toks_gpu == toks_ref

@@ -1,0 +1,685 @@
+// C ABI of the gfx950 backend: weight upload, the StableLM forwarder and the
+// single-matrix entry points. The forward orchestration follows
+// StableLM.forward (stablelm.go:332-387) for one token and StableLM.prefill
+// (prefill.go:33-115) for longer suffixes, with the resident-prefix
+// semantics of nativeMLX.forward (mlx_native.go:324-495).
+#include "tinyoai_hip.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "kernels.h"
+#include "model.h"
+
+namespace tinyoai {
+
+thread_local std::string g_error;
+
+int fail(int code, const char *fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_error = buf;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char *what) {
+  return fail(TINYOAI_EDEVICE, "%s: %s", what, hipGetErrorString(e));
+}
+
+// ---------------------------------------------------------------- matrices
+int64_t gguf_bytes(int32_t dtype, int64_t rows, int64_t cols) {
+  const int64_t n = rows * cols;
+  switch (dtype) {
+    case FMT_F32: return n * 4;
+    case FMT_F16: case FMT_BF16: return n * 2;
+    case FMT_Q8_0: return cols % 32 ? -1 : n / 32 * 34;
+  }
+  return -1;
+}
+
+DevMatrix::~DevMatrix() {
+  if (mem) hipFree(mem);
+}
+
+int DevMatrix::upload(int32_t dtype, int64_t rows, int64_t cols, const void *data, uint64_t nbytes,
+                      hipStream_t st) {
+  if (rows <= 0 || cols <= 0 || rows > INT32_MAX || cols > INT32_MAX)
+    return fail(TINYOAI_EINVAL, "invalid matrix shape [%lld, %lld]", (long long)rows, (long long)cols);
+  if (dtype != FMT_F32 && dtype != FMT_F16 && dtype != FMT_BF16 && dtype != FMT_Q8_0)
+    return fail(TINYOAI_EINVAL, "unsupported tensor type %d", dtype);
+  const int64_t want = gguf_bytes(dtype, rows, cols);
+  if (want < 0) return fail(TINYOAI_EINVAL, "Q8_0 rows must be divisible by 32");
+  if ((int64_t)nbytes != want)
+    return fail(TINYOAI_EINVAL, "tensor [%lld, %lld] of type %d needs %lld bytes, got %llu", (long long)rows,
+                (long long)cols, dtype, (long long)want, (unsigned long long)nbytes);
+  MatDesc m{};
+  m.fmt = dtype;
+  m.rows = (int32_t)rows;
+  m.cols = (int32_t)cols;
+  const int64_t width = dtype == FMT_F32 ? 4 : (dtype == FMT_Q8_0 ? 1 : 2);
+  m.vstride = (cols * width + 15) / 16 * 16;
+  m.mstride = dtype == FMT_Q8_0 ? cols / 32 * 2 : 0;
+  m.chunks = (int32_t)(m.vstride / 16);
+  const size_t vbytes = (size_t)(m.vstride * rows);
+  const size_t mbytes = (size_t)(m.mstride * rows);
+  const size_t total = (vbytes + 255) / 256 * 256 + mbytes + 256;
+  hipError_t e = hipMalloc(&mem, total);
+  if (e != hipSuccess) return fail(TINYOAI_ENOMEM, "hipMalloc(%zu): %s", total, hipGetErrorString(e));
+  bytes = total;
+  m.vals = (const uint8_t *)mem;
+  m.meta = m.mstride ? (const uint8_t *)mem + (vbytes + 255) / 256 * 256 : (const uint8_t *)mem;
+  const bool plain = dtype != FMT_Q8_0 && m.vstride == cols * width;
+  if (plain) {
+    e = hipMemcpyAsync(mem, data, nbytes, hipMemcpyHostToDevice, st);
+    if (e != hipSuccess) return hip_fail(e, "weight upload");
+  } else {
+    void *raw = nullptr;
+    e = hipMalloc(&raw, nbytes);
+    if (e != hipSuccess) return fail(TINYOAI_ENOMEM, "hipMalloc(%llu): %s", (unsigned long long)nbytes, hipGetErrorString(e));
+    e = hipMemcpyAsync(raw, data, nbytes, hipMemcpyHostToDevice, st);
+    if (e == hipSuccess) e = launch_repack(dtype, (const uint8_t *)raw, rows, cols, m, st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    hipFree(raw);
+    if (e != hipSuccess) return hip_fail(e, "weight repack");
+  }
+  desc = m;
+  return TINYOAI_OK;
+}
+
+// ---------------------------------------------------------------- profiling
+Profiler::~Profiler() {
+  for (hipEvent_t e : pool) hipEventDestroy(e);
+}
+
+hipEvent_t Profiler::next() {
+  if (used == pool.size()) {
+    hipEvent_t e;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    pool.push_back(e);
+  }
+  return pool[used++];
+}
+
+void Profiler::begin(int stage, hipStream_t st) {
+  if (!on) return;
+  marks.emplace_back(stage, used);
+  hipEventRecord(next(), st);
+}
+
+void Profiler::end(hipStream_t st) {
+  if (!on) return;
+  hipEventRecord(next(), st);
+}
+
+// Called after the stream has synchronized.
+void Profiler::resolve() {
+  for (auto &m : marks) {
+    float t = 0;
+    if (m.second + 1 < used && hipEventElapsedTime(&t, pool[m.second], pool[m.second + 1]) == hipSuccess) {
+      ms[m.first] += t;
+      count[m.first]++;
+    }
+  }
+  marks.clear();
+  used = 0;
+}
+
+void Profiler::clear() {
+  for (int i = 0; i < ST_COUNT; i++) { ms[i] = 0; count[i] = 0; }
+}
+
+// ---------------------------------------------------------------- StableLM
+StableModel::~StableModel() {
+  free_kv();
+  for (void *p : buffers) hipFree(p);
+  if (h_pinned) hipHostFree(h_pinned);
+  if (params_copied) hipEventDestroy(params_copied);
+  if (stream) hipStreamDestroy(stream);
+}
+
+int StableModel::alloc(void **p, size_t bytes) {
+  hipError_t e = hipMalloc(p, std::max<size_t>(bytes, 256));
+  if (e != hipSuccess) return fail(TINYOAI_ENOMEM, "hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
+  buffers.push_back(*p);
+  return TINYOAI_OK;
+}
+
+void StableModel::free_kv() {
+  for (auto &l : kv) {
+    if (l.k) hipFree(l.k);
+    if (l.v) hipFree(l.v);
+  }
+  kv.clear();
+  cap = 0;
+  offset = 0;
+}
+
+// RoPE table with stableRotate's arithmetic (stablelm.go:311-318): float32
+// frequency and angle, float64 sincos rounded to float32.
+static std::vector<float> rope_table(int max_pos, int rot, double theta) {
+  std::vector<float> t((size_t)max_pos * (rot / 2) * 2);
+  for (int i = 0; i < rot / 2; i++) {
+    const float expo = (float)(2 * i) / (float)rot;
+    const float power = (float)std::pow((double)(float)theta, (double)expo);
+    const float inv = 1.0f / power;
+    for (int p = 0; p < max_pos; p++) {
+      const float angle = (float)p * inv;
+      t[((size_t)p * (rot / 2) + i) * 2] = (float)std::cos((double)angle);
+      t[((size_t)p * (rot / 2) + i) * 2 + 1] = (float)std::sin((double)angle);
+    }
+  }
+  return t;
+}
+
+int StableModel::init(const tinyoai_stablelm_config &c, const tinyoai_tensor *tensors, int n) {
+  cfg = c;
+  if (c.hidden_size <= 0 || c.intermediate_size <= 0 || c.num_hidden_layers <= 0 || c.num_attention_heads <= 0 ||
+      c.num_key_value_heads <= 0 || c.vocab_size <= 0 || c.max_position_embeddings <= 0 ||
+      c.hidden_size % c.num_attention_heads || c.num_attention_heads % c.num_key_value_heads)
+    return fail(TINYOAI_EINVAL, "invalid StableLM dimensions");
+  const int hd = c.hidden_size / c.num_attention_heads;
+  const double rotary = hd * c.partial_rotary_factor;
+  if (!(c.layer_norm_eps > 0) || !(c.rope_theta > 0) || !(c.partial_rotary_factor > 0) ||
+      c.partial_rotary_factor > 1 || rotary != std::trunc(rotary) || (int)rotary % 2 || rotary < 2)
+    return fail(TINYOAI_EINVAL, "invalid LayerNorm or partial RoPE settings");
+  if (hd % 2 || (hd != 8 && hd != 16 && hd != 32 && hd != 64 && hd != 80 && hd != 96 && hd != 128))
+    return fail(TINYOAI_EINVAL, "head width %d is not supported by the attention kernels", hd);
+  dims = StableDims{c.hidden_size, hd, (int)rotary, c.num_attention_heads, c.num_key_value_heads,
+                    c.intermediate_size, c.vocab_size, c.layer_norm_eps, (float)std::sqrt((double)hd)};
+  hipError_t e = hipStreamCreateWithFlags(&stream, hipStreamNonBlocking);
+  if (e != hipSuccess) return hip_fail(e, "hipStreamCreate");
+
+  std::map<std::string, const tinyoai_tensor *> by_name;
+  for (int i = 0; i < n; i++) {
+    if (!tensors[i].name) return fail(TINYOAI_EINVAL, "tensor %d has no name", i);
+    if (!by_name.emplace(tensors[i].name, &tensors[i]).second)
+      return fail(TINYOAI_EINVAL, "duplicate tensor %s", tensors[i].name);
+  }
+  const int d = c.hidden_size, I = c.intermediate_size, kvw = hd * c.num_key_value_heads;
+  auto load = [&](const std::string &name, int64_t rows, int64_t cols, DevMatrix &dst) -> int {
+    auto it = by_name.find(name);
+    if (it == by_name.end()) return fail(TINYOAI_EINVAL, "missing tensor %s", name.c_str());
+    const tinyoai_tensor *t = it->second;
+    if (t->rows != rows || t->cols != cols)
+      return fail(TINYOAI_EINVAL, "tensor %s: shape [%lld %lld], want [%lld %lld]", name.c_str(), (long long)t->rows,
+                  (long long)t->cols, (long long)rows, (long long)cols);
+    int rc = dst.upload(t->dtype, rows, cols, t->data, t->nbytes, stream);
+    if (rc) g_error = "tensor " + name + ": " + g_error;
+    return rc;
+  };
+  // Norm vectors are kept as fp32 (weight.at(i) of any dtype, stablelm.go:303).
+  auto load_vec = [&](const std::string &name, const float **dst) -> int {
+    DevMatrix tmp;
+    int rc = load(name, 1, d, tmp);
+    if (rc) return rc;
+    float *out;
+    if ((rc = alloc((void **)&out, (size_t)d * 4))) return rc;
+    hipError_t e2 = launch_read_values(tmp.desc, 0, d, out, stream);
+    if (e2 == hipSuccess) e2 = hipStreamSynchronize(stream);
+    if (e2 != hipSuccess) return hip_fail(e2, "norm upload");
+    *dst = out;
+    return TINYOAI_OK;
+  };
+  int rc;
+  if ((rc = load("model.embed_tokens.weight", c.vocab_size, d, embed))) return rc;
+  if ((rc = load("lm_head.weight", c.vocab_size, d, head))) return rc;
+  if ((rc = load_vec("model.norm.weight", &norm_w))) return rc;
+  if ((rc = load_vec("model.norm.bias", &norm_b))) return rc;
+  mats.resize((size_t)c.num_hidden_layers * 7);
+  layers.resize(c.num_hidden_layers);
+  for (int l = 0; l < c.num_hidden_layers; l++) {
+    const std::string p = "model.layers." + std::to_string(l) + ".";
+    DevMatrix *m = &mats[(size_t)l * 7];
+    if ((rc = load(p + "self_attn.q_proj.weight", d, d, m[0]))) return rc;
+    if ((rc = load(p + "self_attn.k_proj.weight", kvw, d, m[1]))) return rc;
+    if ((rc = load(p + "self_attn.v_proj.weight", kvw, d, m[2]))) return rc;
+    if ((rc = load(p + "self_attn.o_proj.weight", d, d, m[3]))) return rc;
+    if ((rc = load(p + "mlp.gate_proj.weight", I, d, m[4]))) return rc;
+    if ((rc = load(p + "mlp.up_proj.weight", I, d, m[5]))) return rc;
+    if ((rc = load(p + "mlp.down_proj.weight", d, I, m[6]))) return rc;
+    LayerDev &L = layers[l];
+    L.q = m[0].desc; L.k = m[1].desc; L.v = m[2].desc; L.o = m[3].desc;
+    L.gate = m[4].desc; L.up = m[5].desc; L.down = m[6].desc;
+    if (L.q.fmt != L.k.fmt || L.q.fmt != L.v.fmt || L.gate.fmt != L.up.fmt)
+      return fail(TINYOAI_EINVAL, "layer %d: q/k/v and gate/up must share their storage formats", l);
+    if ((rc = load_vec(p + "input_layernorm.weight", &L.ln_w))) return rc;
+    if ((rc = load_vec(p + "input_layernorm.bias", &L.ln_b))) return rc;
+  }
+  // Device workspaces.
+  const int maxp = c.max_position_embeddings;
+  const std::vector<float> rt = rope_table(maxp, dims.rot, c.rope_theta);
+  if ((rc = alloc((void **)&rope, rt.size() * 4))) return rc;
+  e = hipMemcpyAsync(rope, rt.data(), rt.size() * 4, hipMemcpyHostToDevice, stream);
+  if (e != hipSuccess) return hip_fail(e, "rope upload");
+  chunk = std::min(512, maxp);
+  const size_t w_att = (size_t)dims.heads * hd;
+  if ((rc = alloc((void **)&x, (size_t)d * 4)) || (rc = alloc((void **)&qbuf, w_att * 4)) ||
+      (rc = alloc((void **)&mbuf, (size_t)I * 4)) || (rc = alloc((void **)&abuf, w_att * 4)) ||
+      (rc = alloc((void **)&logits_dev, (size_t)c.vocab_size * 4)) || (rc = alloc((void **)&params, 4096)) ||
+      (rc = alloc((void **)&trace_dev, (size_t)c.num_hidden_layers * d * 4)))
+    return rc;
+  max_splits = maxp / 64 + 1;
+  if ((rc = alloc((void **)&counters, (size_t)chunk * dims.heads * 4))) return rc;
+  e = hipMemsetAsync(counters, 0, (size_t)chunk * dims.heads * 4, stream);
+  if (e != hipSuccess) return hip_fail(e, "counter init");
+  if ((rc = alloc((void **)&partials, (size_t)chunk * dims.heads * max_splits * (hd + 2) * 4))) return rc;
+  const size_t B = chunk;
+  if ((rc = alloc((void **)&X, B * d * 4)) || (rc = alloc((void **)&H, B * d * 4)) ||
+      (rc = alloc((void **)&Q, B * w_att * 4)) || (rc = alloc((void **)&K, B * kvw * 4)) ||
+      (rc = alloc((void **)&V, B * kvw * 4)) || (rc = alloc((void **)&G, B * I * 4)) ||
+      (rc = alloc((void **)&U, B * I * 4)) || (rc = alloc((void **)&A, B * w_att * 4)) ||
+      (rc = alloc((void **)&P, B * d * 4)) || (rc = alloc((void **)&D, B * d * 4)))
+    return rc;
+  e = hipEventCreateWithFlags(&params_copied, hipEventDisableTiming);
+  if (e != hipSuccess) return hip_fail(e, "hipEventCreate");
+  e = hipHostMalloc(&h_pinned, (size_t)c.vocab_size * 4 + 4096 + (size_t)chunk * 4 + 64, hipHostMallocDefault);
+  if (e != hipSuccess) return fail(TINYOAI_ENOMEM, "hipHostMalloc: %s", hipGetErrorString(e));
+  e = hipStreamSynchronize(stream);
+  if (e != hipSuccess) return hip_fail(e, "model upload");
+  const int cus = device_cu_count();
+  grid_in = cus * 4;
+  grid_out = cus * 2;
+  grid_head = cus * 4;
+  return TINYOAI_OK;
+}
+
+// Grows KV to `needed` positions: power-of-two capacity capped at the
+// context (stableContext.resize, prefix_cache.go:14-43), never below the
+// LimitCache reservation; valid positions are copied head by head (growKV,
+// kv_cache.go:101-109).
+int StableModel::ensure_kv(int needed) {
+  if (needed <= cap) return TINYOAI_OK;
+  int want = 1;
+  while (want < needed) want *= 2;
+  want = std::max(want, reserve);
+  want = std::min(want, cfg.max_position_embeddings);
+  const size_t esz = kv_half ? 2 : 4;
+  const size_t per_head = (size_t)dims.hd * esz;
+  std::vector<KVDev> grown(cfg.num_hidden_layers);
+  for (auto &l : grown) {
+    const size_t bytes = (size_t)dims.kv_heads * want * per_head;
+    hipError_t e = hipMalloc(&l.k, bytes);
+    if (e == hipSuccess) e = hipMalloc(&l.v, bytes);
+    if (e != hipSuccess) {
+      for (auto &g : grown) { if (g.k) hipFree(g.k); if (g.v) hipFree(g.v); }
+      return fail(TINYOAI_ENOMEM, "KV allocation of %d positions: %s", want, hipGetErrorString(e));
+    }
+    l.cap = want;
+    l.half = kv_half;
+  }
+  for (int l = 0; l < (int)kv.size() && offset > 0; l++)
+    for (int h = 0; h < dims.kv_heads; h++) {
+      const size_t src = (size_t)h * cap * per_head, dst = (size_t)h * want * per_head;
+      hipMemcpyAsync((char *)grown[l].k + dst, (char *)kv[l].k + src, offset * per_head, hipMemcpyDeviceToDevice, stream);
+      hipMemcpyAsync((char *)grown[l].v + dst, (char *)kv[l].v + src, offset * per_head, hipMemcpyDeviceToDevice, stream);
+    }
+  hipError_t e = hipStreamSynchronize(stream);
+  const int keep = offset;
+  free_kv();
+  kv = grown;
+  cap = want;
+  offset = keep;
+  return e == hipSuccess ? TINYOAI_OK : hip_fail(e, "KV growth");
+}
+
+#define TRY_HIP(expr, what)                 \
+  do {                                      \
+    hipError_t e_ = (expr);                 \
+    if (e_ != hipSuccess) return hip_fail(e_, what); \
+  } while (0)
+
+// A kernel launch attributed to a profiling stage.
+#define STAGE(stage, expr, what)       \
+  do {                                 \
+    prof.begin(stage, stream);         \
+    TRY_HIP(expr, what);               \
+    prof.end(stream);                  \
+  } while (0)
+
+// Copies `count` ints (head[0..nh) then ids) into the device parameter
+// block through the pinned slot, first waiting for the slot's previous copy.
+int StableModel::upload_params(const int *head_vals, int nh, const int32_t *ids, int n) {
+  int *hp = (int *)((char *)h_pinned + (size_t)cfg.vocab_size * 4);
+  if (params_copied) TRY_HIP(hipEventSynchronize(params_copied), "parameter slot");
+  for (int i = 0; i < nh; i++) hp[i] = head_vals[i];
+  if (n) memcpy(hp + 16, ids, (size_t)n * 4);
+  TRY_HIP(hipMemcpyAsync(params, hp, (size_t)(n ? 16 + n : nh) * 4, hipMemcpyHostToDevice, stream), "parameters");
+  TRY_HIP(hipEventRecord(params_copied, stream), "parameter event");
+  return TINYOAI_OK;
+}
+
+int StableModel::decode_step(int token, int pos, bool want_logits) {
+  const int vals[2] = {token, pos};
+  if (int rc = upload_params(vals, 2, nullptr, 0)) return rc;
+  STAGE(ST_EMBED, launch_embed(embed.desc, params, 1, x, stream), "embed");
+  for (int l = 0; l < cfg.num_hidden_layers; l++) {
+    STAGE(ST_DECODE_IN,
+          launch_decode_in(layers[l], dims, kv[l], x, rope, params + 1, qbuf, mbuf, grid_in, stream), "decode_in");
+    STAGE(ST_ATTENTION, launch_attention(dims, kv[l], qbuf, params + 1, 1, pos, partials, counters, abuf, stream),
+          "attention");
+    STAGE(ST_DECODE_OUT, launch_decode_out(layers[l], dims, abuf, mbuf, x, grid_out, stream), "decode_out");
+    if (tracing) TRY_HIP(launch_copy_row(x, trace_dev + (size_t)l * dims.d, dims.d, stream), "trace");
+  }
+  if (want_logits)
+    STAGE(ST_LM_HEAD, launch_ln_matvec(head.desc, norm_w, norm_b, dims.eps, x, logits_dev, grid_head, stream),
+          "lm_head");
+  return TINYOAI_OK;
+}
+
+int StableModel::prefill_chunk(const int32_t *ids, int n, int start, bool want_logits) {
+  const int vals[1] = {start};
+  if (int rc = upload_params(vals, 1, ids, n)) return rc;
+  const int *d_pos0 = params, *d_ids = params + 16;
+  const int d = dims.d, I = dims.inter;
+  STAGE(ST_EMBED, launch_embed(embed.desc, d_ids, n, X, stream), "embed");
+  for (int l = 0; l < cfg.num_hidden_layers; l++) {
+    const LayerDev &w = layers[l];
+    STAGE(ST_PREFILL_NORM, launch_layer_norm_rows(X, w.ln_w, w.ln_b, dims.eps, n, d, H, stream), "layer_norm");
+    STAGE(ST_PREFILL_GEMM, launch_gemm(w.q, H, n, Q, stream), "q_proj");
+    STAGE(ST_PREFILL_GEMM, launch_gemm(w.k, H, n, K, stream), "k_proj");
+    STAGE(ST_PREFILL_GEMM, launch_gemm(w.v, H, n, V, stream), "v_proj");
+    STAGE(ST_PREFILL_ROPE, launch_rope_store(dims, kv[l], Q, K, V, rope, d_pos0, n, stream), "rope_store");
+    STAGE(ST_PREFILL_ATTENTION,
+          launch_attention(dims, kv[l], Q, d_pos0, n, start + n - 1, partials, counters, A, stream), "attention");
+    STAGE(ST_PREFILL_GEMM, launch_gemm(w.o, A, n, P, stream), "o_proj");
+    STAGE(ST_PREFILL_GEMM, launch_gemm(w.gate, H, n, G, stream), "gate_proj");
+    STAGE(ST_PREFILL_GEMM, launch_gemm(w.up, H, n, U, stream), "up_proj");
+    STAGE(ST_PREFILL_ELEMENTWISE, launch_silu_gate(G, U, (int64_t)n * I, stream), "silu_gate");
+    STAGE(ST_PREFILL_GEMM, launch_gemm(w.down, G, n, D, stream), "down_proj");
+    STAGE(ST_PREFILL_ELEMENTWISE, launch_residual(X, P, D, (int64_t)n * d, stream), "residual");
+    if (tracing) TRY_HIP(launch_copy_row(X + (size_t)(n - 1) * d, trace_dev + (size_t)l * d, d, stream), "trace");
+  }
+  if (want_logits) {
+    TRY_HIP(launch_copy_row(X + (size_t)(n - 1) * d, x, d, stream), "last row");
+    STAGE(ST_LM_HEAD, launch_ln_matvec(head.desc, norm_w, norm_b, dims.eps, x, logits_dev, grid_head, stream),
+          "lm_head");
+  }
+  return TINYOAI_OK;
+}
+
+int StableModel::forward(int prefix, const int32_t *tokens, int n, bool want_logits, float *logits) {
+  if (prefix < 0 || prefix > offset || n <= 0 || !tokens || prefix + n > cfg.max_position_embeddings)
+    return fail(TINYOAI_EINVAL, "invalid cached prefix or context length (prefix %d, offset %d, n %d)", prefix,
+                offset, n);
+  if (want_logits && !logits) return fail(TINYOAI_EINVAL, "logits output is required");
+  for (int i = 0; i < n; i++)
+    if (tokens[i] < 0 || tokens[i] >= cfg.vocab_size) return fail(TINYOAI_EINVAL, "invalid token %d", tokens[i]);
+  offset = prefix;
+  int rc = ensure_kv(prefix + n);
+  if (rc) return rc;
+  for (int done = 0; done < n && !rc;) {
+    const int m = std::min(chunk, n - done);
+    const bool last = done + m == n;
+    if (m == 1)
+      rc = decode_step(tokens[done], prefix + done, last && want_logits);
+    else
+      rc = prefill_chunk(tokens + done, m, prefix + done, last && want_logits);
+    done += m;
+  }
+  if (!rc && want_logits) {
+    hipError_t e = hipMemcpyAsync(h_pinned, logits_dev, (size_t)cfg.vocab_size * 4, hipMemcpyDeviceToHost, stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(stream);
+    if (e != hipSuccess) rc = hip_fail(e, "logits");
+    else memcpy(logits, h_pinned, (size_t)cfg.vocab_size * 4);
+  } else if (!rc) {
+    hipError_t e = hipStreamSynchronize(stream);
+    if (e != hipSuccess) rc = hip_fail(e, "forward");
+  }
+  if (rc) {
+    std::string msg = g_error;
+    hipStreamSynchronize(stream);
+    prof.marks.clear();
+    prof.used = 0;
+    free_kv();
+    g_error = msg;
+    return rc;
+  }
+  prof.resolve();
+  offset = prefix + n;
+  return TINYOAI_OK;
+}
+
+}  // namespace tinyoai
+
+using namespace tinyoai;
+
+struct tinyoai_model {
+  std::unique_ptr<StableModel> stable;
+};
+
+struct tinyoai_weight {
+  DevMatrix m;
+  hipStream_t stream = nullptr;
+  ~tinyoai_weight() {
+    if (stream) hipStreamDestroy(stream);
+  }
+};
+
+extern "C" {
+
+const char *tinyoai_last_error(void) { return g_error.c_str(); }
+
+int tinyoai_stablelm_load(const tinyoai_stablelm_config *config, const tinyoai_tensor *tensors, int32_t n_tensors,
+                          tinyoai_model **out) {
+  if (!config || !tensors || !out || n_tensors <= 0) return fail(TINYOAI_EINVAL, "invalid load arguments");
+  *out = nullptr;
+  auto h = std::make_unique<tinyoai_model>();
+  h->stable = std::make_unique<StableModel>();
+  int rc = h->stable->init(*config, tensors, n_tensors);
+  if (rc) return rc;
+  *out = h.release();
+  return TINYOAI_OK;
+}
+
+int tinyoai_stablelm_forward(tinyoai_model *m, int32_t prefix, const int32_t *tokens, int32_t n, int32_t want_logits,
+                             float *logits) {
+  if (!m || !m->stable) return fail(TINYOAI_EINVAL, "not a StableLM handle");
+  return m->stable->forward(prefix, tokens, n, want_logits != 0, logits);
+}
+
+int tinyoai_stablelm_set_kv_bits(tinyoai_model *m, int32_t bits, int32_t *cleared) {
+  if (!m || !m->stable) return fail(TINYOAI_EINVAL, "not a StableLM handle");
+  if (bits != 16 && bits != 32) return fail(TINYOAI_EINVAL, "KV bits must be 16 or 32");
+  StableModel &s = *m->stable;
+  const int half = bits == 16;
+  int c = 0;
+  if (half != s.kv_half) {
+    hipStreamSynchronize(s.stream);
+    s.free_kv();
+    s.kv_half = half;
+    c = 1;
+  }
+  if (cleared) *cleared = c;
+  return TINYOAI_OK;
+}
+
+int tinyoai_stablelm_limit_cache(tinyoai_model *m, int32_t limit, int32_t *cleared) {
+  if (!m || !m->stable) return fail(TINYOAI_EINVAL, "not a StableLM handle");
+  StableModel &s = *m->stable;
+  if (limit <= 0 || limit > s.cfg.max_position_embeddings) return fail(TINYOAI_EINVAL, "invalid cache limit %d", limit);
+  int c = 0;
+  s.reserve = limit;
+  if (s.cap > limit) {
+    hipStreamSynchronize(s.stream);
+    s.free_kv();
+    c = 1;
+  }
+  if (cleared) *cleared = c;
+  return TINYOAI_OK;
+}
+
+int tinyoai_stablelm_reset(tinyoai_model *m) {
+  if (!m || !m->stable) return fail(TINYOAI_EINVAL, "not a StableLM handle");
+  hipStreamSynchronize(m->stable->stream);
+  m->stable->free_kv();
+  return TINYOAI_OK;
+}
+
+int tinyoai_stablelm_offset(const tinyoai_model *m) {
+  if (!m || !m->stable) return fail(TINYOAI_EINVAL, "not a StableLM handle");
+  return m->stable->offset;
+}
+
+int tinyoai_stablelm_close(tinyoai_model *m) {
+  if (!m) return TINYOAI_OK;
+  if (m->stable) hipStreamSynchronize(m->stable->stream);
+  delete m;
+  return TINYOAI_OK;
+}
+
+int tinyoai_stablelm_read_kv(tinyoai_model *m, int32_t layer, int32_t kv_head, int32_t n, float *keys, float *values) {
+  if (!m || !m->stable) return fail(TINYOAI_EINVAL, "not a StableLM handle");
+  StableModel &s = *m->stable;
+  if (layer < 0 || layer >= s.cfg.num_hidden_layers || kv_head < 0 || kv_head >= s.dims.kv_heads || n < 0 ||
+      n > s.offset || !keys || !values)
+    return fail(TINYOAI_EINVAL, "invalid KV read");
+  const int hd = s.dims.hd;
+  std::vector<uint8_t> buf((size_t)n * hd * 4);
+  for (int which = 0; which < 2; which++) {
+    const KVDev &k = s.kv[layer];
+    const size_t esz = k.half ? 2 : 4;
+    const char *src = (const char *)(which ? k.v : k.k) + (size_t)kv_head * k.cap * hd * esz;
+    hipError_t e = hipMemcpy(buf.data(), src, (size_t)n * hd * esz, hipMemcpyDeviceToHost);
+    if (e != hipSuccess) return hip_fail(e, "KV read");
+    float *dst = which ? values : keys;
+    for (size_t i = 0; i < (size_t)n * hd; i++) {
+      if (k.half) {
+        uint16_t h;
+        memcpy(&h, buf.data() + i * 2, 2);
+        dst[i] = (float)*reinterpret_cast<const _Float16 *>(&h);
+      } else {
+        memcpy(&dst[i], buf.data() + i * 4, 4);
+      }
+    }
+  }
+  return TINYOAI_OK;
+}
+
+int tinyoai_stablelm_trace(tinyoai_model *m, int32_t enable) {
+  if (!m || !m->stable) return fail(TINYOAI_EINVAL, "not a StableLM handle");
+  m->stable->tracing = enable != 0;
+  return TINYOAI_OK;
+}
+
+int tinyoai_stablelm_trace_read(tinyoai_model *m, float *residual) {
+  if (!m || !m->stable || !residual) return fail(TINYOAI_EINVAL, "invalid trace read");
+  StableModel &s = *m->stable;
+  hipError_t e = hipStreamSynchronize(s.stream);
+  if (e == hipSuccess)
+    e = hipMemcpy(residual, s.trace_dev, (size_t)s.cfg.num_hidden_layers * s.dims.d * 4, hipMemcpyDeviceToHost);
+  return e == hipSuccess ? TINYOAI_OK : hip_fail(e, "trace read");
+}
+
+int tinyoai_stablelm_profile(tinyoai_model *m, int32_t enable) {
+  if (!m || !m->stable) return fail(TINYOAI_EINVAL, "not a StableLM handle");
+  m->stable->prof.on = enable != 0;
+  m->stable->prof.clear();
+  return TINYOAI_OK;
+}
+
+int tinyoai_stablelm_profile_read(tinyoai_model *m, double *ms, int64_t *counts, int32_t n_stages) {
+  if (!m || !m->stable || !ms || !counts || n_stages < ST_COUNT) return fail(TINYOAI_EINVAL, "invalid profile read");
+  for (int i = 0; i < ST_COUNT; i++) {
+    ms[i] = m->stable->prof.ms[i];
+    counts[i] = m->stable->prof.count[i];
+  }
+  return ST_COUNT;
+}
+
+int tinyoai_weight_upload(int32_t dtype, int64_t rows, int64_t cols, const void *data, uint64_t nbytes,
+                          tinyoai_weight **out) {
+  if (!out || !data) return fail(TINYOAI_EINVAL, "invalid weight upload arguments");
+  *out = nullptr;
+  auto w = std::make_unique<tinyoai_weight>();
+  hipError_t e = hipStreamCreateWithFlags(&w->stream, hipStreamNonBlocking);
+  if (e != hipSuccess) return hip_fail(e, "hipStreamCreate");
+  int rc = w->m.upload(dtype, rows, cols, data, nbytes, w->stream);
+  if (rc) return rc;
+  e = hipStreamSynchronize(w->stream);
+  if (e != hipSuccess) return hip_fail(e, "weight upload");
+  *out = w.release();
+  return TINYOAI_OK;
+}
+
+int tinyoai_weight_read_values(tinyoai_weight *w, int64_t offset, int64_t n, float *out) {
+  if (!w || !out || offset < 0 || n < 0 || offset + n > (int64_t)w->m.desc.rows * w->m.desc.cols)
+    return fail(TINYOAI_EINVAL, "invalid readValues span");
+  if (n == 0) return TINYOAI_OK;
+  float *dev;
+  hipError_t e = hipMalloc(&dev, (size_t)n * 4);
+  if (e != hipSuccess) return fail(TINYOAI_ENOMEM, "hipMalloc: %s", hipGetErrorString(e));
+  e = launch_read_values(w->m.desc, offset, n, dev, w->stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(out, dev, (size_t)n * 4, hipMemcpyDeviceToHost, w->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(w->stream);
+  hipFree(dev);
+  return e == hipSuccess ? TINYOAI_OK : hip_fail(e, "readValues");
+}
+
+int tinyoai_weight_mul_device(tinyoai_weight *w, const float *x_dev, int32_t n, float *out_dev, void *stream) {
+  if (!w || !x_dev || !out_dev || n <= 0) return fail(TINYOAI_EINVAL, "invalid product arguments");
+  hipStream_t st = stream ? (hipStream_t)stream : w->stream;
+  hipError_t e;
+  if (n == 1)
+    e = launch_ln_matvec(w->m.desc, nullptr, nullptr, 0.0, x_dev, out_dev, device_cu_count() * 4, st);
+  else
+    e = launch_gemm(w->m.desc, x_dev, n, out_dev, st);
+  return e == hipSuccess ? TINYOAI_OK : hip_fail(e, "product launch");
+}
+
+int tinyoai_weight_mul(tinyoai_weight *w, const float *x, int32_t n, float *out) {
+  if (!w || !x || !out || n <= 0) return fail(TINYOAI_EINVAL, "invalid product arguments");
+  const MatDesc &m = w->m.desc;
+  float *dx = nullptr, *dout = nullptr;
+  hipError_t e = hipMalloc(&dx, (size_t)n * m.cols * 4);
+  if (e == hipSuccess) e = hipMalloc(&dout, (size_t)n * m.rows * 4);
+  if (e != hipSuccess) {
+    hipFree(dx);
+    return fail(TINYOAI_ENOMEM, "hipMalloc: %s", hipGetErrorString(e));
+  }
+  e = hipMemcpyAsync(dx, x, (size_t)n * m.cols * 4, hipMemcpyHostToDevice, w->stream);
+  int rc = e == hipSuccess ? tinyoai_weight_mul_device(w, dx, n, dout, w->stream) : hip_fail(e, "product input");
+  if (!rc) {
+    e = hipMemcpyAsync(out, dout, (size_t)n * m.rows * 4, hipMemcpyDeviceToHost, w->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(w->stream);
+    if (e != hipSuccess) rc = hip_fail(e, "product output");
+  }
+  hipStreamSynchronize(w->stream);
+  hipFree(dx);
+  hipFree(dout);
+  return rc;
+}
+
+int tinyoai_weight_free(tinyoai_weight *w) {
+  if (w) {
+    hipStreamSynchronize(w->stream);
+    delete w;
+  }
+  return TINYOAI_OK;
+}
+
+int tinyoai_llama_load(const tinyoai_llama_config *, const float *, uint64_t, tinyoai_model **out) {
+  if (out) *out = nullptr;
+  return fail(TINYOAI_EINVAL, "legacy Llama backend is not built yet");
+}
+int tinyoai_llama_forward(tinyoai_model *, int32_t, const int32_t *, int32_t, int32_t, float *) {
+  return fail(TINYOAI_EINVAL, "legacy Llama backend is not built yet");
+}
+int tinyoai_llama_reset(tinyoai_model *) { return fail(TINYOAI_EINVAL, "legacy Llama backend is not built yet"); }
+int tinyoai_llama_close(tinyoai_model *m) {
+  delete m;
+  return TINYOAI_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,101 @@
+// Host-side model state behind the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <string>
+#include <vector>
+
+#include "kernels.h"
+#include "tinyoai_hip.h"
+
+namespace tinyoai {
+
+extern thread_local std::string g_error;
+int fail(int code, const char *fmt, ...);
+int hip_fail(hipError_t e, const char *what);
+
+// One weight matrix in HBM, in the plane layout of formats.h.
+struct DevMatrix {
+  MatDesc desc{};
+  void *mem = nullptr;
+  size_t bytes = 0;
+  DevMatrix() = default;
+  DevMatrix(const DevMatrix &) = delete;
+  DevMatrix &operator=(const DevMatrix &) = delete;
+  DevMatrix(DevMatrix &&o) noexcept : desc(o.desc), mem(o.mem), bytes(o.bytes) { o.mem = nullptr; }
+  ~DevMatrix();
+  int upload(int32_t dtype, int64_t rows, int64_t cols, const void *data, uint64_t nbytes, hipStream_t st);
+};
+
+// Stage timings with hipEvents on the model's stream, the device-side
+// counterpart of stableProfile (stablelm.go:227-250). Off by default; when
+// on, every kernel launch is bracketed by two events, resolved after the
+// forward synchronizes.
+enum Stage : int {
+  ST_EMBED, ST_DECODE_IN, ST_ATTENTION, ST_DECODE_OUT, ST_LM_HEAD, ST_PREFILL_NORM, ST_PREFILL_GEMM,
+  ST_PREFILL_ROPE, ST_PREFILL_ATTENTION, ST_PREFILL_ELEMENTWISE, ST_COUNT
+};
+
+struct Profiler {
+  bool on = false;
+  std::vector<hipEvent_t> pool;
+  std::vector<std::pair<int, size_t>> marks;  // (stage, index of start event)
+  size_t used = 0;
+  double ms[ST_COUNT] = {};
+  int64_t count[ST_COUNT] = {};
+  ~Profiler();
+  hipEvent_t next();
+  void begin(int stage, hipStream_t st);
+  void end(hipStream_t st);
+  void resolve();
+  void clear();
+};
+
+// A StableLM resident on one GPU with its KV cache (stableState,
+// stablelm.go:216-225, kept in HBM).
+struct StableModel {
+  tinyoai_stablelm_config cfg{};
+  StableDims dims{};
+  hipStream_t stream = nullptr;
+  DevMatrix embed, head;
+  std::vector<DevMatrix> mats;
+  std::vector<LayerDev> layers;
+  const float *norm_w = nullptr, *norm_b = nullptr;
+  float *rope = nullptr;
+
+  // KV: one [kv_heads][cap][hd] K and V buffer per layer.
+  std::vector<KVDev> kv;
+  int cap = 0, offset = 0, reserve = 0, kv_half = 0;
+
+  // decode workspaces
+  float *x = nullptr, *qbuf = nullptr, *mbuf = nullptr, *abuf = nullptr, *logits_dev = nullptr;
+  int *params = nullptr;
+  float *partials = nullptr;
+  unsigned *counters = nullptr;
+  int max_splits = 0;
+  // prefill workspaces, `chunk` tokens each
+  int chunk = 0;
+  float *X = nullptr, *H = nullptr, *Q = nullptr, *K = nullptr, *V = nullptr, *G = nullptr, *U = nullptr,
+        *A = nullptr, *P = nullptr, *D = nullptr;
+  void *h_pinned = nullptr;
+  hipEvent_t params_copied = nullptr;  // last H2D copy out of h_pinned's parameter slot
+  bool tracing = false;
+  float *trace_dev = nullptr;
+  int grid_in = 0, grid_out = 0, grid_head = 0;
+
+  std::vector<void *> buffers;
+  Profiler prof;
+
+  ~StableModel();
+  int init(const tinyoai_stablelm_config &c, const tinyoai_tensor *tensors, int n);
+  int alloc(void **p, size_t bytes);
+  void free_kv();
+  int ensure_kv(int needed);
+  int upload_params(const int *head_vals, int nh, const int32_t *ids, int n);
+  int decode_step(int token, int pos, bool want_logits);
+  int prefill_chunk(const int32_t *ids, int n, int start, bool want_logits);
+  int forward(int prefix, const int32_t *tokens, int n, bool want_logits, float *logits);
+};
+
+}  // namespace tinyoai

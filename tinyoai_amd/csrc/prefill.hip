@@ -1,0 +1,158 @@
+// Prefill-path kernels (a chunk of n tokens) for gfx950: row LayerNorm,
+// the token-major projection GEMM, RoPE + KV store, SiLU-gate and the
+// parallel residual. Follows prefill.go:33-115 step for step.
+#include <algorithm>
+
+#include "kernels.h"
+
+namespace {
+
+__global__ __launch_bounds__(256) void layer_norm_rows_kernel(const float *x, const float *w, const float *b,
+                                                               double eps, int d, float *out) {
+  extern __shared__ __align__(16) float lds[];
+  double *red = reinterpret_cast<double *>(lds + ((d + 3) & ~3));
+  const int64_t row = blockIdx.x;
+  for (int i = threadIdx.x; i < d; i += blockDim.x) lds[i] = x[row * d + i];
+  __syncthreads();
+  layer_norm_lds(lds, d, w, b, eps, red);
+  for (int i = threadIdx.x; i < d; i += blockDim.x) out[row * d + i] = lds[i];
+}
+
+// out[n][N] = x[n][K] * W[N][K]^T, fp32 SIMT tiles of 64 tokens x 64 rows,
+// each thread a 4 x 4 micro-tile; weights dequantized into LDS.
+constexpr int kTM = 64, kTN = 64, kTK = 32;
+
+__global__ __launch_bounds__(256) void gemm_simt_kernel(MatDesc w, const float *__restrict__ x, int n,
+                                                         float *__restrict__ out) {
+  __shared__ float xs[kTK][kTM + 4];
+  __shared__ float ws[kTK][kTN + 4];
+  const int m0 = blockIdx.y * kTM, n0 = blockIdx.x * kTN;
+  const int K = w.cols, N = w.rows;
+  const int tx = threadIdx.x % 16, ty = threadIdx.x / 16;
+  float acc[4][4] = {};
+  for (int k0 = 0; k0 < K; k0 += kTK) {
+    for (int e = threadIdx.x; e < kTM * kTK; e += 256) {
+      const int r = e / kTK, c = e % kTK;
+      const int tok = m0 + r, col = k0 + c;
+      xs[c][r] = (tok < n && col < K) ? x[(int64_t)tok * K + col] : 0.f;
+      const int row = n0 + r;
+      ws[c][r] = (row < N && col < K) ? mat_value(w, row, col) : 0.f;
+    }
+    __syncthreads();
+#pragma unroll 8
+    for (int c = 0; c < kTK; c++) {
+      float a[4], b[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        a[i] = xs[c][ty * 4 + i];
+        b[i] = ws[c][tx * 4 + i];
+      }
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int jj = 0; jj < 4; jj++) acc[i][jj] = fmaf(a[i], b[jj], acc[i][jj]);
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int tok = m0 + ty * 4 + i;
+    if (tok >= n) continue;
+#pragma unroll
+    for (int jj = 0; jj < 4; jj++) {
+      const int row = n0 + tx * 4 + jj;
+      if (row < N) out[(int64_t)tok * N + row] = acc[i][jj];
+    }
+  }
+}
+
+__device__ __forceinline__ void kv_put(void *base, int half, int64_t idx, float v) {
+  if (half)
+    reinterpret_cast<uint16_t *>(base)[idx] = float_to_half(v);
+  else
+    reinterpret_cast<float *>(base)[idx] = v;
+}
+
+// One block per token: stableRotate on q and k (stablelm.go:309-326), then
+// storeKV of every KV head at its absolute position (prefill.go:74-84).
+__global__ void rope_store_kernel(StableDims s, KVDev kv, float *q, const float *k, const float *v,
+                                  const float *rope, const int *pos0) {
+  const int j = blockIdx.x;
+  const int pos = *pos0 + j;
+  const int rh = s.rot / 2, kvw = s.kv_heads * s.hd;
+  float *qj = q + (int64_t)j * s.heads * s.hd;
+  for (int e = threadIdx.x; e < s.heads * rh; e += blockDim.x) {
+    const int h = e / rh, i = e % rh;
+    const float cs = rope[((int64_t)pos * rh + i) * 2], sn = rope[((int64_t)pos * rh + i) * 2 + 1];
+    float *p = qj + h * s.hd;
+    const float a = p[i], b = p[i + rh];
+    p[i] = __fsub_rn(__fmul_rn(a, cs), __fmul_rn(b, sn));
+    p[i + rh] = __fadd_rn(__fmul_rn(b, cs), __fmul_rn(a, sn));
+  }
+  const float *kj = k + (int64_t)j * kvw, *vj = v + (int64_t)j * kvw;
+  for (int e = threadIdx.x; e < kvw; e += blockDim.x) {
+    const int h = e / s.hd, dim = e % s.hd;
+    float val = kj[e];
+    if (dim < s.rot) {
+      const int i = dim % rh;
+      const float cs = rope[((int64_t)pos * rh + i) * 2], sn = rope[((int64_t)pos * rh + i) * 2 + 1];
+      const float a = kj[h * s.hd + i], b = kj[h * s.hd + i + rh];
+      val = dim < rh ? __fsub_rn(__fmul_rn(a, cs), __fmul_rn(b, sn)) : __fadd_rn(__fmul_rn(b, cs), __fmul_rn(a, sn));
+    }
+    const int64_t at = ((int64_t)h * kv.cap + pos) * s.hd + dim;
+    kv_put(kv.k, kv.half, at, val);
+    kv_put(kv.v, kv.half, at, vj[e]);
+  }
+}
+
+__global__ void silu_gate_kernel(float *g, const float *u, int64_t n) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    g[i] = silu_gate(g[i], u[i]);
+}
+
+__global__ void residual_kernel(float *x, const float *p, const float *d, int64_t n) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    x[i] = __fadd_rn(__fadd_rn(x[i], p[i]), d[i]);
+}
+
+__global__ void copy_kernel(const float *src, float *dst, int n) {
+  for (int i = threadIdx.x; i < n; i += blockDim.x) dst[i] = src[i];
+}
+
+int elementwise_grid(int64_t n) { return (int)std::min<int64_t>((n + 255) / 256, 4096); }
+
+}  // namespace
+
+hipError_t launch_layer_norm_rows(const float *x, const float *w, const float *b, double eps, int n, int d,
+                                  float *out, hipStream_t st) {
+  const size_t lds = (size_t)((d + 3) & ~3) * 4 + 8 * sizeof(double);
+  hipLaunchKernelGGL(layer_norm_rows_kernel, dim3(n), dim3(256), lds, st, x, w, b, eps, d, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_gemm(const MatDesc &w, const float *x, int n, float *out, hipStream_t st) {
+  dim3 grid((w.rows + kTN - 1) / kTN, (n + kTM - 1) / kTM);
+  hipLaunchKernelGGL(gemm_simt_kernel, grid, dim3(256), 0, st, w, x, n, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_rope_store(const StableDims &s, const KVDev &kv, float *q, const float *k, const float *v,
+                             const float *rope, const int *pos0, int n, hipStream_t st) {
+  hipLaunchKernelGGL(rope_store_kernel, dim3(n), dim3(256), 0, st, s, kv, q, k, v, rope, pos0);
+  return hipGetLastError();
+}
+
+hipError_t launch_silu_gate(float *g, const float *u, int64_t n, hipStream_t st) {
+  hipLaunchKernelGGL(silu_gate_kernel, dim3(elementwise_grid(n)), dim3(256), 0, st, g, u, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_residual(float *x, const float *p, const float *d, int64_t n, hipStream_t st) {
+  hipLaunchKernelGGL(residual_kernel, dim3(elementwise_grid(n)), dim3(256), 0, st, x, p, d, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_copy_row(const float *src, float *dst, int n, hipStream_t st) {
+  hipLaunchKernelGGL(copy_kernel, dim3(1), dim3(256), 0, st, src, dst, n);
+  return hipGetLastError();
+}

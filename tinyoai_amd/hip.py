@@ -1,0 +1,232 @@
+"""ctypes binding of libtinyoai_hip.so (include/tinyoai_hip.h).
+
+The library must have been built (``python -m tinyoai_amd.build`` or
+``__graft_entry__.build()``); there is no CPU fallback: a missing or
+unloadable library raises immediately.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+from . import weights as W
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libtinyoai_hip.so")
+
+EXPORTS = [
+    "tinyoai_last_error", "tinyoai_stablelm_load", "tinyoai_stablelm_forward", "tinyoai_stablelm_set_kv_bits",
+    "tinyoai_stablelm_limit_cache", "tinyoai_stablelm_reset", "tinyoai_stablelm_offset", "tinyoai_stablelm_close",
+    "tinyoai_stablelm_read_kv", "tinyoai_stablelm_trace", "tinyoai_stablelm_trace_read",
+    "tinyoai_stablelm_profile", "tinyoai_stablelm_profile_read", "tinyoai_llama_load",
+    "tinyoai_llama_forward", "tinyoai_llama_reset", "tinyoai_llama_close", "tinyoai_weight_upload",
+    "tinyoai_weight_read_values", "tinyoai_weight_mul", "tinyoai_weight_mul_device", "tinyoai_weight_free",
+]
+
+
+class TinyoaiError(RuntimeError):
+    pass
+
+
+class Tensor(C.Structure):
+    _fields_ = [("name", C.c_char_p), ("dtype", C.c_int32), ("rows", C.c_int64), ("cols", C.c_int64),
+                ("data", C.c_void_p), ("nbytes", C.c_uint64)]
+
+
+class StableLMConfig(C.Structure):
+    _fields_ = [("vocab_size", C.c_int32), ("hidden_size", C.c_int32), ("intermediate_size", C.c_int32),
+                ("num_hidden_layers", C.c_int32), ("num_attention_heads", C.c_int32),
+                ("num_key_value_heads", C.c_int32), ("max_position_embeddings", C.c_int32),
+                ("bos_token_id", C.c_int32), ("eos_token_id", C.c_int32), ("layer_norm_eps", C.c_double),
+                ("rope_theta", C.c_double), ("partial_rotary_factor", C.c_double)]
+
+
+class LlamaConfig(C.Structure):
+    _fields_ = [("dim", C.c_int32), ("hidden_dim", C.c_int32), ("n_layers", C.c_int32), ("n_heads", C.c_int32),
+                ("n_kv_heads", C.c_int32), ("vocab_size", C.c_int32), ("seq_len", C.c_int32)]
+
+
+_lib = None
+
+
+def lib():
+    """Loads the HIP library; raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise TinyoaiError(f"{LIB_PATH} is missing: build it with `python -m tinyoai_amd.build`")
+        L = C.CDLL(LIB_PATH)
+        P, fp, ip = C.c_void_p, C.POINTER(C.c_float), C.POINTER(C.c_int32)
+        L.tinyoai_last_error.restype = C.c_char_p
+        L.tinyoai_stablelm_load.argtypes = [C.POINTER(StableLMConfig), C.POINTER(Tensor), C.c_int32, C.POINTER(P)]
+        L.tinyoai_stablelm_forward.argtypes = [P, C.c_int32, ip, C.c_int32, C.c_int32, fp]
+        L.tinyoai_stablelm_set_kv_bits.argtypes = [P, C.c_int32, ip]
+        L.tinyoai_stablelm_limit_cache.argtypes = [P, C.c_int32, ip]
+        L.tinyoai_stablelm_reset.argtypes = [P]
+        L.tinyoai_stablelm_offset.argtypes = [P]
+        L.tinyoai_stablelm_close.argtypes = [P]
+        L.tinyoai_stablelm_read_kv.argtypes = [P, C.c_int32, C.c_int32, C.c_int32, fp, fp]
+        L.tinyoai_stablelm_trace.argtypes = [P, C.c_int32]
+        L.tinyoai_stablelm_trace_read.argtypes = [P, fp]
+        L.tinyoai_stablelm_profile.argtypes = [P, C.c_int32]
+        L.tinyoai_stablelm_profile_read.argtypes = [P, C.POINTER(C.c_double), C.POINTER(C.c_int64), C.c_int32]
+        L.tinyoai_llama_load.argtypes = [C.POINTER(LlamaConfig), fp, C.c_uint64, C.POINTER(P)]
+        L.tinyoai_llama_forward.argtypes = [P, C.c_int32, ip, C.c_int32, C.c_int32, fp]
+        L.tinyoai_llama_reset.argtypes = [P]
+        L.tinyoai_llama_close.argtypes = [P]
+        L.tinyoai_weight_upload.argtypes = [C.c_int32, C.c_int64, C.c_int64, P, C.c_uint64, C.POINTER(P)]
+        L.tinyoai_weight_read_values.argtypes = [P, C.c_int64, C.c_int64, fp]
+        L.tinyoai_weight_mul.argtypes = [P, fp, C.c_int32, fp]
+        L.tinyoai_weight_mul_device.argtypes = [P, P, C.c_int32, P, P]
+        L.tinyoai_weight_free.argtypes = [P]
+        _lib = L
+    return _lib
+
+
+def check(rc: int) -> int:
+    if rc < 0:
+        raise TinyoaiError(lib().tinyoai_last_error().decode(errors="replace"))
+    return rc
+
+
+def _fp(a: np.ndarray):
+    assert a.dtype == np.float32 and a.flags.c_contiguous
+    return a.ctypes.data_as(C.POINTER(C.c_float))
+
+
+def _ip(a: np.ndarray):
+    assert a.dtype == np.int32 and a.flags.c_contiguous
+    return a.ctypes.data_as(C.POINTER(C.c_int32))
+
+
+class Weight:
+    """One weight matrix in HBM (weightTensor, safetensors.go:193-280)."""
+
+    def __init__(self, t: W.Tensor):
+        self.rows, self.cols, self.dtype = t.rows, t.cols, t.dtype
+        h = C.c_void_p()
+        check(lib().tinyoai_weight_upload(t.dtype, t.rows, t.cols, t.data.ctypes.data, t.data.size, C.byref(h)))
+        self.h = h
+
+    def read_values(self, offset: int, n: int) -> np.ndarray:
+        out = np.empty(n, np.float32)
+        check(lib().tinyoai_weight_read_values(self.h, offset, n, _fp(out)))
+        return out
+
+    def mul(self, x: np.ndarray) -> np.ndarray:
+        """x [n, cols] -> [n, rows] (mulScratch for n == 1, mulBatch otherwise)."""
+        x = np.ascontiguousarray(np.atleast_2d(x), np.float32)
+        out = np.empty((x.shape[0], self.rows), np.float32)
+        check(lib().tinyoai_weight_mul(self.h, _fp(x), x.shape[0], _fp(out)))
+        return out
+
+    def mul_device(self, x_ptr: int, n: int, out_ptr: int, stream: int = 0) -> None:
+        check(lib().tinyoai_weight_mul_device(self.h, x_ptr, n, out_ptr, stream or None))
+
+    def close(self):
+        if self.h:
+            lib().tinyoai_weight_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+STABLELM_TENSORS = ("model.embed_tokens.weight", "lm_head.weight", "model.norm.weight", "model.norm.bias")
+LAYER_TENSORS = ("input_layernorm.weight", "input_layernorm.bias", "self_attn.q_proj.weight",
+                 "self_attn.k_proj.weight", "self_attn.v_proj.weight", "self_attn.o_proj.weight",
+                 "mlp.gate_proj.weight", "mlp.up_proj.weight", "mlp.down_proj.weight")
+
+
+class StableLMForwarder:
+    """The HIP StableLM forwarder: the mlxForwarder contract (mlx.go:45-51)
+    plus SetKVBits / LimitCache (mlx_kv.go:78-91, mlx_native.go:231-244)."""
+
+    def __init__(self, config: dict, tensors: dict):
+        c = W.validate_stablelm_config(config)
+        self.config = c
+        self.vocab = c["vocab_size"]
+        cfg = StableLMConfig(c["vocab_size"], c["hidden_size"], c["intermediate_size"], c["num_hidden_layers"],
+                             c["num_attention_heads"], c["num_key_value_heads"], c["max_position_embeddings"],
+                             c.get("bos_token_id", 0), c.get("eos_token_id", 0), c["layer_norm_eps"],
+                             c["rope_theta"], c["partial_rotary_factor"])
+        names = list(STABLELM_TENSORS) + [f"model.layers.{i}.{n}" for i in range(c["num_hidden_layers"])
+                                          for n in LAYER_TENSORS]
+        arr = (Tensor * len(names))()
+        keep = []
+        for i, n in enumerate(names):
+            t = tensors[n]
+            b = n.encode()
+            keep.append(b)
+            arr[i] = Tensor(b, t.dtype, t.rows, t.cols, t.data.ctypes.data, t.data.size)
+        h = C.c_void_p()
+        check(lib().tinyoai_stablelm_load(C.byref(cfg), arr, len(names), C.byref(h)))
+        self.h = h
+        self._logits = np.empty(self.vocab, np.float32)
+
+    def forward(self, prefix: int, tokens, want_logits: bool = True) -> np.ndarray | None:
+        toks = np.ascontiguousarray(tokens, np.int32)
+        check(lib().tinyoai_stablelm_forward(self.h, prefix, _ip(toks), toks.size, int(want_logits),
+                                             _fp(self._logits)))
+        return self._logits.copy() if want_logits else None
+
+    def set_kv_bits(self, bits: int) -> bool:
+        cleared = C.c_int32()
+        check(lib().tinyoai_stablelm_set_kv_bits(self.h, bits, C.byref(cleared)))
+        return bool(cleared.value)
+
+    def limit_cache(self, limit: int) -> bool:
+        cleared = C.c_int32()
+        check(lib().tinyoai_stablelm_limit_cache(self.h, limit, C.byref(cleared)))
+        return bool(cleared.value)
+
+    def reset(self) -> None:
+        check(lib().tinyoai_stablelm_reset(self.h))
+
+    @property
+    def offset(self) -> int:
+        return check(lib().tinyoai_stablelm_offset(self.h))
+
+    def read_kv(self, layer: int, kv_head: int, n: int):
+        hd = self.config["hidden_size"] // self.config["num_attention_heads"]
+        k = np.empty(n * hd, np.float32)
+        v = np.empty(n * hd, np.float32)
+        check(lib().tinyoai_stablelm_read_kv(self.h, layer, kv_head, n, _fp(k), _fp(v)))
+        return k.reshape(n, hd), v.reshape(n, hd)
+
+    def trace(self, enable: bool = True) -> None:
+        check(lib().tinyoai_stablelm_trace(self.h, int(enable)))
+
+    def trace_read(self) -> np.ndarray:
+        c = self.config
+        out = np.empty((c["num_hidden_layers"], c["hidden_size"]), np.float32)
+        check(lib().tinyoai_stablelm_trace_read(self.h, _fp(out)))
+        return out
+
+    STAGES = ("embedding", "decode_in", "attention", "decode_out", "lm_head", "prefill_layer_norm",
+              "prefill_projections", "prefill_rotary_kv_write", "prefill_attention", "prefill_elementwise")
+
+    def profile(self, enable: bool = True) -> None:
+        check(lib().tinyoai_stablelm_profile(self.h, int(enable)))
+
+    def profile_read(self) -> dict:
+        n = len(self.STAGES)
+        ms = (C.c_double * n)()
+        counts = (C.c_int64 * n)()
+        check(lib().tinyoai_stablelm_profile_read(self.h, ms, counts, n))
+        return {s: (ms[i], counts[i]) for i, s in enumerate(self.STAGES)}
+
+    def close(self) -> None:
+        if self.h:
+            lib().tinyoai_stablelm_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
