@@ -125,7 +125,6 @@ def main():
     for _ in range(args.warmup):
         step()
         print("[bench] warmup step done", file=sys.stderr, flush=True)
-    fwd.profile(True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     prefill_s, decode_s, streams = [], [], []
@@ -137,8 +136,14 @@ def main():
         print(f"[bench] step {i}: prefill {p * 1e3:.1f} ms, decode {d * 1e3:.1f} ms", file=sys.stderr, flush=True)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    # Per-kernel durations: one more step of the same workload with every
+    # kernel bracketed by hipEvents on the library's stream (launched
+    # directly instead of through the decode graph, so each can be timed).
+    fwd.profile(True)
+    _, _, prof_stream = step()
     prof = fwd.profile_read()
     fwd.profile(False)
+    streams.append(prof_stream)
     decode_forwards = (args.generate - 1) * args.steps
     decode_tok_s = decode_forwards / sum(decode_s)
     mean_prefill = sum(prefill_s) / len(prefill_s)

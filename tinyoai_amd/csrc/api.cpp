@@ -156,7 +156,9 @@ int StableModel::alloc(void **p, size_t bytes) {
   return TINYOAI_OK;
 }
 
+// Graphs bake in the KV pointers, so they go with the buffers.
 void StableModel::free_kv() {
+  drop_graphs();
   for (auto &l : kv) {
     if (l.k) hipFree(l.k);
     if (l.v) hipFree(l.v);
@@ -289,9 +291,14 @@ int StableModel::init(const tinyoai_stablelm_config &c, const tinyoai_tensor *te
   e = hipStreamSynchronize(stream);
   if (e != hipSuccess) return hip_fail(e, "model upload");
   const int cus = device_cu_count();
-  grid_in = cus * 4;
-  grid_out = cus * 2;
-  grid_head = cus * 4;
+  // One large block per CU for the matvecs (measured on MI355X at the 3B
+  // shapes): each block stages its activations once and its waves stream rows.
+  grid_in = cus;
+  threads_in = 1024;
+  grid_out = cus;
+  threads_out = 640;
+  grid_head = cus * 2;
+  threads_head = 512;
   return TINYOAI_OK;
 }
 
@@ -360,21 +367,59 @@ int StableModel::upload_params(const int *head_vals, int nh, const int32_t *ids,
   return TINYOAI_OK;
 }
 
-int StableModel::decode_step(int token, int pos, bool want_logits) {
-  const int vals[2] = {token, pos};
-  if (int rc = upload_params(vals, 2, nullptr, 0)) return rc;
-  STAGE(ST_EMBED, launch_embed(embed.desc, params, 1, x, stream), "embed");
+// The kernels of one decode token; token and position come from `params`.
+// The attention launch shape (steps, splits) is fixed by the caller so the
+// sequence can be captured once per shape.
+int StableModel::enqueue_decode(int steps, int splits, bool want_logits) {
   for (int l = 0; l < cfg.num_hidden_layers; l++) {
     STAGE(ST_DECODE_IN,
-          launch_decode_in(layers[l], dims, kv[l], x, rope, params + 1, qbuf, mbuf, grid_in, stream), "decode_in");
-    STAGE(ST_ATTENTION, launch_attention(dims, kv[l], qbuf, params + 1, 1, pos, partials, counters, abuf, stream),
+          launch_decode_in(layers[l], dims, kv[l], x, l == 0 ? &embed.desc : nullptr, params, rope, params + 1, qbuf,
+                           mbuf, grid_in, threads_in, stream),
+          "decode_in");
+    STAGE(ST_ATTENTION,
+          launch_attention(dims, kv[l], qbuf, params + 1, 1, 0, partials, counters, abuf, stream, steps, splits),
           "attention");
-    STAGE(ST_DECODE_OUT, launch_decode_out(layers[l], dims, abuf, mbuf, x, grid_out, stream), "decode_out");
+    STAGE(ST_DECODE_OUT, launch_decode_out(layers[l], dims, abuf, mbuf, x, grid_out, threads_out, stream), "decode_out");
     if (tracing) TRY_HIP(launch_copy_row(x, trace_dev + (size_t)l * dims.d, dims.d, stream), "trace");
   }
   if (want_logits)
-    STAGE(ST_LM_HEAD, launch_ln_matvec(head.desc, norm_w, norm_b, dims.eps, x, logits_dev, grid_head, stream),
+    STAGE(ST_LM_HEAD, launch_ln_matvec(head.desc, norm_w, norm_b, dims.eps, x, logits_dev, grid_head, threads_head, stream),
           "lm_head");
+  return TINYOAI_OK;
+}
+
+void StableModel::drop_graphs() {
+  for (auto &g : graphs) hipGraphExecDestroy(g.second);
+  graphs.clear();
+}
+
+// One token at `pos` (StableLM.forward, stablelm.go:332-387). Replays a HIP
+// graph of the whole layer stack keyed by the attention launch shape;
+// profiling runs launch the kernels directly so each can be timed.
+int StableModel::decode_step(int token, int pos, bool want_logits) {
+  const int vals[2] = {token, pos};
+  if (int rc = upload_params(vals, 2, nullptr, 0)) return rc;
+  const int steps = attention_steps(pos, dims.heads), splits = attention_splits(pos, steps);
+  if (prof.on || !use_graphs) return enqueue_decode(steps, splits, want_logits);
+  const int64_t key = ((int64_t)steps << 40) | ((int64_t)splits << 8) | (want_logits ? 2 : 0) | (tracing ? 1 : 0);
+  auto it = graphs.find(key);
+  if (it == graphs.end()) {
+    hipGraph_t g = nullptr;
+    TRY_HIP(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal), "graph capture");
+    int rc = enqueue_decode(steps, splits, want_logits);
+    hipError_t e = hipStreamEndCapture(stream, &g);
+    if (rc) {
+      if (g) hipGraphDestroy(g);
+      return rc;
+    }
+    if (e != hipSuccess) return hip_fail(e, "graph capture");
+    hipGraphExec_t exec = nullptr;
+    e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+    hipGraphDestroy(g);
+    if (e != hipSuccess) return hip_fail(e, "graph instantiate");
+    it = graphs.emplace(key, exec).first;
+  }
+  TRY_HIP(hipGraphLaunch(it->second, stream), "graph launch");
   return TINYOAI_OK;
 }
 
@@ -403,7 +448,7 @@ int StableModel::prefill_chunk(const int32_t *ids, int n, int start, bool want_l
   }
   if (want_logits) {
     TRY_HIP(launch_copy_row(X + (size_t)(n - 1) * d, x, d, stream), "last row");
-    STAGE(ST_LM_HEAD, launch_ln_matvec(head.desc, norm_w, norm_b, dims.eps, x, logits_dev, grid_head, stream),
+    STAGE(ST_LM_HEAD, launch_ln_matvec(head.desc, norm_w, norm_b, dims.eps, x, logits_dev, grid_head, threads_head, stream),
           "lm_head");
   }
   return TINYOAI_OK;
@@ -632,7 +677,7 @@ int tinyoai_weight_mul_device(tinyoai_weight *w, const float *x_dev, int32_t n, 
   hipStream_t st = stream ? (hipStream_t)stream : w->stream;
   hipError_t e;
   if (n == 1)
-    e = launch_ln_matvec(w->m.desc, nullptr, nullptr, 0.0, x_dev, out_dev, device_cu_count() * 4, st);
+    e = launch_ln_matvec(w->m.desc, nullptr, nullptr, 0.0, x_dev, out_dev, device_cu_count() * 4, 256, st);
   else
     e = launch_gemm(w->m.desc, x_dev, n, out_dev, st);
   return e == hipSuccess ? TINYOAI_OK : hip_fail(e, "product launch");

@@ -5,10 +5,14 @@
 //   decode_in   LayerNorm(x) once per block into LDS, then every weight row
 //               that reads it (q, k, v, gate, up) in one pass over HBM, with
 //               RoPE, the KV append and SiLU-gate applied in the epilogue;
-//   attention   split-K flash decode; the last block of a head combines;
+//               layer 0 also gathers the token's embedding row here;
+//   attention   split-K flash decode; blocks of a head combine through the
+//               last-arriving block;
 //   decode_out  x = (x + o*a) + down*m over the o and down rows.
 // Rows are handed out in "units" of two: a rotary pair (i, i + rot/2) of a
 // q or k head, two adjacent non-rotary rows, or gate row i with up row i.
+// Each wave streams its units with the next batch of weight loads in flight
+// (stream_units, formats.h).
 #include <algorithm>
 
 #include "kernels.h"
@@ -30,66 +34,102 @@ struct InArgs {
   LayerDev w;
   StableDims s;
   KVDev kv;
-  const float *x, *rope;
+  float *x;             // residual [d]; written here when emb is set
+  MatDesc emb;          // embedding table (layer 0, when use_emb)
+  int use_emb;
+  const int *token;     // token id (layer 0)
+  const float *rope;
   const int *pos;
   float *q_out, *m_out;
   int xlen;  // LDS vector length (>= d, covers padded chunks)
 };
 
-template <int FA, int FM, int U>
-__global__ __launch_bounds__(kThreads) void decode_in_kernel(InArgs a) {
+template <int F, int U, int T>
+__global__ __launch_bounds__(T) void decode_in_kernel(InArgs a) {
   extern __shared__ __align__(16) float lds[];
-  double *red = reinterpret_cast<double *>(lds + ((a.xlen + 3) & ~3));
+  constexpr int VPC = Fmt<F>::VPC;
+  const int nch = a.w.q.chunks;
+  float4 *xq = reinterpret_cast<float4 *>(lds + ((a.xlen + 3) & ~3));
+  double *red = reinterpret_cast<double *>(xq + (VPC / 4) * nch);
+  float *rope_row = reinterpret_cast<float *>(red + 16);  // cos/sin at pos, [rot/2][2]
   const StableDims &s = a.s;
-  for (int i = threadIdx.x; i < a.xlen; i += kThreads) lds[i] = i < s.d ? a.x[i] : 0.f;
-  __syncthreads();
-  layer_norm_lds(lds, s.d, a.w.ln_w, a.w.ln_b, s.eps, red);
   const int pos = *a.pos;
   const int lane = threadIdx.x & 63;
   const int half_hd = s.hd / 2, rh = s.rot / 2;
   const int nq = s.heads * half_hd, nk = s.kv_heads * half_hd;
   const int natt = nq + 2 * nk, total = natt + s.inter;
-  for (int u = blockIdx.x * kWaves + (threadIdx.x >> 6); u < total; u += gridDim.x * kWaves) {
+
+  auto prologue = [&]() {
+    if (a.use_emb) {  // embedding row (stablelm.go:338), bit-exact readValues
+      const MatDesc &e = a.emb;
+      const int64_t row = *a.token;
+      for (int i = threadIdx.x; i < s.d; i += T) {
+        const float v = mat_value(e, row, i);
+        lds[i] = v;
+        if (blockIdx.x == 0) a.x[i] = v;
+      }
+    } else {
+      for (int i = threadIdx.x; i < s.d; i += T) lds[i] = a.x[i];
+    }
+    __syncthreads();
+    layer_norm_lds(lds, s.d, a.w.ln_w, a.w.ln_b, s.eps, red);
+    stage_x(xq, lds, s.d, nch, VPC);
+    for (int i = threadIdx.x; i < s.rot; i += T) rope_row[i] = a.rope[(int64_t)pos * s.rot + i];
+    __syncthreads();
+  };
+  auto unit = [&](int u, Seg2 &g) {
     if (u < natt) {
-      int kind = u < nq ? 0 : (u < nq + nk ? 1 : 2);  // q, k, v
+      const int kind = u < nq ? 0 : (u < nq + nk ? 1 : 2);
       const int uu = kind == 0 ? u : (kind == 1 ? u - nq : u - nq - nk);
       const int head = uu / half_hd, j = uu % half_hd;
       const MatDesc &M = kind == 0 ? a.w.q : (kind == 1 ? a.w.k : a.w.v);
-      int d0, d1;
-      const bool rotary = kind != 2 && j < rh;
-      if (kind == 2) { d0 = 2 * j; d1 = d0 + 1; }
-      else if (rotary) { d0 = j; d1 = j + rh; }
-      else { d0 = s.rot + 2 * (j - rh); d1 = d0 + 1; }
+      int d0;
+      if (kind == 2) d0 = 2 * j;
+      else if (j < rh) d0 = j;
+      else d0 = s.rot + 2 * (j - rh);
+      const int d1 = (kind != 2 && j < rh) ? j + rh : d0 + 1;
       const int64_t r0 = (int64_t)head * s.hd + d0, r1 = (int64_t)head * s.hd + d1;
-      float v0, v1;
-      seg2_dot<FA, U>(M.vals + r0 * M.vstride, M.meta + r0 * M.mstride, lds, M.chunks,
-                      M.vals + r1 * M.vstride, M.meta + r1 * M.mstride, lds, M.chunks, v0, v1);
-      if (lane == 0) {
-        if (rotary) {  // stableRotate (stablelm.go:309-326) with table sin/cos
-          const float cs = a.rope[((int64_t)pos * rh + j) * 2], sn = a.rope[((int64_t)pos * rh + j) * 2 + 1];
-          const float x0 = __fsub_rn(__fmul_rn(v0, cs), __fmul_rn(v1, sn));
-          const float x1 = __fadd_rn(__fmul_rn(v1, cs), __fmul_rn(v0, sn));
-          v0 = x0;
-          v1 = x1;
-        }
-        if (kind == 0) {
-          a.q_out[r0] = v0;
-          a.q_out[r1] = v1;
-        } else {  // storeKV (kv_cache.go:55-65), head-major [kvh][cap][hd]
-          const int64_t base = ((int64_t)head * a.kv.cap + pos) * s.hd;
-          store_kv(a.kv, base + d0, v0, kind == 1);
-          store_kv(a.kv, base + d1, v1, kind == 1);
-        }
+      g = Seg2{M.vals + r0 * M.vstride, M.meta + r0 * M.mstride, M.vals + r1 * M.vstride, M.meta + r1 * M.mstride,
+               xq, xq, nch, nch};
+    } else {
+      const int64_t i = u - natt;
+      const MatDesc &G = a.w.gate, &P = a.w.up;
+      g = Seg2{G.vals + i * G.vstride, G.meta + i * G.mstride, P.vals + i * P.vstride, P.meta + i * P.mstride,
+               xq, xq, nch, nch};
+    }
+  };
+  auto done = [&](int u, float v0, float v1) {
+    if (lane != 0) return;
+    if (u < natt) {
+      const int kind = u < nq ? 0 : (u < nq + nk ? 1 : 2);
+      const int uu = kind == 0 ? u : (kind == 1 ? u - nq : u - nq - nk);
+      const int head = uu / half_hd, j = uu % half_hd;
+      const bool rotary = kind != 2 && j < rh;
+      int d0;
+      if (kind == 2) d0 = 2 * j;
+      else if (rotary) d0 = j;
+      else d0 = s.rot + 2 * (j - rh);
+      const int d1 = rotary ? j + rh : d0 + 1;
+      if (rotary) {  // stableRotate (stablelm.go:309-326) with table sin/cos
+        const float cs = rope_row[2 * j], sn = rope_row[2 * j + 1];
+        const float x0 = __fsub_rn(__fmul_rn(v0, cs), __fmul_rn(v1, sn));
+        const float x1 = __fadd_rn(__fmul_rn(v1, cs), __fmul_rn(v0, sn));
+        v0 = x0;
+        v1 = x1;
+      }
+      if (kind == 0) {
+        a.q_out[head * s.hd + d0] = v0;
+        a.q_out[head * s.hd + d1] = v1;
+      } else {  // storeKV (kv_cache.go:55-65), head-major [kvh][cap][hd]
+        const int64_t base = ((int64_t)head * a.kv.cap + pos) * s.hd;
+        store_kv(a.kv, base + d0, v0, kind == 1);
+        store_kv(a.kv, base + d1, v1, kind == 1);
       }
     } else {
-      const int i = u - natt;
-      const MatDesc &G = a.w.gate, &P = a.w.up;
-      float g, up;
-      seg2_dot<FM, U>(G.vals + (int64_t)i * G.vstride, G.meta + (int64_t)i * G.mstride, lds, G.chunks,
-                      P.vals + (int64_t)i * P.vstride, P.meta + (int64_t)i * P.mstride, lds, P.chunks, g, up);
-      if (lane == 0) a.m_out[i] = silu_gate(g, up);
+      a.m_out[u - natt] = silu_gate(v0, v1);
     }
-  }
+  };
+  stream_units<F, U>(blockIdx.x * (T / 64) + (threadIdx.x >> 6), gridDim.x * (T / 64), total, prologue, unit, done);
 }
 
 struct OutArgs {
@@ -99,29 +139,26 @@ struct OutArgs {
   float *x;
 };
 
-template <int FA, int FM, int U>
-__global__ __launch_bounds__(kThreads) void decode_out_kernel(OutArgs p) {
-  extern __shared__ __align__(16) float lds[];
-  float *xa = lds, *xm = lds + ((p.la + 3) & ~3);
-  for (int i = threadIdx.x; i < p.la; i += kThreads) xa[i] = i < p.d ? p.a[i] : 0.f;
-  for (int i = threadIdx.x; i < p.lm; i += kThreads) xm[i] = i < p.inter ? p.m[i] : 0.f;
-  __syncthreads();
-  const int lane = threadIdx.x & 63;
+template <int F, int U, int T>
+__global__ __launch_bounds__(T) void decode_out_kernel(OutArgs p) {
+  extern __shared__ __align__(16) float4 xq_lds[];
+  constexpr int VPC = Fmt<F>::VPC;
   const MatDesc &O = p.w.o, &D = p.w.down;
-  for (int r = blockIdx.x * kWaves + (threadIdx.x >> 6); r < p.d; r += gridDim.x * kWaves) {
-    float ao, ad;
-    if constexpr (FA == FM) {
-      seg2_dot<FA, U>(O.vals + (int64_t)r * O.vstride, O.meta + (int64_t)r * O.mstride, xa, O.chunks,
-                      D.vals + (int64_t)r * D.vstride, D.meta + (int64_t)r * D.mstride, xm, D.chunks, ao, ad);
-    } else {
-      float unused;
-      seg2_dot<FA, U>(O.vals + (int64_t)r * O.vstride, O.meta + (int64_t)r * O.mstride, xa, O.chunks,
-                      nullptr, nullptr, nullptr, 0, ao, unused);
-      seg2_dot<FM, U>(D.vals + (int64_t)r * D.vstride, D.meta + (int64_t)r * D.mstride, xm, D.chunks,
-                      nullptr, nullptr, nullptr, 0, ad, unused);
-    }
+  float4 *xa = xq_lds, *xm = xq_lds + (VPC / 4) * O.chunks;
+  const int lane = threadIdx.x & 63;
+  auto prologue = [&]() {
+    stage_x(xa, p.a, p.d, O.chunks, VPC);
+    stage_x(xm, p.m, p.inter, D.chunks, VPC);
+    __syncthreads();
+  };
+  auto unit = [&](int r, Seg2 &g) {
+    g = Seg2{O.vals + (int64_t)r * O.vstride, O.meta + (int64_t)r * O.mstride, D.vals + (int64_t)r * D.vstride,
+             D.meta + (int64_t)r * D.mstride, xa, xm, O.chunks, D.chunks};
+  };
+  auto done = [&](int r, float ao, float ad) {
     if (lane == 0) p.x[r] = __fadd_rn(__fadd_rn(p.x[r], ao), ad);
-  }
+  };
+  stream_units<F, U>(blockIdx.x * (T / 64) + (threadIdx.x >> 6), gridDim.x * (T / 64), p.d, prologue, unit, done);
 }
 
 struct LnMvArgs {
@@ -133,29 +170,35 @@ struct LnMvArgs {
   int xlen;
 };
 
-template <int F, int U>
-__global__ __launch_bounds__(kThreads) void ln_matvec_kernel(LnMvArgs a) {
+template <int F, int U, int T>
+__global__ __launch_bounds__(T) void ln_matvec_kernel(LnMvArgs a) {
   extern __shared__ __align__(16) float lds[];
-  double *red = reinterpret_cast<double *>(lds + ((a.xlen + 3) & ~3));
+  constexpr int VPC = Fmt<F>::VPC;
   const int cols = a.w.cols;
-  for (int i = threadIdx.x; i < a.xlen; i += kThreads) lds[i] = i < cols ? a.x[i] : 0.f;
-  __syncthreads();
-  if (a.ln_w) layer_norm_lds(lds, cols, a.ln_w, a.ln_b, a.eps, red);
   const int lane = threadIdx.x & 63;
   const MatDesc &M = a.w;
-  const int units = (M.rows + 1) / 2;
-  for (int u = blockIdx.x * kWaves + (threadIdx.x >> 6); u < units; u += gridDim.x * kWaves) {
+  float4 *xq = reinterpret_cast<float4 *>(lds + ((cols + 3) & ~3));
+  double *red = reinterpret_cast<double *>(xq + (VPC / 4) * M.chunks);
+  auto prologue = [&]() {
+    for (int i = threadIdx.x; i < cols; i += T) lds[i] = a.x[i];
+    __syncthreads();
+    if (a.ln_w) layer_norm_lds(lds, cols, a.ln_w, a.ln_b, a.eps, red);
+    stage_x(xq, lds, cols, M.chunks, VPC);
+    __syncthreads();
+  };
+  auto unit = [&](int u, Seg2 &g) {
     const int64_t r0 = 2 * (int64_t)u, r1 = r0 + 1;
     const bool two = r1 < M.rows;
-    float v0, v1;
-    seg2_dot<F, U>(M.vals + r0 * M.vstride, M.meta + r0 * M.mstride, lds, M.chunks,
-                   two ? M.vals + r1 * M.vstride : nullptr, two ? M.meta + r1 * M.mstride : nullptr, lds,
-                   two ? M.chunks : 0, v0, v1);
-    if (lane == 0) {
-      a.out[r0] = v0;
-      if (two) a.out[r1] = v1;
-    }
-  }
+    g = Seg2{M.vals + r0 * M.vstride, M.meta + r0 * M.mstride, two ? M.vals + r1 * M.vstride : nullptr,
+             two ? M.meta + r1 * M.mstride : nullptr, xq, xq, M.chunks, two ? M.chunks : 0};
+  };
+  auto done = [&](int u, float v0, float v1) {
+    if (lane != 0) return;
+    a.out[2 * (int64_t)u] = v0;
+    if (2 * u + 1 < M.rows) a.out[2 * (int64_t)u + 1] = v1;
+  };
+  stream_units<F, U>(blockIdx.x * (T / 64) + (threadIdx.x >> 6), gridDim.x * (T / 64), (M.rows + 1) / 2, prologue,
+                     unit, done);
 }
 
 __global__ void embed_kernel(MatDesc emb, const int *ids, float *x) {
@@ -165,8 +208,6 @@ __global__ void embed_kernel(MatDesc emb, const int *ids, float *x) {
 }
 
 // ---------------------------------------------------------------- attention
-constexpr int kSplit = 64;  // positions per block (4 steps of 16)
-
 struct AttArgs {
   StableDims s;
   KVDev kv;
@@ -177,6 +218,14 @@ struct AttArgs {
   unsigned *counters;
   float *out;
 };
+
+// Agent-scope relaxed atomic store / load of a partial result.
+__device__ __forceinline__ void publish(float *p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float observe(const float *p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 // Loads N consecutive KV values starting at element e into float registers.
 template <int N, bool HALF>
@@ -217,35 +266,45 @@ __device__ __forceinline__ void load_kv(const void *base, int64_t e, float *r) {
   }
 }
 
-// One wave per (split, head, query). Lane = 4 * position-in-step + dim group:
-// four lanes share a position, each holding hd/4 dimensions.
-template <int HD, bool HALF>
-__global__ __launch_bounds__(64) void attention_kernel(AttArgs a) {
+// One block of 4 waves per (split, head, query); a split covers
+// 4 * STEPS * 16 positions. Lane = 4 * position-in-step + dim group: four
+// lanes share a position, each holding hd/4 dimensions. Online-softmax
+// partials combine across the waves in LDS, then across the splits of a
+// (query, head) in the last block to finish (the others exit).
+template <int HD, bool HALF, int STEPS>
+__global__ __launch_bounds__(kThreads) void attention_kernel(AttArgs a) {
   constexpr int DPL = HD / 4;
+  constexpr int SPLIT = kWaves * STEPS * 16;
+  __shared__ float s_m[kWaves], s_l[kWaves], s_o[kWaves][HD];
+  __shared__ float s_e[512];
+  __shared__ int s_last;
   const StableDims &s = a.s;
   const int split = blockIdx.x, h = blockIdx.y, j = blockIdx.z;
   const int pos = *a.pos0 + j;
   const int npos = pos + 1;
-  const int nsplit = (npos + kSplit - 1) / kSplit;
+  const int nsplit = (npos + SPLIT - 1) / SPLIT;
   if (split >= nsplit) return;
-  const int lane = threadIdx.x, g = lane & 3, pl = lane >> 2;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane & 3, pl = lane >> 2;
   const int kvh = h / (s.heads / s.kv_heads);
   const float *q = a.q + (int64_t)j * s.heads * HD + h * HD + g * DPL;
   float qr[DPL];
 #pragma unroll
   for (int i = 0; i < DPL; i++) qr[i] = q[i];
   const int64_t head_base = (int64_t)kvh * a.kv.cap * HD;
-  float score[kSplit / 16];
+  const int t0 = split * SPLIT + wave * STEPS * 16 + pl;
+  float kr[STEPS][DPL];
+#pragma unroll
+  for (int st = 0; st < STEPS; st++)
+    if (t0 + st * 16 < npos) load_kv<DPL, HALF>(a.kv.k, head_base + (int64_t)(t0 + st * 16) * HD + g * DPL, kr[st]);
+  float score[STEPS];
   float mx = -INFINITY;
 #pragma unroll
-  for (int st = 0; st < kSplit / 16; st++) {
-    const int t = split * kSplit + st * 16 + pl;
+  for (int st = 0; st < STEPS; st++) {
+    const int t = t0 + st * 16;
     float p = 0.f;
     if (t < npos) {
-      float kr[DPL];
-      load_kv<DPL, HALF>(a.kv.k, head_base + (int64_t)t * HD + g * DPL, kr);
 #pragma unroll
-      for (int i = 0; i < DPL; i++) p = fmaf(qr[i], kr[i], p);
+      for (int i = 0; i < DPL; i++) p = fmaf(qr[i], kr[st][i], p);
     }
     p += __shfl_xor(p, 1, 64);
     p += __shfl_xor(p, 2, 64);
@@ -253,20 +312,21 @@ __global__ __launch_bounds__(64) void attention_kernel(AttArgs a) {
     mx = fmaxf(mx, score[st]);
   }
   mx = wave_max(mx);
+  float vr[STEPS][DPL];
+#pragma unroll
+  for (int st = 0; st < STEPS; st++)
+    if (t0 + st * 16 < npos) load_kv<DPL, HALF>(a.kv.v, head_base + (int64_t)(t0 + st * 16) * HD + g * DPL, vr[st]);
   float o[DPL];
 #pragma unroll
   for (int i = 0; i < DPL; i++) o[i] = 0.f;
   float l = 0.f;
 #pragma unroll
-  for (int st = 0; st < kSplit / 16; st++) {
-    const int t = split * kSplit + st * 16 + pl;
-    if (t < npos) {
+  for (int st = 0; st < STEPS; st++) {
+    if (t0 + st * 16 < npos) {
       const float w = expf(score[st] - mx);
       if (g == 0) l += w;
-      float vr[DPL];
-      load_kv<DPL, HALF>(a.kv.v, head_base + (int64_t)t * HD + g * DPL, vr);
 #pragma unroll
-      for (int i = 0; i < DPL; i++) o[i] = fmaf(w, vr[i], o[i]);
+      for (int i = 0; i < DPL; i++) o[i] = fmaf(w, vr[st][i], o[i]);
     }
   }
   l = wave_sum(l);
@@ -279,57 +339,177 @@ __global__ __launch_bounds__(64) void attention_kernel(AttArgs a) {
     v += __shfl_xor(v, 32, 64);
     o[i] = v;
   }
-  const int64_t qh = (int64_t)j * s.heads + h;
-  float *part = a.partials + (qh * a.max_splits + split) * (HD + 2);
-  if (lane == 0) { part[0] = mx; part[1] = l; }
+  if (lane == 0) { s_m[wave] = mx; s_l[wave] = l; }
   if (pl == 0) {
 #pragma unroll
-    for (int i = 0; i < DPL; i++) part[2 + g * DPL + i] = o[i];
+    for (int i = 0; i < DPL; i++) s_o[wave][g * DPL + i] = o[i];
   }
-  __threadfence();
-  int last = 0;
-  if (lane == 0) last = atomicAdd(&a.counters[qh], 1u) == (unsigned)(nsplit - 1);
-  last = __shfl(last, 0, 64);
-  if (!last) return;
-  __threadfence();
-  // Combine the splits of this (query, head).
+  __syncthreads();
+  // combine the waves (a wave with no valid position has m = -inf, l = 0)
+  float M = s_m[0];
+#pragma unroll
+  for (int w = 1; w < kWaves; w++) M = fmaxf(M, s_m[w]);
+  float L = 0.f, ew[kWaves];
+#pragma unroll
+  for (int w = 0; w < kWaves; w++) {
+    ew[w] = expf(s_m[w] - M);
+    L = fmaf(s_l[w], ew[w], L);
+  }
+  const int64_t qh = (int64_t)j * s.heads + h;
+  float *outp = a.out + (int64_t)j * s.heads * HD + h * HD;
+  if (nsplit == 1) {
+    for (int d = tid; d < HD; d += kThreads) {
+      float acc = 0.f;
+#pragma unroll
+      for (int w = 0; w < kWaves; w++) acc = fmaf(s_o[w][d], ew[w], acc);
+      outp[d] = acc / L;
+    }
+    return;
+  }
+  // Cross-block combine. Partials and the arrival counter are exchanged with
+  // agent-scope relaxed atomics (cache-coherent across XCDs, sc1 accesses)
+  // and ordered by waiting for the stores before the arrival increment; an
+  // agent-scope fence would write back and invalidate the whole L2 instead.
+  float *part = a.partials + (qh * a.max_splits + split) * (HD + 2);
+  if (tid == 0) {
+    publish(part, M);
+    publish(part + 1, L);
+  }
+  for (int d = tid; d < HD; d += kThreads) {
+    float acc = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; w++) acc = fmaf(s_o[w][d], ew[w], acc);
+    publish(part + 2 + d, acc);
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores have completed
+  __syncthreads();
+  if (tid == 0)
+    s_last = __hip_atomic_fetch_add(&a.counters[qh], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+             (unsigned)(nsplit - 1);
+  __syncthreads();
+  if (!s_last) return;
+  // Last block of this (query, head): every other split has published.
   const float *base = a.partials + qh * a.max_splits * (HD + 2);
   float m = -INFINITY;
-  for (int sp = lane; sp < nsplit; sp += 64) m = fmaxf(m, base[sp * (HD + 2)]);
+  for (int sp = tid; sp < nsplit; sp += kThreads) m = fmaxf(m, observe(base + sp * (HD + 2)));
   m = wave_max(m);
-  float L = 0.f;
-  for (int sp = lane; sp < nsplit; sp += 64) {
-    const float ms = base[sp * (HD + 2)];
-    L += base[sp * (HD + 2) + 1] * expf(ms - m);
+  if (lane == 0) s_m[wave] = m;
+  __syncthreads();
+  m = fmaxf(fmaxf(s_m[0], s_m[1]), fmaxf(s_m[2], s_m[3]));
+  float lsum = 0.f;
+  for (int sp = tid; sp < nsplit; sp += kThreads) {
+    const float e = expf(observe(base + sp * (HD + 2)) - m);
+    s_e[sp] = e;
+    lsum = fmaf(observe(base + sp * (HD + 2) + 1), e, lsum);
   }
-  L = wave_sum(L);
-  for (int dim = lane; dim < HD; dim += 64) {
+  lsum = wave_sum(lsum);
+  __syncthreads();
+  if (lane == 0) s_l[wave] = lsum;
+  __syncthreads();
+  const float Ltot = (s_l[0] + s_l[1]) + (s_l[2] + s_l[3]);
+  for (int d = tid; d < HD; d += kThreads) {
     float acc = 0.f;
-    for (int sp = 0; sp < nsplit; sp++) {
-      const float ms = base[sp * (HD + 2)];
-      acc = fmaf(base[sp * (HD + 2) + 2 + dim], expf(ms - m), acc);
-    }
-    a.out[(int64_t)j * s.heads * HD + h * HD + dim] = acc / L;
+#pragma unroll 8
+    for (int sp = 0; sp < nsplit; sp++) acc = fmaf(observe(base + sp * (HD + 2) + 2 + d), s_e[sp], acc);
+    outp[d] = acc / Ltot;
   }
-  if (lane == 0) a.counters[qh] = 0u;
+  if (tid == 0) __hip_atomic_store(&a.counters[qh], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int HD, bool HALF>
+hipError_t launch_attention_hd(const AttArgs &a, int nq, int splits, int steps, hipStream_t st) {
+  dim3 grid(splits, a.s.heads, nq);
+  switch (steps) {
+    case 1: hipLaunchKernelGGL((attention_kernel<HD, HALF, 1>), grid, dim3(kThreads), 0, st, a); break;
+    case 2: hipLaunchKernelGGL((attention_kernel<HD, HALF, 2>), grid, dim3(kThreads), 0, st, a); break;
+    case 4: hipLaunchKernelGGL((attention_kernel<HD, HALF, 4>), grid, dim3(kThreads), 0, st, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
 }
 
 template <int HD>
-hipError_t launch_attention_hd(const AttArgs &a, int nq, int max_pos, hipStream_t st) {
-  dim3 grid((max_pos + kSplit) / kSplit, a.s.heads, nq);
-  if (a.kv.half)
-    hipLaunchKernelGGL((attention_kernel<HD, true>), grid, dim3(64), 0, st, a);
-  else
-    hipLaunchKernelGGL((attention_kernel<HD, false>), grid, dim3(64), 0, st, a);
-  return hipGetLastError();
+hipError_t launch_attention_kv(const AttArgs &a, int nq, int splits, int steps, hipStream_t st) {
+  return a.kv.half ? launch_attention_hd<HD, true>(a, nq, splits, steps, st)
+                   : launch_attention_hd<HD, false>(a, nq, splits, steps, st);
 }
 
 int round_up(int v, int m) { return (v + m - 1) / m * m; }
 
-template <int F, int U>
-hipError_t ln_matvec_launch(const LnMvArgs &a, int grid, hipStream_t st) {
-  const size_t lds = (size_t)round_up(a.xlen, 4) * 4 + 8 * sizeof(double);
-  hipLaunchKernelGGL((ln_matvec_kernel<F, U>), dim3(grid), dim3(kThreads), lds, st, a);
+// Batch width U (chunks per lane per batch): the smallest instantiated
+// value that covers a whole unit, else 8 with several batches per unit.
+int pick_u(int chunks_per_unit) {
+  static const int us[] = {1, 2, 4, 5, 8, 10};
+  for (int u : us)
+    if (64 * u >= chunks_per_unit) return u;
+  return 8;
+}
+
+#define TINYOAI_DISPATCH_U(U, LAUNCH) \
+  switch (U) {                        \
+    case 1: LAUNCH(1); break;         \
+    case 2: LAUNCH(2); break;         \
+    case 4: LAUNCH(4); break;         \
+    case 5: LAUNCH(5); break;         \
+    case 8: LAUNCH(8); break;         \
+    case 10: LAUNCH(10); break;       \
+  }
+
+#define TINYOAI_DISPATCH_T(T, LAUNCH)                   \
+  switch (T) {                                          \
+    case 256: TINYOAI_DISPATCH_U(U, LAUNCH##256) break; \
+    case 512: TINYOAI_DISPATCH_U(U, LAUNCH##512) break; \
+    case 640: TINYOAI_DISPATCH_U(U, LAUNCH##640) break; \
+    case 1024: TINYOAI_DISPATCH_U(U, LAUNCH##1024) break; \
+    default: return hipErrorInvalidValue;               \
+  }
+
+template <int F>
+hipError_t ln_matvec_launch(const LnMvArgs &a, int grid, int threads, hipStream_t st) {
+  const size_t lds = (size_t)round_up(a.w.cols, 4) * 4 + (size_t)a.w.chunks * Fmt<F>::VPC * 4 + 16 * sizeof(double);
+  const int U = pick_u(2 * a.w.chunks);
+#define L256(U_) hipLaunchKernelGGL((ln_matvec_kernel<F, U_, 256>), dim3(grid), dim3(256), lds, st, a)
+#define L512(U_) hipLaunchKernelGGL((ln_matvec_kernel<F, U_, 512>), dim3(grid), dim3(512), lds, st, a)
+#define L640(U_) hipLaunchKernelGGL((ln_matvec_kernel<F, U_, 640>), dim3(grid), dim3(640), lds, st, a)
+#define L1024(U_) hipLaunchKernelGGL((ln_matvec_kernel<F, U_, 1024>), dim3(grid), dim3(1024), lds, st, a)
+  TINYOAI_DISPATCH_T(threads, L)
+#undef L256
+#undef L512
+#undef L640
+#undef L1024
+  return hipGetLastError();
+}
+
+template <int F>
+hipError_t decode_in_launch(const InArgs &a, int grid, int threads, hipStream_t st) {
+  const size_t lds = (size_t)round_up(a.xlen, 4) * 4 + (size_t)a.w.q.chunks * Fmt<F>::VPC * 4 +
+                     16 * sizeof(double) + (size_t)a.s.rot * 4;
+  const int U = pick_u(2 * a.w.q.chunks);
+#define L256(U_) hipLaunchKernelGGL((decode_in_kernel<F, U_, 256>), dim3(grid), dim3(256), lds, st, a)
+#define L512(U_) hipLaunchKernelGGL((decode_in_kernel<F, U_, 512>), dim3(grid), dim3(512), lds, st, a)
+#define L640(U_) hipLaunchKernelGGL((decode_in_kernel<F, U_, 640>), dim3(grid), dim3(640), lds, st, a)
+#define L1024(U_) hipLaunchKernelGGL((decode_in_kernel<F, U_, 1024>), dim3(grid), dim3(1024), lds, st, a)
+  TINYOAI_DISPATCH_T(threads, L)
+#undef L256
+#undef L512
+#undef L640
+#undef L1024
+  return hipGetLastError();
+}
+
+template <int F>
+hipError_t decode_out_launch(const OutArgs &p, int grid, int threads, hipStream_t st) {
+  const size_t lds = (size_t)(p.w.o.chunks + p.w.down.chunks) * Fmt<F>::VPC * 4;
+  const int U = pick_u(p.w.o.chunks + p.w.down.chunks);
+#define L256(U_) hipLaunchKernelGGL((decode_out_kernel<F, U_, 256>), dim3(grid), dim3(256), lds, st, p)
+#define L512(U_) hipLaunchKernelGGL((decode_out_kernel<F, U_, 512>), dim3(grid), dim3(512), lds, st, p)
+#define L640(U_) hipLaunchKernelGGL((decode_out_kernel<F, U_, 640>), dim3(grid), dim3(640), lds, st, p)
+#define L1024(U_) hipLaunchKernelGGL((decode_out_kernel<F, U_, 1024>), dim3(grid), dim3(1024), lds, st, p)
+  TINYOAI_DISPATCH_T(threads, L)
+#undef L256
+#undef L512
+#undef L640
+#undef L1024
   return hipGetLastError();
 }
 
@@ -346,70 +526,72 @@ int device_cu_count() {
   return cus;
 }
 
-#define TINYOAI_FMT_PAIR(FA, FM)                                                                     \
-  if (w.q.fmt == FA && w.gate.fmt == FM) {                                                           \
-    hipLaunchKernelGGL((decode_in_kernel<FA, FM, 4>), dim3(grid), dim3(kThreads), lds, st, a);       \
-    return hipGetLastError();                                                                        \
+hipError_t launch_decode_in(const LayerDev &w, const StableDims &s, const KVDev &kv, float *x, const MatDesc *emb,
+                            const int *token, const float *rope, const int *pos, float *q_out, float *m_out, int grid,
+                            int threads, hipStream_t st) {
+  InArgs a{w, s, kv, x, emb ? *emb : MatDesc{}, emb != nullptr, token, rope, pos, q_out, m_out, 0};
+  a.xlen = s.d;
+  if (w.q.fmt != w.gate.fmt || w.q.chunks != w.gate.chunks) return hipErrorInvalidValue;
+  switch (w.q.fmt) {
+    case FMT_Q8_0: return decode_in_launch<FMT_Q8_0>(a, grid, threads, st);
+    case FMT_BF16: return decode_in_launch<FMT_BF16>(a, grid, threads, st);
+    case FMT_F32: return decode_in_launch<FMT_F32>(a, grid, threads, st);
+    case FMT_F16: return decode_in_launch<FMT_F16>(a, grid, threads, st);
   }
-
-hipError_t launch_decode_in(const LayerDev &w, const StableDims &s, const KVDev &kv, const float *x,
-                            const float *rope, const int *pos, float *q_out, float *m_out, int grid,
-                            hipStream_t st) {
-  InArgs a{w, s, kv, x, rope, pos, q_out, m_out, 0};
-  a.xlen = std::max(w.q.chunks * values_per_chunk(w.q.fmt), w.gate.chunks * values_per_chunk(w.gate.fmt));
-  a.xlen = std::max(a.xlen, s.d);
-  const size_t lds = (size_t)round_up(a.xlen, 4) * 4 + 8 * sizeof(double);
-  TINYOAI_FMT_PAIR(FMT_Q8_0, FMT_Q8_0)
-  TINYOAI_FMT_PAIR(FMT_BF16, FMT_BF16)
-  TINYOAI_FMT_PAIR(FMT_F32, FMT_F32)
-  TINYOAI_FMT_PAIR(FMT_F16, FMT_F16)
   return hipErrorInvalidValue;
 }
-#undef TINYOAI_FMT_PAIR
-
-#define TINYOAI_FMT_PAIR(FA, FM)                                                                     \
-  if (w.o.fmt == FA && w.down.fmt == FM) {                                                           \
-    hipLaunchKernelGGL((decode_out_kernel<FA, FM, 4>), dim3(grid), dim3(kThreads), lds, st, p);      \
-    return hipGetLastError();                                                                        \
-  }
 
 hipError_t launch_decode_out(const LayerDev &w, const StableDims &s, const float *a, const float *m, float *x,
-                             int grid, hipStream_t st) {
+                             int grid, int threads, hipStream_t st) {
+  if (w.o.fmt != w.down.fmt) return hipErrorInvalidValue;
   OutArgs p{w, s.d, s.inter, 0, 0, a, m, x};
-  p.la = std::max(w.o.chunks * values_per_chunk(w.o.fmt), s.d);
-  p.lm = std::max(w.down.chunks * values_per_chunk(w.down.fmt), s.inter);
-  const size_t lds = (size_t)(round_up(p.la, 4) + round_up(p.lm, 4)) * 4;
-  TINYOAI_FMT_PAIR(FMT_Q8_0, FMT_Q8_0)
-  TINYOAI_FMT_PAIR(FMT_BF16, FMT_BF16)
-  TINYOAI_FMT_PAIR(FMT_F32, FMT_F32)
-  TINYOAI_FMT_PAIR(FMT_F16, FMT_F16)
+  switch (w.o.fmt) {
+    case FMT_Q8_0: return decode_out_launch<FMT_Q8_0>(p, grid, threads, st);
+    case FMT_BF16: return decode_out_launch<FMT_BF16>(p, grid, threads, st);
+    case FMT_F32: return decode_out_launch<FMT_F32>(p, grid, threads, st);
+    case FMT_F16: return decode_out_launch<FMT_F16>(p, grid, threads, st);
+  }
   return hipErrorInvalidValue;
 }
-#undef TINYOAI_FMT_PAIR
+
+int attention_steps(int max_pos, int heads) {
+  // Positions per block (64 * steps): the widest blocks measured fastest on
+  // gfx950 at 640 to 8K positions, as long as enough blocks remain.
+  const int npos = max_pos + 1;
+  int steps = 4;
+  while (steps > 1 && (npos + 64 * steps - 1) / (64 * steps) * heads < 64) steps /= 2;
+  return steps;
+}
+
+int attention_splits(int max_pos, int steps) { return (max_pos + 64 * steps) / (64 * steps); }
 
 hipError_t launch_attention(const StableDims &s, const KVDev &kv, const float *q, const int *pos0, int nq,
-                            int max_pos, float *partials, unsigned *counters, float *out, hipStream_t st) {
-  AttArgs a{s, kv, q, pos0, (max_pos + kSplit) / kSplit, partials, counters, out};
+                            int max_pos, float *partials, unsigned *counters, float *out, hipStream_t st, int steps,
+                            int splits) {
+  if (steps <= 0) steps = attention_steps(max_pos, s.heads);
+  if (splits <= 0) splits = attention_splits(max_pos, steps);
+  if (splits > 512) return hipErrorInvalidValue;  // combine scratch holds 512 splits
+  AttArgs a{s, kv, q, pos0, splits, partials, counters, out};
   switch (s.hd) {
-    case 8: return launch_attention_hd<8>(a, nq, max_pos, st);
-    case 16: return launch_attention_hd<16>(a, nq, max_pos, st);
-    case 32: return launch_attention_hd<32>(a, nq, max_pos, st);
-    case 64: return launch_attention_hd<64>(a, nq, max_pos, st);
-    case 80: return launch_attention_hd<80>(a, nq, max_pos, st);
-    case 96: return launch_attention_hd<96>(a, nq, max_pos, st);
-    case 128: return launch_attention_hd<128>(a, nq, max_pos, st);
+    case 8: return launch_attention_kv<8>(a, nq, splits, steps, st);
+    case 16: return launch_attention_kv<16>(a, nq, splits, steps, st);
+    case 32: return launch_attention_kv<32>(a, nq, splits, steps, st);
+    case 64: return launch_attention_kv<64>(a, nq, splits, steps, st);
+    case 80: return launch_attention_kv<80>(a, nq, splits, steps, st);
+    case 96: return launch_attention_kv<96>(a, nq, splits, steps, st);
+    case 128: return launch_attention_kv<128>(a, nq, splits, steps, st);
   }
   return hipErrorInvalidValue;
 }
 
 hipError_t launch_ln_matvec(const MatDesc &w, const float *ln_w, const float *ln_b, double eps, const float *x,
-                            float *out, int grid, hipStream_t st) {
+                            float *out, int grid, int threads, hipStream_t st) {
   LnMvArgs a{w, ln_w, ln_b, eps, x, out, std::max(w.chunks * values_per_chunk(w.fmt), w.cols)};
   switch (w.fmt) {
-    case FMT_Q8_0: return ln_matvec_launch<FMT_Q8_0, 4>(a, grid, st);
-    case FMT_BF16: return ln_matvec_launch<FMT_BF16, 4>(a, grid, st);
-    case FMT_F32: return ln_matvec_launch<FMT_F32, 4>(a, grid, st);
-    case FMT_F16: return ln_matvec_launch<FMT_F16, 4>(a, grid, st);
+    case FMT_Q8_0: return ln_matvec_launch<FMT_Q8_0>(a, grid, threads, st);
+    case FMT_BF16: return ln_matvec_launch<FMT_BF16>(a, grid, threads, st);
+    case FMT_F32: return ln_matvec_launch<FMT_F32>(a, grid, threads, st);
+    case FMT_F16: return ln_matvec_launch<FMT_F16>(a, grid, threads, st);
   }
   return hipErrorInvalidValue;
 }

@@ -48,19 +48,44 @@ __device__ __forceinline__ float hw_half(uint16_t h) {
   return __half2float(__ushort_as_half(h));  // v_cvt_f32_f16: exact, keeps subnormals
 }
 
-// Dot product of one 16-byte chunk with the matching x values (LDS, 16-byte
-// aligned), fp32 with fused multiply-adds. Q8_0 returns the unscaled sum.
+// ---------------------------------------------------------------- x in LDS
+// The activation vector of a product is staged in LDS "transposed": for
+// chunk c (VPC values) and quad q < VPC/4, the float4 of values
+// x[c*VPC + 4q .. 4q + 3] sits at xq[q * nch + c]. Lanes reading chunks
+// c, c+1, ... then touch consecutive 16-byte words (conflict-free), where a
+// plain layout would put them VPC*4 bytes apart.
+// x may live in global memory or LDS.
+__device__ __forceinline__ void stage_x(float4 *xq, const float *x, int len, int nch, int vpc) {
+  const int quads = vpc / 4;
+  const bool aligned = (reinterpret_cast<uintptr_t>(x) & 15) == 0;
+  for (int i = threadIdx.x; i < quads * nch; i += blockDim.x) {
+    const int q = i / nch, c = i % nch;
+    const int k = c * vpc + 4 * q;
+    float4 v;
+    if (aligned && k + 3 < len) {
+      v = *reinterpret_cast<const float4 *>(x + k);
+    } else {
+      v.x = k < len ? x[k] : 0.f;
+      v.y = k + 1 < len ? x[k + 1] : 0.f;
+      v.z = k + 2 < len ? x[k + 2] : 0.f;
+      v.w = k + 3 < len ? x[k + 3] : 0.f;
+    }
+    xq[i] = v;
+  }
+}
+
+// Dot product of one 16-byte weight chunk with its x values (fp32, fused
+// multiply-adds). Q8_0 returns the sum before the block scale.
 template <int F>
-__device__ __forceinline__ float chunk_dot(const uint4 w, const float *x);
+__device__ __forceinline__ float chunk_dot(const uint4 w, const float4 *xq, int nch, int c);
 
 template <>
-__device__ __forceinline__ float chunk_dot<FMT_Q8_0>(const uint4 w, const float *x) {
-  const float4 *x4 = reinterpret_cast<const float4 *>(x);
+__device__ __forceinline__ float chunk_dot<FMT_Q8_0>(const uint4 w, const float4 *xq, int nch, int c) {
   const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
   float a = 0.f, b = 0.f;
 #pragma unroll
   for (int k = 0; k < 4; k++) {
-    const float4 xv = x4[k];
+    const float4 xv = xq[k * nch + c];
     const uint32_t v = ws[k];
     a = fmaf((float)(int8_t)(v), xv.x, a);
     b = fmaf((float)(int8_t)(v >> 8), xv.y, b);
@@ -71,9 +96,8 @@ __device__ __forceinline__ float chunk_dot<FMT_Q8_0>(const uint4 w, const float 
 }
 
 template <>
-__device__ __forceinline__ float chunk_dot<FMT_BF16>(const uint4 w, const float *x) {
-  const float4 *x4 = reinterpret_cast<const float4 *>(x);
-  const float4 x0 = x4[0], x1 = x4[1];
+__device__ __forceinline__ float chunk_dot<FMT_BF16>(const uint4 w, const float4 *xq, int nch, int c) {
+  const float4 x0 = xq[c], x1 = xq[nch + c];
   float a = __uint_as_float(w.x << 16) * x0.x;
   float b = __uint_as_float(w.x & 0xffff0000u) * x0.y;
   a = fmaf(__uint_as_float(w.y << 16), x0.z, a);
@@ -86,9 +110,8 @@ __device__ __forceinline__ float chunk_dot<FMT_BF16>(const uint4 w, const float 
 }
 
 template <>
-__device__ __forceinline__ float chunk_dot<FMT_F16>(const uint4 w, const float *x) {
-  const float4 *x4 = reinterpret_cast<const float4 *>(x);
-  const float4 x0 = x4[0], x1 = x4[1];
+__device__ __forceinline__ float chunk_dot<FMT_F16>(const uint4 w, const float4 *xq, int nch, int c) {
+  const float4 x0 = xq[c], x1 = xq[nch + c];
   float a = hw_half((uint16_t)w.x) * x0.x;
   float b = hw_half((uint16_t)(w.x >> 16)) * x0.y;
   a = fmaf(hw_half((uint16_t)w.y), x0.z, a);
@@ -101,23 +124,13 @@ __device__ __forceinline__ float chunk_dot<FMT_F16>(const uint4 w, const float *
 }
 
 template <>
-__device__ __forceinline__ float chunk_dot<FMT_F32>(const uint4 w, const float *x) {
-  const float4 xv = *reinterpret_cast<const float4 *>(x);
+__device__ __forceinline__ float chunk_dot<FMT_F32>(const uint4 w, const float4 *xq, int nch, int c) {
+  const float4 xv = xq[c];
   float a = __uint_as_float(w.x) * xv.x;
   float b = __uint_as_float(w.y) * xv.y;
   a = fmaf(__uint_as_float(w.z), xv.z, a);
   b = fmaf(__uint_as_float(w.w), xv.w, b);
   return a + b;
-}
-
-// Scale applied to a chunk's partial sum (Q8_0 block scale; 1 otherwise).
-template <int F>
-__device__ __forceinline__ float chunk_scale(const uint8_t *meta_row, int c) {
-  if constexpr (F == FMT_Q8_0) {
-    return hw_half(reinterpret_cast<const uint16_t *>(meta_row)[c >> 1]);
-  } else {
-    return 1.0f;
-  }
 }
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -129,46 +142,82 @@ __device__ __forceinline__ uint4 load_chunk(const uint8_t *p) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
-// Wave-cooperative dot products of two row segments with LDS-resident
-// vectors: segment 0 (row p0, vector x0, n0 chunks) and segment 1 (row p1,
-// x1, n1 chunks), streamed as one chunk sequence so each lane keeps U loads
-// in flight. Results are reduced across the wave (every lane gets them).
+// ---------------------------------------------------------------- streaming
+// A unit of matvec work: one or two row segments, each with its own staged
+// x vector (xq0 / xq1 with n0 / n1 chunks). n1 == 0 means one segment.
+struct Seg2 {
+  const uint8_t *v0, *m0, *v1, *m1;
+  const float4 *x0, *x1;
+  int n0, n1;
+};
+
+// One batch of U chunks per lane: the weight bytes and, for Q8_0, the raw
+// fp16 block scale. Scales stay raw until the chunk is consumed: converting
+// at load time would make every load wait for its predecessor.
+template <int U>
+struct Batch {
+  uint4 w[U];
+  uint16_t s[U];
+};
+
+// Issues every load of a batch back to back. Lanes past the end load a
+// valid chunk (the last one) whose value is never consumed, so the loads
+// need no branches.
 template <int F, int U>
-__device__ __forceinline__ void seg2_dot(const uint8_t *__restrict__ v0, const uint8_t *__restrict__ m0,
-                                         const float *x0, int n0,
-                                         const uint8_t *__restrict__ v1, const uint8_t *__restrict__ m1,
-                                         const float *x1, int n1, float &out0, float &out1) {
-  constexpr int VPC = Fmt<F>::VPC;
-  const int lane = threadIdx.x & 63;
-  const int total = n0 + n1;
-  float acc0 = 0.f, acc1 = 0.f;
-  for (int base = 0; base < total; base += 64 * U) {
-    uint4 w[U];
-    float s[U];
+__device__ __forceinline__ void batch_issue(Batch<U> &b, const Seg2 &g, int base, int lane) {
+  const int total = g.n0 + g.n1;
 #pragma unroll
-    for (int u = 0; u < U; u++) {
-      const int c = base + u * 64 + lane;
-      const bool seg1 = c >= n0;
-      const int cc = seg1 ? c - n0 : c;
-      if (c < total) {
-        w[u] = load_chunk((seg1 ? v1 : v0) + (int64_t)cc * 16);
-        s[u] = chunk_scale<F>(seg1 ? m1 : m0, cc);
-      }
-    }
+  for (int u = 0; u < U; u++) {
+    const int c = min(base + u * 64 + lane, total - 1);
+    const bool seg1 = c >= g.n0;
+    const int cc = seg1 ? c - g.n0 : c;
+    b.w[u] = load_chunk((seg1 ? g.v1 : g.v0) + (int64_t)cc * 16);
+    if constexpr (F == FMT_Q8_0) b.s[u] = reinterpret_cast<const uint16_t *>(seg1 ? g.m1 : g.m0)[cc >> 1];
+  }
+}
+
+template <int F, int U>
+__device__ __forceinline__ void batch_consume(const Batch<U> &b, const Seg2 &g, int base, int lane, float &acc0,
+                                              float &acc1) {
+  const int total = g.n0 + g.n1;
 #pragma unroll
-    for (int u = 0; u < U; u++) {
-      const int c = base + u * 64 + lane;
-      const bool seg1 = c >= n0;
-      const int cc = seg1 ? c - n0 : c;
-      if (c < total) {
-        float p = chunk_dot<F>(w[u], (seg1 ? x1 : x0) + cc * VPC);
-        if constexpr (F == FMT_Q8_0) p *= s[u];
-        if (seg1) acc1 += p; else acc0 += p;
-      }
+  for (int u = 0; u < U; u++) {
+    const int c = base + u * 64 + lane;
+    if (c < total) {
+      const bool seg1 = c >= g.n0;
+      const int cc = seg1 ? c - g.n0 : c;
+      float p = chunk_dot<F>(b.w[u], seg1 ? g.x1 : g.x0, seg1 ? g.n1 : g.n0, cc);
+      if constexpr (F == FMT_Q8_0) p *= hw_half(b.s[u]);
+      if (seg1) acc1 += p; else acc0 += p;
     }
   }
-  out0 = wave_sum(acc0);
-  out1 = wave_sum(acc1);
+}
+
+// Runs units first, first + stride, ... (< n_units) through one wave, each
+// as batches of 64 * U chunks (one batch when U covers the unit). The first
+// batch is issued before `prologue()` (the block's LDS staging, which the
+// weights do not depend on); `unit(u, g)` describes unit u; `done(u, r0, r1)`
+// receives the two wave-reduced dot products (every lane calls it).
+template <int F, int U, typename Prologue, typename UnitFn, typename Done>
+__device__ __forceinline__ void stream_units(int first, int stride, int n_units, Prologue prologue, UnitFn unit,
+                                             Done done) {
+  const int lane = threadIdx.x & 63;
+  Seg2 g{};
+  Batch<U> b;
+  if (first < n_units) {
+    unit(first, g);
+    batch_issue<F, U>(b, g, 0, lane);
+  }
+  prologue();
+  for (int u = first; u < n_units; u += stride) {
+    if (u != first) unit(u, g);
+    float acc0 = 0.f, acc1 = 0.f;
+    for (int base = 0; base < g.n0 + g.n1; base += 64 * U) {
+      if (u != first || base != 0) batch_issue<F, U>(b, g, base, lane);
+      batch_consume<F, U>(b, g, base, lane, acc0, acc1);
+    }
+    done(u, wave_sum(acc0), wave_sum(acc1));
+  }
 }
 
 // Bit-exact value at (row, col): readValues (matmul.go:12-50) on the

@@ -27,22 +27,33 @@ struct KVDev {
 };
 
 // ---- decode (one token) ----
+// Matvec launches take their grid and block size (256, 512, 640 or 1024
+// threads) from the caller; blocks loop over their share of the rows.
 // LayerNorm(x) -> q/k/v/gate/up with RoPE, KV append and SiLU-gate fused
-// into the epilogue. pos is read from device memory.
-hipError_t launch_decode_in(const LayerDev &w, const StableDims &s, const KVDev &kv, const float *x,
-                            const float *rope, const int *pos, float *q_out, float *m_out,
-                            int grid, hipStream_t st);
+// into the epilogue. pos (and token) are read from device memory. With
+// `emb` (a host-side descriptor, copied), x is first set to the embedding
+// row of *token (layer 0).
+hipError_t launch_decode_in(const LayerDev &w, const StableDims &s, const KVDev &kv, float *x, const MatDesc *emb,
+                            const int *token, const float *rope, const int *pos, float *q_out, float *m_out,
+                            int grid, int threads, hipStream_t st);
 // x += o * a + down * m (stablelm.go:365-377).
 hipError_t launch_decode_out(const LayerDev &w, const StableDims &s, const float *a, const float *m,
-                             float *x, int grid, hipStream_t st);
+                             float *x, int grid, int threads, hipStream_t st);
 // Split-K flash decode with in-kernel combine for nq queries at positions
-// pos0 + j (j < nq): q [nq][heads*hd] -> out [nq][heads*hd].
+// pos0 + j (j < nq): q [nq][heads*hd] -> out [nq][heads*hd]. A block covers
+// 64 * steps positions; `splits` blocks per (query, head) must cover
+// max_pos + 1 positions (<= 0: derived from max_pos). partials holds
+// nq * heads * splits * (hd + 2) floats; counters (nq * heads) start at 0
+// and are left at 0.
 hipError_t launch_attention(const StableDims &s, const KVDev &kv, const float *q, const int *pos0, int nq,
-                            int max_pos, float *partials, unsigned *counters, float *out, hipStream_t st);
+                            int max_pos, float *partials, unsigned *counters, float *out, hipStream_t st,
+                            int steps = 0, int splits = 0);
+int attention_steps(int max_pos, int heads);
+int attention_splits(int max_pos, int steps);
 // out[rows] = W * LN(x) (LN skipped when ln_w is null), for the logits head
 // and single-matrix products.
 hipError_t launch_ln_matvec(const MatDesc &w, const float *ln_w, const float *ln_b, double eps,
-                            const float *x, float *out, int grid, hipStream_t st);
+                            const float *x, float *out, int grid, int threads, hipStream_t st);
 // x[n][cols] = rows ids[j] of an embedding matrix, bit-exact dequantized.
 hipError_t launch_embed(const MatDesc &emb, const int *ids, int n, float *x, hipStream_t st);
 

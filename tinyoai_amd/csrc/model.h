@@ -3,6 +3,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <map>
 #include <string>
 #include <vector>
 
@@ -83,9 +84,13 @@ struct StableModel {
   bool tracing = false;
   float *trace_dev = nullptr;
   int grid_in = 0, grid_out = 0, grid_head = 0;
+  int threads_in = 256, threads_out = 256, threads_head = 256;
 
   std::vector<void *> buffers;
   Profiler prof;
+  // Decode graphs by attention launch shape (valid for the current KV).
+  std::map<int64_t, hipGraphExec_t> graphs;
+  bool use_graphs = true;
 
   ~StableModel();
   int init(const tinyoai_stablelm_config &c, const tinyoai_tensor *tensors, int n);
@@ -93,6 +98,8 @@ struct StableModel {
   void free_kv();
   int ensure_kv(int needed);
   int upload_params(const int *head_vals, int nh, const int32_t *ids, int n);
+  int enqueue_decode(int steps, int splits, bool want_logits);
+  void drop_graphs();
   int decode_step(int token, int pos, bool want_logits);
   int prefill_chunk(const int32_t *ids, int n, int start, bool want_logits);
   int forward(int prefix, const int32_t *tokens, int n, bool want_logits, float *logits);
