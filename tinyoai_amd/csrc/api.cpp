@@ -53,23 +53,19 @@ DevMatrix::~DevMatrix() {
   if (mem) hipFree(mem);
 }
 
-int DevMatrix::upload(int32_t dtype, int64_t rows, int64_t cols, const void *data, uint64_t nbytes,
-                      hipStream_t st) {
+static int64_t value_width(int32_t dtype) { return dtype == FMT_F32 ? 4 : (dtype == FMT_Q8_0 ? 1 : 2); }
+
+int DevMatrix::create(int32_t dtype, int64_t rows, int64_t cols, hipStream_t st) {
   if (rows <= 0 || cols <= 0 || rows > INT32_MAX || cols > INT32_MAX)
     return fail(TINYOAI_EINVAL, "invalid matrix shape [%lld, %lld]", (long long)rows, (long long)cols);
   if (dtype != FMT_F32 && dtype != FMT_F16 && dtype != FMT_BF16 && dtype != FMT_Q8_0)
     return fail(TINYOAI_EINVAL, "unsupported tensor type %d", dtype);
-  const int64_t want = gguf_bytes(dtype, rows, cols);
-  if (want < 0) return fail(TINYOAI_EINVAL, "Q8_0 rows must be divisible by 32");
-  if ((int64_t)nbytes != want)
-    return fail(TINYOAI_EINVAL, "tensor [%lld, %lld] of type %d needs %lld bytes, got %llu", (long long)rows,
-                (long long)cols, dtype, (long long)want, (unsigned long long)nbytes);
+  if (dtype == FMT_Q8_0 && cols % 32) return fail(TINYOAI_EINVAL, "Q8_0 rows must be divisible by 32");
   MatDesc m{};
   m.fmt = dtype;
   m.rows = (int32_t)rows;
   m.cols = (int32_t)cols;
-  const int64_t width = dtype == FMT_F32 ? 4 : (dtype == FMT_Q8_0 ? 1 : 2);
-  m.vstride = (cols * width + 15) / 16 * 16;
+  m.vstride = (cols * value_width(dtype) + 15) / 16 * 16;
   m.mstride = dtype == FMT_Q8_0 ? cols / 32 * 2 : 0;
   m.chunks = (int32_t)(m.vstride / 16);
   const size_t vbytes = (size_t)(m.vstride * rows);
@@ -78,24 +74,72 @@ int DevMatrix::upload(int32_t dtype, int64_t rows, int64_t cols, const void *dat
   hipError_t e = hipMalloc(&mem, total);
   if (e != hipSuccess) return fail(TINYOAI_ENOMEM, "hipMalloc(%zu): %s", total, hipGetErrorString(e));
   bytes = total;
+  e = hipMemsetAsync(mem, 0, total, st);  // row padding reads as zeros
+  if (e != hipSuccess) return hip_fail(e, "weight init");
   m.vals = (const uint8_t *)mem;
   m.meta = m.mstride ? (const uint8_t *)mem + (vbytes + 255) / 256 * 256 : (const uint8_t *)mem;
-  const bool plain = dtype != FMT_Q8_0 && m.vstride == cols * width;
-  if (plain) {
-    e = hipMemcpyAsync(mem, data, nbytes, hipMemcpyHostToDevice, st);
-    if (e != hipSuccess) return hip_fail(e, "weight upload");
-  } else {
-    void *raw = nullptr;
-    e = hipMalloc(&raw, nbytes);
-    if (e != hipSuccess) return fail(TINYOAI_ENOMEM, "hipMalloc(%llu): %s", (unsigned long long)nbytes, hipGetErrorString(e));
-    e = hipMemcpyAsync(raw, data, nbytes, hipMemcpyHostToDevice, st);
-    if (e == hipSuccess) e = launch_repack(dtype, (const uint8_t *)raw, rows, cols, m, st);
-    if (e == hipSuccess) e = hipStreamSynchronize(st);
-    hipFree(raw);
-    if (e != hipSuccess) return hip_fail(e, "weight repack");
-  }
   desc = m;
   return TINYOAI_OK;
+}
+
+int DevMatrix::place(int32_t dtype, int64_t rows, int64_t cols, const void *data, uint64_t nbytes, const RowMap &map,
+                     int64_t col0, hipStream_t st) {
+  const MatDesc &m = desc;
+  if (!mem || dtype != m.fmt) return fail(TINYOAI_EINVAL, "tensor type %d does not match its matrix (%d)", dtype, m.fmt);
+  const int64_t want = gguf_bytes(dtype, rows, cols);
+  if (want < 0 || rows <= 0) return fail(TINYOAI_EINVAL, "invalid tensor shape [%lld, %lld]", (long long)rows, (long long)cols);
+  if ((int64_t)nbytes != want)
+    return fail(TINYOAI_EINVAL, "tensor [%lld, %lld] of type %d needs %lld bytes, got %llu", (long long)rows,
+                (long long)cols, dtype, (long long)want, (unsigned long long)nbytes);
+  // Every destination row and byte must fall inside the matrix.
+  int64_t last_row;
+  switch (map.kind) {
+    case ROWMAP_HEADS:
+      if (map.hd <= 0 || rows % map.hd || map.rot < 0 || map.rot % 2 || map.rot > map.hd)
+        return fail(TINYOAI_EINVAL, "invalid head row map");
+      last_row = map.offset + rows - 1;
+      break;
+    case ROWMAP_INTERLEAVE: last_row = map.offset + 2 * (rows - 1) + map.phase; break;
+    default: last_row = map.offset + rows - 1;
+  }
+  if (map.offset < 0 || last_row >= m.rows || col0 < 0 || (col0 + cols) * value_width(dtype) > m.vstride ||
+      (dtype == FMT_Q8_0 && (col0 % 32 || (col0 + cols) / 32 * 2 > m.mstride)))
+    return fail(TINYOAI_EINVAL, "tensor [%lld, %lld] does not fit its place in a [%d, %d] matrix", (long long)rows,
+                (long long)cols, m.rows, m.cols);
+  const int64_t width = value_width(dtype);
+  hipError_t e;
+  if (dtype != FMT_Q8_0 && map.kind == ROWMAP_IDENTITY && col0 == 0 && m.vstride == cols * width) {
+    e = hipMemcpyAsync((uint8_t *)mem + map.offset * m.vstride, data, nbytes, hipMemcpyHostToDevice, st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    return e == hipSuccess ? TINYOAI_OK : hip_fail(e, "weight upload");
+  }
+  void *raw = nullptr;
+  e = hipMalloc(&raw, nbytes);
+  if (e != hipSuccess) return fail(TINYOAI_ENOMEM, "hipMalloc(%llu): %s", (unsigned long long)nbytes, hipGetErrorString(e));
+  e = hipMemcpyAsync(raw, data, nbytes, hipMemcpyHostToDevice, st);
+  if (e == hipSuccess) e = launch_repack(dtype, (const uint8_t *)raw, rows, cols, m, map, col0, st);
+  if (e == hipSuccess) e = hipStreamSynchronize(st);
+  hipFree(raw);
+  return e == hipSuccess ? TINYOAI_OK : hip_fail(e, "weight repack");
+}
+
+int DevMatrix::upload(int32_t dtype, int64_t rows, int64_t cols, const void *data, uint64_t nbytes, hipStream_t st) {
+  const int64_t want = gguf_bytes(dtype, rows, cols);
+  if (want >= 0 && (int64_t)nbytes != want)
+    return fail(TINYOAI_EINVAL, "tensor [%lld, %lld] of type %d needs %lld bytes, got %llu", (long long)rows,
+                (long long)cols, dtype, (long long)want, (unsigned long long)nbytes);
+  int rc = create(dtype, rows, cols, st);
+  return rc ? rc : place(dtype, rows, cols, data, nbytes, RowMap{ROWMAP_IDENTITY, 0, 0, 0, 0}, 0, st);
+}
+
+MatDesc column_view(const MatDesc &m, int64_t col0, int64_t cols) {
+  MatDesc v = m;
+  const int64_t width = value_width(m.fmt);
+  v.vals = m.vals + col0 * width;
+  v.meta = m.fmt == FMT_Q8_0 ? m.meta + col0 / 32 * 2 : m.meta;
+  v.cols = (int32_t)cols;
+  v.chunks = (int32_t)((cols * width + 15) / 16);
+  return v;
 }
 
 // ---------------------------------------------------------------- profiling
@@ -239,23 +283,55 @@ int StableModel::init(const tinyoai_stablelm_config &c, const tinyoai_tensor *te
   if ((rc = load("lm_head.weight", c.vocab_size, d, head))) return rc;
   if ((rc = load_vec("model.norm.weight", &norm_w))) return rc;
   if ((rc = load_vec("model.norm.bias", &norm_b))) return rc;
-  mats.resize((size_t)c.num_hidden_layers * 7);
+  mats.resize((size_t)c.num_hidden_layers * 2);
   layers.resize(c.num_hidden_layers);
+  win_rows = d + 2 * kvw + 2 * I;
+  auto find = [&](const std::string &name, int64_t rows, int64_t cols, const tinyoai_tensor **t) -> int {
+    auto it = by_name.find(name);
+    if (it == by_name.end()) return fail(TINYOAI_EINVAL, "missing tensor %s", name.c_str());
+    *t = it->second;
+    if ((*t)->rows != rows || (*t)->cols != cols)
+      return fail(TINYOAI_EINVAL, "tensor %s: shape [%lld %lld], want [%lld %lld]", name.c_str(),
+                  (long long)(*t)->rows, (long long)(*t)->cols, (long long)rows, (long long)cols);
+    return TINYOAI_OK;
+  };
+  auto place = [&](DevMatrix &dst, const std::string &name, const tinyoai_tensor *t, const RowMap &map,
+                   int64_t col0) -> int {
+    int rc2 = dst.place(t->dtype, t->rows, t->cols, t->data, t->nbytes, map, col0, stream);
+    if (rc2) g_error = "tensor " + name + ": " + g_error;
+    return rc2;
+  };
   for (int l = 0; l < c.num_hidden_layers; l++) {
     const std::string p = "model.layers." + std::to_string(l) + ".";
-    DevMatrix *m = &mats[(size_t)l * 7];
-    if ((rc = load(p + "self_attn.q_proj.weight", d, d, m[0]))) return rc;
-    if ((rc = load(p + "self_attn.k_proj.weight", kvw, d, m[1]))) return rc;
-    if ((rc = load(p + "self_attn.v_proj.weight", kvw, d, m[2]))) return rc;
-    if ((rc = load(p + "self_attn.o_proj.weight", d, d, m[3]))) return rc;
-    if ((rc = load(p + "mlp.gate_proj.weight", I, d, m[4]))) return rc;
-    if ((rc = load(p + "mlp.up_proj.weight", I, d, m[5]))) return rc;
-    if ((rc = load(p + "mlp.down_proj.weight", d, I, m[6]))) return rc;
+    static const char *names[7] = {"self_attn.q_proj.weight", "self_attn.k_proj.weight", "self_attn.v_proj.weight",
+                                   "self_attn.o_proj.weight", "mlp.gate_proj.weight",    "mlp.up_proj.weight",
+                                   "mlp.down_proj.weight"};
+    const int64_t shape[7][2] = {{d, d}, {kvw, d}, {kvw, d}, {d, d}, {I, d}, {I, d}, {d, I}};
+    const tinyoai_tensor *t[7];
+    for (int i = 0; i < 7; i++)
+      if ((rc = find(p + names[i], shape[i][0], shape[i][1], &t[i]))) return rc;
+    const int32_t fin = t[0]->dtype, fout = t[3]->dtype;
+    if (t[1]->dtype != fin || t[2]->dtype != fin || t[4]->dtype != fin || t[5]->dtype != fin || t[6]->dtype != fout)
+      return fail(TINYOAI_EINVAL,
+                  "layer %d: q/k/v/gate/up must share one storage format, and o/down another", l);
+    // win: [q | k | v | gate/up interleaved], rotary pairs adjacent in q and k.
+    DevMatrix &win = mats[(size_t)l * 2], &wout = mats[(size_t)l * 2 + 1];
+    if ((rc = win.create(fin, win_rows, d, stream))) return rc;
+    if ((rc = place(win, p + names[0], t[0], RowMap{ROWMAP_HEADS, 0, hd, dims.rot, 0}, 0)) ||
+        (rc = place(win, p + names[1], t[1], RowMap{ROWMAP_HEADS, d, hd, dims.rot, 0}, 0)) ||
+        (rc = place(win, p + names[2], t[2], RowMap{ROWMAP_IDENTITY, d + kvw, 0, 0, 0}, 0)) ||
+        (rc = place(win, p + names[4], t[4], RowMap{ROWMAP_INTERLEAVE, d + 2 * kvw, 0, 0, 0}, 0)) ||
+        (rc = place(win, p + names[5], t[5], RowMap{ROWMAP_INTERLEAVE, d + 2 * kvw, 0, 0, 1}, 0)))
+      return rc;
+    // wout: [o | down] per output row, down starting on a chunk boundary.
+    const int64_t vpc = values_per_chunk(fout), down0 = (d + vpc - 1) / vpc * vpc;
+    if ((rc = wout.create(fout, d, down0 + I, stream))) return rc;
+    if ((rc = place(wout, p + names[3], t[3], RowMap{ROWMAP_IDENTITY, 0, 0, 0, 0}, 0)) ||
+        (rc = place(wout, p + names[6], t[6], RowMap{ROWMAP_IDENTITY, 0, 0, 0, 0}, down0)))
+      return rc;
     LayerDev &L = layers[l];
-    L.q = m[0].desc; L.k = m[1].desc; L.v = m[2].desc; L.o = m[3].desc;
-    L.gate = m[4].desc; L.up = m[5].desc; L.down = m[6].desc;
-    if (L.q.fmt != L.k.fmt || L.q.fmt != L.v.fmt || L.gate.fmt != L.up.fmt)
-      return fail(TINYOAI_EINVAL, "layer %d: q/k/v and gate/up must share their storage formats", l);
+    L.win = win.desc;
+    L.wout = wout.desc;
     if ((rc = load_vec(p + "input_layernorm.weight", &L.ln_w))) return rc;
     if ((rc = load_vec(p + "input_layernorm.bias", &L.ln_b))) return rc;
   }
@@ -277,12 +353,12 @@ int StableModel::init(const tinyoai_stablelm_config &c, const tinyoai_tensor *te
   e = hipMemsetAsync(counters, 0, (size_t)chunk * dims.heads * 4, stream);
   if (e != hipSuccess) return hip_fail(e, "counter init");
   if ((rc = alloc((void **)&partials, (size_t)chunk * dims.heads * max_splits * (hd + 2) * 4))) return rc;
-  const size_t B = chunk;
+  const size_t B = chunk, wide = std::max(d, I);
   if ((rc = alloc((void **)&X, B * d * 4)) || (rc = alloc((void **)&H, B * d * 4)) ||
-      (rc = alloc((void **)&Q, B * w_att * 4)) || (rc = alloc((void **)&K, B * kvw * 4)) ||
-      (rc = alloc((void **)&V, B * kvw * 4)) || (rc = alloc((void **)&G, B * I * 4)) ||
-      (rc = alloc((void **)&U, B * I * 4)) || (rc = alloc((void **)&A, B * w_att * 4)) ||
-      (rc = alloc((void **)&P, B * d * 4)) || (rc = alloc((void **)&D, B * d * 4)))
+      (rc = alloc((void **)&Y, B * win_rows * 4)) || (rc = alloc((void **)&Q, B * w_att * 4)) ||
+      (rc = alloc((void **)&M, B * I * 4)) || (rc = alloc((void **)&A, B * w_att * 4)) ||
+      (rc = alloc((void **)&P, B * d * 4)) || (rc = alloc((void **)&D, B * d * 4)) ||
+      (rc = alloc((void **)&XH, B * wide * 2)) || (rc = alloc((void **)&XL, B * wide * 2)))
     return rc;
   e = hipEventCreateWithFlags(&params_copied, hipEventDisableTiming);
   if (e != hipSuccess) return hip_fail(e, "hipEventCreate");
@@ -423,6 +499,25 @@ int StableModel::decode_step(int token, int pos, bool want_logits) {
   return TINYOAI_OK;
 }
 
+// y[n][ldy] = x[n][ldx] * W^T: on the matrix cores when the format allows
+// (activations split into bf16 hi/lo planes first), else the vector-unit
+// GEMM.
+int StableModel::project(const MatDesc &w, const float *x, int ldx, int n, float *y, int ldy) {
+  if (gemm_mfma_supported(w)) {
+    const bool two = gemm_planes(w) == 2;
+    STAGE(ST_PREFILL_GEMM, launch_split_bf16(x, ldx, w.cols, n, XH, two ? XL : nullptr, stream), "bf16 split");
+    STAGE(ST_PREFILL_GEMM, launch_gemm_mfma(w, XH, two ? XL : nullptr, n, y, ldy, stream), "projection");
+  } else {
+    if (ldx != w.cols || ldy != w.rows) return fail(TINYOAI_EINVAL, "vector-unit GEMM needs dense operands");
+    STAGE(ST_PREFILL_GEMM, launch_gemm(w, x, n, y, stream), "projection");
+  }
+  return TINYOAI_OK;
+}
+
+// n tokens at positions start.. (StableLM.prefill, prefill.go:33-115): per
+// layer LayerNorm, one product with win and its fused epilogue, causal
+// attention over the cache, the o and down products over the two column
+// ranges of wout, and the parallel residual.
 int StableModel::prefill_chunk(const int32_t *ids, int n, int start, bool want_logits) {
   const int vals[1] = {start};
   if (int rc = upload_params(vals, 1, ids, n)) return rc;
@@ -431,18 +526,16 @@ int StableModel::prefill_chunk(const int32_t *ids, int n, int start, bool want_l
   STAGE(ST_EMBED, launch_embed(embed.desc, d_ids, n, X, stream), "embed");
   for (int l = 0; l < cfg.num_hidden_layers; l++) {
     const LayerDev &w = layers[l];
+    const int64_t vpc = values_per_chunk(w.wout.fmt), down0 = (d + vpc - 1) / vpc * vpc;
+    const MatDesc wo = column_view(w.wout, 0, d), wd = column_view(w.wout, down0, I);
+    int rc;
     STAGE(ST_PREFILL_NORM, launch_layer_norm_rows(X, w.ln_w, w.ln_b, dims.eps, n, d, H, stream), "layer_norm");
-    STAGE(ST_PREFILL_GEMM, launch_gemm(w.q, H, n, Q, stream), "q_proj");
-    STAGE(ST_PREFILL_GEMM, launch_gemm(w.k, H, n, K, stream), "k_proj");
-    STAGE(ST_PREFILL_GEMM, launch_gemm(w.v, H, n, V, stream), "v_proj");
-    STAGE(ST_PREFILL_ROPE, launch_rope_store(dims, kv[l], Q, K, V, rope, d_pos0, n, stream), "rope_store");
+    if ((rc = project(w.win, H, d, n, Y, win_rows))) return rc;
+    STAGE(ST_PREFILL_EPILOGUE, launch_in_epilogue(dims, kv[l], Y, win_rows, rope, d_pos0, n, Q, M, stream),
+          "in_epilogue");
     STAGE(ST_PREFILL_ATTENTION,
           launch_attention(dims, kv[l], Q, d_pos0, n, start + n - 1, partials, counters, A, stream), "attention");
-    STAGE(ST_PREFILL_GEMM, launch_gemm(w.o, A, n, P, stream), "o_proj");
-    STAGE(ST_PREFILL_GEMM, launch_gemm(w.gate, H, n, G, stream), "gate_proj");
-    STAGE(ST_PREFILL_GEMM, launch_gemm(w.up, H, n, U, stream), "up_proj");
-    STAGE(ST_PREFILL_ELEMENTWISE, launch_silu_gate(G, U, (int64_t)n * I, stream), "silu_gate");
-    STAGE(ST_PREFILL_GEMM, launch_gemm(w.down, G, n, D, stream), "down_proj");
+    if ((rc = project(wo, A, d, n, P, d)) || (rc = project(wd, M, I, n, D, d))) return rc;
     STAGE(ST_PREFILL_ELEMENTWISE, launch_residual(X, P, D, (int64_t)n * d, stream), "residual");
     if (tracing) TRY_HIP(launch_copy_row(X + (size_t)(n - 1) * d, trace_dev + (size_t)l * d, d, stream), "trace");
   }
@@ -507,7 +600,10 @@ struct tinyoai_model {
 struct tinyoai_weight {
   DevMatrix m;
   hipStream_t stream = nullptr;
+  uint16_t *planes = nullptr;  // bf16 hi/lo planes of the last batched product's input
+  size_t planes_bytes = 0;
   ~tinyoai_weight() {
+    if (planes) hipFree(planes);
     if (stream) hipStreamDestroy(stream);
   }
 };
@@ -675,11 +771,31 @@ int tinyoai_weight_read_values(tinyoai_weight *w, int64_t offset, int64_t n, flo
 int tinyoai_weight_mul_device(tinyoai_weight *w, const float *x_dev, int32_t n, float *out_dev, void *stream) {
   if (!w || !x_dev || !out_dev || n <= 0) return fail(TINYOAI_EINVAL, "invalid product arguments");
   hipStream_t st = stream ? (hipStream_t)stream : w->stream;
+  const MatDesc &m = w->m.desc;
   hipError_t e;
-  if (n == 1)
-    e = launch_ln_matvec(w->m.desc, nullptr, nullptr, 0.0, x_dev, out_dev, device_cu_count() * 4, 256, st);
-  else
-    e = launch_gemm(w->m.desc, x_dev, n, out_dev, st);
+  if (n == 1) {
+    e = launch_ln_matvec(m, nullptr, nullptr, 0.0, x_dev, out_dev, device_cu_count() * 4, 256, st);
+  } else if (gemm_mfma_supported(m)) {
+    // Batched products on the matrix cores; the plane buffer grows on demand
+    // (the stream is drained before an old buffer is released).
+    const size_t plane = (size_t)n * m.cols * 2, need = plane * gemm_planes(m);
+    if (need > w->planes_bytes) {
+      if (w->planes) {
+        hipStreamSynchronize(st);
+        hipFree(w->planes);
+        w->planes = nullptr;
+        w->planes_bytes = 0;
+      }
+      e = hipMalloc(&w->planes, need);
+      if (e != hipSuccess) return fail(TINYOAI_ENOMEM, "hipMalloc(%zu): %s", need, hipGetErrorString(e));
+      w->planes_bytes = need;
+    }
+    uint16_t *hi = w->planes, *lo = gemm_planes(m) == 2 ? w->planes + plane / 2 : nullptr;
+    e = launch_split_bf16(x_dev, m.cols, m.cols, n, hi, lo, st);
+    if (e == hipSuccess) e = launch_gemm_mfma(m, hi, lo, n, out_dev, m.rows, st);
+  } else {
+    e = launch_gemm(m, x_dev, n, out_dev, st);
+  }
   return e == hipSuccess ? TINYOAI_OK : hip_fail(e, "product launch");
 }
 

@@ -1,34 +1,26 @@
 // Decode-path kernels (one token through a StableLM layer) for gfx950.
 //
 // StableLM's parallel residual (stablelm.go:365-377) lets a layer run as
-// three launches:
-//   decode_in   LayerNorm(x) once per block into LDS, then every weight row
-//               that reads it (q, k, v, gate, up) in one pass over HBM, with
-//               RoPE, the KV append and SiLU-gate applied in the epilogue;
-//               layer 0 also gathers the token's embedding row here;
+// three launches over the fused matrices of LayerDev (kernels.h):
+//   decode_in   LayerNorm(x) once per block into LDS, then every row of win
+//               (q, k, v, gate, up) in one pass over HBM, with RoPE, the KV
+//               append and SiLU-gate applied in the epilogue; layer 0 also
+//               gathers the token's embedding row here;
 //   attention   split-K flash decode; blocks of a head combine through the
 //               last-arriving block;
-//   decode_out  x = (x + o*a) + down*m over the o and down rows.
-// Rows are handed out in "units" of two: a rotary pair (i, i + rot/2) of a
-// q or k head, two adjacent non-rotary rows, or gate row i with up row i.
-// Each wave streams its units with the next batch of weight loads in flight
-// (stream_units, formats.h).
+//   decode_out  x = (x + o*a) + down*m, one wout row [o | down] per unit.
+// decode_in hands out win rows in pairs (2u, 2u + 1): a rotary pair, two
+// adjacent non-rotary dims, or gate row i with up row i. Each wave streams
+// its units with the next batch of weight loads in flight (stream_units,
+// formats.h).
 #include <algorithm>
 
-#include "kernels.h"
+#include "epilogue.h"
 
 namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
-
-__device__ __forceinline__ void store_kv(const KVDev &kv, int64_t idx, float v, bool k) {
-  void *base = k ? kv.k : kv.v;
-  if (kv.half)
-    reinterpret_cast<uint16_t *>(base)[idx] = float_to_half(v);
-  else
-    reinterpret_cast<float *>(base)[idx] = v;
-}
 
 struct InArgs {
   LayerDev w;
@@ -41,23 +33,20 @@ struct InArgs {
   const float *rope;
   const int *pos;
   float *q_out, *m_out;
-  int xlen;  // LDS vector length (>= d, covers padded chunks)
 };
 
 template <int F, int U, int T>
 __global__ __launch_bounds__(T) void decode_in_kernel(InArgs a) {
   extern __shared__ __align__(16) float lds[];
   constexpr int VPC = Fmt<F>::VPC;
-  const int nch = a.w.q.chunks;
-  float4 *xq = reinterpret_cast<float4 *>(lds + ((a.xlen + 3) & ~3));
+  const MatDesc &W = a.w.win;
+  const int nch = W.chunks;
+  const StableDims &s = a.s;
+  float4 *xq = reinterpret_cast<float4 *>(lds + ((s.d + 3) & ~3));
   double *red = reinterpret_cast<double *>(xq + (VPC / 4) * nch);
   float *rope_row = reinterpret_cast<float *>(red + 16);  // cos/sin at pos, [rot/2][2]
-  const StableDims &s = a.s;
   const int pos = *a.pos;
   const int lane = threadIdx.x & 63;
-  const int half_hd = s.hd / 2, rh = s.rot / 2;
-  const int nq = s.heads * half_hd, nk = s.kv_heads * half_hd;
-  const int natt = nq + 2 * nk, total = natt + s.inter;
 
   auto prologue = [&]() {
     if (a.use_emb) {  // embedding row (stablelm.go:338), bit-exact readValues
@@ -78,63 +67,20 @@ __global__ __launch_bounds__(T) void decode_in_kernel(InArgs a) {
     __syncthreads();
   };
   auto unit = [&](int u, Seg2 &g) {
-    if (u < natt) {
-      const int kind = u < nq ? 0 : (u < nq + nk ? 1 : 2);
-      const int uu = kind == 0 ? u : (kind == 1 ? u - nq : u - nq - nk);
-      const int head = uu / half_hd, j = uu % half_hd;
-      const MatDesc &M = kind == 0 ? a.w.q : (kind == 1 ? a.w.k : a.w.v);
-      int d0;
-      if (kind == 2) d0 = 2 * j;
-      else if (j < rh) d0 = j;
-      else d0 = s.rot + 2 * (j - rh);
-      const int d1 = (kind != 2 && j < rh) ? j + rh : d0 + 1;
-      const int64_t r0 = (int64_t)head * s.hd + d0, r1 = (int64_t)head * s.hd + d1;
-      g = Seg2{M.vals + r0 * M.vstride, M.meta + r0 * M.mstride, M.vals + r1 * M.vstride, M.meta + r1 * M.mstride,
-               xq, xq, nch, nch};
-    } else {
-      const int64_t i = u - natt;
-      const MatDesc &G = a.w.gate, &P = a.w.up;
-      g = Seg2{G.vals + i * G.vstride, G.meta + i * G.mstride, P.vals + i * P.vstride, P.meta + i * P.mstride,
-               xq, xq, nch, nch};
-    }
+    const uint8_t *v0 = W.vals + 2 * (int64_t)u * W.vstride, *m0 = W.meta + 2 * (int64_t)u * W.mstride;
+    g = Seg2{v0, m0, v0 + W.vstride, m0 + W.mstride, xq, xq, nch, nch};
   };
   auto done = [&](int u, float v0, float v1) {
-    if (lane != 0) return;
-    if (u < natt) {
-      const int kind = u < nq ? 0 : (u < nq + nk ? 1 : 2);
-      const int uu = kind == 0 ? u : (kind == 1 ? u - nq : u - nq - nk);
-      const int head = uu / half_hd, j = uu % half_hd;
-      const bool rotary = kind != 2 && j < rh;
-      int d0;
-      if (kind == 2) d0 = 2 * j;
-      else if (rotary) d0 = j;
-      else d0 = s.rot + 2 * (j - rh);
-      const int d1 = rotary ? j + rh : d0 + 1;
-      if (rotary) {  // stableRotate (stablelm.go:309-326) with table sin/cos
-        const float cs = rope_row[2 * j], sn = rope_row[2 * j + 1];
-        const float x0 = __fsub_rn(__fmul_rn(v0, cs), __fmul_rn(v1, sn));
-        const float x1 = __fadd_rn(__fmul_rn(v1, cs), __fmul_rn(v0, sn));
-        v0 = x0;
-        v1 = x1;
-      }
-      if (kind == 0) {
-        a.q_out[head * s.hd + d0] = v0;
-        a.q_out[head * s.hd + d1] = v1;
-      } else {  // storeKV (kv_cache.go:55-65), head-major [kvh][cap][hd]
-        const int64_t base = ((int64_t)head * a.kv.cap + pos) * s.hd;
-        store_kv(a.kv, base + d0, v0, kind == 1);
-        store_kv(a.kv, base + d1, v1, kind == 1);
-      }
-    } else {
-      a.m_out[u - natt] = silu_gate(v0, v1);
-    }
+    if (lane == 0) in_pair_epilogue(s, a.kv, rope_row, pos, u, v0, v1, a.q_out, a.m_out);
   };
-  stream_units<F, U>(blockIdx.x * (T / 64) + (threadIdx.x >> 6), gridDim.x * (T / 64), total, prologue, unit, done);
+  stream_units<F, U>(blockIdx.x * (T / 64) + (threadIdx.x >> 6), gridDim.x * (T / 64), W.rows / 2, prologue, unit,
+                     done);
 }
 
 struct OutArgs {
-  LayerDev w;
-  int d, inter, la, lm;  // la, lm: LDS lengths of a and m
+  MatDesc w;
+  int d, inter;
+  int na, nm;  // chunks of the o and down parts of a wout row
   const float *a, *m;
   float *x;
 };
@@ -143,17 +89,20 @@ template <int F, int U, int T>
 __global__ __launch_bounds__(T) void decode_out_kernel(OutArgs p) {
   extern __shared__ __align__(16) float4 xq_lds[];
   constexpr int VPC = Fmt<F>::VPC;
-  const MatDesc &O = p.w.o, &D = p.w.down;
-  float4 *xa = xq_lds, *xm = xq_lds + (VPC / 4) * O.chunks;
+  const MatDesc &W = p.w;
+  float4 *xa = xq_lds, *xm = xq_lds + (VPC / 4) * p.na;
   const int lane = threadIdx.x & 63;
+  // Q8_0: the o part holds d / 32 blocks, so the down scales start after
+  // d / 16 bytes of the scale plane.
+  const int64_t moff = F == FMT_Q8_0 ? p.d / 16 : 0;
   auto prologue = [&]() {
-    stage_x(xa, p.a, p.d, O.chunks, VPC);
-    stage_x(xm, p.m, p.inter, D.chunks, VPC);
+    stage_x(xa, p.a, p.d, p.na, VPC);
+    stage_x(xm, p.m, p.inter, p.nm, VPC);
     __syncthreads();
   };
   auto unit = [&](int r, Seg2 &g) {
-    g = Seg2{O.vals + (int64_t)r * O.vstride, O.meta + (int64_t)r * O.mstride, D.vals + (int64_t)r * D.vstride,
-             D.meta + (int64_t)r * D.mstride, xa, xm, O.chunks, D.chunks};
+    const uint8_t *v0 = W.vals + (int64_t)r * W.vstride, *m0 = W.meta + (int64_t)r * W.mstride;
+    g = Seg2{v0, m0, v0 + (int64_t)p.na * 16, m0 + moff, xa, xm, p.na, p.nm};
   };
   auto done = [&](int r, float ao, float ad) {
     if (lane == 0) p.x[r] = __fadd_rn(__fadd_rn(p.x[r], ao), ad);
@@ -482,9 +431,9 @@ hipError_t ln_matvec_launch(const LnMvArgs &a, int grid, int threads, hipStream_
 
 template <int F>
 hipError_t decode_in_launch(const InArgs &a, int grid, int threads, hipStream_t st) {
-  const size_t lds = (size_t)round_up(a.xlen, 4) * 4 + (size_t)a.w.q.chunks * Fmt<F>::VPC * 4 +
+  const size_t lds = (size_t)round_up(a.s.d, 4) * 4 + (size_t)a.w.win.chunks * Fmt<F>::VPC * 4 +
                      16 * sizeof(double) + (size_t)a.s.rot * 4;
-  const int U = pick_u(2 * a.w.q.chunks);
+  const int U = pick_u(2 * a.w.win.chunks);
 #define L256(U_) hipLaunchKernelGGL((decode_in_kernel<F, U_, 256>), dim3(grid), dim3(256), lds, st, a)
 #define L512(U_) hipLaunchKernelGGL((decode_in_kernel<F, U_, 512>), dim3(grid), dim3(512), lds, st, a)
 #define L640(U_) hipLaunchKernelGGL((decode_in_kernel<F, U_, 640>), dim3(grid), dim3(640), lds, st, a)
@@ -498,9 +447,13 @@ hipError_t decode_in_launch(const InArgs &a, int grid, int threads, hipStream_t 
 }
 
 template <int F>
-hipError_t decode_out_launch(const OutArgs &p, int grid, int threads, hipStream_t st) {
-  const size_t lds = (size_t)(p.w.o.chunks + p.w.down.chunks) * Fmt<F>::VPC * 4;
-  const int U = pick_u(p.w.o.chunks + p.w.down.chunks);
+hipError_t decode_out_launch(OutArgs p, int grid, int threads, hipStream_t st) {
+  constexpr int VPC = Fmt<F>::VPC;
+  if (p.d % VPC || (F == FMT_Q8_0 && p.d % 32)) return hipErrorInvalidValue;
+  p.na = p.d / VPC;
+  p.nm = p.w.chunks - p.na;
+  const size_t lds = (size_t)p.w.chunks * VPC * 4;
+  const int U = pick_u(p.w.chunks);
 #define L256(U_) hipLaunchKernelGGL((decode_out_kernel<F, U_, 256>), dim3(grid), dim3(256), lds, st, p)
 #define L512(U_) hipLaunchKernelGGL((decode_out_kernel<F, U_, 512>), dim3(grid), dim3(512), lds, st, p)
 #define L640(U_) hipLaunchKernelGGL((decode_out_kernel<F, U_, 640>), dim3(grid), dim3(640), lds, st, p)
@@ -529,10 +482,9 @@ int device_cu_count() {
 hipError_t launch_decode_in(const LayerDev &w, const StableDims &s, const KVDev &kv, float *x, const MatDesc *emb,
                             const int *token, const float *rope, const int *pos, float *q_out, float *m_out, int grid,
                             int threads, hipStream_t st) {
-  InArgs a{w, s, kv, x, emb ? *emb : MatDesc{}, emb != nullptr, token, rope, pos, q_out, m_out, 0};
-  a.xlen = s.d;
-  if (w.q.fmt != w.gate.fmt || w.q.chunks != w.gate.chunks) return hipErrorInvalidValue;
-  switch (w.q.fmt) {
+  InArgs a{w, s, kv, x, emb ? *emb : MatDesc{}, emb != nullptr, token, rope, pos, q_out, m_out};
+  if (w.win.rows % 2) return hipErrorInvalidValue;
+  switch (w.win.fmt) {
     case FMT_Q8_0: return decode_in_launch<FMT_Q8_0>(a, grid, threads, st);
     case FMT_BF16: return decode_in_launch<FMT_BF16>(a, grid, threads, st);
     case FMT_F32: return decode_in_launch<FMT_F32>(a, grid, threads, st);
@@ -543,9 +495,8 @@ hipError_t launch_decode_in(const LayerDev &w, const StableDims &s, const KVDev 
 
 hipError_t launch_decode_out(const LayerDev &w, const StableDims &s, const float *a, const float *m, float *x,
                              int grid, int threads, hipStream_t st) {
-  if (w.o.fmt != w.down.fmt) return hipErrorInvalidValue;
-  OutArgs p{w, s.d, s.inter, 0, 0, a, m, x};
-  switch (w.o.fmt) {
+  OutArgs p{w.wout, s.d, s.inter, 0, 0, a, m, x};
+  switch (w.wout.fmt) {
     case FMT_Q8_0: return decode_out_launch<FMT_Q8_0>(p, grid, threads, st);
     case FMT_BF16: return decode_out_launch<FMT_BF16>(p, grid, threads, st);
     case FMT_F32: return decode_out_launch<FMT_F32>(p, grid, threads, st);

@@ -4,11 +4,20 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
 #include "formats.h"
 
-// Per-layer weights of a StableLM block on the device (stablelm.go:113-117).
+// Per-layer weights of a StableLM block (stablelm.go:113-117), fused:
+//   win  rows [q | k | v | gate/up], cols = hidden. Inside each q and k head
+//        the rotary pair (j, j + rot/2) sits on adjacent rows 2j, 2j + 1,
+//        followed by the non-rotary dims in order; gate row i and up row i
+//        sit on rows 2i and 2i + 1 of the MLP section. Every consumer reads
+//        row pairs (2u, 2u + 1).
+//   wout rows = hidden, cols [o (hidden) | down (intermediate)]: the o and
+//        down rows of one output feature, back to back.
 struct LayerDev {
-  MatDesc q, k, v, o, gate, up, down;
+  MatDesc win, wout;
   const float *ln_w, *ln_b;
 };
 
@@ -26,17 +35,27 @@ struct KVDev {
   int half;  // 1 = fp16 storage (floatHalf rounding), 0 = fp32
 };
 
+// Where the rows of an uploaded tensor land in a fused matrix.
+enum : int { ROWMAP_IDENTITY = 0, ROWMAP_HEADS = 1, ROWMAP_INTERLEAVE = 2 };
+struct RowMap {
+  int kind;
+  int64_t offset;   // first destination row
+  int hd, rot;      // ROWMAP_HEADS
+  int phase;        // ROWMAP_INTERLEAVE: 0 -> rows 2i, 1 -> rows 2i + 1
+};
+
 // ---- decode (one token) ----
 // Matvec launches take their grid and block size (256, 512, 640 or 1024
 // threads) from the caller; blocks loop over their share of the rows.
-// LayerNorm(x) -> q/k/v/gate/up with RoPE, KV append and SiLU-gate fused
-// into the epilogue. pos (and token) are read from device memory. With
-// `emb` (a host-side descriptor, copied), x is first set to the embedding
-// row of *token (layer 0).
+//
+// LayerNorm(x) -> win rows with RoPE, KV append and SiLU-gate fused into
+// the epilogue. pos (and token) are read from device memory. With `emb` (a
+// host-side descriptor, copied), x is first set to the embedding row of
+// *token (layer 0).
 hipError_t launch_decode_in(const LayerDev &w, const StableDims &s, const KVDev &kv, float *x, const MatDesc *emb,
                             const int *token, const float *rope, const int *pos, float *q_out, float *m_out,
                             int grid, int threads, hipStream_t st);
-// x += o * a + down * m (stablelm.go:365-377).
+// x = (x + o * a) + down * m (stablelm.go:365-377), one wout row per wave.
 hipError_t launch_decode_out(const LayerDev &w, const StableDims &s, const float *a, const float *m,
                              float *x, int grid, int threads, hipStream_t st);
 // Split-K flash decode with in-kernel combine for nq queries at positions
@@ -60,21 +79,33 @@ hipError_t launch_embed(const MatDesc &emb, const int *ids, int n, float *x, hip
 // ---- prefill (n tokens) ----
 hipError_t launch_layer_norm_rows(const float *x, const float *w, const float *b, double eps, int n, int d,
                                   float *out, hipStream_t st);
-// out[n][rows] = x[n][cols] * W^T.
+// out[n][rows] = x[n][cols] * W^T on the vector units (any format/shape).
 hipError_t launch_gemm(const MatDesc &w, const float *x, int n, float *out, hipStream_t st);
-// RoPE on q [n][heads*hd] (in place) and k; writes k, v into the cache at
-// positions pos0 + j.
-hipError_t launch_rope_store(const StableDims &s, const KVDev &kv, float *q, const float *k, const float *v,
-                             const float *rope, const int *pos0, int n, hipStream_t st);
+// The matrix-core product: y[M][N] (row stride ldy) = X * W^T with X given
+// as bf16 planes [M][K] (xl null: one plane). Q8_0 and BF16 weights with
+// K % 32 == 0.
+bool gemm_mfma_supported(const MatDesc &w);
+int gemm_planes(const MatDesc &w);
+hipError_t launch_gemm_mfma(const MatDesc &w, const uint16_t *xh, const uint16_t *xl, int M, float *y, int ldy,
+                            hipStream_t st);
+// x fp32 [rows][k] (row stride ldx) -> bf16 hi [rows][k] and lo = x - hi.
+hipError_t launch_split_bf16(const float *x, int ldx, int k, int64_t rows, uint16_t *hi, uint16_t *lo,
+                             hipStream_t st);
+// Epilogue of the fused in-projection for n tokens: y [n][win rows] ->
+// RoPE'd q [n][heads*hd], K/V into the cache at positions pos0 + j, and
+// m [n][inter] = SiLU-gate(gate, up).
+hipError_t launch_in_epilogue(const StableDims &s, const KVDev &kv, const float *y, int ldy, const float *rope,
+                              const int *pos0, int n, float *q, float *m, hipStream_t st);
 hipError_t launch_silu_gate(float *g, const float *u, int64_t n, hipStream_t st);
 // x = (x + p) + d elementwise (stablelm.go:375-377).
 hipError_t launch_residual(float *x, const float *p, const float *d, int64_t n, hipStream_t st);
 hipError_t launch_copy_row(const float *src, float *dst, int n, hipStream_t st);
 
 // ---- weights ----
-// Splits raw GGUF-encoded bytes (already in device memory) into planes.
+// Places raw GGUF-encoded bytes (already in device memory) of a
+// [rows][cols] tensor into `dst` under `map`, starting at column col0.
 hipError_t launch_repack(int fmt, const uint8_t *raw, int64_t rows, int64_t cols, const MatDesc &dst,
-                         hipStream_t st);
+                         const RowMap &map, int64_t col0, hipStream_t st);
 hipError_t launch_read_values(const MatDesc &m, int64_t offset, int64_t n, float *out, hipStream_t st);
 
 int device_cu_count();

@@ -26,8 +26,19 @@ struct DevMatrix {
   DevMatrix &operator=(const DevMatrix &) = delete;
   DevMatrix(DevMatrix &&o) noexcept : desc(o.desc), mem(o.mem), bytes(o.bytes) { o.mem = nullptr; }
   ~DevMatrix();
+  // Zeroed planes for a [rows][cols] matrix of format dtype.
+  int create(int32_t dtype, int64_t rows, int64_t cols, hipStream_t st);
+  // Places a GGUF-encoded [rows][cols] tensor of the same format at column
+  // col0 (a value index) under a row map; waits for the copy to finish.
+  int place(int32_t dtype, int64_t rows, int64_t cols, const void *data, uint64_t nbytes, const RowMap &map,
+            int64_t col0, hipStream_t st);
+  // create + place of a whole matrix.
   int upload(int32_t dtype, int64_t rows, int64_t cols, const void *data, uint64_t nbytes, hipStream_t st);
 };
+
+// A column range [col0, col0 + cols) of a matrix as a matrix of its own
+// (col0 on a 16-byte chunk boundary, and on a block boundary for Q8_0).
+MatDesc column_view(const MatDesc &m, int64_t col0, int64_t cols);
 
 // Stage timings with hipEvents on the model's stream, the device-side
 // counterpart of stableProfile (stablelm.go:227-250). Off by default; when
@@ -35,7 +46,7 @@ struct DevMatrix {
 // forward synchronizes.
 enum Stage : int {
   ST_EMBED, ST_DECODE_IN, ST_ATTENTION, ST_DECODE_OUT, ST_LM_HEAD, ST_PREFILL_NORM, ST_PREFILL_GEMM,
-  ST_PREFILL_ROPE, ST_PREFILL_ATTENTION, ST_PREFILL_ELEMENTWISE, ST_COUNT
+  ST_PREFILL_EPILOGUE, ST_PREFILL_ATTENTION, ST_PREFILL_ELEMENTWISE, ST_COUNT
 };
 
 struct Profiler {
@@ -60,7 +71,7 @@ struct StableModel {
   StableDims dims{};
   hipStream_t stream = nullptr;
   DevMatrix embed, head;
-  std::vector<DevMatrix> mats;
+  std::vector<DevMatrix> mats;  // win, wout of each layer
   std::vector<LayerDev> layers;
   const float *norm_w = nullptr, *norm_b = nullptr;
   float *rope = nullptr;
@@ -75,10 +86,13 @@ struct StableModel {
   float *partials = nullptr;
   unsigned *counters = nullptr;
   int max_splits = 0;
-  // prefill workspaces, `chunk` tokens each
-  int chunk = 0;
-  float *X = nullptr, *H = nullptr, *Q = nullptr, *K = nullptr, *V = nullptr, *G = nullptr, *U = nullptr,
-        *A = nullptr, *P = nullptr, *D = nullptr;
+  // prefill workspaces, `chunk` tokens each: residual X, LayerNorm H, win
+  // products Y, RoPE'd queries Q, SiLU-gate M, attention A, o and down
+  // products P and D, bf16 planes XH/XL of the current GEMM operand
+  int chunk = 0, win_rows = 0;
+  float *X = nullptr, *H = nullptr, *Y = nullptr, *Q = nullptr, *M = nullptr, *A = nullptr, *P = nullptr,
+        *D = nullptr;
+  uint16_t *XH = nullptr, *XL = nullptr;
   void *h_pinned = nullptr;
   hipEvent_t params_copied = nullptr;  // last H2D copy out of h_pinned's parameter slot
   bool tracing = false;
@@ -101,6 +115,7 @@ struct StableModel {
   int enqueue_decode(int steps, int splits, bool want_logits);
   void drop_graphs();
   int decode_step(int token, int pos, bool want_logits);
+  int project(const MatDesc &w, const float *x, int ldx, int n, float *y, int ldy);
   int prefill_chunk(const int32_t *ids, int n, int start, bool want_logits);
   int forward(int prefix, const int32_t *tokens, int n, bool want_logits, float *logits);
 };

@@ -1,9 +1,10 @@
-// Prefill-path kernels (a chunk of n tokens) for gfx950: row LayerNorm,
-// the token-major projection GEMM, RoPE + KV store, SiLU-gate and the
-// parallel residual. Follows prefill.go:33-115 step for step.
+// Prefill-path kernels (a chunk of n tokens) for gfx950: row LayerNorm, a
+// vector-unit projection GEMM for formats the matrix cores do not take, the
+// fused in-projection epilogue, SiLU-gate and the parallel residual.
+// Follows prefill.go:33-115 step for step.
 #include <algorithm>
 
-#include "kernels.h"
+#include "epilogue.h"
 
 namespace {
 
@@ -66,42 +67,19 @@ __global__ __launch_bounds__(256) void gemm_simt_kernel(MatDesc w, const float *
   }
 }
 
-__device__ __forceinline__ void kv_put(void *base, int half, int64_t idx, float v) {
-  if (half)
-    reinterpret_cast<uint16_t *>(base)[idx] = float_to_half(v);
-  else
-    reinterpret_cast<float *>(base)[idx] = v;
-}
-
-// One block per token: stableRotate on q and k (stablelm.go:309-326), then
-// storeKV of every KV head at its absolute position (prefill.go:74-84).
-__global__ void rope_store_kernel(StableDims s, KVDev kv, float *q, const float *k, const float *v,
-                                  const float *rope, const int *pos0) {
+// One block per token: the fused in-projection epilogue (RoPE on q and k,
+// storeKV at the token's absolute position, SiLU-gate), as prefill.go:60-96
+// applies it row by row.
+__global__ void in_epilogue_kernel(StableDims s, KVDev kv, const float *y, int ldy, const float *rope,
+                                   const int *pos0, int units, float *q, float *m) {
   const int j = blockIdx.x;
   const int pos = *pos0 + j;
-  const int rh = s.rot / 2, kvw = s.kv_heads * s.hd;
-  float *qj = q + (int64_t)j * s.heads * s.hd;
-  for (int e = threadIdx.x; e < s.heads * rh; e += blockDim.x) {
-    const int h = e / rh, i = e % rh;
-    const float cs = rope[((int64_t)pos * rh + i) * 2], sn = rope[((int64_t)pos * rh + i) * 2 + 1];
-    float *p = qj + h * s.hd;
-    const float a = p[i], b = p[i + rh];
-    p[i] = __fsub_rn(__fmul_rn(a, cs), __fmul_rn(b, sn));
-    p[i + rh] = __fadd_rn(__fmul_rn(b, cs), __fmul_rn(a, sn));
-  }
-  const float *kj = k + (int64_t)j * kvw, *vj = v + (int64_t)j * kvw;
-  for (int e = threadIdx.x; e < kvw; e += blockDim.x) {
-    const int h = e / s.hd, dim = e % s.hd;
-    float val = kj[e];
-    if (dim < s.rot) {
-      const int i = dim % rh;
-      const float cs = rope[((int64_t)pos * rh + i) * 2], sn = rope[((int64_t)pos * rh + i) * 2 + 1];
-      const float a = kj[h * s.hd + i], b = kj[h * s.hd + i + rh];
-      val = dim < rh ? __fsub_rn(__fmul_rn(a, cs), __fmul_rn(b, sn)) : __fadd_rn(__fmul_rn(b, cs), __fmul_rn(a, sn));
-    }
-    const int64_t at = ((int64_t)h * kv.cap + pos) * s.hd + dim;
-    kv_put(kv.k, kv.half, at, val);
-    kv_put(kv.v, kv.half, at, vj[e]);
+  const float *yj = y + (int64_t)j * ldy;
+  const float *rope_row = rope + (int64_t)pos * s.rot;
+  float *qj = q + (int64_t)j * s.heads * s.hd, *mj = m + (int64_t)j * s.inter;
+  for (int u = threadIdx.x; u < units; u += blockDim.x) {
+    const float2 v = *reinterpret_cast<const float2 *>(yj + 2 * u);
+    in_pair_epilogue(s, kv, rope_row, pos, u, v.x, v.y, qj, mj);
   }
 }
 
@@ -136,9 +114,11 @@ hipError_t launch_gemm(const MatDesc &w, const float *x, int n, float *out, hipS
   return hipGetLastError();
 }
 
-hipError_t launch_rope_store(const StableDims &s, const KVDev &kv, float *q, const float *k, const float *v,
-                             const float *rope, const int *pos0, int n, hipStream_t st) {
-  hipLaunchKernelGGL(rope_store_kernel, dim3(n), dim3(256), 0, st, s, kv, q, k, v, rope, pos0);
+hipError_t launch_in_epilogue(const StableDims &s, const KVDev &kv, const float *y, int ldy, const float *rope,
+                              const int *pos0, int n, float *q, float *m, hipStream_t st) {
+  if (ldy % 2) return hipErrorInvalidValue;
+  const int units = (s.d + 2 * s.kv_heads * s.hd + 2 * s.inter) / 2;
+  hipLaunchKernelGGL(in_epilogue_kernel, dim3(n), dim3(256), 0, st, s, kv, y, ldy, rope, pos0, units, q, m);
   return hipGetLastError();
 }
 

@@ -208,7 +208,7 @@ class StableLMForwarder:
         return out
 
     STAGES = ("embedding", "decode_in", "attention", "decode_out", "lm_head", "prefill_layer_norm",
-              "prefill_projections", "prefill_rotary_kv_write", "prefill_attention", "prefill_elementwise")
+              "prefill_projections", "prefill_epilogue", "prefill_attention", "prefill_elementwise")
 
     def profile(self, enable: bool = True) -> None:
         check(lib().tinyoai_stablelm_profile(self.h, int(enable)))
