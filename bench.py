@@ -49,6 +49,18 @@ def token_bytes(c, pos, kv_bytes=4):
     return L * layer + q8_bytes(V, d) + d // 32 * 34 + L * 2 * kv * kv_bytes * (pos + 2)
 
 
+def measured_traffic():
+    """HBM bytes per decode_in launch from the committed rocprofv3 counter
+    summary (FETCH_SIZE and WRITE_SIZE, scaled by a copy of known size), or
+    None when it is absent."""
+    path = os.path.join(ROOT, "profiles", "decode_in_traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f)["hbm_bytes_per_launch"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def cpu_baseline(config, tensors, threads, prompt_len):
     """The oracle (C restatement of the Go scalar engine) on the host cores:
     a 128-token batched prefill chunk (prefillBatch) and 2 decode forwards
@@ -183,7 +195,7 @@ def main():
         "greedy_stream_stable": all(s == streams[0] for s in streams),
         "roofline": {"kernel": "decode_in (LayerNorm + Q8_0 q/k/v/gate/up matvec + RoPE + KV append + SiLU-gate)",
                      "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                      "algorithmic_bytes_per_launch": nbytes, "avg_launch_us": round(avg_s * 1e6, 2),
                      "launches": count},
         "kernels": kernels,

@@ -74,7 +74,10 @@ const char *tinyoai_last_error(void);
 /* ---------------- StableLM forwarder (mlxForwarder, mlx.go:45-51) ---------------- */
 
 /* Uploads every tensor named by loadStableWeights (stablelm.go:178-191) to
- * HBM and prepares fp32 KV storage (StableLMOptions{KVCache: "f32"}). */
+ * HBM and prepares fp32 KV storage (StableLMOptions{KVCache: "f32"}).
+ * Layer matrices are regrouped per layer into one input-side matrix
+ * (q, k, v, gate, up: one storage format) and one output-side matrix
+ * (o, down: one storage format); other combinations return TINYOAI_EINVAL. */
 int tinyoai_stablelm_load(const tinyoai_stablelm_config *config, const tinyoai_tensor *tensors,
                           int32_t n_tensors, tinyoai_model **out);
 
@@ -120,8 +123,8 @@ int tinyoai_stablelm_trace_read(tinyoai_model *m, float *residual);
  * is added to its stage: 0 embedding, 1 decode_in (layer_norm +
  * projections + rotary + kv_write + SiLU-gate), 2 attention, 3 decode_out
  * (output_projection + down + residual), 4 lm_head, 5 prefill layer_norm,
- * 6 prefill projections, 7 prefill rotary + kv_write, 8 prefill attention,
- * 9 prefill SiLU-gate and residual. Enabling clears the totals.
+ * 6 prefill projections, 7 prefill rotary + kv_write + SiLU-gate, 8 prefill
+ * attention, 9 prefill residual. Enabling clears the totals.
  * profile_read fills ms[] and counts[] (n_stages >= 10) and returns the
  * number of stages. */
 int tinyoai_stablelm_profile(tinyoai_model *m, int32_t enable);
