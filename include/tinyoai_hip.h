@@ -117,6 +117,10 @@ int tinyoai_stablelm_read_kv(tinyoai_model *m, int32_t layer, int32_t kv_head, i
                              float *values);
 int tinyoai_stablelm_trace(tinyoai_model *m, int32_t enable);
 int tinyoai_stablelm_trace_read(tinyoai_model *m, float *residual);
+/* The same trace's attention outputs [layers][heads * head_dim] (attendHeads,
+ * stablelm.go:391-431) and SiLU-gate outputs [layers][intermediate]
+ * (stablelm.go:371-373) of the final token. */
+int tinyoai_stablelm_trace_read_stages(tinyoai_model *m, float *attention, float *gate);
 
 /* Stage timings (stableProfile, stablelm.go:227-250): when enabled, each
  * kernel is bracketed by hipEvents on the handle's stream and its duration
@@ -128,6 +132,18 @@ int tinyoai_stablelm_trace_read(tinyoai_model *m, float *residual);
  * profile_read fills ms[] and counts[] (n_stages >= 10) and returns the
  * number of stages. */
 int tinyoai_stablelm_profile(tinyoai_model *m, int32_t enable);
+/* Decode path for one-token forwards: nonzero (the default) runs each token
+ * as one cooperative launch when the shapes and device allow it; zero runs
+ * three kernels per layer from a replayed HIP graph. Returns 1 when the
+ * single-launch path is available, else 0. */
+int tinyoai_stablelm_set_persistent(tinyoai_model *m, int32_t enable);
+/* Timeline of the last profiled single-launch decode step: for each block
+ * of the launch, 3 + 6 * layers readings of the GPU's 100 MHz real-time
+ * counter (start; per layer: input-side wait over, input rows done,
+ * attention wait over, attention done, output-side wait over, output rows
+ * done; head wait over, head done), [block][reading]. Copies at most
+ * `capacity` values and returns the number available (0: none recorded). */
+int64_t tinyoai_stablelm_decode_timeline(tinyoai_model *m, uint64_t *stamps, int64_t capacity);
 int tinyoai_stablelm_profile_read(tinyoai_model *m, double *ms, int64_t *counts, int32_t n_stages);
 
 /* ---------------- legacy Llama forwarder (llamaMLXForwarder, mlx_llama.go:27-35) ---------------- */

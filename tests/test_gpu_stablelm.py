@@ -171,3 +171,44 @@ def test_three_b_shapes_two_layers(hip, oracle):
         lg = f.forward(64 + step, [tg])
         assert np.max(np.abs(lg - lr)) <= 1e-3 * float(np.ptp(lr))
     assert toks_gpu == toks_ref
+
+
+@pytest.mark.parametrize("dtype,kv_bits", [(W.Q8_0, 32), (W.Q8_0, 16), (W.BF16, 32)])
+def test_persistent_decode_matches_per_kernel_path(hip, dtype, kv_bits):
+    """The single-launch decode (one cooperative kernel per token) against
+    the three-kernels-per-layer path on the same weights, prompt and KV.
+    Logits of 40 decode
+    tokens (crossing several 16-position attention splits) within 2e-5 of
+    their range, identical greedy tokens, identical per-layer residual
+    trace within the same bound."""
+    config = W.validate_stablelm_config(dict(W.STABLELM_3B, num_hidden_layers=3, max_position_embeddings=512))
+    tensors = W.synthetic_stablelm(config, dtype, seed=3)
+    rng = np.random.default_rng(5)
+    prompt = rng.integers(0, 65536, 37).astype(np.int32)
+    fast = hip.StableLMForwarder(config, tensors)
+    ref = hip.StableLMForwarder(config, tensors)
+    for f in (fast, ref):
+        f.set_kv_bits(kv_bits)
+        f.trace(True)
+    assert fast.set_persistent(True)
+    ref.set_persistent(False)
+    lf, lr = fast.forward(0, prompt), ref.forward(0, prompt)
+    assert np.array_equal(lf, lr)  # prefill takes the same kernels in both
+    for step in range(40):
+        tok = int(np.argmax(lr))
+        assert int(np.argmax(lf)) == tok
+        lf = fast.forward(37 + step, [tok])
+        lr = ref.forward(37 + step, [tok])
+        span = float(np.ptp(lr))
+        assert np.max(np.abs(lf - lr)) <= 2e-5 * span, step
+        tf, tr = fast.trace_read(), ref.trace_read()
+        assert np.max(np.abs(tf - tr)) <= 2e-5 * float(np.ptp(tr)), step
+    assert fast.offset == ref.offset == 77
+    k1, v1 = fast.read_kv(2, 5, 77)
+    k2, v2 = ref.read_kv(2, 5, 77)
+    # fp16 KV: an fp32 difference in the last bit can flip the fp16 rounding
+    ulp = 2.0 ** -10 if kv_bits == 16 else 0.0
+    assert np.all(np.abs(k1 - k2) <= 1e-5 * float(np.ptp(k2)) + ulp * np.abs(k2))
+    assert np.all(np.abs(v1 - v2) <= 1e-5 * float(np.ptp(v2)) + ulp * np.abs(v2))
+    fast.close()
+    ref.close()

@@ -345,14 +345,16 @@ int StableModel::init(const tinyoai_stablelm_config &c, const tinyoai_tensor *te
   const size_t w_att = (size_t)dims.heads * hd;
   if ((rc = alloc((void **)&x, (size_t)d * 4)) || (rc = alloc((void **)&qbuf, w_att * 4)) ||
       (rc = alloc((void **)&mbuf, (size_t)I * 4)) || (rc = alloc((void **)&abuf, w_att * 4)) ||
-      (rc = alloc((void **)&logits_dev, (size_t)c.vocab_size * 4)) || (rc = alloc((void **)&params, 4096)) ||
-      (rc = alloc((void **)&trace_dev, (size_t)c.num_hidden_layers * d * 4)))
+      (rc = alloc((void **)&logits_dev, (size_t)c.vocab_size * 4 + 256)) || (rc = alloc((void **)&params, 4096)) ||
+      (rc = alloc((void **)&trace_dev, (size_t)c.num_hidden_layers * d * 4)) ||
+      (rc = alloc((void **)&trace_att, (size_t)c.num_hidden_layers * w_att * 4)) ||
+      (rc = alloc((void **)&trace_gate, (size_t)c.num_hidden_layers * I * 4)))
     return rc;
   max_splits = maxp / 64 + 1;
   if ((rc = alloc((void **)&counters, (size_t)chunk * dims.heads * 4))) return rc;
   e = hipMemsetAsync(counters, 0, (size_t)chunk * dims.heads * 4, stream);
   if (e != hipSuccess) return hip_fail(e, "counter init");
-  if ((rc = alloc((void **)&partials, (size_t)chunk * dims.heads * max_splits * (hd + 2) * 4))) return rc;
+  if ((rc = alloc((void **)&partials, (size_t)chunk * dims.heads * partial_region(max_splits, hd) * 4))) return rc;
   const size_t B = chunk, wide = std::max(d, I);
   if ((rc = alloc((void **)&X, B * d * 4)) || (rc = alloc((void **)&H, B * d * 4)) ||
       (rc = alloc((void **)&Y, B * win_rows * 4)) || (rc = alloc((void **)&Q, B * w_att * 4)) ||
@@ -360,6 +362,22 @@ int StableModel::init(const tinyoai_stablelm_config &c, const tinyoai_tensor *te
       (rc = alloc((void **)&P, B * d * 4)) || (rc = alloc((void **)&D, B * d * 4)) ||
       (rc = alloc((void **)&XH, B * wide * 2)) || (rc = alloc((void **)&XL, B * wide * 2)))
     return rc;
+  // Persistent decode state.
+  const int L = c.num_hidden_layers;
+  psync_words = persistent_sync_words(L, dims.heads);
+  if ((rc = alloc((void **)&layers_dev, sizeof(LayerDev) * L)) || (rc = alloc((void **)&kv_dev, sizeof(KVDev) * L)) ||
+      (rc = alloc((void **)&xs, (size_t)(L + 1) * persistent_stride(d) * 4)) ||
+      (rc = alloc((void **)&qs, (size_t)L * persistent_stride(w_att) * 4)) ||
+      (rc = alloc((void **)&as, (size_t)L * persistent_stride(w_att) * 4)) ||
+      (rc = alloc((void **)&ms, (size_t)L * persistent_stride(I) * 4)) ||
+      (rc = alloc((void **)&psync, psync_words * 4)) ||
+      (rc = alloc((void **)&ppart, (size_t)L * dims.heads * partial_region((maxp + 15) / 16, hd) * 4)))
+    return rc;
+  perr = (unsigned *)(logits_dev + c.vocab_size);
+  e = hipMemcpyAsync(layers_dev, layers.data(), sizeof(LayerDev) * L, hipMemcpyHostToDevice, stream);
+  if (e == hipSuccess) e = hipMemsetAsync(psync, 0, psync_words * 4, stream);
+  if (e == hipSuccess) e = hipMemsetAsync(perr, 0, 4, stream);
+  if (e != hipSuccess) return hip_fail(e, "persistent decode state");
   e = hipEventCreateWithFlags(&params_copied, hipEventDisableTiming);
   if (e != hipSuccess) return hip_fail(e, "hipEventCreate");
   e = hipHostMalloc(&h_pinned, (size_t)c.vocab_size * 4 + 4096 + (size_t)chunk * 4 + 64, hipHostMallocDefault);
@@ -375,7 +393,87 @@ int StableModel::init(const tinyoai_stablelm_config &c, const tinyoai_tensor *te
   threads_out = 640;
   grid_head = cus * 2;
   threads_head = 512;
+  pgrid = persistent_decode_grid(persistent_args(true), layers[0]);
   return TINYOAI_OK;
+}
+
+PersistentDecode StableModel::persistent_args(bool want_logits) const {
+  PersistentDecode a{};
+  a.layers = layers_dev;
+  a.kv = kv_dev;
+  a.L = cfg.num_hidden_layers;
+  a.s = dims;
+  a.emb = embed.desc;
+  a.head = head.desc;
+  a.norm_w = norm_w;
+  a.norm_b = norm_b;
+  a.rope = rope;
+  a.params = params;
+  a.xs = xs;
+  a.qs = qs;
+  a.as = as;
+  a.ms = ms;
+  a.partials = ppart;
+  a.max_splits = (cfg.max_position_embeddings + 15) / 16;
+  a.cap_max = cfg.max_position_embeddings;
+  a.half_kv = kv_half;
+  a.sync = psync;
+  a.err = perr;
+  a.logits = logits_dev;
+  a.epoch = epoch;
+  a.want_logits = want_logits;
+  a.spin_limit = 1u << 20;
+  a.stamps = nullptr;
+  return a;
+}
+
+// Per-layer stage times from the timeline of the last profiled persistent
+// launch, on the critical path: decode_in runs from the last block leaving
+// the previous layer to the last block finishing win rows; attention until
+// the last block sees every head combined; decode_out until the last block
+// has written its rows; lm_head until the last block is done. The counter
+// runs at 100 MHz.
+void StableModel::resolve_timeline() {
+  if (!stamps_pending) return;
+  stamps_pending = false;
+  const int L = cfg.num_hidden_layers, P = persistent_stamps(L);
+  timeline.assign((size_t)pgrid * P, 0);
+  if (hipMemcpy(timeline.data(), pstamps, timeline.size() * 8, hipMemcpyDeviceToHost) != hipSuccess) return;
+  auto latest = [&](int k) {
+    uint64_t v = 0;
+    for (int b = 0; b < pgrid; b++) v = std::max(v, timeline[(size_t)b * P + k]);
+    return v;
+  };
+  auto earliest = [&](int k) {
+    uint64_t v = UINT64_MAX;
+    for (int b = 0; b < pgrid; b++) v = std::min(v, timeline[(size_t)b * P + k]);
+    return v;
+  };
+  auto add = [&](int stage, uint64_t from, uint64_t to) {
+    prof.ms[stage] += to > from ? (double)(to - from) * 1e-5 : 0.0;
+    prof.count[stage]++;
+  };
+  uint64_t t = earliest(0);
+  for (int l = 0; l < L; l++) {
+    const uint64_t in_done = latest(2 + 6 * l), att_done = latest(5 + 6 * l), out_done = latest(6 + 6 * l);
+    add(ST_DECODE_IN, t, in_done);
+    add(ST_ATTENTION, in_done, att_done);
+    add(ST_DECODE_OUT, att_done, out_done);
+    t = out_done;
+  }
+  if (latest(2 + 6 * L)) add(ST_LM_HEAD, t, latest(2 + 6 * L));
+}
+
+// After a forward that used the persistent kernel has synchronized: a set
+// error word means a dependency wait timed out, so the counters are
+// rebuilt from zero.
+int StableModel::check_persistent(int rc) {
+  unsigned word = 0;
+  if (hipMemcpy(&word, perr, 4, hipMemcpyDeviceToHost) != hipSuccess || word == 0) return rc;
+  hipMemset(psync, 0, psync_words * 4);
+  hipMemset(perr, 0, 4);
+  epoch = 0;
+  return rc ? rc : fail(TINYOAI_EDEVICE, "decode step did not complete: a dependency wait timed out");
 }
 
 // Grows KV to `needed` positions: power-of-two capacity capped at the
@@ -414,6 +512,7 @@ int StableModel::ensure_kv(int needed) {
   kv = grown;
   cap = want;
   offset = keep;
+  if (e == hipSuccess) e = hipMemcpy(kv_dev, kv.data(), sizeof(KVDev) * kv.size(), hipMemcpyHostToDevice);
   return e == hipSuccess ? TINYOAI_OK : hip_fail(e, "KV growth");
 }
 
@@ -434,7 +533,7 @@ int StableModel::ensure_kv(int needed) {
 // Copies `count` ints (head[0..nh) then ids) into the device parameter
 // block through the pinned slot, first waiting for the slot's previous copy.
 int StableModel::upload_params(const int *head_vals, int nh, const int32_t *ids, int n) {
-  int *hp = (int *)((char *)h_pinned + (size_t)cfg.vocab_size * 4);
+  int *hp = (int *)((char *)h_pinned + (size_t)cfg.vocab_size * 4 + 64);  // after the logits and error word
   if (params_copied) TRY_HIP(hipEventSynchronize(params_copied), "parameter slot");
   for (int i = 0; i < nh; i++) hp[i] = head_vals[i];
   if (n) memcpy(hp + 16, ids, (size_t)n * 4);
@@ -456,7 +555,12 @@ int StableModel::enqueue_decode(int steps, int splits, bool want_logits) {
           launch_attention(dims, kv[l], qbuf, params + 1, 1, 0, partials, counters, abuf, stream, steps, splits),
           "attention");
     STAGE(ST_DECODE_OUT, launch_decode_out(layers[l], dims, abuf, mbuf, x, grid_out, threads_out, stream), "decode_out");
-    if (tracing) TRY_HIP(launch_copy_row(x, trace_dev + (size_t)l * dims.d, dims.d, stream), "trace");
+    if (tracing) {
+      const int hq = dims.heads * dims.hd;
+      TRY_HIP(launch_copy_row(x, trace_dev + (size_t)l * dims.d, dims.d, stream), "trace");
+      TRY_HIP(launch_copy_row(abuf, trace_att + (size_t)l * hq, hq, stream), "trace");
+      TRY_HIP(launch_copy_row(mbuf, trace_gate + (size_t)l * dims.inter, dims.inter, stream), "trace");
+    }
   }
   if (want_logits)
     STAGE(ST_LM_HEAD, launch_ln_matvec(head.desc, norm_w, norm_b, dims.eps, x, logits_dev, grid_head, threads_head, stream),
@@ -475,6 +579,29 @@ void StableModel::drop_graphs() {
 int StableModel::decode_step(int token, int pos, bool want_logits) {
   const int vals[2] = {token, pos};
   if (int rc = upload_params(vals, 2, nullptr, 0)) return rc;
+  if (pgrid > 0 && use_persistent) {
+    PersistentDecode args = persistent_args(want_logits);
+    if (prof.on) {
+      if (!pstamps && alloc((void **)&pstamps, (size_t)pgrid * persistent_stamps(cfg.num_hidden_layers) * 8))
+        return TINYOAI_ENOMEM;
+      TRY_HIP(hipMemsetAsync(pstamps, 0, (size_t)pgrid * persistent_stamps(cfg.num_hidden_layers) * 8, stream),
+              "timeline");
+      args.stamps = pstamps;
+      stamps_pending = true;
+    }
+    TRY_HIP(launch_persistent_decode(args, layers[0], pgrid, stream), "persistent decode");
+    epoch++;
+    if (tracing) {
+      const int hq = dims.heads * dims.hd;
+      const int64_t sd = persistent_stride(dims.d), sq = persistent_stride(hq), si = persistent_stride(dims.inter);
+      for (int l = 0; l < cfg.num_hidden_layers; l++) {
+        TRY_HIP(launch_copy_row(xs + (l + 1) * sd, trace_dev + (size_t)l * dims.d, dims.d, stream), "trace");
+        TRY_HIP(launch_copy_row(as + l * sq, trace_att + (size_t)l * hq, hq, stream), "trace");
+        TRY_HIP(launch_copy_row(ms + l * si, trace_gate + (size_t)l * dims.inter, dims.inter, stream), "trace");
+      }
+    }
+    return TINYOAI_OK;
+  }
   const int steps = attention_steps(pos, dims.heads), splits = attention_splits(pos, steps);
   if (prof.on || !use_graphs) return enqueue_decode(steps, splits, want_logits);
   const int64_t key = ((int64_t)steps << 40) | ((int64_t)splits << 8) | (want_logits ? 2 : 0) | (tracing ? 1 : 0);
@@ -537,7 +664,11 @@ int StableModel::prefill_chunk(const int32_t *ids, int n, int start, bool want_l
           launch_attention(dims, kv[l], Q, d_pos0, n, start + n - 1, partials, counters, A, stream), "attention");
     if ((rc = project(wo, A, d, n, P, d)) || (rc = project(wd, M, I, n, D, d))) return rc;
     STAGE(ST_PREFILL_ELEMENTWISE, launch_residual(X, P, D, (int64_t)n * d, stream), "residual");
-    if (tracing) TRY_HIP(launch_copy_row(X + (size_t)(n - 1) * d, trace_dev + (size_t)l * d, d, stream), "trace");
+    if (tracing) {
+      TRY_HIP(launch_copy_row(X + (size_t)(n - 1) * d, trace_dev + (size_t)l * d, d, stream), "trace");
+      TRY_HIP(launch_copy_row(A + (size_t)(n - 1) * d, trace_att + (size_t)l * d, d, stream), "trace");
+      TRY_HIP(launch_copy_row(M + (size_t)(n - 1) * I, trace_gate + (size_t)l * I, I, stream), "trace");
+    }
   }
   if (want_logits) {
     TRY_HIP(launch_copy_row(X + (size_t)(n - 1) * d, x, d, stream), "last row");
@@ -566,25 +697,32 @@ int StableModel::forward(int prefix, const int32_t *tokens, int n, bool want_log
       rc = prefill_chunk(tokens + done, m, prefix + done, last && want_logits);
     done += m;
   }
+  // The word after the logits is the persistent decode's error word: it
+  // comes back with the logits.
+  unsigned *err_host = (unsigned *)h_pinned + cfg.vocab_size;
   if (!rc && want_logits) {
-    hipError_t e = hipMemcpyAsync(h_pinned, logits_dev, (size_t)cfg.vocab_size * 4, hipMemcpyDeviceToHost, stream);
+    hipError_t e = hipMemcpyAsync(h_pinned, logits_dev, (size_t)cfg.vocab_size * 4 + 4, hipMemcpyDeviceToHost, stream);
     if (e == hipSuccess) e = hipStreamSynchronize(stream);
     if (e != hipSuccess) rc = hip_fail(e, "logits");
+    else if (*err_host) rc = check_persistent(rc);
     else memcpy(logits, h_pinned, (size_t)cfg.vocab_size * 4);
   } else if (!rc) {
     hipError_t e = hipStreamSynchronize(stream);
     if (e != hipSuccess) rc = hip_fail(e, "forward");
+    else if (n == 1) rc = check_persistent(rc);
   }
   if (rc) {
     std::string msg = g_error;
     hipStreamSynchronize(stream);
     prof.marks.clear();
     prof.used = 0;
+    stamps_pending = false;
     free_kv();
     g_error = msg;
     return rc;
   }
   prof.resolve();
+  resolve_timeline();
   offset = prefix + n;
   return TINYOAI_OK;
 }
@@ -723,11 +861,36 @@ int tinyoai_stablelm_trace_read(tinyoai_model *m, float *residual) {
   return e == hipSuccess ? TINYOAI_OK : hip_fail(e, "trace read");
 }
 
+int tinyoai_stablelm_trace_read_stages(tinyoai_model *m, float *attention, float *gate) {
+  if (!m || !m->stable || !attention || !gate) return fail(TINYOAI_EINVAL, "invalid trace read");
+  StableModel &s = *m->stable;
+  const size_t L = s.cfg.num_hidden_layers;
+  hipError_t e = hipStreamSynchronize(s.stream);
+  if (e == hipSuccess)
+    e = hipMemcpy(attention, s.trace_att, L * s.dims.heads * s.dims.hd * 4, hipMemcpyDeviceToHost);
+  if (e == hipSuccess) e = hipMemcpy(gate, s.trace_gate, L * s.dims.inter * 4, hipMemcpyDeviceToHost);
+  return e == hipSuccess ? TINYOAI_OK : hip_fail(e, "trace read");
+}
+
+int tinyoai_stablelm_set_persistent(tinyoai_model *m, int32_t enable) {
+  if (!m || !m->stable) return fail(TINYOAI_EINVAL, "not a StableLM handle");
+  m->stable->use_persistent = enable != 0;
+  return m->stable->pgrid > 0 ? 1 : 0;
+}
+
 int tinyoai_stablelm_profile(tinyoai_model *m, int32_t enable) {
   if (!m || !m->stable) return fail(TINYOAI_EINVAL, "not a StableLM handle");
   m->stable->prof.on = enable != 0;
   m->stable->prof.clear();
   return TINYOAI_OK;
+}
+
+int64_t tinyoai_stablelm_decode_timeline(tinyoai_model *m, uint64_t *stamps, int64_t capacity) {
+  if (!m || !m->stable || (capacity > 0 && !stamps)) return fail(TINYOAI_EINVAL, "invalid timeline read");
+  const std::vector<uint64_t> &t = m->stable->timeline;
+  const int64_t n = std::min<int64_t>(capacity, (int64_t)t.size());
+  if (n > 0) memcpy(stamps, t.data(), (size_t)n * 8);
+  return (int64_t)t.size();
 }
 
 int tinyoai_stablelm_profile_read(tinyoai_model *m, double *ms, int64_t *counts, int32_t n_stages) {

@@ -168,51 +168,9 @@ struct AttArgs {
   float *out;
 };
 
-// Agent-scope relaxed atomic store / load of a partial result.
+// Agent-scope relaxed atomic store of a partial result.
 __device__ __forceinline__ void publish(float *p, float v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float observe(const float *p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Loads N consecutive KV values starting at element e into float registers.
-template <int N, bool HALF>
-__device__ __forceinline__ void load_kv(const void *base, int64_t e, float *r) {
-  if constexpr (HALF) {
-    const uint16_t *p = reinterpret_cast<const uint16_t *>(base) + e;
-    if constexpr (N % 4 == 0) {
-#pragma unroll
-      for (int i = 0; i < N / 4; i++) {
-        const uint2 v = reinterpret_cast<const uint2 *>(p)[i];
-        r[4 * i] = hw_half((uint16_t)v.x);
-        r[4 * i + 1] = hw_half((uint16_t)(v.x >> 16));
-        r[4 * i + 2] = hw_half((uint16_t)v.y);
-        r[4 * i + 3] = hw_half((uint16_t)(v.y >> 16));
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < N; i++) r[i] = hw_half(p[i]);
-    }
-  } else {
-    const float *p = reinterpret_cast<const float *>(base) + e;
-    if constexpr (N % 4 == 0) {
-#pragma unroll
-      for (int i = 0; i < N / 4; i++) {
-        const float4 v = reinterpret_cast<const float4 *>(p)[i];
-        r[4 * i] = v.x; r[4 * i + 1] = v.y; r[4 * i + 2] = v.z; r[4 * i + 3] = v.w;
-      }
-    } else if constexpr (N % 2 == 0) {
-#pragma unroll
-      for (int i = 0; i < N / 2; i++) {
-        const float2 v = reinterpret_cast<const float2 *>(p)[i];
-        r[2 * i] = v.x; r[2 * i + 1] = v.y;
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < N; i++) r[i] = p[i];
-    }
-  }
 }
 
 // One block of 4 waves per (split, head, query); a split covers
@@ -241,10 +199,17 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttArgs a) {
   for (int i = 0; i < DPL; i++) qr[i] = q[i];
   const int64_t head_base = (int64_t)kvh * a.kv.cap * HD;
   const int t0 = split * SPLIT + wave * STEPS * 16 + pl;
-  float kr[STEPS][DPL];
+  // Narrow blocks issue the V loads with the K loads (one memory round
+  // trip); wide ones load V after the scores to bound register use.
+  constexpr bool kEarlyV = STEPS <= 2;
+  float kr[STEPS][DPL], vr[STEPS][DPL];
 #pragma unroll
   for (int st = 0; st < STEPS; st++)
-    if (t0 + st * 16 < npos) load_kv<DPL, HALF>(a.kv.k, head_base + (int64_t)(t0 + st * 16) * HD + g * DPL, kr[st]);
+    if (t0 + st * 16 < npos) {
+      load_kv<DPL, HALF>(a.kv.k, head_base + (int64_t)(t0 + st * 16) * HD + g * DPL, kr[st]);
+      if constexpr (kEarlyV)
+        load_kv<DPL, HALF>(a.kv.v, head_base + (int64_t)(t0 + st * 16) * HD + g * DPL, vr[st]);
+    }
   float score[STEPS];
   float mx = -INFINITY;
 #pragma unroll
@@ -261,10 +226,11 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttArgs a) {
     mx = fmaxf(mx, score[st]);
   }
   mx = wave_max(mx);
-  float vr[STEPS][DPL];
+  if constexpr (!kEarlyV) {
 #pragma unroll
-  for (int st = 0; st < STEPS; st++)
-    if (t0 + st * 16 < npos) load_kv<DPL, HALF>(a.kv.v, head_base + (int64_t)(t0 + st * 16) * HD + g * DPL, vr[st]);
+    for (int st = 0; st < STEPS; st++)
+      if (t0 + st * 16 < npos) load_kv<DPL, HALF>(a.kv.v, head_base + (int64_t)(t0 + st * 16) * HD + g * DPL, vr[st]);
+  }
   float o[DPL];
 #pragma unroll
   for (int i = 0; i < DPL; i++) o[i] = 0.f;
@@ -315,11 +281,15 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttArgs a) {
     }
     return;
   }
-  // Cross-block combine. Partials and the arrival counter are exchanged with
-  // agent-scope relaxed atomics (cache-coherent across XCDs, sc1 accesses)
-  // and ordered by waiting for the stores before the arrival increment; an
+  // Cross-block combine. Partials are written with agent-scope relaxed
+  // atomic stores (write-through, visible across the XCDs' L2 caches) and
+  // ordered before the arrival increment by waiting for the stores; an
   // agent-scope fence would write back and invalidate the whole L2 instead.
-  float *part = a.partials + (qh * a.max_splits + split) * (HD + 2);
+  // Each (query, head) owns a 256-byte aligned region that only its last
+  // block reads, once, after every store to it: no cache holds a stale copy
+  // of those lines, so plain (pipelined) loads are safe there.
+  float *region = a.partials + qh * partial_region(a.max_splits, HD);
+  float *part = region + split * (HD + 2);
   if (tid == 0) {
     publish(part, M);
     publish(part + 1, L);
@@ -330,7 +300,7 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttArgs a) {
     for (int w = 0; w < kWaves; w++) acc = fmaf(s_o[w][d], ew[w], acc);
     publish(part + 2 + d, acc);
   }
-  __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores have completed
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's partial stores have completed
   __syncthreads();
   if (tid == 0)
     s_last = __hip_atomic_fetch_add(&a.counters[qh], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
@@ -338,18 +308,18 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttArgs a) {
   __syncthreads();
   if (!s_last) return;
   // Last block of this (query, head): every other split has published.
-  const float *base = a.partials + qh * a.max_splits * (HD + 2);
+  const float *base = region;
   float m = -INFINITY;
-  for (int sp = tid; sp < nsplit; sp += kThreads) m = fmaxf(m, observe(base + sp * (HD + 2)));
+  for (int sp = tid; sp < nsplit; sp += kThreads) m = fmaxf(m, base[sp * (HD + 2)]);
   m = wave_max(m);
   if (lane == 0) s_m[wave] = m;
   __syncthreads();
   m = fmaxf(fmaxf(s_m[0], s_m[1]), fmaxf(s_m[2], s_m[3]));
   float lsum = 0.f;
   for (int sp = tid; sp < nsplit; sp += kThreads) {
-    const float e = expf(observe(base + sp * (HD + 2)) - m);
+    const float e = expf(base[sp * (HD + 2)] - m);
     s_e[sp] = e;
-    lsum = fmaf(observe(base + sp * (HD + 2) + 1), e, lsum);
+    lsum = fmaf(base[sp * (HD + 2) + 1], e, lsum);
   }
   lsum = wave_sum(lsum);
   __syncthreads();
@@ -359,7 +329,7 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttArgs a) {
   for (int d = tid; d < HD; d += kThreads) {
     float acc = 0.f;
 #pragma unroll 8
-    for (int sp = 0; sp < nsplit; sp++) acc = fmaf(observe(base + sp * (HD + 2) + 2 + d), s_e[sp], acc);
+    for (int sp = 0; sp < nsplit; sp++) acc = fmaf(base[sp * (HD + 2) + 2 + d], s_e[sp], acc);
     outp[d] = acc / Ltot;
   }
   if (tid == 0) __hip_atomic_store(&a.counters[qh], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -506,10 +476,11 @@ hipError_t launch_decode_out(const LayerDev &w, const StableDims &s, const float
 }
 
 int attention_steps(int max_pos, int heads) {
-  // Positions per block (64 * steps): the widest blocks measured fastest on
-  // gfx950 at 640 to 8K positions, as long as enough blocks remain.
+  // Positions per block (64 * steps): two steps (V loaded with K, one
+  // memory round trip) measured fastest on gfx950 at 512-768 positions;
+  // narrower blocks when that leaves fewer than 64 blocks.
   const int npos = max_pos + 1;
-  int steps = 4;
+  int steps = 2;
   while (steps > 1 && (npos + 64 * steps - 1) / (64 * steps) * heads < 64) steps /= 2;
   return steps;
 }

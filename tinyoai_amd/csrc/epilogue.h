@@ -1,27 +1,38 @@
-// The in-projection epilogue shared by decode (one token, fused into the
-// matvec) and prefill (after the matrix-core product): a row pair of the
-// fused win matrix becomes RoPE'd q, a K/V cache entry, or a SiLU-gate
-// output.
+// Device helpers shared by the decode kernels and the prefill epilogue:
+// the in-projection epilogue (a row pair of the fused win matrix becomes
+// RoPE'd q, a K/V cache entry, or a SiLU-gate output) and KV loads.
 #pragma once
 
 #include "kernels.h"
 
+// Stores seen by other blocks of the same launch: with COH, agent-scope
+// relaxed atomic stores (coherent across the XCDs' L2 caches), else plain.
+template <bool COH, typename V>
+__device__ __forceinline__ void put(V *p, V v) {
+  if constexpr (COH)
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  else
+    *p = v;
+}
+
 // storeKV (kv_cache.go:55-65): fp32 copy, or floatHalf rounding.
+template <bool COH = false>
 __device__ __forceinline__ void kv_put(const KVDev &kv, bool key, int64_t idx, float v) {
   void *base = key ? kv.k : kv.v;
   if (kv.half)
-    reinterpret_cast<uint16_t *>(base)[idx] = float_to_half(v);
+    put<COH>(reinterpret_cast<uint16_t *>(base) + idx, float_to_half(v));
   else
-    reinterpret_cast<float *>(base)[idx] = v;
+    put<COH>(reinterpret_cast<float *>(base) + idx, v);
 }
 
 // Row pair (2u, 2u + 1) of win with dot products v0, v1 for one token at
 // absolute position pos. rope_row holds cos/sin of pos as [rot/2][2].
+template <bool COH = false>
 __device__ __forceinline__ void in_pair_epilogue(const StableDims &s, const KVDev &kv, const float *rope_row, int pos,
                                                  int u, float v0, float v1, float *q_out, float *m_out) {
   const int row = 2 * u, kvw = s.kv_heads * s.hd, rh = s.rot / 2;
   if (row >= s.d + 2 * kvw) {
-    m_out[(row - s.d - 2 * kvw) >> 1] = silu_gate(v0, v1);  // stablelm.go:371-373
+    put<COH>(m_out + ((row - s.d - 2 * kvw) >> 1), silu_gate(v0, v1));  // stablelm.go:371-373
     return;
   }
   int sec, r;  // 0 q, 1 k, 2 v
@@ -41,11 +52,65 @@ __device__ __forceinline__ void in_pair_epilogue(const StableDims &s, const KVDe
     v1 = x1;
   }
   if (sec == 0) {
-    q_out[head * s.hd + d0] = v0;
-    q_out[head * s.hd + d1] = v1;
+    put<COH>(q_out + head * s.hd + d0, v0);
+    put<COH>(q_out + head * s.hd + d1, v1);
   } else {  // head-major [kv_head][cap][hd] at the token's position
     const int64_t base = ((int64_t)head * kv.cap + pos) * s.hd;
-    kv_put(kv, sec == 1, base + d0, v0);
-    kv_put(kv, sec == 1, base + d1, v1);
+    kv_put<COH>(kv, sec == 1, base + d0, v0);
+    kv_put<COH>(kv, sec == 1, base + d1, v1);
+  }
+}
+
+// Loads N consecutive KV values starting at element e into float registers.
+template <int N, bool HALF>
+__device__ __forceinline__ void load_kv(const void *base, int64_t e, float *r) {
+  if constexpr (HALF) {
+    const uint16_t *p = reinterpret_cast<const uint16_t *>(base) + e;
+    if constexpr (N % 4 == 0) {
+#pragma unroll
+      for (int i = 0; i < N / 4; i++) {
+        const uint2 v = reinterpret_cast<const uint2 *>(p)[i];
+        r[4 * i] = hw_half((uint16_t)v.x);
+        r[4 * i + 1] = hw_half((uint16_t)(v.x >> 16));
+        r[4 * i + 2] = hw_half((uint16_t)v.y);
+        r[4 * i + 3] = hw_half((uint16_t)(v.y >> 16));
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < N; i++) r[i] = hw_half(p[i]);
+    }
+  } else {
+    const float *p = reinterpret_cast<const float *>(base) + e;
+    if constexpr (N % 4 == 0) {
+#pragma unroll
+      for (int i = 0; i < N / 4; i++) {
+        const float4 v = reinterpret_cast<const float4 *>(p)[i];
+        r[4 * i] = v.x; r[4 * i + 1] = v.y; r[4 * i + 2] = v.z; r[4 * i + 3] = v.w;
+      }
+    } else if constexpr (N % 2 == 0) {
+#pragma unroll
+      for (int i = 0; i < N / 2; i++) {
+        const float2 v = reinterpret_cast<const float2 *>(p)[i];
+        r[2 * i] = v.x; r[2 * i + 1] = v.y;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < N; i++) r[i] = p[i];
+    }
+  }
+}
+
+// The same with agent-scope atomic loads, for a KV entry written earlier in
+// the same launch by another block.
+template <int N, bool HALF>
+__device__ __forceinline__ void load_kv_coherent(const void *base, int64_t e, float *r) {
+  if constexpr (HALF) {
+    uint16_t *p = const_cast<uint16_t *>(reinterpret_cast<const uint16_t *>(base)) + e;
+#pragma unroll
+    for (int i = 0; i < N; i++) r[i] = hw_half(__hip_atomic_load(p + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+  } else {
+    float *p = const_cast<float *>(reinterpret_cast<const float *>(base)) + e;
+#pragma unroll
+    for (int i = 0; i < N; i++) r[i] = __hip_atomic_load(p + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }

@@ -135,11 +135,20 @@ __device__ __forceinline__ float chunk_dot<FMT_F32>(const uint4 w, const float4 
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
+// Weights live in global memory; saying so keeps the loads global_load
+// (not flat) where the compiler cannot trace a pointer back to a kernel
+// argument.
+#define TINYOAI_GLOBAL __attribute__((address_space(1)))
+
 // One 16-byte chunk of a weight row, streamed past the caches (each weight
 // byte is read once per token).
 __device__ __forceinline__ uint4 load_chunk(const uint8_t *p) {
-  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+  const u32x4 v = __builtin_nontemporal_load((const TINYOAI_GLOBAL u32x4 *)p);
   return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+__device__ __forceinline__ uint16_t load_scale(const uint8_t *meta, int block) {
+  return ((const TINYOAI_GLOBAL uint16_t *)meta)[block];
 }
 
 // ---------------------------------------------------------------- streaming
@@ -172,51 +181,84 @@ __device__ __forceinline__ void batch_issue(Batch<U> &b, const Seg2 &g, int base
     const bool seg1 = c >= g.n0;
     const int cc = seg1 ? c - g.n0 : c;
     b.w[u] = load_chunk((seg1 ? g.v1 : g.v0) + (int64_t)cc * 16);
-    if constexpr (F == FMT_Q8_0) b.s[u] = reinterpret_cast<const uint16_t *>(seg1 ? g.m1 : g.m0)[cc >> 1];
+    if constexpr (F == FMT_Q8_0) b.s[u] = load_scale(seg1 ? g.m1 : g.m0, cc >> 1);
   }
 }
 
-template <int F, int U>
-__device__ __forceinline__ void batch_consume(const Batch<U> &b, const Seg2 &g, int base, int lane, float &acc0,
-                                              float &acc1) {
+// Consumes the chunks base + u * 64 + lane of a batch into acc0 (segment 0)
+// and acc1 (segment 1). Branch-free: a lane past the end computes on its
+// clamped (valid) chunk and contributes 0, so no per-chunk exec-mask
+// branches are emitted. With SERIAL, the scheduler may not hoist the LDS
+// reads of later chunks above earlier ones (bounds register use where a
+// kernel keeps other state live). Only chunks with lo <= c < hi count.
+template <int F, int U, bool SERIAL = false>
+__device__ __forceinline__ void batch_consume_range(const Batch<U> &b, const Seg2 &g, int base, int lane, int lo,
+                                                    int hi, float &acc0, float &acc1) {
   const int total = g.n0 + g.n1;
+  hi = min(hi, total);
 #pragma unroll
   for (int u = 0; u < U; u++) {
     const int c = base + u * 64 + lane;
-    if (c < total) {
-      const bool seg1 = c >= g.n0;
-      const int cc = seg1 ? c - g.n0 : c;
-      float p = chunk_dot<F>(b.w[u], seg1 ? g.x1 : g.x0, seg1 ? g.n1 : g.n0, cc);
-      if constexpr (F == FMT_Q8_0) p *= hw_half(b.s[u]);
-      if (seg1) acc1 += p; else acc0 += p;
-    }
+    const int cl = min(c, total - 1);
+    const bool seg1 = cl >= g.n0;
+    const int cc = seg1 ? cl - g.n0 : cl;
+    float p = chunk_dot<F>(b.w[u], seg1 ? g.x1 : g.x0, seg1 ? g.n1 : g.n0, cc);
+    if constexpr (F == FMT_Q8_0) p *= hw_half(b.s[u]);
+    p = (c >= lo && c < hi) ? p : 0.f;
+    acc0 += seg1 ? 0.f : p;
+    acc1 += seg1 ? p : 0.f;
+    if constexpr (SERIAL) __builtin_amdgcn_sched_barrier(0);
   }
 }
 
+template <int F, int U, bool SERIAL = false>
+__device__ __forceinline__ void batch_consume(const Batch<U> &b, const Seg2 &g, int base, int lane, float &acc0,
+                                              float &acc1) {
+  batch_consume_range<F, U, SERIAL>(b, g, base, lane, 0, g.n0 + g.n1, acc0, acc1);
+}
+
 // Runs units first, first + stride, ... (< n_units) through one wave, each
-// as batches of 64 * U chunks (one batch when U covers the unit). The first
-// batch is issued before `prologue()` (the block's LDS staging, which the
-// weights do not depend on); `unit(u, g)` describes unit u; `done(u, r0, r1)`
-// receives the two wave-reduced dot products (every lane calls it).
+// as batches of 64 * U chunks (one batch when U covers the unit). Two
+// batches are in flight: the next batch (of this unit or the next one) is
+// issued before the current one is consumed, and the first before
+// `prologue()` (the block's LDS staging, which the weights do not depend
+// on). `unit(u, g)` describes unit u; `done(u, r0, r1)` receives the two
+// wave-reduced dot products (every lane calls it).
 template <int F, int U, typename Prologue, typename UnitFn, typename Done>
 __device__ __forceinline__ void stream_units(int first, int stride, int n_units, Prologue prologue, UnitFn unit,
                                              Done done) {
   const int lane = threadIdx.x & 63;
-  Seg2 g{};
-  Batch<U> b;
-  if (first < n_units) {
-    unit(first, g);
+  Seg2 g{}, gn{};
+  Batch<U> b, bn;
+  int u = first, base = 0;
+  if (u < n_units) {
+    unit(u, g);
     batch_issue<F, U>(b, g, 0, lane);
   }
   prologue();
-  for (int u = first; u < n_units; u += stride) {
-    if (u != first) unit(u, g);
-    float acc0 = 0.f, acc1 = 0.f;
-    for (int base = 0; base < g.n0 + g.n1; base += 64 * U) {
-      if (u != first || base != 0) batch_issue<F, U>(b, g, base, lane);
-      batch_consume<F, U>(b, g, base, lane, acc0, acc1);
+  float acc0 = 0.f, acc1 = 0.f;
+  while (u < n_units) {
+    int nu = u, nbase = base + 64 * U;
+    if (nbase >= g.n0 + g.n1) {
+      nu = u + stride;
+      nbase = 0;
     }
-    done(u, wave_sum(acc0), wave_sum(acc1));
+    const bool more = nu < n_units;
+    if (more) {
+      if (nu != u) unit(nu, gn);
+      else gn = g;
+      batch_issue<F, U>(bn, gn, nbase, lane);
+    }
+    batch_consume<F, U>(b, g, base, lane, acc0, acc1);
+    if (nu != u) {
+      done(u, wave_sum(acc0), wave_sum(acc1));
+      acc0 = acc1 = 0.f;
+    }
+    if (!more) break;
+    b = bn;
+    g = gn;
+    u = nu;
+    base = nbase;
   }
 }
 

@@ -96,9 +96,27 @@ struct StableModel {
   void *h_pinned = nullptr;
   hipEvent_t params_copied = nullptr;  // last H2D copy out of h_pinned's parameter slot
   bool tracing = false;
-  float *trace_dev = nullptr;
+  float *trace_dev = nullptr, *trace_att = nullptr, *trace_gate = nullptr;  // [L][d], [L][heads*hd], [L][inter]
   int grid_in = 0, grid_out = 0, grid_head = 0;
   int threads_in = 256, threads_out = 256, threads_head = 256;
+
+  // Persistent decode (one cooperative launch per token): device copies of
+  // the layer and KV descriptors, per-layer handoff buffers, counters.
+  LayerDev *layers_dev = nullptr;
+  KVDev *kv_dev = nullptr;
+  float *xs = nullptr, *qs = nullptr, *as = nullptr, *ms = nullptr;
+  float *ppart = nullptr;  // attention partials [L][heads][max_pos / 16][hd + 2]
+  unsigned *psync = nullptr, *perr = nullptr;  // perr: the word after the logits
+  size_t psync_words = 0;
+  int pgrid = 0;
+  unsigned epoch = 0;
+  bool use_persistent = false;
+  // Phase timeline of profiled persistent launches ([block][point] of the
+  // real-time counter), resolved into the profile stages after a forward.
+  uint64_t *pstamps = nullptr;
+  bool stamps_pending = false;
+  std::vector<uint64_t> timeline;
+  void resolve_timeline();
 
   std::vector<void *> buffers;
   Profiler prof;
@@ -115,6 +133,8 @@ struct StableModel {
   int enqueue_decode(int steps, int splits, bool want_logits);
   void drop_graphs();
   int decode_step(int token, int pos, bool want_logits);
+  PersistentDecode persistent_args(bool want_logits) const;
+  int check_persistent(int rc);
   int project(const MatDesc &w, const float *x, int ldx, int n, float *y, int ldy);
   int prefill_chunk(const int32_t *ids, int n, int start, bool want_logits);
   int forward(int prefix, const int32_t *tokens, int n, bool want_logits, float *logits);

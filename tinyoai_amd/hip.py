@@ -19,6 +19,7 @@ EXPORTS = [
     "tinyoai_last_error", "tinyoai_stablelm_load", "tinyoai_stablelm_forward", "tinyoai_stablelm_set_kv_bits",
     "tinyoai_stablelm_limit_cache", "tinyoai_stablelm_reset", "tinyoai_stablelm_offset", "tinyoai_stablelm_close",
     "tinyoai_stablelm_read_kv", "tinyoai_stablelm_trace", "tinyoai_stablelm_trace_read",
+    "tinyoai_stablelm_trace_read_stages", "tinyoai_stablelm_decode_timeline", "tinyoai_stablelm_set_persistent",
     "tinyoai_stablelm_profile", "tinyoai_stablelm_profile_read", "tinyoai_llama_load",
     "tinyoai_llama_forward", "tinyoai_llama_reset", "tinyoai_llama_close", "tinyoai_weight_upload",
     "tinyoai_weight_read_values", "tinyoai_weight_mul", "tinyoai_weight_mul_device", "tinyoai_weight_free",
@@ -69,6 +70,10 @@ def lib():
         L.tinyoai_stablelm_read_kv.argtypes = [P, C.c_int32, C.c_int32, C.c_int32, fp, fp]
         L.tinyoai_stablelm_trace.argtypes = [P, C.c_int32]
         L.tinyoai_stablelm_trace_read.argtypes = [P, fp]
+        L.tinyoai_stablelm_trace_read_stages.argtypes = [P, fp, fp]
+        L.tinyoai_stablelm_decode_timeline.argtypes = [P, C.POINTER(C.c_uint64), C.c_int64]
+        L.tinyoai_stablelm_decode_timeline.restype = C.c_int64
+        L.tinyoai_stablelm_set_persistent.argtypes = [P, C.c_int32]
         L.tinyoai_stablelm_profile.argtypes = [P, C.c_int32]
         L.tinyoai_stablelm_profile_read.argtypes = [P, C.POINTER(C.c_double), C.POINTER(C.c_int64), C.c_int32]
         L.tinyoai_llama_load.argtypes = [C.POINTER(LlamaConfig), fp, C.c_uint64, C.POINTER(P)]
@@ -207,8 +212,35 @@ class StableLMForwarder:
         check(lib().tinyoai_stablelm_trace_read(self.h, _fp(out)))
         return out
 
+    def trace_read_stages(self) -> tuple[np.ndarray, np.ndarray]:
+        """Per-layer attention outputs [layers][heads * head_dim] and
+        SiLU-gate outputs [layers][intermediate] of the traced token."""
+        c = self.config
+        L = c["num_hidden_layers"]
+        att = np.empty((L, c["hidden_size"]), np.float32)
+        gate = np.empty((L, c["intermediate_size"]), np.float32)
+        check(lib().tinyoai_stablelm_trace_read_stages(self.h, _fp(att), _fp(gate)))
+        return att, gate
+
     STAGES = ("embedding", "decode_in", "attention", "decode_out", "lm_head", "prefill_layer_norm",
               "prefill_projections", "prefill_epilogue", "prefill_attention", "prefill_elementwise")
+
+    def set_persistent(self, enable: bool) -> bool:
+        """Selects the single-launch decode path (default) or three kernels
+        per layer; returns whether the single-launch path is available."""
+        return bool(check(lib().tinyoai_stablelm_set_persistent(self.h, int(enable))))
+
+    def decode_timeline(self) -> np.ndarray:
+        """Phase timeline of the last profiled single-launch decode step:
+        [blocks][3 + 6 * layers] readings of the 100 MHz GPU clock (empty
+        when none was recorded)."""
+        n = lib().tinyoai_stablelm_decode_timeline(self.h, None, 0)
+        check(n if n < 0 else 0)
+        out = np.zeros(n, np.uint64)
+        if n:
+            lib().tinyoai_stablelm_decode_timeline(self.h, out.ctypes.data_as(C.POINTER(C.c_uint64)), n)
+        points = 3 + 6 * self.config["num_hidden_layers"]
+        return out.reshape(-1, points)
 
     def profile(self, enable: bool = True) -> None:
         check(lib().tinyoai_stablelm_profile(self.h, int(enable)))
