@@ -61,6 +61,34 @@ def measured_traffic():
         return None
 
 
+def llama_stories(prompt_len=32, generate=256, seed=260):
+    """The legacy Llama workload (stories260K checkpoint, fp32): BOS + a
+    seeded 31-token prompt of ids in [3, 512), then 256 greedy tokens, one
+    forward each. Latency-bound (1 MB of weights per token)."""
+    import numpy as np
+    from tinyoai_amd import hip, weights as W
+    c, w = W.read_llama2c(os.path.join(ROOT, "tests", "golden", "stories260K.bin"))
+    f = hip.LlamaForwarder(c, w)
+    rng = np.random.default_rng(seed)
+    ids = np.concatenate([[1], rng.integers(3, 512, prompt_len - 1)]).astype(np.int32)
+
+    def run():
+        logits = f.forward(0, ids)
+        toks = []
+        for i in range(generate):
+            toks.append(int(np.argmax(logits)))
+            logits = f.forward(prompt_len + i, [toks[-1]])
+        return toks
+
+    run()  # warm-up: graph capture
+    t0 = time.perf_counter()
+    toks = run()
+    dt = time.perf_counter() - t0
+    f.close()
+    return {"workload": "stories260K Llama-2 fp32, 32-token prompt + 256 greedy tokens", "tok_s": round(generate / dt, 1),
+            "ms_per_token": round(dt / generate * 1e3, 4), "first_tokens": toks[:8]}
+
+
 def cpu_baseline(config, tensors, threads, prompt_len):
     """The oracle (C restatement of the Go scalar engine) on the host cores:
     a 128-token batched prefill chunk (prefillBatch) and 2 decode forwards
@@ -201,6 +229,7 @@ def main():
         "kernels": kernels,
     }
     fwd.close()
+    out["llama"] = llama_stories()
     if not args.no_cpu:
         print("[bench] timing the CPU oracle", file=sys.stderr, flush=True)
         out["cpu_baseline"] = cpu_baseline(config, tensors, args.cpu_threads, args.prompt)

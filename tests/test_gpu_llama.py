@@ -1,0 +1,107 @@
+"""The legacy Llama forwarder on the GPU against the oracle's
+Model.transformer restatement (model.go:407-481).
+
+Mirrors TestLlamaMLXForwardParity (mlx_llama_native_test.go:51-134): the
+prompt in 64-token chunks with every logit row, then greedy tokens one at a
+time; every row within KL 1e-6 of the CPU engine's distribution, the same
+argmax, finite values. The reference prompt is BPE text; no tokenizer runs
+here, so the prompt is BOS followed by seeded ids in [3, 512).
+"""
+import os
+
+import numpy as np
+import pytest
+
+from tinyoai_amd import weights as W
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+@pytest.fixture(scope="module")
+def stories():
+    return W.read_llama2c(os.path.join(GOLDEN, "stories260K.bin"))
+
+
+def _kl(want, got):
+    p = np.exp(want.astype(np.float64) - want.max())
+    p /= p.sum()
+    q = np.exp(got.astype(np.float64) - got.max())
+    q /= q.sum()
+    return float(np.sum(p * (np.log(p) - np.log(q))))
+
+
+def _check(want, got):
+    assert np.all(np.isfinite(got))
+    assert int(np.argmax(want)) == int(np.argmax(got))
+    assert _kl(want, got) <= 1e-6
+
+
+@pytest.mark.parametrize("prompt,generated", [(128, 256), (480, 32)])
+def test_forward_parity(oracle, stories, prompt, generated):
+    from tinyoai_amd import hip
+    c, w = stories
+    ref = oracle.Llama(c, w)
+    f = hip.LlamaForwarder(c, w)
+    rng = np.random.default_rng(prompt)
+    ids = np.concatenate([[1], rng.integers(3, 512, prompt - 1)]).astype(np.int32)
+    want = None
+    for pos in range(0, prompt, 64):
+        end = min(pos + 64, prompt)
+        got = f.forward(pos, ids[pos:end], all_logits=True)
+        assert got.shape == (end - pos, c["vocab_size"])
+        for i in range(pos, end):
+            want = ref.transformer(int(ids[i]), i)
+            _check(want, got[i - pos])
+    for i in range(generated):
+        tok = int(np.argmax(want))
+        got = f.forward(prompt + i, [tok])
+        want = ref.transformer(tok, prompt + i)
+        _check(want, got)
+    f.close()
+    ref.close()
+
+
+def test_grouped_query_shapes(oracle):
+    """A seeded llama2.c model with wider heads and 4:1 grouped KV: per-step
+    logits within 1e-3 of their range (fp32 path) and the same greedy ids."""
+    from tinyoai_amd import hip
+    c = dict(dim=256, hidden_dim=688, n_layers=3, n_heads=8, n_kv_heads=2, vocab_size=1000, seq_len=160)
+    w = W.synthetic_llama(c, seed=9)
+    ref = oracle.Llama(c, w)
+    f = hip.LlamaForwarder(c, w)
+    tok = 1
+    for pos in range(100):
+        got = f.forward(pos, [tok])
+        want = ref.transformer(tok, pos)
+        assert np.max(np.abs(got - want)) <= 1e-3 * float(np.ptp(want)), pos
+        assert int(np.argmax(got)) == int(np.argmax(want)), pos
+        tok = int(np.argmax(want))
+    f.close()
+    ref.close()
+
+
+def test_prefix_rewind_and_errors(stories):
+    """Forward replaces the suffix after prefix (rewind allowed); invalid
+    prefixes, tokens and lengths are rejected and reset the cache."""
+    from tinyoai_amd import hip
+    c, w = stories
+    f = hip.LlamaForwarder(c, w)
+    ids = np.array([1, 50, 60, 70, 80, 90], np.int32)
+    full = f.forward(0, ids, all_logits=True)
+    again = f.forward(3, ids[3:], all_logits=True)  # rewind to 3 and redo
+    assert np.array_equal(again, full[3:])
+    last = f.forward(0, ids)
+    assert np.array_equal(last, full[-1])
+    for bad in [lambda: f.forward(7, [5]),           # prefix beyond the cache
+                lambda: f.forward(0, [512]),         # token outside the vocabulary
+                lambda: f.forward(0, [-1]),
+                lambda: f.forward(0, np.zeros(c["seq_len"] + 1, np.int32))]:
+        with pytest.raises(hip.TinyoaiError):
+            bad()
+    f.reset()
+    with pytest.raises(hip.TinyoaiError):
+        f.forward(1, [5])  # nothing resident after reset
+    assert np.array_equal(f.forward(0, ids, all_logits=True), full)
+    f.close()

@@ -19,7 +19,7 @@ BUILD = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "libtinyoai_hip.so")
 ARCH = os.environ.get("TINYOAI_OFFLOAD_ARCH", "gfx950")
 
-SOURCES = ["api.cpp", "decode.hip", "prefill.hip", "weights.hip", "gemm.hip", "persistent.hip"]
+SOURCES = ["api.cpp", "llama.cpp", "decode.hip", "prefill.hip", "weights.hip", "gemm.hip", "persistent.hip"]
 FLAGS = ["-O3", "-std=c++17", "-fPIC", "-x", "hip", f"--offload-arch={ARCH}", "-ffp-contract=off",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
          "-Wall", "-Wno-unused-function", "-Wno-unused-variable", "-Wno-unused-value", "-Wno-unused-result",

@@ -243,7 +243,8 @@ int StableModel::init(const tinyoai_stablelm_config &c, const tinyoai_tensor *te
   if (hd % 2 || (hd != 8 && hd != 16 && hd != 32 && hd != 64 && hd != 80 && hd != 96 && hd != 128))
     return fail(TINYOAI_EINVAL, "head width %d is not supported by the attention kernels", hd);
   dims = StableDims{c.hidden_size, hd, (int)rotary, c.num_attention_heads, c.num_key_value_heads,
-                    c.intermediate_size, c.vocab_size, c.layer_norm_eps, (float)std::sqrt((double)hd)};
+                    c.intermediate_size, c.vocab_size, c.layer_norm_eps, (float)std::sqrt((double)hd),
+                    /*norm=*/0, /*rope_adjacent=*/0, /*silu=*/0, c.hidden_size, hd * c.num_key_value_heads};
   hipError_t e = hipStreamCreateWithFlags(&stream, hipStreamNonBlocking);
   if (e != hipSuccess) return hip_fail(e, "hipStreamCreate");
 
@@ -554,7 +555,7 @@ int StableModel::enqueue_decode(int steps, int splits, bool want_logits) {
     STAGE(ST_ATTENTION,
           launch_attention(dims, kv[l], qbuf, params + 1, 1, 0, partials, counters, abuf, stream, steps, splits),
           "attention");
-    STAGE(ST_DECODE_OUT, launch_decode_out(layers[l], dims, abuf, mbuf, x, grid_out, threads_out, stream), "decode_out");
+    STAGE(ST_DECODE_OUT, launch_decode_out(layers[l].wout, dims.d, dims.inter, abuf, mbuf, x, grid_out, threads_out, stream), "decode_out");
     if (tracing) {
       const int hq = dims.heads * dims.hd;
       TRY_HIP(launch_copy_row(x, trace_dev + (size_t)l * dims.d, dims.d, stream), "trace");
@@ -563,7 +564,7 @@ int StableModel::enqueue_decode(int steps, int splits, bool want_logits) {
     }
   }
   if (want_logits)
-    STAGE(ST_LM_HEAD, launch_ln_matvec(head.desc, norm_w, norm_b, dims.eps, x, logits_dev, grid_head, threads_head, stream),
+    STAGE(ST_LM_HEAD, launch_ln_matvec(head.desc, norm_w, norm_b, dims.eps, 0, x, logits_dev, grid_head, threads_head, stream),
           "lm_head");
   return TINYOAI_OK;
 }
@@ -672,7 +673,7 @@ int StableModel::prefill_chunk(const int32_t *ids, int n, int start, bool want_l
   }
   if (want_logits) {
     TRY_HIP(launch_copy_row(X + (size_t)(n - 1) * d, x, d, stream), "last row");
-    STAGE(ST_LM_HEAD, launch_ln_matvec(head.desc, norm_w, norm_b, dims.eps, x, logits_dev, grid_head, threads_head, stream),
+    STAGE(ST_LM_HEAD, launch_ln_matvec(head.desc, norm_w, norm_b, dims.eps, 0, x, logits_dev, grid_head, threads_head, stream),
           "lm_head");
   }
   return TINYOAI_OK;
@@ -730,10 +731,6 @@ int StableModel::forward(int prefix, const int32_t *tokens, int n, bool want_log
 }  // namespace tinyoai
 
 using namespace tinyoai;
-
-struct tinyoai_model {
-  std::unique_ptr<StableModel> stable;
-};
 
 struct tinyoai_weight {
   DevMatrix m;
@@ -937,7 +934,7 @@ int tinyoai_weight_mul_device(tinyoai_weight *w, const float *x_dev, int32_t n, 
   const MatDesc &m = w->m.desc;
   hipError_t e;
   if (n == 1) {
-    e = launch_ln_matvec(m, nullptr, nullptr, 0.0, x_dev, out_dev, device_cu_count() * 4, 256, st);
+    e = launch_ln_matvec(m, nullptr, nullptr, 0.0, 0, x_dev, out_dev, device_cu_count() * 4, 256, st);
   } else if (gemm_mfma_supported(m)) {
     // Batched products on the matrix cores; the plane buffer grows on demand
     // (the stream is drained before an old buffer is released).
@@ -990,19 +987,6 @@ int tinyoai_weight_free(tinyoai_weight *w) {
     hipStreamSynchronize(w->stream);
     delete w;
   }
-  return TINYOAI_OK;
-}
-
-int tinyoai_llama_load(const tinyoai_llama_config *, const float *, uint64_t, tinyoai_model **out) {
-  if (out) *out = nullptr;
-  return fail(TINYOAI_EINVAL, "legacy Llama backend is not built yet");
-}
-int tinyoai_llama_forward(tinyoai_model *, int32_t, const int32_t *, int32_t, int32_t, float *) {
-  return fail(TINYOAI_EINVAL, "legacy Llama backend is not built yet");
-}
-int tinyoai_llama_reset(tinyoai_model *) { return fail(TINYOAI_EINVAL, "legacy Llama backend is not built yet"); }
-int tinyoai_llama_close(tinyoai_model *m) {
-  delete m;
   return TINYOAI_OK;
 }
 

@@ -61,7 +61,7 @@ __global__ __launch_bounds__(T) void decode_in_kernel(InArgs a) {
       for (int i = threadIdx.x; i < s.d; i += T) lds[i] = a.x[i];
     }
     __syncthreads();
-    layer_norm_lds(lds, s.d, a.w.ln_w, a.w.ln_b, s.eps, red);
+    norm_lds(s, lds, a.w.ln_w, a.w.ln_b, red);
     stage_x(xq, lds, s.d, nch, VPC);
     for (int i = threadIdx.x; i < s.rot; i += T) rope_row[i] = a.rope[(int64_t)pos * s.rot + i];
     __syncthreads();
@@ -79,8 +79,8 @@ __global__ __launch_bounds__(T) void decode_in_kernel(InArgs a) {
 
 struct OutArgs {
   MatDesc w;
-  int d, inter;
-  int na, nm;  // chunks of the o and down parts of a wout row
+  int ka, km;  // values of the o and down parts of a wout row
+  int na, nm;  // their chunks
   const float *a, *m;
   float *x;
 };
@@ -92,12 +92,12 @@ __global__ __launch_bounds__(T) void decode_out_kernel(OutArgs p) {
   const MatDesc &W = p.w;
   float4 *xa = xq_lds, *xm = xq_lds + (VPC / 4) * p.na;
   const int lane = threadIdx.x & 63;
-  // Q8_0: the o part holds d / 32 blocks, so the down scales start after
-  // d / 16 bytes of the scale plane.
-  const int64_t moff = F == FMT_Q8_0 ? p.d / 16 : 0;
+  // Q8_0: the o part holds ka / 32 blocks, so the down scales start after
+  // ka / 16 bytes of the scale plane.
+  const int64_t moff = F == FMT_Q8_0 ? p.ka / 16 : 0;
   auto prologue = [&]() {
-    stage_x(xa, p.a, p.d, p.na, VPC);
-    stage_x(xm, p.m, p.inter, p.nm, VPC);
+    stage_x(xa, p.a, p.ka, p.na, VPC);
+    if (p.nm) stage_x(xm, p.m, p.km, p.nm, VPC);
     __syncthreads();
   };
   auto unit = [&](int r, Seg2 &g) {
@@ -107,13 +107,15 @@ __global__ __launch_bounds__(T) void decode_out_kernel(OutArgs p) {
   auto done = [&](int r, float ao, float ad) {
     if (lane == 0) p.x[r] = __fadd_rn(__fadd_rn(p.x[r], ao), ad);
   };
-  stream_units<F, U>(blockIdx.x * (T / 64) + (threadIdx.x >> 6), gridDim.x * (T / 64), p.d, prologue, unit, done);
+  stream_units<F, U>(blockIdx.x * (T / 64) + (threadIdx.x >> 6), gridDim.x * (T / 64), p.w.rows, prologue, unit,
+                     done);
 }
 
 struct LnMvArgs {
   MatDesc w;
   const float *ln_w, *ln_b;
   double eps;
+  int norm;
   const float *x;
   float *out;
   int xlen;
@@ -131,7 +133,10 @@ __global__ __launch_bounds__(T) void ln_matvec_kernel(LnMvArgs a) {
   auto prologue = [&]() {
     for (int i = threadIdx.x; i < cols; i += T) lds[i] = a.x[i];
     __syncthreads();
-    if (a.ln_w) layer_norm_lds(lds, cols, a.ln_w, a.ln_b, a.eps, red);
+    if (a.ln_w) {
+      if (a.norm) rms_norm_lds(lds, cols, a.ln_w, (float)a.eps, red);
+      else layer_norm_lds(lds, cols, a.ln_w, a.ln_b, a.eps, red);
+    }
     stage_x(xq, lds, cols, M.chunks, VPC);
     __syncthreads();
   };
@@ -419,9 +424,10 @@ hipError_t decode_in_launch(const InArgs &a, int grid, int threads, hipStream_t 
 template <int F>
 hipError_t decode_out_launch(OutArgs p, int grid, int threads, hipStream_t st) {
   constexpr int VPC = Fmt<F>::VPC;
-  if (p.d % VPC || (F == FMT_Q8_0 && p.d % 32)) return hipErrorInvalidValue;
-  p.na = p.d / VPC;
+  if (F == FMT_Q8_0 && p.ka % 32) return hipErrorInvalidValue;
+  p.na = (p.ka + VPC - 1) / VPC;
   p.nm = p.w.chunks - p.na;
+  if (p.nm < 0 || (p.km == 0) != (p.nm == 0) || (int64_t)p.nm * VPC < p.km) return hipErrorInvalidValue;
   const size_t lds = (size_t)p.w.chunks * VPC * 4;
   const int U = pick_u(p.w.chunks);
 #define L256(U_) hipLaunchKernelGGL((decode_out_kernel<F, U_, 256>), dim3(grid), dim3(256), lds, st, p)
@@ -463,10 +469,10 @@ hipError_t launch_decode_in(const LayerDev &w, const StableDims &s, const KVDev 
   return hipErrorInvalidValue;
 }
 
-hipError_t launch_decode_out(const LayerDev &w, const StableDims &s, const float *a, const float *m, float *x,
+hipError_t launch_decode_out(const MatDesc &wout, int ka, int km, const float *a, const float *m, float *x,
                              int grid, int threads, hipStream_t st) {
-  OutArgs p{w.wout, s.d, s.inter, 0, 0, a, m, x};
-  switch (w.wout.fmt) {
+  OutArgs p{wout, ka, km, 0, 0, a, m, x};
+  switch (wout.fmt) {
     case FMT_Q8_0: return decode_out_launch<FMT_Q8_0>(p, grid, threads, st);
     case FMT_BF16: return decode_out_launch<FMT_BF16>(p, grid, threads, st);
     case FMT_F32: return decode_out_launch<FMT_F32>(p, grid, threads, st);
@@ -506,9 +512,9 @@ hipError_t launch_attention(const StableDims &s, const KVDev &kv, const float *q
   return hipErrorInvalidValue;
 }
 
-hipError_t launch_ln_matvec(const MatDesc &w, const float *ln_w, const float *ln_b, double eps, const float *x,
-                            float *out, int grid, int threads, hipStream_t st) {
-  LnMvArgs a{w, ln_w, ln_b, eps, x, out, std::max(w.chunks * values_per_chunk(w.fmt), w.cols)};
+hipError_t launch_ln_matvec(const MatDesc &w, const float *ln_w, const float *ln_b, double eps, int norm,
+                            const float *x, float *out, int grid, int threads, hipStream_t st) {
+  LnMvArgs a{w, ln_w, ln_b, eps, norm, x, out, std::max(w.chunks * values_per_chunk(w.fmt), w.cols)};
   switch (w.fmt) {
     case FMT_Q8_0: return ln_matvec_launch<FMT_Q8_0>(a, grid, threads, st);
     case FMT_BF16: return ln_matvec_launch<FMT_BF16>(a, grid, threads, st);

@@ -101,9 +101,30 @@ __device__ __forceinline__ void layer_norm_lds(float *x, int n, const float *__r
   __syncthreads();
 }
 
+// RMSNorm (model.go:591-600) of an LDS-resident row, in place: the sum of
+// float32 squares (accumulated in float64, then rounded), ss / n + eps and
+// 1 / float32(sqrt(.)) in float32, out = w * (inv * x).
+__device__ __forceinline__ void rms_norm_lds(float *x, int n, const float *__restrict__ w, float eps, double *red) {
+  double s = 0;
+  for (int i = threadIdx.x; i < n; i += blockDim.x) s += (double)__fmul_rn(x[i], x[i]);
+  const float ss = (float)block_sum_d(s, red);
+  const float mean = __fadd_rn(__fdiv_rn(ss, (float)n), eps);
+  const float inv = __fdiv_rn(1.0f, (float)sqrt((double)mean));
+  __syncthreads();
+  for (int i = threadIdx.x; i < n; i += blockDim.x) x[i] = __fmul_rn(w[i], __fmul_rn(inv, x[i]));
+  __syncthreads();
+}
+
 // SiLU-gate (stablelm.go:371-373): (g / (1 + f32(exp(-f64(g))))) * u.
 __device__ __forceinline__ float silu_gate(float g, float u) {
   float e = (float)exp(-(double)g);
   float den = __fadd_rn(1.0f, e);
   return __fmul_rn(__fdiv_rn(g, den), u);
+}
+
+// The legacy Llama's SwiGLU (model.go:463-470): s = 1 / (1 + e), (g * s) * u.
+__device__ __forceinline__ float silu_gate_llama(float g, float u) {
+  float e = (float)exp(-(double)g);
+  float s = __fdiv_rn(1.0f, __fadd_rn(1.0f, e));
+  return __fmul_rn(__fmul_rn(g, s), u);
 }

@@ -25,26 +25,36 @@ __device__ __forceinline__ void kv_put(const KVDev &kv, bool key, int64_t idx, f
     put<COH>(reinterpret_cast<float *>(base) + idx, v);
 }
 
+// The layer's input normalisation of an LDS-resident row (all threads).
+__device__ __forceinline__ void norm_lds(const StableDims &s, float *x, const float *w, const float *b,
+                                         double *red) {
+  if (s.norm) rms_norm_lds(x, s.d, w, (float)s.eps, red);
+  else layer_norm_lds(x, s.d, w, b, s.eps, red);
+}
+
 // Row pair (2u, 2u + 1) of win with dot products v0, v1 for one token at
 // absolute position pos. rope_row holds cos/sin of pos as [rot/2][2].
 template <bool COH = false>
 __device__ __forceinline__ void in_pair_epilogue(const StableDims &s, const KVDev &kv, const float *rope_row, int pos,
                                                  int u, float v0, float v1, float *q_out, float *m_out) {
-  const int row = 2 * u, kvw = s.kv_heads * s.hd, rh = s.rot / 2;
-  if (row >= s.d + 2 * kvw) {
-    put<COH>(m_out + ((row - s.d - 2 * kvw) >> 1), silu_gate(v0, v1));  // stablelm.go:371-373
+  const int row = 2 * u, kvw = s.win_kv, rh = s.rot / 2;
+  if (row >= s.win_q + 2 * kvw) {
+    const int i = (row - s.win_q - 2 * kvw) >> 1;
+    put<COH>(m_out + i, s.silu ? silu_gate_llama(v0, v1) : silu_gate(v0, v1));
     return;
   }
   int sec, r;  // 0 q, 1 k, 2 v
-  if (row < s.d) { sec = 0; r = row; }
-  else if (row < s.d + kvw) { sec = 1; r = row - s.d; }
-  else { sec = 2; r = row - s.d - kvw; }
+  if (row < s.win_q) { sec = 0; r = row; }
+  else if (row < s.win_q + kvw) { sec = 1; r = row - s.win_q; }
+  else { sec = 2; r = row - s.win_q - kvw; }
   const int head = r / s.hd, p = r - head * s.hd;
   int d0 = p, d1 = p + 1;
-  if (sec != 2 && p < s.rot) {  // stableRotate (stablelm.go:309-326) on dims (j, j + rot/2)
+  if (sec != 2 && p < s.rot) {  // rotate the pair by the table's cos/sin
     const int j = p >> 1;
-    d0 = j;
-    d1 = j + rh;
+    if (!s.rope_adjacent) {     // stableRotate: dims (j, j + rot/2), stored on adjacent rows
+      d0 = j;
+      d1 = j + rh;
+    }
     const float cs = rope_row[2 * j], sn = rope_row[2 * j + 1];
     const float x0 = __fsub_rn(__fmul_rn(v0, cs), __fmul_rn(v1, sn));
     const float x1 = __fadd_rn(__fmul_rn(v1, cs), __fmul_rn(v0, sn));

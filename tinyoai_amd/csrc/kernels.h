@@ -21,11 +21,16 @@ struct LayerDev {
   const float *ln_w, *ln_b;
 };
 
-// Shapes and constants shared by the StableLM kernels.
+// Shapes and constants of a decoder layer, with the choices that tell
+// StableLM (stablelm.go) and the legacy Llama (model.go) apart.
 struct StableDims {
   int d, hd, rot, heads, kv_heads, inter, vocab;
   double eps;
-  float att_scale;  // float32(sqrt(hd)), attentionScale (stablelm.go:431)
+  float att_scale;  // float32(sqrt(hd)), attentionScale (stablelm.go:431), model.go:433
+  int norm;          // 0: LayerNorm (stablelm.go:288-305); 1: RMSNorm (model.go:591-600)
+  int rope_adjacent; // rotary pairs: 0 (j, j + rot/2) (stablelm.go:309-326); 1 (2j, 2j+1) (model.go:611-618)
+  int silu;          // 0: (g / (1 + e)) * u (stablelm.go:371-373); 1: (g * (1 / (1 + e))) * u (model.go:463-470)
+  int win_q, win_kv; // rows of the q section and of each of the k, v sections of win
 };
 
 // KV cache of one layer: [kv_heads][cap][hd], fp32 or fp16 bits.
@@ -55,9 +60,11 @@ struct RowMap {
 hipError_t launch_decode_in(const LayerDev &w, const StableDims &s, const KVDev &kv, float *x, const MatDesc *emb,
                             const int *token, const float *rope, const int *pos, float *q_out, float *m_out,
                             int grid, int threads, hipStream_t st);
-// x = (x + o * a) + down * m (stablelm.go:365-377), one wout row per wave.
-hipError_t launch_decode_out(const LayerDev &w, const StableDims &s, const float *a, const float *m,
-                             float *x, int grid, int threads, hipStream_t st);
+// x = (x + o * a) + down * m (stablelm.go:365-377), one wout row per wave:
+// a row holds ka values of o then, from the next chunk boundary, km values
+// of down (km = 0: x = x + o * a).
+hipError_t launch_decode_out(const MatDesc &wout, int ka, int km, const float *a, const float *m, float *x,
+                             int grid, int threads, hipStream_t st);
 // Split-K flash decode with in-kernel combine for nq queries at positions
 // pos0 + j (j < nq): q [nq][heads*hd] -> out [nq][heads*hd]. A block covers
 // 64 * steps positions; `splits` blocks per (query, head) must cover
@@ -74,9 +81,9 @@ __host__ __device__ inline int64_t partial_region(int max_splits, int hd) {
   return ((int64_t)max_splits * (hd + 2) + 63) / 64 * 64;
 }
 int attention_splits(int max_pos, int steps);
-// out[rows] = W * LN(x) (LN skipped when ln_w is null), for the logits head
-// and single-matrix products.
-hipError_t launch_ln_matvec(const MatDesc &w, const float *ln_w, const float *ln_b, double eps,
+// out[rows] = W * norm(x) (skipped when ln_w is null; norm as StableDims),
+// for the logits head and single-matrix products.
+hipError_t launch_ln_matvec(const MatDesc &w, const float *ln_w, const float *ln_b, double eps, int norm,
                             const float *x, float *out, int grid, int threads, hipStream_t st);
 // x[n][cols] = rows ids[j] of an embedding matrix, bit-exact dequantized.
 hipError_t launch_embed(const MatDesc &emb, const int *ids, int n, float *x, hipStream_t st);

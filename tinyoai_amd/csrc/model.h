@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 
 #include <map>
+#include <memory>
 #include <string>
 #include <vector>
 
@@ -140,4 +141,45 @@ struct StableModel {
   int forward(int prefix, const int32_t *tokens, int n, bool want_logits, float *logits);
 };
 
+// The legacy Llama of llama2.c checkpoints (Model.transformer,
+// model.go:379-481) on the decode kernels, fp32 weights and KV, one token
+// per step (the reference evaluates a suffix token by token as well).
+struct LlamaModel {
+  tinyoai_llama_config cfg{};
+  StableDims att{}, mlp{};  // attention half (RMSNorm + q/k/v) and MLP half (RMSNorm + w1/w3)
+  hipStream_t stream = nullptr;
+  DevMatrix embed;          // token embeddings, also the classifier (model.go:476-479)
+  std::vector<DevMatrix> mats;  // per layer: win (q|k|v), wo, w1/w3 interleaved, w2
+  std::vector<LayerDev> att_layers, mlp_layers;
+  float *rms_final = nullptr, *rope = nullptr;
+  std::vector<KVDev> kv;    // [kv_heads][seq_len][head] per layer
+  int offset = 0;
+  float *x = nullptr, *qbuf = nullptr, *abuf = nullptr, *hbuf = nullptr, *partials = nullptr;
+  float *head_out = nullptr;    // [vocab]: the head's output of the last step
+  float *logits_dev = nullptr;  // [rows][vocab]: the rows a forward returns
+  int logits_rows = 0;
+  unsigned *counters = nullptr;
+  int *params = nullptr;
+  int max_splits = 0;
+  void *h_pinned = nullptr;
+  hipEvent_t params_copied = nullptr;
+  int grid_in = 1, grid_mlp = 1, grid_out = 1, grid_head = 1;
+  std::map<int64_t, hipGraphExec_t> graphs;
+  std::vector<void *> buffers;
+
+  ~LlamaModel();
+  int init(const tinyoai_llama_config &c, const float *weights, uint64_t n_floats);
+  int alloc(void **p, size_t bytes);
+  int ensure_logits(int rows);
+  int enqueue_step(int steps, int splits, float *logits);
+  int step(int token, int pos, float *logits);
+  int forward(int prefix, const int32_t *tokens, int n, bool all_logits, float *logits);
+};
+
 }  // namespace tinyoai
+
+// One opaque handle type for both model families.
+struct tinyoai_model {
+  std::unique_ptr<tinyoai::StableModel> stable;
+  std::unique_ptr<tinyoai::LlamaModel> llama;
+};

@@ -204,7 +204,7 @@ __global__ __launch_bounds__(kT) void persistent_decode_kernel(PersistentDecode 
         for (int i = tid; i < d; i += kT) xl[i] = x_in[i];
       }
       __syncthreads();
-      layer_norm_lds(xl, d, w.ln_w, w.ln_b, s.eps, red);
+      norm_lds(s, xl, w.ln_w, w.ln_b, red);
       stage_x(xq, xl, d, nch, VPC);
       for (int i = tid; i < s.rot; i += kT) rope_row[i] = a.rope[(int64_t)pos * s.rot + i];
       __syncthreads();
@@ -393,7 +393,7 @@ __global__ __launch_bounds__(kT) void persistent_decode_kernel(PersistentDecode 
     const float *xf = a.xs + (int64_t)a.L * persistent_stride(d);
     for (int i = tid; i < d; i += kT) xl[i] = xf[i];
     __syncthreads();
-    layer_norm_lds(xl, d, a.norm_w, a.norm_b, s.eps, red);
+    norm_lds(s, xl, a.norm_w, a.norm_b, red);
     stage_x(xq, xl, d, hch, VPC);
     __syncthreads();
     stream_units_from<F, UI>(gw, NW, units, b, g, lane, unit, done);

@@ -262,3 +262,41 @@ class StableLMForwarder:
             self.close()
         except Exception:
             pass
+
+
+class LlamaForwarder:
+    """The legacy Llama forwarder (llamaMLXForwarder, mlx_llama.go:27-35)
+    over a llama2.c checkpoint payload in readWeights order."""
+
+    def __init__(self, config: dict, weights: np.ndarray):
+        c = config
+        self.config = c
+        cfg = LlamaConfig(c["dim"], c["hidden_dim"], c["n_layers"], c["n_heads"], c["n_kv_heads"],
+                          c["vocab_size"], c["seq_len"])
+        w = np.ascontiguousarray(weights, np.float32)
+        h = C.c_void_p()
+        check(lib().tinyoai_llama_load(C.byref(cfg), _fp(w), w.size, C.byref(h)))
+        self.h = h
+
+    def forward(self, prefix: int, tokens, all_logits: bool = False) -> np.ndarray:
+        """Forward (mlx_llama_native.go:119-175): every row [n][vocab] when
+        all_logits, else the last row [vocab]."""
+        ids = np.ascontiguousarray(tokens, np.int32)
+        rows = ids.size if all_logits else 1
+        out = np.empty((rows, self.config["vocab_size"]), np.float32)
+        check(lib().tinyoai_llama_forward(self.h, prefix, _ip(ids), ids.size, int(all_logits), _fp(out)))
+        return out if all_logits else out[0]
+
+    def reset(self) -> None:
+        check(lib().tinyoai_llama_reset(self.h))
+
+    def close(self) -> None:
+        if self.h:
+            lib().tinyoai_llama_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
