@@ -104,3 +104,75 @@ def test_isolated_q8_0_kernel_shape(hip, oracle, m):
     dense = oracle.read_values(w, 0, 6912 * 2560).reshape(6912, 2560).astype(np.float64)
     mag = np.abs(x.astype(np.float64)) @ np.abs(dense).T
     assert np.all(np.abs(got - want) <= 2e-5 * np.maximum(1, mag))
+
+
+# ---------------------------------------------------------------- 5/6-bit formats
+KQ_GOLDEN = {"Q5_K": W.Q5_K, "Q6_K": W.Q6_K, "Q5_1": W.Q5_1}
+
+
+def _kq_golden(name):
+    import os
+    base = os.path.join(os.path.dirname(__file__), "golden", name.lower())
+    return np.fromfile(base + ".bin", np.uint8), np.fromfile(base + "-f32.bin", np.float32)
+
+
+@pytest.mark.parametrize("name", sorted(KQ_GOLDEN))
+def test_kquant_golden_on_device(hip, name):
+    """TestKQuantReference (quant_k_test.go:14-62) on the device: readValues of
+    the reference's golden blocks bit for bit, partial spans included."""
+    raw, want = _kq_golden(name)
+    g = hip.Weight(W.Tensor(KQ_GOLDEN[name], 4, 2048, raw))
+    got = g.read_values(0, want.size)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    for start, n in [(0, 1), (255, 3), (257, 511), (1000, 777)]:
+        assert np.array_equal(g.read_values(start, n), want[start:start + n])
+
+
+@pytest.mark.parametrize("dtype", [W.Q4_K, W.Q5_K, W.Q6_K])
+def test_kquant_synthetic_decode(hip, oracle, dtype):
+    """Seeded super-blocks (random bits, scales and mins): device readValues
+    equals the oracle's decodeKBlock bit for bit (Q4_K through its Q5_K
+    embedding, pinned by the golden vectors)."""
+    rng = np.random.default_rng(dtype)
+    t = W.synthetic_kquant(dtype, 12, 1536, rng)
+    want = oracle.read_values(oracle.weight(dtype, 12, 1536, t.data), 0, 12 * 1536)
+    got = hip.Weight(t).read_values(0, 12 * 1536)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_q5_1_tail_row(hip, oracle):
+    """A 7552-wide Q5_1 row (quant_k_test.go:75-87): decode and the one-row
+    product against float64."""
+    raw, want = _kq_golden("Q5_1")
+    t = W.Tensor(W.Q5_1, 1, 7552, raw[: 7552 // 32 * 24])
+    g = hip.Weight(t)
+    assert np.array_equal(g.read_values(0, 7552), want[:7552])
+    x = np.sin(np.arange(7552) * 0.19).astype(np.float32)
+    exp = float(x.astype(np.float64) @ want[:7552].astype(np.float64))
+    assert abs(float(g.mul(x)[0, 0]) - exp) <= 2e-4 * max(1, abs(exp))
+
+
+@pytest.mark.parametrize("dtype", [W.Q5_1, W.Q4_K, W.Q5_K, W.Q6_K])
+@pytest.mark.parametrize("n", [1, 7, 128])
+def test_kquant_products(hip, oracle, dtype, n):
+    """mulScratch (n = 1) and mulBatch (n > 1) of 5/6-bit matrices against
+    float64 of the decoded values: 2e-5 * sum |x w| for the single row,
+    2e-4 * max(1, |y|) batched (the reference's tolerances)."""
+    rng = np.random.default_rng(100 + n)
+    rows, cols = 37, 2560
+    if dtype == W.Q5_1:
+        raw, _ = _kq_golden("Q5_1")
+        reps = -(-rows * cols // 32 * 24 // raw.size)
+        t = W.Tensor(dtype, rows, cols, np.tile(raw, reps)[: rows * cols // 32 * 24].copy())
+    else:
+        t = W.synthetic_kquant(dtype, rows, cols, rng)
+    g = hip.Weight(t)
+    dense = oracle.read_values(oracle.weight(dtype, rows, cols, t.data), 0, rows * cols).reshape(rows, cols)
+    x = rng.standard_normal((n, cols)).astype(np.float32)
+    got = g.mul(x)
+    exp = x.astype(np.float64) @ dense.astype(np.float64).T
+    if n == 1:
+        mag = np.abs(x.astype(np.float64)) @ np.abs(dense.astype(np.float64)).T
+        assert np.all(np.abs(got - exp) <= 2e-5 * np.maximum(1, mag))
+    else:
+        assert np.all(np.abs(got - exp) <= 2e-4 * np.maximum(1, np.abs(exp)))

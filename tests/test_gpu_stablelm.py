@@ -212,3 +212,28 @@ def test_persistent_decode_matches_per_kernel_path(hip, dtype, kv_bits):
     assert np.all(np.abs(v1 - v2) <= 1e-5 * float(np.ptp(v2)) + ulp * np.abs(v2))
     fast.close()
     ref.close()
+
+
+@pytest.mark.parametrize("dtype", [W.Q4_K, W.Q6_K])
+def test_kquant_layers_against_oracle(hip, oracle, dtype):
+    """StableLM-3B layer shapes (two layers) with every matrix in one 5/6-bit
+    format and fp16 KV: prefill and decode logits against the oracle within
+    1e-3 of their range, identical greedy ids."""
+    config = W.validate_stablelm_config(dict(W.STABLELM_3B, num_hidden_layers=2, max_position_embeddings=256))
+    tensors = W.synthetic_stablelm(config, dtype, seed=21)
+    rng = np.random.default_rng(4)
+    prompt = rng.integers(0, 65536, 40).astype(np.int32)
+    oracle.set_threads(8)
+    ref = oracle.StableLM(config, tensors, half_kv=True, capacity=256)
+    f = hip.StableLMForwarder(config, tensors)
+    f.set_kv_bits(16)
+    want = ref.prefill(prompt, 0)
+    got = f.forward(0, prompt)
+    assert np.max(np.abs(got - want)) <= 1e-3 * float(np.ptp(want))
+    for step in range(8):
+        tr, tg = int(np.argmax(want)), int(np.argmax(got))
+        assert tr == tg, step
+        want = ref.forward(tr, 40 + step)
+        got = f.forward(40 + step, [tg])
+        assert np.max(np.abs(got - want)) <= 1e-3 * float(np.ptp(want)), step
+    f.close()

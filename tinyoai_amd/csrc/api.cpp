@@ -45,8 +45,64 @@ int64_t gguf_bytes(int32_t dtype, int64_t rows, int64_t cols) {
     case FMT_F32: return n * 4;
     case FMT_F16: case FMT_BF16: return n * 2;
     case FMT_Q8_0: return cols % 32 ? -1 : n / 32 * 34;
+    case FMT_Q5_1: return cols % 32 ? -1 : n / 32 * 24;
+    case FMT_Q4_K: return cols % 256 ? -1 : n / 256 * 144;
+    case FMT_Q5_K: return cols % 256 ? -1 : n / 256 * 176;
+    case FMT_Q6_K: return cols % 256 ? -1 : n / 256 * 210;
   }
   return -1;
+}
+
+// 5/6-bit GGUF blocks -> the chunk planes of formats.h for one row: per
+// chunk of 32 values the 4-bit low parts (byte b: values b and b + 16),
+// the high bits, and each block's header bytes. Follows the bit layout of
+// decodeKBlock (quant_k.go:31-86); Q4_K is laid out as Q5_K without qh.
+static void kquant_repack_row(int fmt, const uint8_t *raw, int64_t cols, uint8_t *vals, uint8_t *meta,
+                              uint8_t *hbits) {
+  const int64_t chunks = cols / 32;
+  for (int64_t c = 0; c < chunks; c++) {
+    int q[32];
+    if (fmt == FMT_Q5_1) {
+      const uint8_t *b = raw + c * 24;
+      uint32_t high;
+      memcpy(&high, b + 4, 4);
+      for (int i = 0; i < 32; i++) q[i] = ((b[8 + i % 16] >> (i / 16 * 4)) & 15) | ((high >> i) & 1) << 4;
+      memcpy(meta + c * 4, b, 4);
+    } else if (fmt == FMT_Q6_K) {
+      const uint8_t *b = raw + (c / 8) * 210;
+      for (int t = 0; t < 32; t++) {
+        const int i = (int)(c % 8) * 32 + t;
+        const int low = (b[(i / 128) * 64 + i % 64] >> ((i % 128) / 64 * 4)) & 15;
+        const int high = (b[128 + (i / 128) * 32 + i % 32] >> ((i % 128) / 32 * 2)) & 3;
+        q[t] = low | high << 4;
+      }
+      if (c % 8 == 0) {
+        memset(meta + (c / 8) * 32, 0, 32);
+        memcpy(meta + (c / 8) * 32, b + 192, 16);
+        memcpy(meta + (c / 8) * 32 + 16, b + 208, 2);
+      }
+    } else {  // Q4_K / Q5_K
+      const bool q5 = fmt == FMT_Q5_K;
+      const uint8_t *b = raw + (c / 8) * (q5 ? 176 : 144);
+      const int g = (int)(c % 8);
+      for (int j = 0; j < 32; j++) {
+        const int low = (b[(q5 ? 48 : 16) + (g / 2) * 32 + j] >> (g % 2 * 4)) & 15;
+        const int high = q5 ? (b[16 + j] >> g) & 1 : 0;
+        q[j] = low | high << 4;
+      }
+      if (g == 0) memcpy(meta + (c / 8) * 16, b, 16);
+    }
+    for (int i = 0; i < 16; i++) vals[c * 16 + i] = (uint8_t)((q[i] & 15) | (q[i + 16] & 15) << 4);
+    if (fmt == FMT_Q5_1 || fmt == FMT_Q5_K) {
+      uint32_t h = 0;
+      for (int i = 0; i < 32; i++) h |= (uint32_t)((q[i] >> 4) & 1) << i;
+      memcpy(hbits + c * 4, &h, 4);
+    } else if (fmt == FMT_Q6_K) {
+      uint64_t h = 0;
+      for (int i = 0; i < 32; i++) h |= (uint64_t)((q[i] >> 4) & 3) << (2 * i);
+      memcpy(hbits + c * 8, &h, 8);
+    }
+  }
 }
 
 DevMatrix::~DevMatrix() {
@@ -58,26 +114,31 @@ static int64_t value_width(int32_t dtype) { return dtype == FMT_F32 ? 4 : (dtype
 int DevMatrix::create(int32_t dtype, int64_t rows, int64_t cols, hipStream_t st) {
   if (rows <= 0 || cols <= 0 || rows > INT32_MAX || cols > INT32_MAX)
     return fail(TINYOAI_EINVAL, "invalid matrix shape [%lld, %lld]", (long long)rows, (long long)cols);
-  if (dtype != FMT_F32 && dtype != FMT_F16 && dtype != FMT_BF16 && dtype != FMT_Q8_0)
+  if (dtype != FMT_F32 && dtype != FMT_F16 && dtype != FMT_BF16 && dtype != FMT_Q8_0 && !is_kquant(dtype))
     return fail(TINYOAI_EINVAL, "unsupported tensor type %d", dtype);
-  if (dtype == FMT_Q8_0 && cols % 32) return fail(TINYOAI_EINVAL, "Q8_0 rows must be divisible by 32");
+  if (gguf_bytes(dtype, 1, cols) < 0)
+    return fail(TINYOAI_EINVAL, "rows of type %d must hold whole quant blocks (%lld values)", dtype, (long long)cols);
   MatDesc m{};
   m.fmt = dtype;
   m.rows = (int32_t)rows;
   m.cols = (int32_t)cols;
-  m.vstride = (cols * value_width(dtype) + 15) / 16 * 16;
-  m.mstride = dtype == FMT_Q8_0 ? cols / 32 * 2 : 0;
-  m.chunks = (int32_t)(m.vstride / 16);
-  const size_t vbytes = (size_t)(m.vstride * rows);
-  const size_t mbytes = (size_t)(m.mstride * rows);
-  const size_t total = (vbytes + 255) / 256 * 256 + mbytes + 256;
+  const int64_t chunks = is_kquant(dtype) ? cols / 32 : (cols * value_width(dtype) + 15) / 16;
+  m.vstride = chunks * 16;
+  m.chunks = (int32_t)chunks;
+  m.mstride = meta_offset(dtype, chunks);
+  m.hstride = hbits_offset(dtype, chunks);
+  auto round256 = [](size_t v) { return (v + 255) / 256 * 256; };
+  const size_t vbytes = round256((size_t)(m.vstride * rows)), mbytes = round256((size_t)(m.mstride * rows));
+  const size_t hbytes = round256((size_t)(m.hstride * rows));
+  const size_t total = vbytes + mbytes + hbytes + 256;
   hipError_t e = hipMalloc(&mem, total);
   if (e != hipSuccess) return fail(TINYOAI_ENOMEM, "hipMalloc(%zu): %s", total, hipGetErrorString(e));
   bytes = total;
   e = hipMemsetAsync(mem, 0, total, st);  // row padding reads as zeros
   if (e != hipSuccess) return hip_fail(e, "weight init");
   m.vals = (const uint8_t *)mem;
-  m.meta = m.mstride ? (const uint8_t *)mem + (vbytes + 255) / 256 * 256 : (const uint8_t *)mem;
+  m.meta = (const uint8_t *)mem + vbytes;
+  m.hbits = (const uint8_t *)mem + vbytes + mbytes;
   desc = m;
   return TINYOAI_OK;
 }
@@ -102,12 +163,39 @@ int DevMatrix::place(int32_t dtype, int64_t rows, int64_t cols, const void *data
     case ROWMAP_INTERLEAVE: last_row = map.offset + 2 * (rows - 1) + map.phase; break;
     default: last_row = map.offset + rows - 1;
   }
-  if (map.offset < 0 || last_row >= m.rows || col0 < 0 || (col0 + cols) * value_width(dtype) > m.vstride ||
-      (dtype == FMT_Q8_0 && (col0 % 32 || (col0 + cols) / 32 * 2 > m.mstride)))
+  const int64_t blk = dtype == FMT_Q8_0 || dtype == FMT_Q5_1 ? 32 : (is_kquant(dtype) ? 256 : 1);
+  const int64_t used = is_kquant(dtype) ? (col0 + cols) / 32 * 16 : (col0 + cols) * value_width(dtype);
+  if (map.offset < 0 || last_row >= m.rows || col0 < 0 || col0 % blk || used > m.vstride ||
+      (dtype == FMT_Q8_0 && (col0 + cols) / 32 * 2 > m.mstride))
     return fail(TINYOAI_EINVAL, "tensor [%lld, %lld] does not fit its place in a [%d, %d] matrix", (long long)rows,
                 (long long)cols, m.rows, m.cols);
   const int64_t width = value_width(dtype);
   hipError_t e;
+  if (is_kquant(dtype)) {
+    // Repack on the host into the tensor's own planes, then place each
+    // plane's rows on the device.
+    const int64_t chunks = cols / 32, c0 = col0 / 32;
+    const int64_t vb = chunks * 16, mb = meta_offset(dtype, chunks), hb = hbits_offset(dtype, chunks);
+    const int64_t raw_row = gguf_bytes(dtype, 1, cols);
+    std::vector<uint8_t> host((size_t)(rows * (vb + mb + hb)));
+    uint8_t *hv = host.data(), *hm = hv + rows * vb, *hh = hm + rows * mb;
+    for (int64_t r = 0; r < rows; r++)
+      kquant_repack_row(dtype, (const uint8_t *)data + r * raw_row, cols, hv + r * vb, hm + r * mb, hh + r * hb);
+    void *dev = nullptr;
+    e = hipMalloc(&dev, host.size());
+    if (e != hipSuccess) return fail(TINYOAI_ENOMEM, "hipMalloc(%zu): %s", host.size(), hipGetErrorString(e));
+    const uint8_t *dv = (const uint8_t *)dev, *dm = dv + rows * vb, *dh = dm + rows * mb;
+    e = hipMemcpyAsync(dev, host.data(), host.size(), hipMemcpyHostToDevice, st);
+    if (e == hipSuccess)
+      e = launch_place_bytes(dv, rows, vb, (uint8_t *)m.vals, m.vstride, c0 * 16, map, st);
+    if (e == hipSuccess && mb)
+      e = launch_place_bytes(dm, rows, mb, (uint8_t *)m.meta, m.mstride, meta_offset(dtype, c0), map, st);
+    if (e == hipSuccess && hb)
+      e = launch_place_bytes(dh, rows, hb, (uint8_t *)m.hbits, m.hstride, hbits_offset(dtype, c0), map, st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    hipFree(dev);
+    return e == hipSuccess ? TINYOAI_OK : hip_fail(e, "weight repack");
+  }
   if (dtype != FMT_Q8_0 && map.kind == ROWMAP_IDENTITY && col0 == 0 && m.vstride == cols * width) {
     e = hipMemcpyAsync((uint8_t *)mem + map.offset * m.vstride, data, nbytes, hipMemcpyHostToDevice, st);
     if (e == hipSuccess) e = hipStreamSynchronize(st);
@@ -134,11 +222,19 @@ int DevMatrix::upload(int32_t dtype, int64_t rows, int64_t cols, const void *dat
 
 MatDesc column_view(const MatDesc &m, int64_t col0, int64_t cols) {
   MatDesc v = m;
-  const int64_t width = value_width(m.fmt);
-  v.vals = m.vals + col0 * width;
-  v.meta = m.fmt == FMT_Q8_0 ? m.meta + col0 / 32 * 2 : m.meta;
+  if (is_kquant(m.fmt)) {
+    const RowPtr r = row_ptr(m, 0, col0 / 32);
+    v.vals = r.v;
+    v.meta = r.m;
+    v.hbits = r.h;
+    v.chunks = (int32_t)(cols / 32);
+  } else {
+    const int64_t width = value_width(m.fmt);
+    v.vals = m.vals + col0 * width;
+    v.meta = m.fmt == FMT_Q8_0 ? m.meta + col0 / 32 * 2 : m.meta;
+    v.chunks = (int32_t)((cols * width + 15) / 16);
+  }
   v.cols = (int32_t)cols;
-  v.chunks = (int32_t)((cols * width + 15) / 16);
   return v;
 }
 

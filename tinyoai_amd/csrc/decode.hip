@@ -66,10 +66,7 @@ __global__ __launch_bounds__(T) void decode_in_kernel(InArgs a) {
     for (int i = threadIdx.x; i < s.rot; i += T) rope_row[i] = a.rope[(int64_t)pos * s.rot + i];
     __syncthreads();
   };
-  auto unit = [&](int u, Seg2 &g) {
-    const uint8_t *v0 = W.vals + 2 * (int64_t)u * W.vstride, *m0 = W.meta + 2 * (int64_t)u * W.mstride;
-    g = Seg2{v0, m0, v0 + W.vstride, m0 + W.mstride, xq, xq, nch, nch};
-  };
+  auto unit = [&](int u, Seg2 &g) { g = Seg2{row_ptr(W, 2 * (int64_t)u), row_ptr(W, 2 * (int64_t)u + 1), xq, xq, nch, nch}; };
   auto done = [&](int u, float v0, float v1) {
     if (lane == 0) in_pair_epilogue(s, a.kv, rope_row, pos, u, v0, v1, a.q_out, a.m_out);
   };
@@ -92,18 +89,12 @@ __global__ __launch_bounds__(T) void decode_out_kernel(OutArgs p) {
   const MatDesc &W = p.w;
   float4 *xa = xq_lds, *xm = xq_lds + (VPC / 4) * p.na;
   const int lane = threadIdx.x & 63;
-  // Q8_0: the o part holds ka / 32 blocks, so the down scales start after
-  // ka / 16 bytes of the scale plane.
-  const int64_t moff = F == FMT_Q8_0 ? p.ka / 16 : 0;
   auto prologue = [&]() {
     stage_x(xa, p.a, p.ka, p.na, VPC);
     if (p.nm) stage_x(xm, p.m, p.km, p.nm, VPC);
     __syncthreads();
   };
-  auto unit = [&](int r, Seg2 &g) {
-    const uint8_t *v0 = W.vals + (int64_t)r * W.vstride, *m0 = W.meta + (int64_t)r * W.mstride;
-    g = Seg2{v0, m0, v0 + (int64_t)p.na * 16, m0 + moff, xa, xm, p.na, p.nm};
-  };
+  auto unit = [&](int r, Seg2 &g) { g = Seg2{row_ptr(W, r), row_ptr(W, r, p.na), xa, xm, p.na, p.nm}; };
   auto done = [&](int r, float ao, float ad) {
     if (lane == 0) p.x[r] = __fadd_rn(__fadd_rn(p.x[r], ao), ad);
   };
@@ -143,8 +134,7 @@ __global__ __launch_bounds__(T) void ln_matvec_kernel(LnMvArgs a) {
   auto unit = [&](int u, Seg2 &g) {
     const int64_t r0 = 2 * (int64_t)u, r1 = r0 + 1;
     const bool two = r1 < M.rows;
-    g = Seg2{M.vals + r0 * M.vstride, M.meta + r0 * M.mstride, two ? M.vals + r1 * M.vstride : nullptr,
-             two ? M.meta + r1 * M.mstride : nullptr, xq, xq, M.chunks, two ? M.chunks : 0};
+    g = Seg2{row_ptr(M, r0), row_ptr(M, two ? r1 : r0), xq, xq, M.chunks, two ? M.chunks : 0};
   };
   auto done = [&](int u, float v0, float v1) {
     if (lane != 0) return;
@@ -424,7 +414,9 @@ hipError_t decode_in_launch(const InArgs &a, int grid, int threads, hipStream_t 
 template <int F>
 hipError_t decode_out_launch(OutArgs p, int grid, int threads, hipStream_t st) {
   constexpr int VPC = Fmt<F>::VPC;
-  if (F == FMT_Q8_0 && p.ka % 32) return hipErrorInvalidValue;
+  // The down part starts a new quant block (and super-block).
+  const int align = F == FMT_Q8_0 || F == FMT_Q5_1 ? 32 : (is_kquant(F) ? 256 : 1);
+  if (p.ka % align) return hipErrorInvalidValue;
   p.na = (p.ka + VPC - 1) / VPC;
   p.nm = p.w.chunks - p.na;
   if (p.nm < 0 || (p.km == 0) != (p.nm == 0) || (int64_t)p.nm * VPC < p.km) return hipErrorInvalidValue;
@@ -465,6 +457,10 @@ hipError_t launch_decode_in(const LayerDev &w, const StableDims &s, const KVDev 
     case FMT_BF16: return decode_in_launch<FMT_BF16>(a, grid, threads, st);
     case FMT_F32: return decode_in_launch<FMT_F32>(a, grid, threads, st);
     case FMT_F16: return decode_in_launch<FMT_F16>(a, grid, threads, st);
+    case FMT_Q5_1: return decode_in_launch<FMT_Q5_1>(a, grid, threads, st);
+    case FMT_Q4_K: return decode_in_launch<FMT_Q4_K>(a, grid, threads, st);
+    case FMT_Q5_K: return decode_in_launch<FMT_Q5_K>(a, grid, threads, st);
+    case FMT_Q6_K: return decode_in_launch<FMT_Q6_K>(a, grid, threads, st);
   }
   return hipErrorInvalidValue;
 }
@@ -477,6 +473,10 @@ hipError_t launch_decode_out(const MatDesc &wout, int ka, int km, const float *a
     case FMT_BF16: return decode_out_launch<FMT_BF16>(p, grid, threads, st);
     case FMT_F32: return decode_out_launch<FMT_F32>(p, grid, threads, st);
     case FMT_F16: return decode_out_launch<FMT_F16>(p, grid, threads, st);
+    case FMT_Q5_1: return decode_out_launch<FMT_Q5_1>(p, grid, threads, st);
+    case FMT_Q4_K: return decode_out_launch<FMT_Q4_K>(p, grid, threads, st);
+    case FMT_Q5_K: return decode_out_launch<FMT_Q5_K>(p, grid, threads, st);
+    case FMT_Q6_K: return decode_out_launch<FMT_Q6_K>(p, grid, threads, st);
   }
   return hipErrorInvalidValue;
 }
@@ -520,6 +520,10 @@ hipError_t launch_ln_matvec(const MatDesc &w, const float *ln_w, const float *ln
     case FMT_BF16: return ln_matvec_launch<FMT_BF16>(a, grid, threads, st);
     case FMT_F32: return ln_matvec_launch<FMT_F32>(a, grid, threads, st);
     case FMT_F16: return ln_matvec_launch<FMT_F16>(a, grid, threads, st);
+    case FMT_Q5_1: return ln_matvec_launch<FMT_Q5_1>(a, grid, threads, st);
+    case FMT_Q4_K: return ln_matvec_launch<FMT_Q4_K>(a, grid, threads, st);
+    case FMT_Q5_K: return ln_matvec_launch<FMT_Q5_K>(a, grid, threads, st);
+    case FMT_Q6_K: return ln_matvec_launch<FMT_Q6_K>(a, grid, threads, st);
   }
   return hipErrorInvalidValue;
 }

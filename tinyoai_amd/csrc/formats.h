@@ -1,13 +1,20 @@
 // Weight formats as laid out in HBM, and the per-format arithmetic the
 // kernels share.
 //
-// On upload every matrix is split into two planes:
-//   vals: the per-value payload, each row padded to a multiple of 16 bytes,
-//         so a lane streams a row with 128-bit loads (a "chunk");
-//   meta: per-block metadata (Q8_0: one fp16 scale per 32 values).
+// On upload every matrix is split into planes:
+//   vals:  the per-value payload, each row padded to a multiple of 16 bytes,
+//          so a lane streams a row with 128-bit loads (a "chunk");
+//   meta:  per-block metadata (Q8_0: one fp16 scale per 32 values);
+//   hbits: the high bits of 5- and 6-bit quants.
 // F32 / F16 / BF16 keep row-major values; Q8_0 keeps its int8 quants in
-// `vals` and its fp16 block scales in `meta`. The bytes are those of the
-// GGUF block {fp16 d, int8 q[32]} (dot.go:31-40), only regrouped.
+// `vals` and its fp16 block scales in `meta`, the bytes of the GGUF block
+// {fp16 d, int8 q[32]} (dot.go:31-40) regrouped. The 5/6-bit formats
+// (decodeKBlock, quant_k.go:31-86) use chunks of 32 values: byte b of a
+// chunk holds the low 4 bits of values b and b + 16; hbits holds bit 4 of
+// value j at bit j (Q5_1, Q5_K: 4 bytes a chunk) or bits 4-5 at bits 2j
+// (Q6_K: 8 bytes); meta keeps each block's own header bytes: Q5_1 {d, m}
+// per 32 values, Q4_K / Q5_K {d, dmin, scales[12]} and Q6_K {scales[16],
+// d} (padded to 32 bytes) per 256 values.
 #pragma once
 
 #include <hip/hip_fp16.h>
@@ -27,10 +34,45 @@ struct MatDesc {
   int32_t rows, cols;   // logical shape [out, in]
   int32_t fmt;
   int32_t chunks;       // 16-byte chunks per row = vstride / 16
+  const uint8_t *hbits; // [rows][hstride] bytes (Q5_1, Q5_K, Q6_K)
+  int64_t hstride;
 };
+
+__host__ __device__ inline bool is_kquant(int fmt) {
+  return fmt == FMT_Q5_1 || fmt == FMT_Q4_K || fmt == FMT_Q5_K || fmt == FMT_Q6_K;
+}
+// Bytes of hbits per chunk, and of meta per chunk (Q8_0, Q5_1) or per
+// 256-value super-block (Q4_K, Q5_K, Q6_K).
+__host__ __device__ inline int hbits_per_chunk(int fmt) {
+  return fmt == FMT_Q6_K ? 8 : (fmt == FMT_Q5_1 || fmt == FMT_Q5_K ? 4 : 0);
+}
+__host__ __device__ inline int meta_per_block(int fmt) {
+  switch (fmt) {
+    case FMT_Q8_0: return 2;
+    case FMT_Q5_1: return 4;
+    case FMT_Q4_K: case FMT_Q5_K: return 16;
+    case FMT_Q6_K: return 32;
+    default: return 0;
+  }
+}
+// Byte offsets of chunk c's metadata and high bits within a row.
+__host__ __device__ inline int64_t meta_offset(int fmt, int64_t c) {
+  switch (fmt) {
+    case FMT_Q8_0: return (c >> 1) * 2;
+    case FMT_Q5_1: return c * 4;
+    case FMT_Q4_K: case FMT_Q5_K: return (c >> 3) * 16;
+    case FMT_Q6_K: return (c >> 3) * 32;
+    default: return 0;
+  }
+}
+__host__ __device__ inline int64_t hbits_offset(int fmt, int64_t c) { return c * hbits_per_chunk(fmt); }
 
 template <int F> struct Fmt;
 template <> struct Fmt<FMT_Q8_0> { static constexpr int VPC = 16; };
+template <> struct Fmt<FMT_Q5_1> { static constexpr int VPC = 32; };
+template <> struct Fmt<FMT_Q4_K> { static constexpr int VPC = 32; };
+template <> struct Fmt<FMT_Q5_K> { static constexpr int VPC = 32; };
+template <> struct Fmt<FMT_Q6_K> { static constexpr int VPC = 32; };
 template <> struct Fmt<FMT_BF16> { static constexpr int VPC = 8; };
 template <> struct Fmt<FMT_F16> { static constexpr int VPC = 8; };
 template <> struct Fmt<FMT_F32> { static constexpr int VPC = 4; };
@@ -40,6 +82,7 @@ __host__ __device__ inline int values_per_chunk(int fmt) {
   switch (fmt) {
     case FMT_Q8_0: return 16;
     case FMT_BF16: case FMT_F16: return 8;
+    case FMT_Q5_1: case FMT_Q4_K: case FMT_Q5_K: case FMT_Q6_K: return 32;
     default: return 4;
   }
 }
@@ -133,6 +176,93 @@ __device__ __forceinline__ float chunk_dot<FMT_F32>(const uint4 w, const float4 
   return a + b;
 }
 
+// ---------------------------------------------------------------- 5/6-bit
+// 6-bit scale and minimum of group g of a Q4_K / Q5_K super-block
+// (quant_k.go:69-77).
+__device__ __forceinline__ void kquant_scale_min(const uint8_t *sc, int g, int &scale, int &minimum) {
+  if (g < 4) {
+    scale = sc[g] & 63;
+    minimum = sc[g + 4] & 63;
+  } else {
+    scale = (sc[g + 4] & 15) | ((sc[g - 4] >> 6) << 4);
+    minimum = (sc[g + 4] >> 4) | ((sc[g] >> 6) << 4);
+  }
+}
+
+// Per-chunk constants of the value formula, from the chunk's meta bytes
+// (and, for Q6_K, its fp16 d): value = (q * a) + b for Q5_1, (q * a) - b
+// for Q4_K / Q5_K, (q - 32) * (a or a2) for Q6_K (a for values 0-15, a2
+// for 16-31), each step rounded as decodeKBlock rounds it.
+struct KConst {
+  float a, b, a2;
+};
+
+template <int F>
+__device__ __forceinline__ KConst kquant_const(const uint4 mt, uint16_t d6, int cc) {
+  KConst k{};
+  if constexpr (F == FMT_Q5_1) {
+    k.a = half_to_float((uint16_t)mt.x);
+    k.b = half_to_float((uint16_t)(mt.x >> 16));
+  } else if constexpr (F == FMT_Q4_K || F == FMT_Q5_K) {
+    const uint32_t w[4] = {mt.x, mt.y, mt.z, mt.w};
+    const uint8_t *bytes = reinterpret_cast<const uint8_t *>(w);
+    int sc, mn;
+    kquant_scale_min(bytes + 4, cc & 7, sc, mn);
+    k.a = __fmul_rn(half_to_float((uint16_t)mt.x), (float)sc);
+    k.b = __fmul_rn(half_to_float((uint16_t)(mt.x >> 16)), (float)mn);
+  } else {
+    const uint32_t w[4] = {mt.x, mt.y, mt.z, mt.w};
+    const int8_t *scales = reinterpret_cast<const int8_t *>(w);
+    const float d = half_to_float(d6);
+    k.a = __fmul_rn(d, (float)scales[2 * (cc & 7)]);
+    k.a2 = __fmul_rn(d, (float)scales[2 * (cc & 7) + 1]);
+  }
+  return k;
+}
+
+// The quant of value j (0..31) of a chunk: low 4 bits from the value
+// bytes, high bits from hbits.
+template <int F>
+__device__ __forceinline__ int kquant_q(uint32_t lo_byte, int j, uint2 h) {
+  const int lo = j < 16 ? (lo_byte & 15) : (lo_byte >> 4);
+  if constexpr (F == FMT_Q5_1 || F == FMT_Q5_K) return lo | (int)((h.x >> j) & 1) << 4;
+  if constexpr (F == FMT_Q6_K) {
+    const uint32_t hw = j < 16 ? h.x : h.y;
+    return lo | (int)((hw >> (2 * (j & 15))) & 3) << 4;
+  }
+  return lo;
+}
+
+template <int F>
+__device__ __forceinline__ float kquant_value(const KConst &k, int q, int j) {
+  if constexpr (F == FMT_Q5_1) return __fadd_rn(__fmul_rn(k.a, (float)q), k.b);
+  if constexpr (F == FMT_Q6_K) return __fmul_rn(j < 16 ? k.a : k.a2, (float)(q - 32));
+  return __fsub_rn(__fmul_rn(k.a, (float)q), k.b);
+}
+
+// Dot product of chunk cc (32 values) with its staged x (quad q of the
+// chunk at xq[q * nch + c]).
+template <int F>
+__device__ __forceinline__ float kchunk_dot(const uint4 w, const uint2 h, const uint4 mt, uint16_t d6, int cc,
+                                            const float4 *xq, int nch, int c) {
+  const KConst k = kquant_const<F>(mt, d6, cc);
+  const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+  float a = 0.f, b = 0.f;
+#pragma unroll
+  for (int qd = 0; qd < 4; qd++) {
+    const float4 xl = xq[qd * nch + c], xh = xq[(qd + 4) * nch + c];
+    const float xlv[4] = {xl.x, xl.y, xl.z, xl.w}, xhv[4] = {xh.x, xh.y, xh.z, xh.w};
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const uint32_t byte = (ws[qd] >> (8 * e)) & 255;
+      const int j = 4 * qd + e;
+      a = fmaf(kquant_value<F>(k, kquant_q<F>(byte, j, h), j), xlv[e], a);
+      b = fmaf(kquant_value<F>(k, kquant_q<F>(byte, j + 16, h), j + 16), xhv[e], b);
+    }
+  }
+  return a + b;
+}
+
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // Weights live in global memory; saying so keeps the loads global_load
@@ -151,11 +281,37 @@ __device__ __forceinline__ uint16_t load_scale(const uint8_t *meta, int block) {
   return ((const TINYOAI_GLOBAL uint16_t *)meta)[block];
 }
 
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Plain (cached) global loads of block headers and high bits, which
+// neighbouring lanes share.
+__device__ __forceinline__ uint4 load_u4(const uint8_t *p, int64_t i) {
+  const u32x4 v = ((const TINYOAI_GLOBAL u32x4 *)p)[i];
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint2 load_u2(const uint8_t *p, int64_t i) {
+  const u32x2 v = ((const TINYOAI_GLOBAL u32x2 *)p)[i];
+  return make_uint2(v.x, v.y);
+}
+__device__ __forceinline__ uint32_t load_u1(const uint8_t *p, int64_t i) {
+  return ((const TINYOAI_GLOBAL uint32_t *)p)[i];
+}
+
 // ---------------------------------------------------------------- streaming
 // A unit of matvec work: one or two row segments, each with its own staged
 // x vector (xq0 / xq1 with n0 / n1 chunks). n1 == 0 means one segment.
+struct RowPtr {
+  const uint8_t *v, *m, *h;  // vals, meta, hbits of a row from some chunk on
+};
+
+// Row `row` of m from chunk c0 (a super-block boundary for Q4_K/Q5_K/Q6_K).
+__host__ __device__ inline RowPtr row_ptr(const MatDesc &m, int64_t row, int64_t c0 = 0) {
+  return RowPtr{m.vals + row * m.vstride + c0 * 16, m.meta + row * m.mstride + meta_offset(m.fmt, c0),
+                m.hbits + row * m.hstride + hbits_offset(m.fmt, c0)};
+}
+
 struct Seg2 {
-  const uint8_t *v0, *m0, *v1, *m1;
+  RowPtr r0, r1;
   const float4 *x0, *x1;
   int n0, n1;
 };
@@ -166,7 +322,9 @@ struct Seg2 {
 template <int U>
 struct Batch {
   uint4 w[U];
-  uint16_t s[U];
+  uint16_t s[U];  // Q8_0 block scale, Q6_K d
+  uint2 h[U];     // high bits (Q5_1, Q5_K, Q6_K)
+  uint4 mt[U];    // block header (Q5_1, Q4_K, Q5_K, Q6_K scales)
 };
 
 // Issues every load of a batch back to back. Lanes past the end load a
@@ -180,8 +338,20 @@ __device__ __forceinline__ void batch_issue(Batch<U> &b, const Seg2 &g, int base
     const int c = min(base + u * 64 + lane, total - 1);
     const bool seg1 = c >= g.n0;
     const int cc = seg1 ? c - g.n0 : c;
-    b.w[u] = load_chunk((seg1 ? g.v1 : g.v0) + (int64_t)cc * 16);
-    if constexpr (F == FMT_Q8_0) b.s[u] = load_scale(seg1 ? g.m1 : g.m0, cc >> 1);
+    const RowPtr &r = seg1 ? g.r1 : g.r0;
+    b.w[u] = load_chunk(r.v + (int64_t)cc * 16);
+    if constexpr (F == FMT_Q8_0) b.s[u] = load_scale(r.m, cc >> 1);
+    if constexpr (F == FMT_Q5_1) {
+      b.mt[u].x = load_u1(r.m, cc);
+      b.h[u].x = load_u1(r.h, cc);
+    }
+    if constexpr (F == FMT_Q4_K || F == FMT_Q5_K) b.mt[u] = load_u4(r.m, cc >> 3);
+    if constexpr (F == FMT_Q5_K) b.h[u].x = load_u1(r.h, cc);
+    if constexpr (F == FMT_Q6_K) {
+      b.mt[u] = load_u4(r.m, (cc >> 3) * 2);
+      b.s[u] = load_scale(r.m + (cc >> 3) * 32 + 16, 0);
+      b.h[u] = load_u2(r.h, cc);
+    }
   }
 }
 
@@ -202,8 +372,13 @@ __device__ __forceinline__ void batch_consume_range(const Batch<U> &b, const Seg
     const int cl = min(c, total - 1);
     const bool seg1 = cl >= g.n0;
     const int cc = seg1 ? cl - g.n0 : cl;
-    float p = chunk_dot<F>(b.w[u], seg1 ? g.x1 : g.x0, seg1 ? g.n1 : g.n0, cc);
-    if constexpr (F == FMT_Q8_0) p *= hw_half(b.s[u]);
+    float p;
+    if constexpr (Fmt<F>::VPC == 32) {
+      p = kchunk_dot<F>(b.w[u], b.h[u], b.mt[u], b.s[u], cc, seg1 ? g.x1 : g.x0, seg1 ? g.n1 : g.n0, cc);
+    } else {
+      p = chunk_dot<F>(b.w[u], seg1 ? g.x1 : g.x0, seg1 ? g.n1 : g.n0, cc);
+      if constexpr (F == FMT_Q8_0) p *= hw_half(b.s[u]);
+    }
     p = (c >= lo && c < hi) ? p : 0.f;
     acc0 += seg1 ? 0.f : p;
     acc1 += seg1 ? p : 0.f;
@@ -262,6 +437,25 @@ __device__ __forceinline__ void stream_units(int first, int stride, int n_units,
   }
 }
 
+// Value (row, col) of a 5/6-bit matrix, bit-exact with decodeKBlock.
+template <int F>
+__device__ __forceinline__ float kquant_at(const MatDesc &m, int64_t row, int64_t col) {
+  const int64_t c = col >> 5;
+  const int j = (int)(col & 31);
+  const RowPtr r = row_ptr(m, row);
+  const uint32_t byte = r.v[c * 16 + (j & 15)];
+  uint2 h{0, 0};
+  uint4 mt{0, 0, 0, 0};
+  uint16_t d6 = 0;
+  const uint8_t *mp = r.m + meta_offset(F, c);
+  if constexpr (F == FMT_Q5_1) mt.x = *reinterpret_cast<const uint32_t *>(mp);
+  else mt = *reinterpret_cast<const uint4 *>(mp);
+  if constexpr (F == FMT_Q6_K) d6 = *reinterpret_cast<const uint16_t *>(mp + 16);
+  if constexpr (F == FMT_Q5_1 || F == FMT_Q5_K) h.x = reinterpret_cast<const uint32_t *>(r.h)[c];
+  if constexpr (F == FMT_Q6_K) h = reinterpret_cast<const uint2 *>(r.h)[c];
+  return kquant_value<F>(kquant_const<F>(mt, d6, (int)c), kquant_q<F>(byte, j, h), j);
+}
+
 // Bit-exact value at (row, col): readValues (matmul.go:12-50) on the
 // repacked planes.
 __device__ __forceinline__ float mat_value(const MatDesc &m, int64_t row, int64_t col) {
@@ -273,6 +467,10 @@ __device__ __forceinline__ float mat_value(const MatDesc &m, int64_t row, int64_
     }
     case FMT_BF16: return bf16_to_float(reinterpret_cast<const uint16_t *>(vr)[col]);
     case FMT_F16: return half_to_float(reinterpret_cast<const uint16_t *>(vr)[col]);
+    case FMT_Q5_1: return kquant_at<FMT_Q5_1>(m, row, col);
+    case FMT_Q4_K: return kquant_at<FMT_Q4_K>(m, row, col);
+    case FMT_Q5_K: return kquant_at<FMT_Q5_K>(m, row, col);
+    case FMT_Q6_K: return kquant_at<FMT_Q6_K>(m, row, col);
     default: return reinterpret_cast<const float *>(vr)[col];
   }
 }

@@ -156,6 +156,10 @@ hipError_t launch_copy_row(const float *src, float *dst, int n, hipStream_t st);
 // [rows][cols] tensor into `dst` under `map`, starting at column col0.
 hipError_t launch_repack(int fmt, const uint8_t *raw, int64_t rows, int64_t cols, const MatDesc &dst,
                          const RowMap &map, int64_t col0, hipStream_t st);
+// Copies `rows` rows of row_bytes from src (contiguous) into dst (stride
+// dst_stride) at byte col0b of the mapped row: placement of one plane.
+hipError_t launch_place_bytes(const uint8_t *src, int64_t rows, int64_t row_bytes, uint8_t *dst, int64_t dst_stride,
+                              int64_t col0b, const RowMap &map, hipStream_t st);
 hipError_t launch_read_values(const MatDesc &m, int64_t offset, int64_t n, float *out, hipStream_t st);
 
 int device_cu_count();

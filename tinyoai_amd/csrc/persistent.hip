@@ -179,8 +179,7 @@ __global__ __launch_bounds__(kT) void persistent_decode_kernel(PersistentDecode 
       const MatDesc &W = w.win;
       const int units = W.rows >> 1, nch = W.chunks;
       auto unit = [&](int u, Seg2 &g) {
-        const uint8_t *v0 = W.vals + 2 * (int64_t)u * W.vstride, *m0 = W.meta + 2 * (int64_t)u * W.mstride;
-        g = Seg2{v0, m0, v0 + W.vstride, m0 + W.mstride, xq, xq, nch, nch};
+        g = Seg2{row_ptr(W, 2 * (int64_t)u), row_ptr(W, 2 * (int64_t)u + 1), xq, xq, nch, nch};
       };
       auto done = [&](int u, float v0, float v1) {
         if (lane == 0) in_pair_epilogue<true>(s, kv, rope_row, pos, u, v0, v1, q, m);
@@ -322,12 +321,8 @@ __global__ __launch_bounds__(kT) void persistent_decode_kernel(PersistentDecode 
     {
       const MatDesc &W = w.wout;
       const int nm = W.chunks - na;
-      const int64_t moff = F == FMT_Q8_0 ? d / 16 : 0;  // down scales follow d/32 o blocks
       const int r0 = gw;
-      auto unit = [&](int r, Seg2 &g) {
-        const uint8_t *v0 = W.vals + (int64_t)r * W.vstride, *m0 = W.meta + (int64_t)r * W.mstride;
-        g = Seg2{v0, m0, v0 + (int64_t)na * 16, m0 + moff, xa, xm, na, nm};
-      };
+      auto unit = [&](int r, Seg2 &g) { g = Seg2{row_ptr(W, r), row_ptr(W, r, na), xa, xm, na, nm}; };
       auto done = [&](int r, float ao, float ad) {
         if (lane == 0) put<true>(x_out + r, __fadd_rn(__fadd_rn(x_in[r], ao), ad));
       };
@@ -373,8 +368,7 @@ __global__ __launch_bounds__(kT) void persistent_decode_kernel(PersistentDecode 
     auto unit = [&](int u, Seg2 &g) {
       const int64_t r0 = 2 * (int64_t)u;
       const bool two = r0 + 1 < H.rows;
-      const uint8_t *v0 = H.vals + r0 * H.vstride, *m0 = H.meta + r0 * H.mstride;
-      g = Seg2{v0, m0, two ? v0 + H.vstride : nullptr, two ? m0 + H.mstride : nullptr, xq, xq, hch, two ? hch : 0};
+      g = Seg2{row_ptr(H, r0), row_ptr(H, two ? r0 + 1 : r0), xq, xq, hch, two ? hch : 0};
     };
     auto done = [&](int u, float v0, float v1) {
       if (lane == 0) {

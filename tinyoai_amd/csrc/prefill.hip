@@ -20,8 +20,10 @@ __global__ __launch_bounds__(256) void layer_norm_rows_kernel(const float *x, co
 }
 
 // out[n][N] = x[n][K] * W[N][K]^T, fp32 SIMT tiles of 64 tokens x 64 rows,
-// each thread a 4 x 4 micro-tile; weights dequantized into LDS.
-constexpr int kTM = 64, kTN = 64, kTK = 32;
+// each thread a 4 x 4 micro-tile; weights dequantized into LDS. As mulBatch
+// does (matmul.go:55-95), products accumulate in float32 within 512-column
+// blocks and the block partials in float64.
+constexpr int kTM = 64, kTN = 64, kTK = 32, kBlockCols = 512;
 
 __global__ __launch_bounds__(256) void gemm_simt_kernel(MatDesc w, const float *__restrict__ x, int n,
                                                          float *__restrict__ out) {
@@ -31,6 +33,7 @@ __global__ __launch_bounds__(256) void gemm_simt_kernel(MatDesc w, const float *
   const int K = w.cols, N = w.rows;
   const int tx = threadIdx.x % 16, ty = threadIdx.x / 16;
   float acc[4][4] = {};
+  double total[4][4] = {};
   for (int k0 = 0; k0 < K; k0 += kTK) {
     for (int e = threadIdx.x; e < kTM * kTK; e += 256) {
       const int r = e / kTK, c = e % kTK;
@@ -54,6 +57,15 @@ __global__ __launch_bounds__(256) void gemm_simt_kernel(MatDesc w, const float *
         for (int jj = 0; jj < 4; jj++) acc[i][jj] = fmaf(a[i], b[jj], acc[i][jj]);
     }
     __syncthreads();
+    if ((k0 + kTK) % kBlockCols == 0 || k0 + kTK >= K) {
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int jj = 0; jj < 4; jj++) {
+          total[i][jj] += (double)acc[i][jj];
+          acc[i][jj] = 0.f;
+        }
+    }
   }
 #pragma unroll
   for (int i = 0; i < 4; i++) {
@@ -62,7 +74,7 @@ __global__ __launch_bounds__(256) void gemm_simt_kernel(MatDesc w, const float *
 #pragma unroll
     for (int jj = 0; jj < 4; jj++) {
       const int row = n0 + tx * 4 + jj;
-      if (row < N) out[(int64_t)tok * N + row] = acc[i][jj];
+      if (row < N) out[(int64_t)tok * N + row] = (float)total[i][jj];
     }
   }
 }

@@ -74,6 +74,15 @@ hipError_t launch_repack(int fmt, const uint8_t *raw, int64_t rows, int64_t cols
   return hipGetLastError();
 }
 
+hipError_t launch_place_bytes(const uint8_t *src, int64_t rows, int64_t row_bytes, uint8_t *dst, int64_t dst_stride,
+                              int64_t col0b, const RowMap &map, hipStream_t st) {
+  MatDesc d{};
+  d.vals = dst;
+  d.vstride = dst_stride;
+  hipLaunchKernelGGL(repack_plain_kernel, dim3(4096), dim3(256), 0, st, src, rows, row_bytes, d, map, col0b);
+  return hipGetLastError();
+}
+
 hipError_t launch_read_values(const MatDesc &m, int64_t offset, int64_t n, float *out, hipStream_t st) {
   hipLaunchKernelGGL(read_values_kernel, dim3(1024), dim3(256), 0, st, m, offset, n, out);
   return hipGetLastError();
