@@ -26,8 +26,12 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
 
 
+WEIGHT_BYTES = {"q8_0": 34 / 32, "bf16": 2.0}  # bytes per weight value
+FORMAT = {"q8_0": "q8_0"}
+
+
 def q8_bytes(rows, cols):
-    return rows * cols // 32 * 34
+    return int(rows * cols * WEIGHT_BYTES[FORMAT["q8_0"]])
 
 
 def decode_in_bytes(c):
@@ -126,6 +130,9 @@ def main():
     ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--seed", type=int, default=1234)
+    ap.add_argument("--dtype", choices=["q8_0", "bf16"], default="q8_0",
+                    help="weight format (bf16 with --prompt 8129 --generate 64 --kv 16: the long-context workload)")
+    ap.add_argument("--kv", type=int, choices=[16, 32], default=32, help="KV cache bits")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the path would shard by "
@@ -140,10 +147,13 @@ def main():
     torch.cuda.set_device(0)
     config = W.validate_stablelm_config(dict(W.STABLELM_3B, num_hidden_layers=args.layers))
     t0 = time.perf_counter()
-    tensors = W.synthetic_stablelm(config, W.Q8_0, seed=args.seed)
+    wdtype = W.Q8_0 if args.dtype == "q8_0" else W.BF16
+    FORMAT["q8_0"] = args.dtype  # byte counts below follow the weight format
+    tensors = W.synthetic_stablelm(config, wdtype, seed=args.seed)
     gen_s = time.perf_counter() - t0
     print(f"[bench] synthetic weights in {gen_s:.1f}s", file=sys.stderr, flush=True)
     fwd = hip.StableLMForwarder(config, tensors)
+    fwd.set_kv_bits(args.kv)
     print("[bench] weights resident in HBM", file=sys.stderr, flush=True)
     rng = np.random.default_rng(args.seed + 1)
     prompt = rng.integers(0, config["vocab_size"], args.prompt).astype(np.int32)
@@ -193,7 +203,7 @@ def main():
     nbytes = decode_in_bytes(config)
     achieved = nbytes / avg_s / 1e9
     mean_pos = args.prompt + (args.generate - 2) / 2
-    roof_tok_s = 1.0 / (token_bytes(config, mean_pos) / (HBM_PEAK_GBS * 1e9))
+    roof_tok_s = 1.0 / (token_bytes(config, mean_pos, args.kv // 8) / (HBM_PEAK_GBS * 1e9))
     kernels = {k: {"avg_us": round(v[0] * 1e3 / v[1], 2) if v[1] else None, "launches": v[1]}
                for k, v in prof.items()}
 
@@ -210,11 +220,11 @@ def main():
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic",
-        "config": {"workload": f"StableLM-3B-shape GGUF Q8_0, {args.prompt}-token prompt + {args.generate} greedy "
-                               f"tokens, fp32 KV", "layers": config["num_hidden_layers"],
+        "config": {"workload": f"StableLM-3B-shape GGUF {args.dtype.upper()}, {args.prompt}-token prompt + "
+                               f"{args.generate} greedy tokens, fp{args.kv} KV", "layers": config["num_hidden_layers"],
                    "hidden": config["hidden_size"], "heads": config["num_attention_heads"], "head_dim": 80,
                    "intermediate": config["intermediate_size"], "vocab": config["vocab_size"],
-                   "prompt_tokens": args.prompt, "generated_tokens": args.generate, "kv": "f32",
+                   "prompt_tokens": args.prompt, "generated_tokens": args.generate, "kv": f"f{args.kv}",
                    "weights_seed": args.seed},
         "prefill_s": round(mean_prefill, 4),
         "prefill_tok_s": round(args.prompt / mean_prefill, 1),

@@ -725,7 +725,8 @@ int StableModel::decode_step(int token, int pos, bool want_logits) {
 
 // y[n][ldy] = x[n][ldx] * W^T: on the matrix cores when the format allows
 // (activations split into bf16 hi/lo planes first), else the vector-unit
-// GEMM.
+// GEMM. Every output row depends only on its own input row, whatever the
+// chunk size (a prefix reused from the cache gives the same results).
 int StableModel::project(const MatDesc &w, const float *x, int ldx, int n, float *y, int ldy) {
   if (gemm_mfma_supported(w)) {
     const bool two = gemm_planes(w) == 2;
@@ -757,8 +758,11 @@ int StableModel::prefill_chunk(const int32_t *ids, int n, int start, bool want_l
     if ((rc = project(w.win, H, d, n, Y, win_rows))) return rc;
     STAGE(ST_PREFILL_EPILOGUE, launch_in_epilogue(dims, kv[l], Y, win_rows, rope, d_pos0, n, Q, M, stream),
           "in_epilogue");
-    STAGE(ST_PREFILL_ATTENTION,
-          launch_attention(dims, kv[l], Q, d_pos0, n, start + n - 1, partials, counters, A, stream), "attention");
+    if (flash_prefill_supported(dims.hd))
+      STAGE(ST_PREFILL_ATTENTION, launch_flash_prefill(dims, kv[l], Q, d_pos0, n, A, stream), "attention");
+    else
+      STAGE(ST_PREFILL_ATTENTION,
+            launch_attention(dims, kv[l], Q, d_pos0, n, start + n - 1, partials, counters, A, stream), "attention");
     if ((rc = project(wo, A, d, n, P, d)) || (rc = project(wd, M, I, n, D, d))) return rc;
     STAGE(ST_PREFILL_ELEMENTWISE, launch_residual(X, P, D, (int64_t)n * d, stream), "residual");
     if (tracing) {

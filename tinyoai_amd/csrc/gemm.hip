@@ -50,8 +50,16 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
   __shared__ float ss[2][kBN];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
-  const int m0 = blockIdx.y * kBM, n0 = blockIdx.x * kBN;
   const int K = g.w.cols, N = g.w.rows, nk = K / kBK;
+  // Tile order: workgroups are dispatched round-robin over the 8 XCDs, each
+  // with its own L2. Consecutive workgroups of one XCD take the M tiles of
+  // one N tile, so a weight tile is fetched from HBM once and re-read from
+  // that XCD's L2 by the other M tiles.
+  const int MT = (g.M + kBM - 1) / kBM, NT = (N + kBN - 1) / kBN;
+  const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
+  const int nt = xcd + 8 * (slot / MT), mt = slot % MT;
+  if (nt >= NT) return;  // the grid rounds NT up to a multiple of 8
+  const int m0 = mt * kBM, n0 = nt * kBN;
   const int srow = tid >> 1, shalf = tid & 1;  // staging: one row half (16 K values) per thread
 
   uint4 rah0, rah1, ral0, ral1, rb[2];
@@ -176,7 +184,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
 
 template <int WF, int XS>
 hipError_t gemm_launch(const GemmArgs &g, hipStream_t st) {
-  dim3 grid((g.w.rows + kBN - 1) / kBN, (g.M + kBM - 1) / kBM);
+  const int NT = (g.w.rows + kBN - 1) / kBN, MT = (g.M + kBM - 1) / kBM;
+  dim3 grid((NT + 7) / 8 * 8 * MT);
   hipLaunchKernelGGL((gemm_kernel<WF, XS>), grid, dim3(256), 0, st, g);
   return hipGetLastError();
 }

@@ -74,6 +74,11 @@ hipError_t launch_decode_out(const MatDesc &wout, int ka, int km, const float *a
 hipError_t launch_attention(const StableDims &s, const KVDev &kv, const float *q, const int *pos0, int nq,
                             int max_pos, float *partials, unsigned *counters, float *out, hipStream_t st,
                             int steps = 0, int splits = 0);
+// Causal attention of n prefill queries on the matrix cores (head widths
+// 64, 80, 96, 128): q [n][heads*hd] at positions pos0 + j -> out.
+bool flash_prefill_supported(int hd);
+hipError_t launch_flash_prefill(const StableDims &s, const KVDev &kv, const float *q, const int *pos0, int n,
+                                float *out, hipStream_t st);
 int attention_steps(int max_pos, int heads);
 // Floats per (query, head) in the partials buffer: max_splits records of
 // hd + 2, rounded to 256 bytes.
