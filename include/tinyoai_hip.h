@@ -132,11 +132,18 @@ int tinyoai_stablelm_trace_read_stages(tinyoai_model *m, float *attention, float
  * profile_read fills ms[] and counts[] (n_stages >= 10) and returns the
  * number of stages. */
 int tinyoai_stablelm_profile(tinyoai_model *m, int32_t enable);
-/* Decode path for one-token forwards: nonzero (the default) runs each token
- * as one cooperative launch when the shapes and device allow it; zero runs
- * three kernels per layer from a replayed HIP graph. Returns 1 when the
- * single-launch path is available, else 0. */
+/* Decode path for one-token forwards: nonzero runs each token as one
+ * cooperative launch when the shapes and device allow it; zero (the
+ * default) runs three kernels per layer from a replayed HIP graph. Returns 1
+ * when the single-launch path is available, else 0. */
 int tinyoai_stablelm_set_persistent(tinyoai_model *m, int32_t enable);
+/* Launch shape of a decode matrix kernel: stage 0 decode_in, 1 decode_out,
+ * 2 lm_head; `grid` blocks (> 0) of `threads` threads (256 or 512). Takes
+ * effect from the next forward (cached graphs are dropped); a shape the
+ * kernel cannot run makes that forward fail. The shape changes speed; the
+ * per-row arithmetic stays the same (only the float64 sums of the
+ * normalisation moments are grouped by wave). Returns 0 or TINYOAI_EINVAL. */
+int tinyoai_stablelm_set_launch(tinyoai_model *m, int32_t stage, int32_t grid, int32_t threads);
 /* Timeline of the last profiled single-launch decode step: for each block
  * of the launch, 3 + 6 * layers readings of the GPU's 100 MHz real-time
  * counter (start; per layer: input-side wait over, input rows done,

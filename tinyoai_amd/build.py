@@ -19,7 +19,11 @@ BUILD = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "libtinyoai_hip.so")
 ARCH = os.environ.get("TINYOAI_OFFLOAD_ARCH", "gfx950")
 
-SOURCES = ["api.cpp", "llama.cpp", "decode.hip", "prefill.hip", "weights.hip", "gemm.hip", "persistent.hip"]
+# The streaming matrix-vector kernels come one weight format per file
+# (matvec_<format>.hip), so they compile in parallel.
+MATVEC_FORMATS = ["q8_0", "bf16", "f32", "f16", "q5_1", "q4_k", "q5_k", "q6_k"]
+SOURCES = ["decode.hip", "persistent.hip", "api.cpp", "llama.cpp", "prefill.hip", "weights.hip", "gemm.hip",
+           "flash.hip"] + [f"matvec_{f}.hip" for f in MATVEC_FORMATS]
 FLAGS = ["-O3", "-std=c++17", "-fPIC", "-x", "hip", f"--offload-arch={ARCH}", "-ffp-contract=off",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
          "-Wall", "-Wno-unused-function", "-Wno-unused-variable", "-Wno-unused-value", "-Wno-unused-result",
@@ -44,10 +48,12 @@ def _compile(src: str) -> str:
 
 def build(verbose: bool = False) -> str:
     os.makedirs(BUILD, exist_ok=True)
-    with cf.ThreadPoolExecutor(max_workers=min(8, len(SOURCES))) as ex:
+    with cf.ThreadPoolExecutor(max_workers=min(os.cpu_count() or 8, 16, len(SOURCES))) as ex:
         objs = list(ex.map(_compile, SOURCES))
     tmp = LIB + ".tmp"
-    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
+    # -z defs: a symbol left undefined (a source missing from SOURCES) fails
+    # the link here instead of the load on the device host.
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,-z,defs", "-o", tmp, *objs]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode:
         raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")

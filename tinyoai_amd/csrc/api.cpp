@@ -434,10 +434,12 @@ int StableModel::init(const tinyoai_stablelm_config &c, const tinyoai_tensor *te
   }
   // Device workspaces.
   const int maxp = c.max_position_embeddings;
-  const std::vector<float> rt = rope_table(maxp, dims.rot, c.rope_theta);
+  rope_host = rope_table(maxp, dims.rot, c.rope_theta);
+  const std::vector<float> &rt = rope_host;
   if ((rc = alloc((void **)&rope, rt.size() * 4))) return rc;
   e = hipMemcpyAsync(rope, rt.data(), rt.size() * 4, hipMemcpyHostToDevice, stream);
   if (e != hipSuccess) return hip_fail(e, "rope upload");
+  if (16 + dims.rot > 1024) return fail(TINYOAI_EINVAL, "rotary width %d too large", dims.rot);
   chunk = std::min(512, maxp);
   const size_t w_att = (size_t)dims.heads * hd;
   if ((rc = alloc((void **)&x, (size_t)d * 4)) || (rc = alloc((void **)&qbuf, w_att * 4)) ||
@@ -477,17 +479,19 @@ int StableModel::init(const tinyoai_stablelm_config &c, const tinyoai_tensor *te
   if (e != hipSuccess) return hip_fail(e, "persistent decode state");
   e = hipEventCreateWithFlags(&params_copied, hipEventDisableTiming);
   if (e != hipSuccess) return hip_fail(e, "hipEventCreate");
-  e = hipHostMalloc(&h_pinned, (size_t)c.vocab_size * 4 + 4096 + (size_t)chunk * 4 + 64, hipHostMallocDefault);
+  e = hipHostMalloc(&h_pinned, (size_t)c.vocab_size * 4 + 4096 + (size_t)std::max(chunk, dims.rot) * 4 + 64,
+                    hipHostMallocDefault);
   if (e != hipSuccess) return fail(TINYOAI_ENOMEM, "hipHostMalloc: %s", hipGetErrorString(e));
   e = hipStreamSynchronize(stream);
   if (e != hipSuccess) return hip_fail(e, "model upload");
   const int cus = device_cu_count();
-  // One large block per CU for the matvecs (measured on MI355X at the 3B
-  // shapes): each block stages its activations once and its waves stream rows.
-  grid_in = cus;
-  threads_in = 1024;
-  grid_out = cus;
-  threads_out = 640;
+  // Row-streaming matvecs (measured on MI355X at the 3B shapes): two
+  // 256-thread blocks per CU for the layer products, 512 threads for the
+  // classifier.
+  grid_in = cus * 2;
+  threads_in = 256;
+  grid_out = cus * 2;
+  threads_out = 256;
   grid_head = cus * 2;
   threads_head = 512;
   pgrid = persistent_decode_grid(persistent_args(true), layers[0]);
@@ -627,14 +631,17 @@ int StableModel::ensure_kv(int needed) {
     prof.end(stream);                  \
   } while (0)
 
-// Copies `count` ints (head[0..nh) then ids) into the device parameter
-// block through the pinned slot, first waiting for the slot's previous copy.
-int StableModel::upload_params(const int *head_vals, int nh, const int32_t *ids, int n) {
+// Copies head[0..nh), then from int 16 on the ids or the float row, into
+// the device parameter block through the pinned slot, first waiting for the
+// slot's previous copy.
+int StableModel::upload_params(const int *head_vals, int nh, const int32_t *ids, int n, const float *row, int nrow) {
   int *hp = (int *)((char *)h_pinned + (size_t)cfg.vocab_size * 4 + 64);  // after the logits and error word
   if (params_copied) TRY_HIP(hipEventSynchronize(params_copied), "parameter slot");
   for (int i = 0; i < nh; i++) hp[i] = head_vals[i];
   if (n) memcpy(hp + 16, ids, (size_t)n * 4);
-  TRY_HIP(hipMemcpyAsync(params, hp, (size_t)(n ? 16 + n : nh) * 4, hipMemcpyHostToDevice, stream), "parameters");
+  if (nrow) memcpy(hp + 16, row, (size_t)nrow * 4);
+  const int count = n ? 16 + n : (nrow ? 16 + nrow : nh);
+  TRY_HIP(hipMemcpyAsync(params, hp, (size_t)count * 4, hipMemcpyHostToDevice, stream), "parameters");
   TRY_HIP(hipEventRecord(params_copied, stream), "parameter event");
   return TINYOAI_OK;
 }
@@ -645,8 +652,9 @@ int StableModel::upload_params(const int *head_vals, int nh, const int32_t *ids,
 int StableModel::enqueue_decode(int steps, int splits, bool want_logits) {
   for (int l = 0; l < cfg.num_hidden_layers; l++) {
     STAGE(ST_DECODE_IN,
-          launch_decode_in(layers[l], dims, kv[l], x, l == 0 ? &embed.desc : nullptr, params, rope, params + 1, qbuf,
-                           mbuf, grid_in, threads_in, stream),
+          launch_decode_in(layers[l], dims, kv[l], x, l == 0 ? &embed.desc : nullptr, params,
+                           reinterpret_cast<const float *>(params + 16), params + 1, qbuf, mbuf, grid_in, threads_in,
+                           stream),
           "decode_in");
     STAGE(ST_ATTENTION,
           launch_attention(dims, kv[l], qbuf, params + 1, 1, 0, partials, counters, abuf, stream, steps, splits),
@@ -675,7 +683,7 @@ void StableModel::drop_graphs() {
 // profiling runs launch the kernels directly so each can be timed.
 int StableModel::decode_step(int token, int pos, bool want_logits) {
   const int vals[2] = {token, pos};
-  if (int rc = upload_params(vals, 2, nullptr, 0)) return rc;
+  if (int rc = upload_params(vals, 2, nullptr, 0, rope_host.data() + (size_t)pos * dims.rot, dims.rot)) return rc;
   if (pgrid > 0 && use_persistent) {
     PersistentDecode args = persistent_args(want_logits);
     if (prof.on) {
@@ -973,6 +981,21 @@ int tinyoai_stablelm_set_persistent(tinyoai_model *m, int32_t enable) {
   if (!m || !m->stable) return fail(TINYOAI_EINVAL, "not a StableLM handle");
   m->stable->use_persistent = enable != 0;
   return m->stable->pgrid > 0 ? 1 : 0;
+}
+
+int tinyoai_stablelm_set_launch(tinyoai_model *m, int32_t stage, int32_t grid, int32_t threads) {
+  if (!m || !m->stable) return fail(TINYOAI_EINVAL, "not a StableLM handle");
+  if (grid <= 0 || grid > (1 << 20) || (threads != 256 && threads != 512))
+    return fail(TINYOAI_EINVAL, "launch shape %d x %d", grid, threads);
+  StableModel &s = *m->stable;
+  switch (stage) {
+    case 0: s.grid_in = grid; s.threads_in = threads; break;
+    case 1: s.grid_out = grid; s.threads_out = threads; break;
+    case 2: s.grid_head = grid; s.threads_head = threads; break;
+    default: return fail(TINYOAI_EINVAL, "launch stage %d", stage);
+  }
+  s.drop_graphs();
+  return TINYOAI_OK;
 }
 
 int tinyoai_stablelm_profile(tinyoai_model *m, int32_t enable) {

@@ -1,149 +1,18 @@
-// Decode-path kernels (one token through a StableLM layer) for gfx950.
+// Decode-path attention and embedding kernels for gfx950, and the format
+// dispatch of the streaming matrix-vector kernels (matvec.h).
 //
 // StableLM's parallel residual (stablelm.go:365-377) lets a layer run as
 // three launches over the fused matrices of LayerDev (kernels.h):
-//   decode_in   LayerNorm(x) once per block into LDS, then every row of win
-//               (q, k, v, gate, up) in one pass over HBM, with RoPE, the KV
-//               append and SiLU-gate applied in the epilogue; layer 0 also
-//               gathers the token's embedding row here;
-//   attention   split-K flash decode; blocks of a head combine through the
-//               last-arriving block;
-//   decode_out  x = (x + o*a) + down*m, one wout row [o | down] per unit.
-// decode_in hands out win rows in pairs (2u, 2u + 1): a rotary pair, two
-// adjacent non-rotary dims, or gate row i with up row i. Each wave streams
-// its units with the next batch of weight loads in flight (stream_units,
-// formats.h).
+// decode_in (matvec.h), attention (here: split-K flash decode; blocks of a
+// head combine through the last-arriving block) and decode_out (matvec.h).
 #include <algorithm>
 
-#include "epilogue.h"
+#include "matvec.h"
 
 namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
-
-struct InArgs {
-  LayerDev w;
-  StableDims s;
-  KVDev kv;
-  float *x;             // residual [d]; written here when emb is set
-  MatDesc emb;          // embedding table (layer 0, when use_emb)
-  int use_emb;
-  const int *token;     // token id (layer 0)
-  const float *rope;
-  const int *pos;
-  float *q_out, *m_out;
-};
-
-template <int F, int U, int T>
-__global__ __launch_bounds__(T) void decode_in_kernel(InArgs a) {
-  extern __shared__ __align__(16) float lds[];
-  constexpr int VPC = Fmt<F>::VPC;
-  const MatDesc &W = a.w.win;
-  const int nch = W.chunks;
-  const StableDims &s = a.s;
-  float4 *xq = reinterpret_cast<float4 *>(lds + ((s.d + 3) & ~3));
-  double *red = reinterpret_cast<double *>(xq + (VPC / 4) * nch);
-  float *rope_row = reinterpret_cast<float *>(red + 16);  // cos/sin at pos, [rot/2][2]
-  const int pos = *a.pos;
-  const int lane = threadIdx.x & 63;
-
-  auto prologue = [&]() {
-    if (a.use_emb) {  // embedding row (stablelm.go:338), bit-exact readValues
-      const MatDesc &e = a.emb;
-      const int64_t row = *a.token;
-      for (int i = threadIdx.x; i < s.d; i += T) {
-        const float v = mat_value(e, row, i);
-        lds[i] = v;
-        if (blockIdx.x == 0) a.x[i] = v;
-      }
-    } else {
-      for (int i = threadIdx.x; i < s.d; i += T) lds[i] = a.x[i];
-    }
-    __syncthreads();
-    norm_lds(s, lds, a.w.ln_w, a.w.ln_b, red);
-    stage_x(xq, lds, s.d, nch, VPC);
-    for (int i = threadIdx.x; i < s.rot; i += T) rope_row[i] = a.rope[(int64_t)pos * s.rot + i];
-    __syncthreads();
-  };
-  auto unit = [&](int u, Seg2 &g) { g = Seg2{row_ptr(W, 2 * (int64_t)u), row_ptr(W, 2 * (int64_t)u + 1), xq, xq, nch, nch}; };
-  auto done = [&](int u, float v0, float v1) {
-    if (lane == 0) in_pair_epilogue(s, a.kv, rope_row, pos, u, v0, v1, a.q_out, a.m_out);
-  };
-  stream_units<F, U>(blockIdx.x * (T / 64) + (threadIdx.x >> 6), gridDim.x * (T / 64), W.rows / 2, prologue, unit,
-                     done);
-}
-
-struct OutArgs {
-  MatDesc w;
-  int ka, km;  // values of the o and down parts of a wout row
-  int na, nm;  // their chunks
-  const float *a, *m;
-  float *x;
-};
-
-template <int F, int U, int T>
-__global__ __launch_bounds__(T) void decode_out_kernel(OutArgs p) {
-  extern __shared__ __align__(16) float4 xq_lds[];
-  constexpr int VPC = Fmt<F>::VPC;
-  const MatDesc &W = p.w;
-  float4 *xa = xq_lds, *xm = xq_lds + (VPC / 4) * p.na;
-  const int lane = threadIdx.x & 63;
-  auto prologue = [&]() {
-    stage_x(xa, p.a, p.ka, p.na, VPC);
-    if (p.nm) stage_x(xm, p.m, p.km, p.nm, VPC);
-    __syncthreads();
-  };
-  auto unit = [&](int r, Seg2 &g) { g = Seg2{row_ptr(W, r), row_ptr(W, r, p.na), xa, xm, p.na, p.nm}; };
-  auto done = [&](int r, float ao, float ad) {
-    if (lane == 0) p.x[r] = __fadd_rn(__fadd_rn(p.x[r], ao), ad);
-  };
-  stream_units<F, U>(blockIdx.x * (T / 64) + (threadIdx.x >> 6), gridDim.x * (T / 64), p.w.rows, prologue, unit,
-                     done);
-}
-
-struct LnMvArgs {
-  MatDesc w;
-  const float *ln_w, *ln_b;
-  double eps;
-  int norm;
-  const float *x;
-  float *out;
-  int xlen;
-};
-
-template <int F, int U, int T>
-__global__ __launch_bounds__(T) void ln_matvec_kernel(LnMvArgs a) {
-  extern __shared__ __align__(16) float lds[];
-  constexpr int VPC = Fmt<F>::VPC;
-  const int cols = a.w.cols;
-  const int lane = threadIdx.x & 63;
-  const MatDesc &M = a.w;
-  float4 *xq = reinterpret_cast<float4 *>(lds + ((cols + 3) & ~3));
-  double *red = reinterpret_cast<double *>(xq + (VPC / 4) * M.chunks);
-  auto prologue = [&]() {
-    for (int i = threadIdx.x; i < cols; i += T) lds[i] = a.x[i];
-    __syncthreads();
-    if (a.ln_w) {
-      if (a.norm) rms_norm_lds(lds, cols, a.ln_w, (float)a.eps, red);
-      else layer_norm_lds(lds, cols, a.ln_w, a.ln_b, a.eps, red);
-    }
-    stage_x(xq, lds, cols, M.chunks, VPC);
-    __syncthreads();
-  };
-  auto unit = [&](int u, Seg2 &g) {
-    const int64_t r0 = 2 * (int64_t)u, r1 = r0 + 1;
-    const bool two = r1 < M.rows;
-    g = Seg2{row_ptr(M, r0), row_ptr(M, two ? r1 : r0), xq, xq, M.chunks, two ? M.chunks : 0};
-  };
-  auto done = [&](int u, float v0, float v1) {
-    if (lane != 0) return;
-    a.out[2 * (int64_t)u] = v0;
-    if (2 * u + 1 < M.rows) a.out[2 * (int64_t)u + 1] = v1;
-  };
-  stream_units<F, U>(blockIdx.x * (T / 64) + (threadIdx.x >> 6), gridDim.x * (T / 64), (M.rows + 1) / 2, prologue,
-                     unit, done);
-}
 
 __global__ void embed_kernel(MatDesc emb, const int *ids, float *x) {
   const int j = blockIdx.x;
@@ -348,101 +217,15 @@ hipError_t launch_attention_kv(const AttArgs &a, int nq, int splits, int steps, 
                    : launch_attention_hd<HD, false>(a, nq, splits, steps, st);
 }
 
-int round_up(int v, int m) { return (v + m - 1) / m * m; }
-
-// Batch width U (chunks per lane per batch): the smallest instantiated
-// value that covers a whole unit, else 8 with several batches per unit.
-int pick_u(int chunks_per_unit) {
-  static const int us[] = {1, 2, 4, 5, 8, 10};
-  for (int u : us)
-    if (64 * u >= chunks_per_unit) return u;
-  return 8;
-}
-
-#define TINYOAI_DISPATCH_U(U, LAUNCH) \
-  switch (U) {                        \
-    case 1: LAUNCH(1); break;         \
-    case 2: LAUNCH(2); break;         \
-    case 4: LAUNCH(4); break;         \
-    case 5: LAUNCH(5); break;         \
-    case 8: LAUNCH(8); break;         \
-    case 10: LAUNCH(10); break;       \
-  }
-
-#define TINYOAI_DISPATCH_T(T, LAUNCH)                   \
-  switch (T) {                                          \
-    case 256: TINYOAI_DISPATCH_U(U, LAUNCH##256) break; \
-    case 512: TINYOAI_DISPATCH_U(U, LAUNCH##512) break; \
-    case 640: TINYOAI_DISPATCH_U(U, LAUNCH##640) break; \
-    case 1024: TINYOAI_DISPATCH_U(U, LAUNCH##1024) break; \
-    default: return hipErrorInvalidValue;               \
-  }
-
-template <int F>
-hipError_t ln_matvec_launch(const LnMvArgs &a, int grid, int threads, hipStream_t st) {
-  const size_t lds = (size_t)round_up(a.w.cols, 4) * 4 + (size_t)a.w.chunks * Fmt<F>::VPC * 4 + 16 * sizeof(double);
-  const int U = pick_u(2 * a.w.chunks);
-#define L256(U_) hipLaunchKernelGGL((ln_matvec_kernel<F, U_, 256>), dim3(grid), dim3(256), lds, st, a)
-#define L512(U_) hipLaunchKernelGGL((ln_matvec_kernel<F, U_, 512>), dim3(grid), dim3(512), lds, st, a)
-#define L640(U_) hipLaunchKernelGGL((ln_matvec_kernel<F, U_, 640>), dim3(grid), dim3(640), lds, st, a)
-#define L1024(U_) hipLaunchKernelGGL((ln_matvec_kernel<F, U_, 1024>), dim3(grid), dim3(1024), lds, st, a)
-  TINYOAI_DISPATCH_T(threads, L)
-#undef L256
-#undef L512
-#undef L640
-#undef L1024
-  return hipGetLastError();
-}
-
-template <int F>
-hipError_t decode_in_launch(const InArgs &a, int grid, int threads, hipStream_t st) {
-  const size_t lds = (size_t)round_up(a.s.d, 4) * 4 + (size_t)a.w.win.chunks * Fmt<F>::VPC * 4 +
-                     16 * sizeof(double) + (size_t)a.s.rot * 4;
-  const int U = pick_u(2 * a.w.win.chunks);
-#define L256(U_) hipLaunchKernelGGL((decode_in_kernel<F, U_, 256>), dim3(grid), dim3(256), lds, st, a)
-#define L512(U_) hipLaunchKernelGGL((decode_in_kernel<F, U_, 512>), dim3(grid), dim3(512), lds, st, a)
-#define L640(U_) hipLaunchKernelGGL((decode_in_kernel<F, U_, 640>), dim3(grid), dim3(640), lds, st, a)
-#define L1024(U_) hipLaunchKernelGGL((decode_in_kernel<F, U_, 1024>), dim3(grid), dim3(1024), lds, st, a)
-  TINYOAI_DISPATCH_T(threads, L)
-#undef L256
-#undef L512
-#undef L640
-#undef L1024
-  return hipGetLastError();
-}
-
-template <int F>
-hipError_t decode_out_launch(OutArgs p, int grid, int threads, hipStream_t st) {
-  constexpr int VPC = Fmt<F>::VPC;
-  // The down part starts a new quant block (and super-block).
-  const int align = F == FMT_Q8_0 || F == FMT_Q5_1 ? 32 : (is_kquant(F) ? 256 : 1);
-  if (p.ka % align) return hipErrorInvalidValue;
-  p.na = (p.ka + VPC - 1) / VPC;
-  p.nm = p.w.chunks - p.na;
-  if (p.nm < 0 || (p.km == 0) != (p.nm == 0) || (int64_t)p.nm * VPC < p.km) return hipErrorInvalidValue;
-  const size_t lds = (size_t)p.w.chunks * VPC * 4;
-  const int U = pick_u(p.w.chunks);
-#define L256(U_) hipLaunchKernelGGL((decode_out_kernel<F, U_, 256>), dim3(grid), dim3(256), lds, st, p)
-#define L512(U_) hipLaunchKernelGGL((decode_out_kernel<F, U_, 512>), dim3(grid), dim3(512), lds, st, p)
-#define L640(U_) hipLaunchKernelGGL((decode_out_kernel<F, U_, 640>), dim3(grid), dim3(640), lds, st, p)
-#define L1024(U_) hipLaunchKernelGGL((decode_out_kernel<F, U_, 1024>), dim3(grid), dim3(1024), lds, st, p)
-  TINYOAI_DISPATCH_T(threads, L)
-#undef L256
-#undef L512
-#undef L640
-#undef L1024
-  return hipGetLastError();
-}
-
 }  // namespace
 
 int device_cu_count() {
   static int cus = 0;
   if (!cus) {
     int dev = 0;
-    hipGetDevice(&dev);
-    hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-    if (cus <= 0) cus = 256;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+      cus = 256;
   }
   return cus;
 }
@@ -451,16 +234,16 @@ hipError_t launch_decode_in(const LayerDev &w, const StableDims &s, const KVDev 
                             const int *token, const float *rope, const int *pos, float *q_out, float *m_out, int grid,
                             int threads, hipStream_t st) {
   InArgs a{w, s, kv, x, emb ? *emb : MatDesc{}, emb != nullptr, token, rope, pos, q_out, m_out};
-  if (w.win.rows % 2) return hipErrorInvalidValue;
+  if (w.win.rows % 2 || !planes_fit(w.win)) return hipErrorInvalidValue;
   switch (w.win.fmt) {
-    case FMT_Q8_0: return decode_in_launch<FMT_Q8_0>(a, grid, threads, st);
-    case FMT_BF16: return decode_in_launch<FMT_BF16>(a, grid, threads, st);
-    case FMT_F32: return decode_in_launch<FMT_F32>(a, grid, threads, st);
-    case FMT_F16: return decode_in_launch<FMT_F16>(a, grid, threads, st);
-    case FMT_Q5_1: return decode_in_launch<FMT_Q5_1>(a, grid, threads, st);
-    case FMT_Q4_K: return decode_in_launch<FMT_Q4_K>(a, grid, threads, st);
-    case FMT_Q5_K: return decode_in_launch<FMT_Q5_K>(a, grid, threads, st);
-    case FMT_Q6_K: return decode_in_launch<FMT_Q6_K>(a, grid, threads, st);
+    case FMT_Q8_0: return run_decode_in<FMT_Q8_0>(a, grid, threads, st);
+    case FMT_BF16: return run_decode_in<FMT_BF16>(a, grid, threads, st);
+    case FMT_F32: return run_decode_in<FMT_F32>(a, grid, threads, st);
+    case FMT_F16: return run_decode_in<FMT_F16>(a, grid, threads, st);
+    case FMT_Q5_1: return run_decode_in<FMT_Q5_1>(a, grid, threads, st);
+    case FMT_Q4_K: return run_decode_in<FMT_Q4_K>(a, grid, threads, st);
+    case FMT_Q5_K: return run_decode_in<FMT_Q5_K>(a, grid, threads, st);
+    case FMT_Q6_K: return run_decode_in<FMT_Q6_K>(a, grid, threads, st);
   }
   return hipErrorInvalidValue;
 }
@@ -468,15 +251,16 @@ hipError_t launch_decode_in(const LayerDev &w, const StableDims &s, const KVDev 
 hipError_t launch_decode_out(const MatDesc &wout, int ka, int km, const float *a, const float *m, float *x,
                              int grid, int threads, hipStream_t st) {
   OutArgs p{wout, ka, km, 0, 0, a, m, x};
+  if (!planes_fit(wout)) return hipErrorInvalidValue;
   switch (wout.fmt) {
-    case FMT_Q8_0: return decode_out_launch<FMT_Q8_0>(p, grid, threads, st);
-    case FMT_BF16: return decode_out_launch<FMT_BF16>(p, grid, threads, st);
-    case FMT_F32: return decode_out_launch<FMT_F32>(p, grid, threads, st);
-    case FMT_F16: return decode_out_launch<FMT_F16>(p, grid, threads, st);
-    case FMT_Q5_1: return decode_out_launch<FMT_Q5_1>(p, grid, threads, st);
-    case FMT_Q4_K: return decode_out_launch<FMT_Q4_K>(p, grid, threads, st);
-    case FMT_Q5_K: return decode_out_launch<FMT_Q5_K>(p, grid, threads, st);
-    case FMT_Q6_K: return decode_out_launch<FMT_Q6_K>(p, grid, threads, st);
+    case FMT_Q8_0: return run_decode_out<FMT_Q8_0>(p, grid, threads, st);
+    case FMT_BF16: return run_decode_out<FMT_BF16>(p, grid, threads, st);
+    case FMT_F32: return run_decode_out<FMT_F32>(p, grid, threads, st);
+    case FMT_F16: return run_decode_out<FMT_F16>(p, grid, threads, st);
+    case FMT_Q5_1: return run_decode_out<FMT_Q5_1>(p, grid, threads, st);
+    case FMT_Q4_K: return run_decode_out<FMT_Q4_K>(p, grid, threads, st);
+    case FMT_Q5_K: return run_decode_out<FMT_Q5_K>(p, grid, threads, st);
+    case FMT_Q6_K: return run_decode_out<FMT_Q6_K>(p, grid, threads, st);
   }
   return hipErrorInvalidValue;
 }
@@ -515,15 +299,16 @@ hipError_t launch_attention(const StableDims &s, const KVDev &kv, const float *q
 hipError_t launch_ln_matvec(const MatDesc &w, const float *ln_w, const float *ln_b, double eps, int norm,
                             const float *x, float *out, int grid, int threads, hipStream_t st) {
   LnMvArgs a{w, ln_w, ln_b, eps, norm, x, out, std::max(w.chunks * values_per_chunk(w.fmt), w.cols)};
+  if (!planes_fit(w)) return hipErrorInvalidValue;
   switch (w.fmt) {
-    case FMT_Q8_0: return ln_matvec_launch<FMT_Q8_0>(a, grid, threads, st);
-    case FMT_BF16: return ln_matvec_launch<FMT_BF16>(a, grid, threads, st);
-    case FMT_F32: return ln_matvec_launch<FMT_F32>(a, grid, threads, st);
-    case FMT_F16: return ln_matvec_launch<FMT_F16>(a, grid, threads, st);
-    case FMT_Q5_1: return ln_matvec_launch<FMT_Q5_1>(a, grid, threads, st);
-    case FMT_Q4_K: return ln_matvec_launch<FMT_Q4_K>(a, grid, threads, st);
-    case FMT_Q5_K: return ln_matvec_launch<FMT_Q5_K>(a, grid, threads, st);
-    case FMT_Q6_K: return ln_matvec_launch<FMT_Q6_K>(a, grid, threads, st);
+    case FMT_Q8_0: return run_ln_matvec<FMT_Q8_0>(a, grid, threads, st);
+    case FMT_BF16: return run_ln_matvec<FMT_BF16>(a, grid, threads, st);
+    case FMT_F32: return run_ln_matvec<FMT_F32>(a, grid, threads, st);
+    case FMT_F16: return run_ln_matvec<FMT_F16>(a, grid, threads, st);
+    case FMT_Q5_1: return run_ln_matvec<FMT_Q5_1>(a, grid, threads, st);
+    case FMT_Q4_K: return run_ln_matvec<FMT_Q4_K>(a, grid, threads, st);
+    case FMT_Q5_K: return run_ln_matvec<FMT_Q5_K>(a, grid, threads, st);
+    case FMT_Q6_K: return run_ln_matvec<FMT_Q6_K>(a, grid, threads, st);
   }
   return hipErrorInvalidValue;
 }

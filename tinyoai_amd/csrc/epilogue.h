@@ -15,16 +15,6 @@ __device__ __forceinline__ void put(V *p, V v) {
     *p = v;
 }
 
-// storeKV (kv_cache.go:55-65): fp32 copy, or floatHalf rounding.
-template <bool COH = false>
-__device__ __forceinline__ void kv_put(const KVDev &kv, bool key, int64_t idx, float v) {
-  void *base = key ? kv.k : kv.v;
-  if (kv.half)
-    put<COH>(reinterpret_cast<uint16_t *>(base) + idx, float_to_half(v));
-  else
-    put<COH>(reinterpret_cast<float *>(base) + idx, v);
-}
-
 // The layer's input normalisation of an LDS-resident row (all threads).
 __device__ __forceinline__ void norm_lds(const StableDims &s, float *x, const float *w, const float *b,
                                          double *red) {
@@ -33,14 +23,16 @@ __device__ __forceinline__ void norm_lds(const StableDims &s, float *x, const fl
 }
 
 // Row pair (2u, 2u + 1) of win with dot products v0, v1 for one token at
-// absolute position pos. rope_row holds cos/sin of pos as [rot/2][2].
-template <bool COH = false>
-__device__ __forceinline__ void in_pair_epilogue(const StableDims &s, const KVDev &kv, const float *rope_row, int pos,
-                                                 int u, float v0, float v1, float *q_out, float *m_out) {
+// absolute position pos. rope_row holds cos/sin of pos as [rot/2][2]. The
+// outputs go through `out`: out.f32(float *, float) and, for an fp16 KV
+// cache, out.f16(uint16_t *, uint16_t).
+template <typename Out>
+__device__ __forceinline__ void in_pair_outputs(const StableDims &s, const KVDev &kv, const float *rope_row, int pos,
+                                                int u, float v0, float v1, float *q_out, float *m_out, Out &&out) {
   const int row = 2 * u, kvw = s.win_kv, rh = s.rot / 2;
   if (row >= s.win_q + 2 * kvw) {
     const int i = (row - s.win_q - 2 * kvw) >> 1;
-    put<COH>(m_out + i, s.silu ? silu_gate_llama(v0, v1) : silu_gate(v0, v1));
+    out.f32(m_out + i, s.silu ? silu_gate_llama(v0, v1) : silu_gate(v0, v1));
     return;
   }
   int sec, r;  // 0 q, 1 k, 2 v
@@ -62,13 +54,33 @@ __device__ __forceinline__ void in_pair_epilogue(const StableDims &s, const KVDe
     v1 = x1;
   }
   if (sec == 0) {
-    put<COH>(q_out + head * s.hd + d0, v0);
-    put<COH>(q_out + head * s.hd + d1, v1);
-  } else {  // head-major [kv_head][cap][hd] at the token's position
+    out.f32(q_out + head * s.hd + d0, v0);
+    out.f32(q_out + head * s.hd + d1, v1);
+  } else {  // head-major [kv_head][cap][hd] at the token's position (storeKV, kv_cache.go:55-65)
     const int64_t base = ((int64_t)head * kv.cap + pos) * s.hd;
-    kv_put<COH>(kv, sec == 1, base + d0, v0);
-    kv_put<COH>(kv, sec == 1, base + d1, v1);
+    void *dst = sec == 1 ? kv.k : kv.v;
+    if (kv.half) {
+      out.f16(reinterpret_cast<uint16_t *>(dst) + base + d0, float_to_half(v0));
+      out.f16(reinterpret_cast<uint16_t *>(dst) + base + d1, float_to_half(v1));
+    } else {
+      out.f32(reinterpret_cast<float *>(dst) + base + d0, v0);
+      out.f32(reinterpret_cast<float *>(dst) + base + d1, v1);
+    }
   }
+}
+
+// The same outputs stored directly (plain, or with COH agent-scope atomic
+// stores).
+template <bool COH>
+struct DirectStores {
+  __device__ void f32(float *p, float v) const { put<COH>(p, v); }
+  __device__ void f16(uint16_t *p, uint16_t v) const { put<COH>(p, v); }
+};
+
+template <bool COH = false>
+__device__ __forceinline__ void in_pair_epilogue(const StableDims &s, const KVDev &kv, const float *rope_row, int pos,
+                                                 int u, float v0, float v1, float *q_out, float *m_out) {
+  in_pair_outputs(s, kv, rope_row, pos, u, v0, v1, q_out, m_out, DirectStores<COH>{});
 }
 
 // Loads N consecutive KV values starting at element e into float registers.

@@ -97,23 +97,34 @@ __device__ __forceinline__ float hw_half(uint16_t h) {
 // x[c*VPC + 4q .. 4q + 3] sits at xq[q * nch + c]. Lanes reading chunks
 // c, c+1, ... then touch consecutive 16-byte words (conflict-free), where a
 // plain layout would put them VPC*4 bytes apart.
-// x may live in global memory or LDS.
+// x may live in global memory or LDS. Each thread loads four float4 before
+// it stores any, so a block stages up to 4 * blockDim float4 in one memory
+// round trip (a store to LDS could alias x, so the compiler would not
+// overlap the iterations of a plain loop).
 __device__ __forceinline__ void stage_x(float4 *xq, const float *x, int len, int nch, int vpc) {
-  const int quads = vpc / 4;
+  const int quads = vpc / 4, n = quads * nch;
   const bool aligned = (reinterpret_cast<uintptr_t>(x) & 15) == 0;
-  for (int i = threadIdx.x; i < quads * nch; i += blockDim.x) {
-    const int q = i / nch, c = i % nch;
-    const int k = c * vpc + 4 * q;
-    float4 v;
-    if (aligned && k + 3 < len) {
-      v = *reinterpret_cast<const float4 *>(x + k);
-    } else {
-      v.x = k < len ? x[k] : 0.f;
-      v.y = k + 1 < len ? x[k + 1] : 0.f;
-      v.z = k + 2 < len ? x[k + 2] : 0.f;
-      v.w = k + 3 < len ? x[k + 3] : 0.f;
+  for (int i0 = threadIdx.x; i0 < n; i0 += 4 * blockDim.x) {
+    float4 v[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int i = i0 + j * blockDim.x;
+      const int q = i / nch, c = i % nch;
+      const int k = c * vpc + 4 * q;
+      if (i >= n) {
+        v[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+      } else if (aligned && k + 3 < len) {
+        v[j] = *reinterpret_cast<const float4 *>(x + k);
+      } else {
+        v[j].x = k < len ? x[k] : 0.f;
+        v[j].y = k + 1 < len ? x[k + 1] : 0.f;
+        v[j].z = k + 2 < len ? x[k + 2] : 0.f;
+        v[j].w = k + 3 < len ? x[k + 3] : 0.f;
+      }
     }
-    xq[i] = v;
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+      if (i0 + j * blockDim.x < n) xq[i0 + j * blockDim.x] = v[j];
   }
 }
 
@@ -277,7 +288,10 @@ __device__ __forceinline__ uint4 load_chunk(const uint8_t *p) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
-__device__ __forceinline__ uint16_t load_scale(const uint8_t *meta, int block) {
+// A 16-bit block scale, zero-extended into a 32-bit register (kept 32-bit
+// in a batch: 16-bit batch fields were copied between the two batch
+// buffers at the loop's back edge, each copy waiting for its load).
+__device__ __forceinline__ uint32_t load_scale(const uint8_t *meta, int block) {
   return ((const TINYOAI_GLOBAL uint16_t *)meta)[block];
 }
 
@@ -322,7 +336,7 @@ struct Seg2 {
 template <int U>
 struct Batch {
   uint4 w[U];
-  uint16_t s[U];  // Q8_0 block scale, Q6_K d
+  uint32_t s[U];  // Q8_0 block scale, Q6_K d (zero-extended fp16 bits)
   uint2 h[U];     // high bits (Q5_1, Q5_K, Q6_K)
   uint4 mt[U];    // block header (Q5_1, Q4_K, Q5_K, Q6_K scales)
 };
@@ -355,6 +369,37 @@ __device__ __forceinline__ void batch_issue(Batch<U> &b, const Seg2 &g, int base
   }
 }
 
+// Buffer descriptors of a matrix's planes (gfx9 raw buffers: base, no
+// stride, a byte count). The streaming kernels address a plane with 32-bit
+// per-lane offsets; a load at an offset past the count returns zeros
+// without a memory request (a lane without a chunk loads at kOffNone).
+struct Planes {
+  __amdgpu_buffer_rsrc_t v, m, h;
+  const uint8_t *vb, *mb, *hb;
+};
+
+// Every plane below 2^31 bytes: offsets fit a signed 32-bit register and
+// 2^31 lies past every plane.
+__host__ __device__ inline bool planes_fit(const MatDesc &M) {
+  return (int64_t)M.rows * M.vstride < 0x80000000ll && (int64_t)M.rows * M.mstride < 0x80000000ll &&
+         (int64_t)M.rows * M.hstride < 0x80000000ll;
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t plane_rsrc(const uint8_t *p, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(p), (short)0, (int)(uint32_t)bytes, 0x00020000);
+}
+
+__device__ __forceinline__ Planes make_planes(const MatDesc &M) {
+  Planes P;
+  P.v = plane_rsrc(M.vals, (int64_t)M.rows * M.vstride);
+  P.m = plane_rsrc(M.meta, (int64_t)M.rows * M.mstride);
+  P.h = plane_rsrc(M.hbits, (int64_t)M.rows * M.hstride);
+  P.vb = M.vals;
+  P.mb = M.meta;
+  P.hb = M.hbits;
+  return P;
+}
+
 // Consumes the chunks base + u * 64 + lane of a batch into acc0 (segment 0)
 // and acc1 (segment 1). Branch-free: a lane past the end computes on its
 // clamped (valid) chunk and contributes 0, so no per-chunk exec-mask
@@ -374,10 +419,10 @@ __device__ __forceinline__ void batch_consume_range(const Batch<U> &b, const Seg
     const int cc = seg1 ? cl - g.n0 : cl;
     float p;
     if constexpr (Fmt<F>::VPC == 32) {
-      p = kchunk_dot<F>(b.w[u], b.h[u], b.mt[u], b.s[u], cc, seg1 ? g.x1 : g.x0, seg1 ? g.n1 : g.n0, cc);
+      p = kchunk_dot<F>(b.w[u], b.h[u], b.mt[u], (uint16_t)b.s[u], cc, seg1 ? g.x1 : g.x0, seg1 ? g.n1 : g.n0, cc);
     } else {
       p = chunk_dot<F>(b.w[u], seg1 ? g.x1 : g.x0, seg1 ? g.n1 : g.n0, cc);
-      if constexpr (F == FMT_Q8_0) p *= hw_half(b.s[u]);
+      if constexpr (F == FMT_Q8_0) p *= hw_half((uint16_t)b.s[u]);
     }
     p = (c >= lo && c < hi) ? p : 0.f;
     acc0 += seg1 ? 0.f : p;
@@ -390,51 +435,6 @@ template <int F, int U, bool SERIAL = false>
 __device__ __forceinline__ void batch_consume(const Batch<U> &b, const Seg2 &g, int base, int lane, float &acc0,
                                               float &acc1) {
   batch_consume_range<F, U, SERIAL>(b, g, base, lane, 0, g.n0 + g.n1, acc0, acc1);
-}
-
-// Runs units first, first + stride, ... (< n_units) through one wave, each
-// as batches of 64 * U chunks (one batch when U covers the unit). Two
-// batches are in flight: the next batch (of this unit or the next one) is
-// issued before the current one is consumed, and the first before
-// `prologue()` (the block's LDS staging, which the weights do not depend
-// on). `unit(u, g)` describes unit u; `done(u, r0, r1)` receives the two
-// wave-reduced dot products (every lane calls it).
-template <int F, int U, typename Prologue, typename UnitFn, typename Done>
-__device__ __forceinline__ void stream_units(int first, int stride, int n_units, Prologue prologue, UnitFn unit,
-                                             Done done) {
-  const int lane = threadIdx.x & 63;
-  Seg2 g{}, gn{};
-  Batch<U> b, bn;
-  int u = first, base = 0;
-  if (u < n_units) {
-    unit(u, g);
-    batch_issue<F, U>(b, g, 0, lane);
-  }
-  prologue();
-  float acc0 = 0.f, acc1 = 0.f;
-  while (u < n_units) {
-    int nu = u, nbase = base + 64 * U;
-    if (nbase >= g.n0 + g.n1) {
-      nu = u + stride;
-      nbase = 0;
-    }
-    const bool more = nu < n_units;
-    if (more) {
-      if (nu != u) unit(nu, gn);
-      else gn = g;
-      batch_issue<F, U>(bn, gn, nbase, lane);
-    }
-    batch_consume<F, U>(b, g, base, lane, acc0, acc1);
-    if (nu != u) {
-      done(u, wave_sum(acc0), wave_sum(acc1));
-      acc0 = acc1 = 0.f;
-    }
-    if (!more) break;
-    b = bn;
-    g = gn;
-    u = nu;
-    base = nbase;
-  }
 }
 
 // Value (row, col) of a 5/6-bit matrix, bit-exact with decodeKBlock.

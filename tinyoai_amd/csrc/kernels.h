@@ -50,13 +50,15 @@ struct RowMap {
 };
 
 // ---- decode (one token) ----
-// Matvec launches take their grid and block size (256, 512, 640 or 1024
-// threads) from the caller; blocks loop over their share of the rows.
+// Matvec launches take their grid and block size (256 or 512 threads) from
+// the caller; blocks stream their share of the rows.
 //
 // LayerNorm(x) -> win rows with RoPE, KV append and SiLU-gate fused into
-// the epilogue. pos (and token) are read from device memory. With `emb` (a
-// host-side descriptor, copied), x is first set to the embedding row of
-// *token (layer 0).
+// the epilogue. pos (and token) are read from device memory; `rope` is the
+// token's row of the rotary table (rot floats: cos, sin per pair), so no
+// load waits for pos before the weights stream. With `emb` (a host-side
+// descriptor, copied), x is first set to the embedding row of *token
+// (layer 0).
 hipError_t launch_decode_in(const LayerDev &w, const StableDims &s, const KVDev &kv, float *x, const MatDesc *emb,
                             const int *token, const float *rope, const int *pos, float *q_out, float *m_out,
                             int grid, int threads, hipStream_t st);

@@ -121,7 +121,8 @@ int LlamaModel::init(const tinyoai_llama_config &c, const float *w, uint64_t n_f
     mlp_layers[l] = LayerDev{m[2].desc, m[3].desc, rms_ffn_dev + l * dim, nullptr};
   }
   // Rotation table [pos][hs/2][cos, sin] from the checkpoint's tables.
-  std::vector<float> rt((size_t)seq * hs);
+  std::vector<float> &rt = rope_host;
+  rt.assign((size_t)seq * hs, 0.f);
   for (int64_t t = 0; t < seq; t++)
     for (int i = 0; i < hs / 2; i++) {
       rt[(size_t)t * hs + 2 * i] = fcr[t * (hs / 2) + i];
@@ -176,14 +177,15 @@ int LlamaModel::ensure_logits(int rows) {
 // `logits` (device, null: none).
 int LlamaModel::enqueue_step(int steps, int splits, float *logits) {
   const int *pos = params + 1;
+  const float *rope_row = reinterpret_cast<const float *>(params + 16);
   for (int l = 0; l < cfg.n_layers; l++) {
-    TRY_HIP(launch_decode_in(att_layers[l], att, kv[l], x, l == 0 ? &embed.desc : nullptr, params, rope, pos, qbuf,
+    TRY_HIP(launch_decode_in(att_layers[l], att, kv[l], x, l == 0 ? &embed.desc : nullptr, params, rope_row, pos, qbuf,
                              hbuf, grid_in, 256, stream),
             "attention projections");
     TRY_HIP(launch_attention(att, kv[l], qbuf, pos, 1, 0, partials, counters, abuf, stream, steps, splits),
             "attention");
     TRY_HIP(launch_decode_out(att_layers[l].wout, cfg.dim, 0, abuf, nullptr, x, grid_out, 256, stream), "wo");
-    TRY_HIP(launch_decode_in(mlp_layers[l], mlp, kv[l], x, nullptr, params, rope, pos, qbuf, hbuf, grid_mlp, 256,
+    TRY_HIP(launch_decode_in(mlp_layers[l], mlp, kv[l], x, nullptr, params, rope_row, pos, qbuf, hbuf, grid_mlp, 256,
                              stream),
             "w1/w3");
     TRY_HIP(launch_decode_out(mlp_layers[l].wout, cfg.hidden_dim, 0, hbuf, nullptr, x, grid_out, 256, stream), "w2");
@@ -201,7 +203,8 @@ int LlamaModel::step(int token, int pos, float *logits) {
   TRY_HIP(hipEventSynchronize(params_copied), "parameter slot");
   hp[0] = token;
   hp[1] = pos;
-  TRY_HIP(hipMemcpyAsync(params, hp, 8, hipMemcpyHostToDevice, stream), "parameters");
+  memcpy(hp + 16, rope_host.data() + (size_t)pos * att.rot, (size_t)att.rot * 4);  // the token's rotary row
+  TRY_HIP(hipMemcpyAsync(params, hp, (size_t)(16 + att.rot) * 4, hipMemcpyHostToDevice, stream), "parameters");
   TRY_HIP(hipEventRecord(params_copied, stream), "parameter event");
   const int steps = attention_steps(pos, att.heads), splits = attention_splits(pos, steps);
   const int64_t key = ((int64_t)steps << 40) | ((int64_t)splits << 8) | (logits ? 1 : 0);

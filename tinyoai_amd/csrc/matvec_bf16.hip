@@ -1,0 +1,4 @@
+// Decode matrix-vector kernels for BF16 weights (matvec.h).
+#include "matvec.h"
+
+TINYOAI_MATVEC_DEFINE(FMT_BF16)

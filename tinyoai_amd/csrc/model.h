@@ -76,6 +76,7 @@ struct StableModel {
   std::vector<LayerDev> layers;
   const float *norm_w = nullptr, *norm_b = nullptr;
   float *rope = nullptr;
+  std::vector<float> rope_host;  // [pos][rot]: a decode token's row travels with its parameters
 
   // KV: one [kv_heads][cap][hd] K and V buffer per layer.
   std::vector<KVDev> kv;
@@ -130,7 +131,8 @@ struct StableModel {
   int alloc(void **p, size_t bytes);
   void free_kv();
   int ensure_kv(int needed);
-  int upload_params(const int *head_vals, int nh, const int32_t *ids, int n);
+  int upload_params(const int *head_vals, int nh, const int32_t *ids, int n, const float *row = nullptr,
+                    int nrow = 0);
   int enqueue_decode(int steps, int splits, bool want_logits);
   void drop_graphs();
   int decode_step(int token, int pos, bool want_logits);
@@ -152,6 +154,7 @@ struct LlamaModel {
   std::vector<DevMatrix> mats;  // per layer: win (q|k|v), wo, w1/w3 interleaved, w2
   std::vector<LayerDev> att_layers, mlp_layers;
   float *rms_final = nullptr, *rope = nullptr;
+  std::vector<float> rope_host;  // [pos][hs]
   std::vector<KVDev> kv;    // [kv_heads][seq_len][head] per layer
   int offset = 0;
   float *x = nullptr, *qbuf = nullptr, *abuf = nullptr, *hbuf = nullptr, *partials = nullptr;

@@ -20,6 +20,7 @@ EXPORTS = [
     "tinyoai_stablelm_limit_cache", "tinyoai_stablelm_reset", "tinyoai_stablelm_offset", "tinyoai_stablelm_close",
     "tinyoai_stablelm_read_kv", "tinyoai_stablelm_trace", "tinyoai_stablelm_trace_read",
     "tinyoai_stablelm_trace_read_stages", "tinyoai_stablelm_decode_timeline", "tinyoai_stablelm_set_persistent",
+    "tinyoai_stablelm_set_launch",
     "tinyoai_stablelm_profile", "tinyoai_stablelm_profile_read", "tinyoai_llama_load",
     "tinyoai_llama_forward", "tinyoai_llama_reset", "tinyoai_llama_close", "tinyoai_weight_upload",
     "tinyoai_weight_read_values", "tinyoai_weight_mul", "tinyoai_weight_mul_device", "tinyoai_weight_free",
@@ -74,6 +75,7 @@ def lib():
         L.tinyoai_stablelm_decode_timeline.argtypes = [P, C.POINTER(C.c_uint64), C.c_int64]
         L.tinyoai_stablelm_decode_timeline.restype = C.c_int64
         L.tinyoai_stablelm_set_persistent.argtypes = [P, C.c_int32]
+        L.tinyoai_stablelm_set_launch.argtypes = [P, C.c_int32, C.c_int32, C.c_int32]
         L.tinyoai_stablelm_profile.argtypes = [P, C.c_int32]
         L.tinyoai_stablelm_profile_read.argtypes = [P, C.POINTER(C.c_double), C.POINTER(C.c_int64), C.c_int32]
         L.tinyoai_llama_load.argtypes = [C.POINTER(LlamaConfig), fp, C.c_uint64, C.POINTER(P)]
@@ -226,9 +228,16 @@ class StableLMForwarder:
               "prefill_projections", "prefill_epilogue", "prefill_attention", "prefill_elementwise")
 
     def set_persistent(self, enable: bool) -> bool:
-        """Selects the single-launch decode path (default) or three kernels
-        per layer; returns whether the single-launch path is available."""
+        """Selects the single-launch decode path or three kernels per layer
+        (the default); returns whether the single-launch path is available."""
         return bool(check(lib().tinyoai_stablelm_set_persistent(self.h, int(enable))))
+
+    LAUNCH_STAGES = {"decode_in": 0, "decode_out": 1, "lm_head": 2}
+
+    def set_launch(self, stage: str, grid: int, threads: int) -> None:
+        """Launch shape (blocks, threads per block) of a decode matrix
+        kernel; results do not depend on it."""
+        check(lib().tinyoai_stablelm_set_launch(self.h, self.LAUNCH_STAGES[stage], int(grid), int(threads)))
 
     def decode_timeline(self) -> np.ndarray:
         """Phase timeline of the last profiled single-launch decode step:
