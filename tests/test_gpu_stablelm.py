@@ -214,6 +214,31 @@ def test_persistent_decode_matches_per_kernel_path(hip, dtype, kv_bits):
     ref.close()
 
 
+def test_f32_weights_against_oracle(hip, oracle):
+    """F32 weights at the 3B layer shapes (a wout row spans 8 column slices
+    of five chunks per lane: 512-thread blocks). Prefill and 12 decode
+    logits against the oracle within 1e-3 of their range, identical greedy
+    ids."""
+    config = W.validate_stablelm_config(dict(W.STABLELM_3B, num_hidden_layers=2, vocab_size=4096,
+                                             max_position_embeddings=256))
+    tensors = W.synthetic_stablelm(config, W.F32, seed=17)
+    rng = np.random.default_rng(9)
+    prompt = rng.integers(0, 4096, 30).astype(np.int32)
+    oracle.set_threads(8)
+    ref = oracle.StableLM(config, tensors, capacity=256)
+    f = hip.StableLMForwarder(config, tensors)
+    want = ref.prefill(prompt, 0)
+    got = f.forward(0, prompt)
+    assert np.max(np.abs(got - want)) <= 1e-3 * float(np.ptp(want))
+    for step in range(12):
+        tr, tg = int(np.argmax(want)), int(np.argmax(got))
+        assert tr == tg, step
+        want = ref.forward(tr, 30 + step)
+        got = f.forward(30 + step, [tg])
+        assert np.max(np.abs(got - want)) <= 1e-3 * float(np.ptp(want)), step
+    f.close()
+
+
 @pytest.mark.parametrize("dtype", [W.Q4_K, W.Q6_K])
 def test_kquant_layers_against_oracle(hip, oracle, dtype):
     """StableLM-3B layer shapes (two layers) with every matrix in one 5/6-bit

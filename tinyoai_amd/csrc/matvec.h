@@ -71,12 +71,12 @@ TINYOAI_MATVEC_DECLARE(FMT_Q6_K)
 namespace tinyoai_matvec {
 
 // Chunks per lane of a wave's column slice: a lane keeps CPL * VPC x
-// values in registers (48 for Q8_0, 40 for BF16 / F16, 16 for F32, 64 for
+// values in registers (48 for Q8_0, 40 for BF16 / F16, 20 for F32, 64 for
 // the 32-value chunks), so the 3B rows (2560 columns) fit one slice except
-// in F32.
+// in F32 (two), and a 3B wout row (2560 + 6912 columns) at most eight.
 template <int F>
 constexpr int cpl_for() {
-  return F == FMT_Q8_0 ? 3 : (F == FMT_BF16 || F == FMT_F16) ? 5 : F == FMT_F32 ? 4 : 2;
+  return F == FMT_Q8_0 ? 3 : (F == FMT_BF16 || F == FMT_F16 || F == FMT_F32) ? 5 : 2;
 }
 
 __host__ __device__ inline int round_up(int v, int m) { return (v + m - 1) / m * m; }

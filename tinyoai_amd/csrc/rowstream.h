@@ -91,6 +91,15 @@ struct RowBatch {
   uint4 mt[R][CPL];    // block header (Q5_1, Q4_K, Q5_K, Q6_K)
 };
 
+// Calls f(integral_constant<n>) for the wave-uniform n in [1, N].
+template <int N, typename Fn>
+__device__ __forceinline__ void group_of_size(int n, Fn &&f) {
+  if constexpr (N >= 1) {
+    if (n == N) f(std::integral_constant<int, N>{});
+    else group_of_size<N - 1>(n, f);
+  }
+}
+
 // Issues the loads of rows row[0..R). Row offsets are wave-uniform.
 template <int F, int CPL, int R>
 __device__ __forceinline__ void rows_issue(RowBatch<CPL, R> &b, const LaneChunks<CPL> &L, const Planes &P,
@@ -362,23 +371,11 @@ __device__ __forceinline__ void stream_rows(const MatDesc &M, int n_units, int s
   };
   using P1 = std::integral_constant<int, PRE>;
   using P0 = std::integral_constant<int, 0>;
-  static_assert(K == 4, "the group dispatch below covers N = 1..4");
   int left = nb;
-  switch (min(left, K)) {  // the first group (PRE batches already issued)
-    case 1: group(std::integral_constant<int, 1>{}, P1{}); break;
-    case 2: group(std::integral_constant<int, 2>{}, P1{}); break;
-    case 3: group(std::integral_constant<int, 3>{}, P1{}); break;
-    case 4: group(std::integral_constant<int, 4>{}, P1{}); break;
-    default: break;
-  }
+  if (left > 0) group_of_size<K>(min(left, K), [&](auto n_tag) { group(n_tag, P1{}); });  // PRE batches issued
   left -= min(left, K);
   while (left > 0) {
-    switch (min(left, K)) {
-      case 1: group(std::integral_constant<int, 1>{}, P0{}); break;
-      case 2: group(std::integral_constant<int, 2>{}, P0{}); break;
-      case 3: group(std::integral_constant<int, 3>{}, P0{}); break;
-      default: group(std::integral_constant<int, 4>{}, P0{}); break;
-    }
+    group_of_size<K>(min(left, K), [&](auto n_tag) { group(n_tag, P0{}); });
     left -= min(left, K);
   }
   if (S == 1) return;
