@@ -458,7 +458,7 @@ int StableModel::init(const tinyoai_stablelm_config &c, const tinyoai_tensor *te
   if ((rc = alloc((void **)&X, B * d * 4)) || (rc = alloc((void **)&H, B * d * 4)) ||
       (rc = alloc((void **)&Y, B * win_rows * 4)) || (rc = alloc((void **)&Q, B * w_att * 4)) ||
       (rc = alloc((void **)&M, B * I * 4)) || (rc = alloc((void **)&A, B * w_att * 4)) ||
-      (rc = alloc((void **)&P, B * d * 4)) || (rc = alloc((void **)&D, B * d * 4)) ||
+      (rc = alloc((void **)&P, kPrefillSplits * B * d * 4)) || (rc = alloc((void **)&D, kPrefillSplits * B * d * 4)) ||
       (rc = alloc((void **)&XH, B * wide * 2)) || (rc = alloc((void **)&XL, B * wide * 2)))
     return rc;
   // Persistent decode state.
@@ -735,11 +735,16 @@ int StableModel::decode_step(int token, int pos, bool want_logits) {
 // (activations split into bf16 hi/lo planes first), else the vector-unit
 // GEMM. Every output row depends only on its own input row, whatever the
 // chunk size (a prefix reused from the cache gives the same results).
-int StableModel::project(const MatDesc &w, const float *x, int ldx, int n, float *y, int ldy) {
+int StableModel::project(const MatDesc &w, const float *x, int ldx, int n, float *y, int ldy, int *splits) {
+  if (splits) *splits = 1;
   if (gemm_mfma_supported(w)) {
     const bool two = gemm_planes(w) == 2;
+    // K-split partial products (summed by the caller) where the output
+    // tiles alone would leave most of the device idle.
+    const int ks = splits ? gemm_splits(w, n, kPrefillSplits) : 1;
+    if (splits) *splits = ks;
     STAGE(ST_PREFILL_GEMM, launch_split_bf16(x, ldx, w.cols, n, XH, two ? XL : nullptr, stream), "bf16 split");
-    STAGE(ST_PREFILL_GEMM, launch_gemm_mfma(w, XH, two ? XL : nullptr, n, y, ldy, stream), "projection");
+    STAGE(ST_PREFILL_GEMM, launch_gemm_mfma(w, XH, two ? XL : nullptr, n, y, ldy, stream, ks), "projection");
   } else {
     if (ldx != w.cols || ldy != w.rows) return fail(TINYOAI_EINVAL, "vector-unit GEMM needs dense operands");
     STAGE(ST_PREFILL_GEMM, launch_gemm(w, x, n, y, stream), "projection");
@@ -771,8 +776,9 @@ int StableModel::prefill_chunk(const int32_t *ids, int n, int start, bool want_l
     else
       STAGE(ST_PREFILL_ATTENTION,
             launch_attention(dims, kv[l], Q, d_pos0, n, start + n - 1, partials, counters, A, stream), "attention");
-    if ((rc = project(wo, A, d, n, P, d)) || (rc = project(wd, M, I, n, D, d))) return rc;
-    STAGE(ST_PREFILL_ELEMENTWISE, launch_residual(X, P, D, (int64_t)n * d, stream), "residual");
+    int sp = 1, sd = 1;
+    if ((rc = project(wo, A, d, n, P, d, &sp)) || (rc = project(wd, M, I, n, D, d, &sd))) return rc;
+    STAGE(ST_PREFILL_ELEMENTWISE, launch_residual(X, P, sp, D, sd, (int64_t)n * d, stream), "residual");
     if (tracing) {
       TRY_HIP(launch_copy_row(X + (size_t)(n - 1) * d, trace_dev + (size_t)l * d, d, stream), "trace");
       TRY_HIP(launch_copy_row(A + (size_t)(n - 1) * d, trace_att + (size_t)l * d, d, stream), "trace");

@@ -12,6 +12,8 @@
 // (4 x 4 tiles of 16 x 16), K step 32, double-buffered LDS. LDS rows are
 // padded to 80 bytes so the 16-byte fragment reads of 16 consecutive rows
 // cover all 64 banks once.
+#include <algorithm>
+
 #include "kernels.h"
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -41,7 +43,14 @@ struct GemmArgs {
   int M;
   float *y;
   int ldy;
+  int ksplit;                 // K ranges summed separately: split s writes y + s * M * ldy
 };
+
+// The K steps of split s of `splits` (nk steps in all): [k_lo, k_hi).
+__device__ __forceinline__ void split_range(int nk, int splits, int s, int &k_lo, int &k_hi) {
+  k_lo = (int)((int64_t)nk * s / splits);
+  k_hi = (int)((int64_t)nk * (s + 1) / splits);
+}
 
 template <int WF, int XS>
 __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
@@ -56,10 +65,14 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
   // one N tile, so a weight tile is fetched from HBM once and re-read from
   // that XCD's L2 by the other M tiles.
   const int MT = (g.M + kBM - 1) / kBM, NT = (N + kBN - 1) / kBN;
-  const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
+  const int per_split = (NT + 7) / 8 * 8 * MT, b = blockIdx.x % per_split, split = blockIdx.x / per_split;
+  const int xcd = b & 7, slot = b >> 3;
   const int nt = xcd + 8 * (slot / MT), mt = slot % MT;
   if (nt >= NT) return;  // the grid rounds NT up to a multiple of 8
   const int m0 = mt * kBM, n0 = nt * kBN;
+  int k_lo, k_hi;
+  split_range(nk, g.ksplit, split, k_lo, k_hi);
+  float *y = g.y + (int64_t)split * g.M * g.ldy;
   const int srow = tid >> 1, shalf = tid & 1;  // staging: one row half (16 K values) per thread
 
   uint4 rah0, rah1, ral0, ral1, rb[2];
@@ -130,13 +143,15 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
   for (int i = 0; i < 4; i++)
 #pragma unroll
     for (int j = 0; j < 4; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-  gload(0);
-  lstore(0);
+  if (k_lo < k_hi) {
+    gload(k_lo);
+    lstore(0);
+  }
   __syncthreads();
   const int frow = lane & 15, fk = (lane >> 4) * 8;
-  for (int kb = 0; kb < nk; kb++) {
-    const int cur = kb & 1;
-    if (kb + 1 < nk) gload(kb + 1);
+  for (int kb = k_lo; kb < k_hi; kb++) {
+    const int cur = (kb - k_lo) & 1;
+    if (kb + 1 < k_hi) gload(kb + 1);
     bf16x8 bfr[4];
 #pragma unroll
     for (int ni = 0; ni < 4; ni++)
@@ -164,7 +179,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
         }
       }
     }
-    if (kb + 1 < nk) lstore(cur ^ 1);
+    if (kb + 1 < k_hi) lstore(cur ^ 1);
     __syncthreads();
   }
   // D fragment: lane holds rows 4 * (lane / 16) + i of column lane % 16.
@@ -177,15 +192,209 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         const int m = m0 + wm * 64 + mi * 16 + (lane >> 4) * 4 + i;
-        if (m < g.M) g.y[(int64_t)m * g.ldy + n] = acc[mi][ni][i];
+        if (m < g.M) y[(int64_t)m * g.ldy + n] = acc[mi][ni][i];
+      }
+    }
+}
+
+// ------------------------------------------------------------ large tiles
+// 128 (M) x 256 (N) per 256-thread block, four waves of 64 x 128 (4 x 8
+// tiles of 16 x 16), K step 64 (two MFMA k-steps), double-buffered LDS
+// with rows of 64 bf16 padded to 144 bytes (16 consecutive rows of a
+// 16-byte fragment read cover all 64 banks once). Each K step is 128 MFMAs
+// per wave (with XS = 2), about 2000 cycles, which covers the global loads
+// of the next step, issued before it.
+constexpr int kLM = 128, kLN = 256, kLK = 64, kLRow = 72;  // LDS row: 72 bf16 = 144 B
+
+template <int WF, int XS>
+__global__ __launch_bounds__(256) void gemm_large_kernel(GemmArgs g) {
+  extern __shared__ __align__(16) uint16_t lds16[];
+  // per stage: A planes [XS][kLM][kLRow], B [kLN][kLRow], scales [2][kLN] floats (Q8_0)
+  constexpr int kA = kLM * kLRow, kB = kLN * kLRow;
+  constexpr int kStage = XS * kA + kB + (WF == FMT_Q8_0 ? 2 * kLN * 2 : 0);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int K = g.w.cols, N = g.w.rows, nk = (K + kLK - 1) / kLK;
+  const int MT = (g.M + kLM - 1) / kLM, NT = (N + kLN - 1) / kLN;
+  // Workgroups go round-robin to the 8 XCDs (one L2 each): consecutive
+  // workgroups of an XCD take the M tiles of one N tile, so its weight
+  // tile comes from HBM once.
+  const int per_split = (NT + 7) / 8 * 8 * MT, b = blockIdx.x % per_split, split = blockIdx.x / per_split;
+  const int xcd = b & 7, slot = b >> 3;
+  const int nt = xcd + 8 * (slot / MT), mt = slot % MT;
+  if (nt >= NT) return;
+  const int m0 = mt * kLM, n0 = nt * kLN;
+  int k_lo, k_hi;
+  split_range(nk, g.ksplit, split, k_lo, k_hi);
+  float *y = g.y + (int64_t)split * g.M * g.ldy;
+
+  // Staging: A chunk q = tid + 256 i (i < 4) of a plane is row q / 8,
+  // 8-value column group q % 8; B (BF16) chunk q = tid + 256 i (i < 8);
+  // B (Q8_0, 16 int8 per chunk) chunk q = tid + 256 i (i < 4): row q / 4,
+  // 16-value group q % 4.
+  uint4 ra[XS][4];
+  constexpr int NB = WF == FMT_BF16 ? 8 : 4;
+  uint4 rb[NB];
+  uint32_t rs[2] = {0, 0};
+  auto gload = [&](int kb) {
+    const int k0 = kb * kLK;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int q = tid + 256 * i, row = q >> 3, kc = k0 + (q & 7) * 8;
+      const bool ok = m0 + row < g.M && kc < K;
+      const int64_t off = (int64_t)(m0 + row) * K + kc;
+      ra[0][i] = ok ? *reinterpret_cast<const uint4 *>(g.xh + off) : make_uint4(0, 0, 0, 0);
+      if constexpr (XS == 2) ra[1][i] = ok ? *reinterpret_cast<const uint4 *>(g.xl + off) : make_uint4(0, 0, 0, 0);
+    }
+    if constexpr (WF == FMT_BF16) {
+#pragma unroll
+      for (int i = 0; i < NB; i++) {
+        const int q = tid + 256 * i, row = q >> 3, kc = k0 + (q & 7) * 8;
+        const bool ok = n0 + row < N && kc < K;
+        rb[i] = ok ? *reinterpret_cast<const uint4 *>(g.w.vals + (int64_t)(n0 + row) * g.w.vstride + (int64_t)kc * 2)
+                   : make_uint4(0, 0, 0, 0);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < NB; i++) {
+        const int q = tid + 256 * i, row = q >> 2, kc = k0 + (q & 3) * 16;
+        const bool ok = n0 + row < N && kc < K;
+        rb[i] = ok ? *reinterpret_cast<const uint4 *>(g.w.vals + (int64_t)(n0 + row) * g.w.vstride + kc)
+                   : make_uint4(0, 0, 0, 0);
+      }
+      // the two Q8_0 block scales of row tid (and tid + ... covered by 256 rows = kLN)
+      const int n = n0 + tid;
+      const uint16_t *sp = reinterpret_cast<const uint16_t *>(g.w.meta + (int64_t)n * g.w.mstride);
+      rs[0] = n < N && k0 < K ? sp[k0 / 32] : 0;
+      rs[1] = n < N && k0 + 32 < K ? sp[k0 / 32 + 1] : 0;
+    }
+  };
+  auto lstore = [&](int buf) {
+    uint16_t *st = lds16 + buf * kStage;
+#pragma unroll
+    for (int p = 0; p < XS; p++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int q = tid + 256 * i, row = q >> 3, c = (q & 7) * 8;
+        *reinterpret_cast<uint4 *>(st + p * kA + row * kLRow + c) = ra[p][i];
+      }
+    uint16_t *sb = st + XS * kA;
+    if constexpr (WF == FMT_BF16) {
+#pragma unroll
+      for (int i = 0; i < NB; i++) {
+        const int q = tid + 256 * i, row = q >> 3, c = (q & 7) * 8;
+        *reinterpret_cast<uint4 *>(sb + row * kLRow + c) = rb[i];
+      }
+    } else {  // 16 int8 -> 16 bf16, exact
+#pragma unroll
+      for (int i = 0; i < NB; i++) {
+        const int q = tid + 256 * i, row = q >> 2, c = (q & 3) * 16;
+        const uint32_t ws[4] = {rb[i].x, rb[i].y, rb[i].z, rb[i].w};
+        uint32_t o[8];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          const uint32_t v = ws[j];
+          o[2 * j] = bf16_bits((float)(int8_t)v) | bf16_bits((float)(int8_t)(v >> 8)) << 16;
+          o[2 * j + 1] = bf16_bits((float)(int8_t)(v >> 16)) | bf16_bits((float)(int8_t)(v >> 24)) << 16;
+        }
+        uint4 *d = reinterpret_cast<uint4 *>(sb + row * kLRow + c);
+        d[0] = make_uint4(o[0], o[1], o[2], o[3]);
+        d[1] = make_uint4(o[4], o[5], o[6], o[7]);
+      }
+      float *ss = reinterpret_cast<float *>(sb + kB);
+      ss[tid] = hw_half((uint16_t)rs[0]);
+      ss[kLN + tid] = hw_half((uint16_t)rs[1]);
+    }
+  };
+
+  f32x4 acc[4][8];
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < 8; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  if (k_lo < k_hi) {
+    gload(k_lo);
+    lstore(0);
+  }
+  __syncthreads();
+  const int frow = lane & 15, fk = (lane >> 4) * 8;
+  for (int kb = k_lo; kb < k_hi; kb++) {
+    const int cur = (kb - k_lo) & 1;
+    if (kb + 1 < k_hi) gload(kb + 1);
+    const uint16_t *st = lds16 + cur * kStage;
+    const uint16_t *sb = st + XS * kA;
+#pragma unroll
+    for (int ks = 0; ks < 2; ks++) {
+      bf16x8 bfr[8];
+#pragma unroll
+      for (int ni = 0; ni < 8; ni++)
+        bfr[ni] = *reinterpret_cast<const bf16x8 *>(sb + (wn * 128 + ni * 16 + frow) * kLRow + ks * 32 + fk);
+      float sc[8];
+      if constexpr (WF == FMT_Q8_0) {
+        const float *ss = reinterpret_cast<const float *>(sb + kB);
+#pragma unroll
+        for (int ni = 0; ni < 8; ni++) sc[ni] = ss[ks * kLN + wn * 128 + ni * 16 + frow];
+      }
+#pragma unroll
+      for (int mi = 0; mi < 4; mi++) {
+        const int r = (wm * 64 + mi * 16 + frow) * kLRow + ks * 32 + fk;
+        const bf16x8 ah = *reinterpret_cast<const bf16x8 *>(st + r);
+        bf16x8 al;
+        if constexpr (XS == 2) al = *reinterpret_cast<const bf16x8 *>(st + kA + r);
+#pragma unroll
+        for (int ni = 0; ni < 8; ni++) {
+          if constexpr (WF == FMT_Q8_0) {
+            f32x4 t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bfr[ni], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+            if constexpr (XS == 2) t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bfr[ni], t, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[mi][ni][i] = fmaf(sc[ni], t[i], acc[mi][ni][i]);
+          } else {
+            acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bfr[ni], acc[mi][ni], 0, 0, 0);
+            if constexpr (XS == 2)
+              acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bfr[ni], acc[mi][ni], 0, 0, 0);
+          }
+        }
+      }
+    }
+    if (kb + 1 < k_hi) lstore(cur ^ 1);
+    __syncthreads();
+  }
+  // D fragment: lane holds rows 4 * (lane / 16) + i of column lane % 16.
+#pragma unroll
+  for (int mi = 0; mi < 4; mi++)
+#pragma unroll
+    for (int ni = 0; ni < 8; ni++) {
+      const int n = n0 + wn * 128 + ni * 16 + frow;
+      if (n >= N) continue;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int m = m0 + wm * 64 + mi * 16 + (lane >> 4) * 4 + i;
+        if (m < g.M) y[(int64_t)m * g.ldy + n] = acc[mi][ni][i];
       }
     }
 }
 
 template <int WF, int XS>
+constexpr size_t gemm_large_lds() {
+  return (size_t)2 * (XS * kLM * kLRow + kLN * kLRow + (WF == FMT_Q8_0 ? 2 * kLN * 2 : 0)) * 2;
+}
+
+template <int WF, int XS>
+hipError_t gemm_large_launch(const GemmArgs &g, hipStream_t st) {
+  constexpr size_t lds = gemm_large_lds<WF, XS>();
+  static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemm_large_kernel<WF, XS>),
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  if (attr != hipSuccess) return attr;
+  const int NT = (g.w.rows + kLN - 1) / kLN, MT = (g.M + kLM - 1) / kLM;
+  dim3 grid((NT + 7) / 8 * 8 * MT * g.ksplit);
+  hipLaunchKernelGGL((gemm_large_kernel<WF, XS>), grid, dim3(256), lds, st, g);
+  return hipGetLastError();
+}
+
+template <int WF, int XS>
 hipError_t gemm_launch(const GemmArgs &g, hipStream_t st) {
   const int NT = (g.w.rows + kBN - 1) / kBN, MT = (g.M + kBM - 1) / kBM;
-  dim3 grid((NT + 7) / 8 * 8 * MT);
+  dim3 grid((NT + 7) / 8 * 8 * MT * g.ksplit);
   hipLaunchKernelGGL((gemm_kernel<WF, XS>), grid, dim3(256), 0, st, g);
   return hipGetLastError();
 }
@@ -206,10 +415,21 @@ hipError_t launch_split_bf16(const float *x, int ldx, int k, int64_t rows, uint1
   return hipGetLastError();
 }
 
+int gemm_splits(const MatDesc &w, int M, int max_splits) {
+  const bool large = w.fmt == FMT_BF16;
+  const int NT = (w.rows + (large ? kLN : kBN) - 1) / (large ? kLN : kBN);
+  const int MT = (M + (large ? kLM : kBM) - 1) / (large ? kLM : kBM);
+  const int nk = (w.cols + (large ? kLK : kBK) - 1) / (large ? kLK : kBK);
+  // about one block per CU, at least 4 K steps per split
+  int s = std::max(1, 256 / std::max(1, NT * MT));
+  s = std::min({s, max_splits, std::max(1, nk / 4)});
+  return s;
+}
+
 hipError_t launch_gemm_mfma(const MatDesc &w, const uint16_t *xh, const uint16_t *xl, int M, float *y, int ldy,
-                            hipStream_t st) {
-  if (!gemm_mfma_supported(w)) return hipErrorInvalidValue;
-  GemmArgs g{w, xh, xl, M, y, ldy};
+                            hipStream_t st, int ksplit) {
+  if (!gemm_mfma_supported(w) || ksplit < 1) return hipErrorInvalidValue;
+  GemmArgs g{w, xh, xl, M, y, ldy, ksplit};
   if (w.fmt == FMT_Q8_0) return xl ? gemm_launch<FMT_Q8_0, 2>(g, st) : gemm_launch<FMT_Q8_0, 1>(g, st);
-  return xl ? gemm_launch<FMT_BF16, 2>(g, st) : gemm_launch<FMT_BF16, 1>(g, st);
+  return xl ? gemm_large_launch<FMT_BF16, 2>(g, st) : gemm_large_launch<FMT_BF16, 1>(g, st);
 }

@@ -140,11 +140,15 @@ hipError_t launch_layer_norm_rows(const float *x, const float *w, const float *b
 hipError_t launch_gemm(const MatDesc &w, const float *x, int n, float *out, hipStream_t st);
 // The matrix-core product: y[M][N] (row stride ldy) = X * W^T with X given
 // as bf16 planes [M][K] (xl null: one plane). Q8_0 and BF16 weights with
-// K % 32 == 0.
+// K % 32 == 0. With ksplit > 1 the K range is cut in ksplit parts whose
+// products go to y + s * M * ldy (s < ksplit), for the caller to sum;
+// gemm_splits: the split count that fills the device for this shape (at
+// most max_splits).
 bool gemm_mfma_supported(const MatDesc &w);
 int gemm_planes(const MatDesc &w);
+int gemm_splits(const MatDesc &w, int M, int max_splits);
 hipError_t launch_gemm_mfma(const MatDesc &w, const uint16_t *xh, const uint16_t *xl, int M, float *y, int ldy,
-                            hipStream_t st);
+                            hipStream_t st, int ksplit = 1);
 // x fp32 [rows][k] (row stride ldx) -> bf16 hi [rows][k] and lo = x - hi.
 hipError_t launch_split_bf16(const float *x, int ldx, int k, int64_t rows, uint16_t *hi, uint16_t *lo,
                              hipStream_t st);
@@ -155,7 +159,9 @@ hipError_t launch_in_epilogue(const StableDims &s, const KVDev &kv, const float 
                               const int *pos0, int n, float *q, float *m, hipStream_t st);
 hipError_t launch_silu_gate(float *g, const float *u, int64_t n, hipStream_t st);
 // x = (x + p) + d elementwise (stablelm.go:375-377).
-hipError_t launch_residual(float *x, const float *p, const float *d, int64_t n, hipStream_t st);
+// x = (x + sum_s p[s]) + sum_s d[s] over sp and sd partial products n
+// floats apart (K-split GEMM outputs), summed in order.
+hipError_t launch_residual(float *x, const float *p, int sp, const float *d, int sd, int64_t n, hipStream_t st);
 hipError_t launch_copy_row(const float *src, float *dst, int n, hipStream_t st);
 
 // ---- weights ----

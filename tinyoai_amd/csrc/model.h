@@ -88,6 +88,7 @@ struct StableModel {
   float *partials = nullptr;
   unsigned *counters = nullptr;
   int max_splits = 0;
+  static constexpr int kPrefillSplits = 8;  // K-split partial products P and D can hold
   // prefill workspaces, `chunk` tokens each: residual X, LayerNorm H, win
   // products Y, RoPE'd queries Q, SiLU-gate M, attention A, o and down
   // products P and D, bf16 planes XH/XL of the current GEMM operand
@@ -138,7 +139,9 @@ struct StableModel {
   int decode_step(int token, int pos, bool want_logits);
   PersistentDecode persistent_args(bool want_logits) const;
   int check_persistent(int rc);
-  int project(const MatDesc &w, const float *x, int ldx, int n, float *y, int ldy);
+  // y = x * W^T; with `splits`, the product may come as *splits K-split
+  // partials n * ldy floats apart (y holds kPrefillSplits of them).
+  int project(const MatDesc &w, const float *x, int ldx, int n, float *y, int ldy, int *splits = nullptr);
   int prefill_chunk(const int32_t *ids, int n, int start, bool want_logits);
   int forward(int prefix, const int32_t *tokens, int n, bool want_logits, float *logits);
 };

@@ -100,9 +100,13 @@ __global__ void silu_gate_kernel(float *g, const float *u, int64_t n) {
     g[i] = silu_gate(g[i], u[i]);
 }
 
-__global__ void residual_kernel(float *x, const float *p, const float *d, int64_t n) {
-  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
-    x[i] = __fadd_rn(__fadd_rn(x[i], p[i]), d[i]);
+__global__ void residual_kernel(float *x, const float *p, int sp, const float *d, int sd, int64_t n) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    float o = p[i], m = d[i];
+    for (int s = 1; s < sp; s++) o = __fadd_rn(o, p[s * n + i]);
+    for (int s = 1; s < sd; s++) m = __fadd_rn(m, d[s * n + i]);
+    x[i] = __fadd_rn(__fadd_rn(x[i], o), m);
+  }
 }
 
 __global__ void copy_kernel(const float *src, float *dst, int n) {
@@ -139,8 +143,9 @@ hipError_t launch_silu_gate(float *g, const float *u, int64_t n, hipStream_t st)
   return hipGetLastError();
 }
 
-hipError_t launch_residual(float *x, const float *p, const float *d, int64_t n, hipStream_t st) {
-  hipLaunchKernelGGL(residual_kernel, dim3(elementwise_grid(n)), dim3(256), 0, st, x, p, d, n);
+hipError_t launch_residual(float *x, const float *p, int sp, const float *d, int sd, int64_t n, hipStream_t st) {
+  if (sp < 1 || sd < 1) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(residual_kernel, dim3(elementwise_grid(n)), dim3(256), 0, st, x, p, sp, d, sd, n);
   return hipGetLastError();
 }
 
