@@ -20,6 +20,11 @@
 #include "kernels.h"
 #include "model.h"
 
+LaunchTiming &launch_timing() {
+  thread_local LaunchTiming t;
+  return t;
+}
+
 namespace tinyoai {
 
 thread_local std::string g_error;
@@ -252,24 +257,42 @@ hipEvent_t Profiler::next() {
   return pool[used++];
 }
 
+// begin records event i on the stream and offers events i + 1, i + 2 to
+// the launch; end records event i + 3 and keeps the dispatch's pair when
+// the launch took it.
 void Profiler::begin(int stage, hipStream_t st) {
   if (!on) return;
-  marks.emplace_back(stage, used);
-  hipEventRecord(next(), st);
+  const size_t i = used;
+  hipEvent_t e0 = next(), e1 = next(), e2 = next();
+  if (!e0 || !e1 || !e2) return;
+  hipEventRecord(e0, st);
+  marks.push_back(Mark{stage, i, i});
+  launch_timing() = LaunchTiming{e1, e2, false};
 }
 
 void Profiler::end(hipStream_t st) {
-  if (!on) return;
-  hipEventRecord(next(), st);
+  if (!on || marks.empty()) return;
+  LaunchTiming &lt = launch_timing();
+  Mark &m = marks.back();
+  const size_t i = m.a;
+  if (lt.used) {
+    m.a = i + 1;
+    m.b = i + 2;
+  } else {
+    hipEvent_t e3 = next();
+    if (e3) hipEventRecord(e3, st);
+    m.b = used - 1;
+  }
+  lt = LaunchTiming{};
 }
 
 // Called after the stream has synchronized.
 void Profiler::resolve() {
   for (auto &m : marks) {
     float t = 0;
-    if (m.second + 1 < used && hipEventElapsedTime(&t, pool[m.second], pool[m.second + 1]) == hipSuccess) {
-      ms[m.first] += t;
-      count[m.first]++;
+    if (m.b > m.a && m.b < used && hipEventElapsedTime(&t, pool[m.a], pool[m.b]) == hipSuccess) {
+      ms[m.stage] += t;
+      count[m.stage]++;
     }
   }
   marks.clear();

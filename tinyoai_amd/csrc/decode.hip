@@ -203,9 +203,9 @@ template <int HD, bool HALF>
 hipError_t launch_attention_hd(const AttArgs &a, int nq, int splits, int steps, hipStream_t st) {
   dim3 grid(splits, a.s.heads, nq);
   switch (steps) {
-    case 1: hipLaunchKernelGGL((attention_kernel<HD, HALF, 1>), grid, dim3(kThreads), 0, st, a); break;
-    case 2: hipLaunchKernelGGL((attention_kernel<HD, HALF, 2>), grid, dim3(kThreads), 0, st, a); break;
-    case 4: hipLaunchKernelGGL((attention_kernel<HD, HALF, 4>), grid, dim3(kThreads), 0, st, a); break;
+    case 1: TINYOAI_TIMED_LAUNCH((attention_kernel<HD, HALF, 1>), grid, dim3(kThreads), 0, st, a); break;
+    case 2: TINYOAI_TIMED_LAUNCH((attention_kernel<HD, HALF, 2>), grid, dim3(kThreads), 0, st, a); break;
+    case 4: TINYOAI_TIMED_LAUNCH((attention_kernel<HD, HALF, 4>), grid, dim3(kThreads), 0, st, a); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

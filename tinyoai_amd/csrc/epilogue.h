@@ -58,7 +58,11 @@ __device__ __forceinline__ void in_pair_outputs(const StableDims &s, const KVDev
     out.f32(q_out + head * s.hd + d1, v1);
   } else {  // head-major [kv_head][cap][hd] at the token's position (storeKV, kv_cache.go:55-65)
     const int64_t base = ((int64_t)head * kv.cap + pos) * s.hd;
-    void *dst = sec == 1 ? kv.k : kv.v;
+    // The cache base as arithmetic on the two addresses: a choice between
+    // the two fields made the compiler keep them in per-lane scratch memory
+    // (stored by every thread at kernel start, read back per store).
+    const uintptr_t ka = reinterpret_cast<uintptr_t>(kv.k), va = reinterpret_cast<uintptr_t>(kv.v);
+    void *dst = reinterpret_cast<void *>(ka + (sec == 1 ? uintptr_t(0) : va - ka));
     if (kv.half) {
       out.f16(reinterpret_cast<uint16_t *>(dst) + base + d0, float_to_half(v0));
       out.f16(reinterpret_cast<uint16_t *>(dst) + base + d1, float_to_half(v1));

@@ -188,18 +188,6 @@ __device__ __forceinline__ float chunk_dot<FMT_F32>(const uint4 w, const float4 
 }
 
 // ---------------------------------------------------------------- 5/6-bit
-// 6-bit scale and minimum of group g of a Q4_K / Q5_K super-block
-// (quant_k.go:69-77).
-__device__ __forceinline__ void kquant_scale_min(const uint8_t *sc, int g, int &scale, int &minimum) {
-  if (g < 4) {
-    scale = sc[g] & 63;
-    minimum = sc[g + 4] & 63;
-  } else {
-    scale = (sc[g + 4] & 15) | ((sc[g - 4] >> 6) << 4);
-    minimum = (sc[g + 4] >> 4) | ((sc[g] >> 6) << 4);
-  }
-}
-
 // Per-chunk constants of the value formula, from the chunk's meta bytes
 // (and, for Q6_K, its fp16 d): value = (q * a) + b for Q5_1, (q * a) - b
 // for Q4_K / Q5_K, (q - 32) * (a or a2) for Q6_K (a for values 0-15, a2
@@ -208,6 +196,14 @@ struct KConst {
   float a, b, a2;
 };
 
+// Byte i (0..15, little-endian) of a 16-byte header held in registers. A
+// selection among the four words, not a byte pointer into them: indexing
+// a local array at a run-time position puts it in per-lane scratch memory.
+__device__ __forceinline__ uint32_t header_byte(const uint4 mt, int i) {
+  const uint32_t w = i < 8 ? (i < 4 ? mt.x : mt.y) : (i < 12 ? mt.z : mt.w);
+  return (w >> (8 * (i & 3))) & 255u;
+}
+
 template <int F>
 __device__ __forceinline__ KConst kquant_const(const uint4 mt, uint16_t d6, int cc) {
   KConst k{};
@@ -215,18 +211,24 @@ __device__ __forceinline__ KConst kquant_const(const uint4 mt, uint16_t d6, int 
     k.a = half_to_float((uint16_t)mt.x);
     k.b = half_to_float((uint16_t)(mt.x >> 16));
   } else if constexpr (F == FMT_Q4_K || F == FMT_Q5_K) {
-    const uint32_t w[4] = {mt.x, mt.y, mt.z, mt.w};
-    const uint8_t *bytes = reinterpret_cast<const uint8_t *>(w);
-    int sc, mn;
-    kquant_scale_min(bytes + 4, cc & 7, sc, mn);
-    k.a = __fmul_rn(half_to_float((uint16_t)mt.x), (float)sc);
-    k.b = __fmul_rn(half_to_float((uint16_t)(mt.x >> 16)), (float)mn);
+    // the 12 scale bytes follow {d, dmin}: header bytes 4..15 (quant_k.go:69-77)
+    const int g = cc & 7;
+    auto sc = [&](int i) { return (int)header_byte(mt, 4 + i); };
+    int scale, minimum;
+    if (g < 4) {
+      scale = sc(g) & 63;
+      minimum = sc(g + 4) & 63;
+    } else {
+      scale = (sc(g + 4) & 15) | ((sc(g - 4) >> 6) << 4);
+      minimum = (sc(g + 4) >> 4) | ((sc(g) >> 6) << 4);
+    }
+    k.a = __fmul_rn(half_to_float((uint16_t)mt.x), (float)scale);
+    k.b = __fmul_rn(half_to_float((uint16_t)(mt.x >> 16)), (float)minimum);
   } else {
-    const uint32_t w[4] = {mt.x, mt.y, mt.z, mt.w};
-    const int8_t *scales = reinterpret_cast<const int8_t *>(w);
     const float d = half_to_float(d6);
-    k.a = __fmul_rn(d, (float)scales[2 * (cc & 7)]);
-    k.a2 = __fmul_rn(d, (float)scales[2 * (cc & 7) + 1]);
+    const int g = cc & 7;
+    k.a = __fmul_rn(d, (float)(int8_t)header_byte(mt, 2 * g));
+    k.a2 = __fmul_rn(d, (float)(int8_t)header_byte(mt, 2 * g + 1));
   }
   return k;
 }

@@ -2,11 +2,33 @@
 // the C ABI) calls only these; each returns hipSuccess or the launch error.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
 
 #include "formats.h"
+
+// Kernel timing for the stage profiler. While `start` is set, the decode
+// kernels launch through hipExtLaunchKernelGGL with `start` and `stop`,
+// which the dispatch records when the kernel begins and ends (events
+// recorded around a launch also count the launch gap), and set `used`.
+struct LaunchTiming {
+  hipEvent_t start = nullptr, stop = nullptr;
+  bool used = false;
+};
+LaunchTiming &launch_timing();  // the calling thread's
+
+#define TINYOAI_TIMED_LAUNCH(KERNEL, GRID, BLOCK, LDS, STREAM, ...)                                        \
+  do {                                                                                                       \
+    LaunchTiming &lt_ = launch_timing();                                                                     \
+    if (lt_.start) {                                                                                         \
+      hipExtLaunchKernelGGL(KERNEL, GRID, BLOCK, LDS, STREAM, lt_.start, lt_.stop, 0, __VA_ARGS__);         \
+      lt_.used = true;                                                                                       \
+    } else {                                                                                                 \
+      hipLaunchKernelGGL(KERNEL, GRID, BLOCK, LDS, STREAM, __VA_ARGS__);                                     \
+    }                                                                                                        \
+  } while (0)
 
 // Per-layer weights of a StableLM block (stablelm.go:113-117), fused:
 //   win  rows [q | k | v | gate/up], cols = hidden. Inside each q and k head

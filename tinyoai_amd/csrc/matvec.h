@@ -245,11 +245,11 @@ int fit_threads(int chunks, int split, int threads) {
   return need > threads ? 512 : threads;
 }
 
-#define TINYOAI_LAUNCH_T(KERNEL, ARGS)                                                              \
-  switch (threads) {                                                                                \
-    case 256: hipLaunchKernelGGL((KERNEL<F, 256>), dim3(grid), dim3(256), lds, st, ARGS); break;     \
-    case 512: hipLaunchKernelGGL((KERNEL<F, 512>), dim3(grid), dim3(512), lds, st, ARGS); break;     \
-    default: return hipErrorInvalidValue;                                                           \
+#define TINYOAI_LAUNCH_T(KERNEL, ARGS)                                                                  \
+  switch (threads) {                                                                                    \
+    case 256: TINYOAI_TIMED_LAUNCH((KERNEL<F, 256>), dim3(grid), dim3(256), lds, st, ARGS); break;       \
+    case 512: TINYOAI_TIMED_LAUNCH((KERNEL<F, 512>), dim3(grid), dim3(512), lds, st, ARGS); break;       \
+    default: return hipErrorInvalidValue;                                                               \
   }
 
 template <int F>

@@ -53,7 +53,13 @@ enum Stage : int {
 struct Profiler {
   bool on = false;
   std::vector<hipEvent_t> pool;
-  std::vector<std::pair<int, size_t>> marks;  // (stage, index of start event)
+  // (stage, start event, stop event): the events recorded around the
+  // launch, or those its dispatch recorded (LaunchTiming)
+  struct Mark {
+    int stage;
+    size_t a, b;
+  };
+  std::vector<Mark> marks;
   size_t used = 0;
   double ms[ST_COUNT] = {};
   int64_t count[ST_COUNT] = {};
