@@ -227,11 +227,9 @@ __host__ __device__ inline void slice_range(const SliceShape &sh, int nch, int s
 // each of the lane's chunks (zeros past the vector); `pre()` issues the
 // loads the prologue needs, and with PREWAIT the wave waits for them
 // before any weight load goes out (they are not queued behind the weight
-// stream); the first PRE batches; `prologue()` (block-wide staging, with
-// barriers); without XFIRST the x load; then the groups, which first
-// bring the batches in flight up to kAhead. PRE (0 or 1) batches go out
-// before the prologue: a wave that issued many loads into the grid's flood
-// stalls in the issue, and a prologue barrier waits for the slowest wave. With AUX,
+// stream); the first PRE batches (at most a group); `prologue()`
+// (block-wide staging, with barriers); without XFIRST the x load; then the
+// groups, which first bring the batches in flight up to kAhead. With AUX,
 // `aux_load(row)` is issued with each batch (a per-row operand for done,
 // e.g. the residual). `done(u, r, aux, out)` receives unit u's sums
 // r[R][2] and aux[R] (wave-uniform; every lane calls it) and hands its
@@ -249,7 +247,7 @@ __device__ __forceinline__ void stream_rows(const MatDesc &M, int n_units, int s
   // the choice of buffer descriptor (a per-lane choice would make the
   // compiler loop over the lanes' descriptors around every load).
   constexpr int W = T / 64;
-  static_assert(PRE == 0 || PRE == 1, "at most one batch before the prologue");
+  static_assert(PRE >= 0 && PRE <= kRowGroup, "batches before the prologue: at most a group");
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const SliceShape sh = slice_shape(M.chunks, split, CPL);
   const int S = sh.S, RG = W / S;
@@ -316,11 +314,6 @@ __device__ __forceinline__ void stream_rows(const MatDesc &M, int n_units, int s
   if constexpr (XFIRST) load_x();
   pre();
   if constexpr (PREWAIT) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  if constexpr (PRE > 0) {
-    if (nb > 0) issue(0);  // older than every later load: no effect on later wait counts
-  }
-  prologue();
-  if constexpr (!XFIRST) load_x();
   // One group of N batches, P0 of them already issued; step k issues the
   // batches up to k + kAhead, then consumes batch k; the units' results
   // follow the last consume (result code between the consumes reuses
@@ -369,10 +362,25 @@ __device__ __forceinline__ void stream_rows(const MatDesc &M, int n_units, int s
     __builtin_amdgcn_sched_barrier(0);
     first_j += N * RG;
   };
-  using P1 = std::integral_constant<int, PRE>;
   using P0 = std::integral_constant<int, 0>;
+  // The first group issues its first min(N, PRE) batches before the
+  // prologue (older than every later load, so later wait counts stay
+  // exact); a wave with no units still runs the prologue (its barriers).
+  auto first = [&](auto n_tag) {
+    constexpr int N = decltype(n_tag)::value, PI = N < PRE ? N : PRE;
+#pragma unroll
+    for (int t = 0; t < PI; t++) issue(t);
+    prologue();
+    if constexpr (!XFIRST) load_x();
+    group(n_tag, std::integral_constant<int, PI>{});
+  };
   int left = nb;
-  if (left > 0) group_of_size<K>(min(left, K), [&](auto n_tag) { group(n_tag, P1{}); });  // PRE batches issued
+  if (left > 0) {
+    group_of_size<K>(min(left, K), first);
+  } else {
+    prologue();
+    if constexpr (!XFIRST) load_x();
+  }
   left -= min(left, K);
   while (left > 0) {
     group_of_size<K>(min(left, K), [&](auto n_tag) { group(n_tag, P0{}); });
