@@ -781,6 +781,13 @@ int StableModel::project(const MatDesc &w, const float *x, int ldx, int n, float
   return TINYOAI_OK;
 }
 
+int StableModel::project_planes(const MatDesc &w, int n, float *y, int ldy, int *splits) {
+  const int ks = splits ? gemm_splits(w, n, kPrefillSplits) : 1;
+  if (splits) *splits = ks;
+  STAGE(ST_PREFILL_GEMM, launch_gemm_mfma(w, XH, XL, n, y, ldy, stream, ks), "projection");
+  return TINYOAI_OK;
+}
+
 // n tokens at positions start.. (StableLM.prefill, prefill.go:33-115): per
 // layer LayerNorm, one product with win and its fused epilogue, causal
 // attention over the cache, the o and down products over the two column
@@ -796,17 +803,32 @@ int StableModel::prefill_chunk(const int32_t *ids, int n, int start, bool want_l
     const int64_t vpc = values_per_chunk(w.wout.fmt), down0 = (d + vpc - 1) / vpc * vpc;
     const MatDesc wo = column_view(w.wout, 0, d), wd = column_view(w.wout, down0, I);
     int rc;
-    STAGE(ST_PREFILL_NORM, launch_layer_norm_rows(X, w.ln_w, w.ln_b, dims.eps, n, d, H, stream), "layer_norm");
-    if ((rc = project(w.win, H, d, n, Y, win_rows))) return rc;
-    STAGE(ST_PREFILL_EPILOGUE, launch_in_epilogue(dims, kv[l], Y, win_rows, rope, d_pos0, n, Q, M, stream),
+    // Inputs of matrix-core projections leave their producers as the bf16
+    // planes XH, XL (no separate split pass); the fp32 copies are kept where
+    // another format or the trace needs them. The planes are reused in
+    // order: LayerNorm -> win, SiLU-gate -> down, attention -> o.
+    const bool pin = gemm_mfma_supported(w.win), pd = gemm_mfma_supported(wd);
+    const bool flash = flash_prefill_supported(dims.hd), po = flash && gemm_mfma_supported(wo);
+    STAGE(ST_PREFILL_NORM,
+          launch_layer_norm_rows(X, w.ln_w, w.ln_b, dims.eps, n, d, pin ? nullptr : H, stream, pin ? XH : nullptr,
+                                 pin ? XL : nullptr),
+          "layer_norm");
+    if ((rc = pin ? project_planes(w.win, n, Y, win_rows) : project(w.win, H, d, n, Y, win_rows))) return rc;
+    STAGE(ST_PREFILL_EPILOGUE,
+          launch_in_epilogue(dims, kv[l], Y, win_rows, rope, d_pos0, n, Q, pd && !tracing ? nullptr : M, stream,
+                             pd ? XH : nullptr, pd ? XL : nullptr),
           "in_epilogue");
-    if (flash_prefill_supported(dims.hd))
-      STAGE(ST_PREFILL_ATTENTION, launch_flash_prefill(dims, kv[l], Q, d_pos0, n, A, stream), "attention");
+    int sp = 1, sd = 1;
+    if ((rc = pd ? project_planes(wd, n, D, d, &sd) : project(wd, M, I, n, D, d, &sd))) return rc;
+    if (flash)
+      STAGE(ST_PREFILL_ATTENTION,
+            launch_flash_prefill(dims, kv[l], Q, d_pos0, n, po && !tracing ? nullptr : A, stream, po ? XH : nullptr,
+                                 po ? XL : nullptr),
+            "attention");
     else
       STAGE(ST_PREFILL_ATTENTION,
             launch_attention(dims, kv[l], Q, d_pos0, n, start + n - 1, partials, counters, A, stream), "attention");
-    int sp = 1, sd = 1;
-    if ((rc = project(wo, A, d, n, P, d, &sp)) || (rc = project(wd, M, I, n, D, d, &sd))) return rc;
+    if ((rc = po ? project_planes(wo, n, P, d, &sp) : project(wo, A, d, n, P, d, &sp))) return rc;
     STAGE(ST_PREFILL_ELEMENTWISE, launch_residual(X, P, sp, D, sd, (int64_t)n * d, stream), "residual");
     if (tracing) {
       TRY_HIP(launch_copy_row(X + (size_t)(n - 1) * d, trace_dev + (size_t)l * d, d, stream), "trace");

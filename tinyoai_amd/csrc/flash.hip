@@ -23,7 +23,8 @@ struct FlashArgs {
   const float *q;  // [n][heads][hd]
   const int *pos0;
   int n;
-  float *out;      // [n][heads][hd]
+  float *out;      // [n][heads][hd] (may be null)
+  uint16_t *oh, *ol;  // the same as bf16 operand planes (null: none)
 };
 
 // x = hi + lo to about 2^-22. The empty asm pins x as one fp32 value: when x
@@ -290,11 +291,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
                           : __shfl(l_run, (v >> 2) * 8 + g * 4 + (v & 3), 64);
     const int qi = qw + (v >> 2) * 8 + g * 4 + (v & 3);
     if (qi >= a.n) continue;
-    float *op = a.out + ((int64_t)qi * s.heads + h) * HD;
+    const int64_t ob = ((int64_t)qi * s.heads + h) * HD;
 #pragma unroll
     for (int t = 0; t < DT; t++) {
       const int dd = t * 32 + col;
-      if (dd < HD) op[dd] = o[t][v] / lq;
+      if (dd < HD) {
+        const float r = o[t][v] / lq;
+        if (a.out) a.out[ob + dd] = r;
+        if (a.oh) store_bf16_split(a.oh, a.ol, ob + dd, r);
+      }
     }
   }
 }
@@ -314,8 +319,9 @@ hipError_t flash32_launch(const FlashArgs &a, hipStream_t st) {
 bool flash_prefill_supported(int hd) { return hd == 64 || hd == 80 || hd == 96 || hd == 128; }
 
 hipError_t launch_flash_prefill(const StableDims &s, const KVDev &kv, const float *q, const int *pos0, int n,
-                                float *out, hipStream_t st) {
-  FlashArgs a{s, kv, q, pos0, n, out};
+                                float *out, hipStream_t st, uint16_t *oh, uint16_t *ol) {
+  if (!oh != !ol || (!out && !oh)) return hipErrorInvalidValue;
+  FlashArgs a{s, kv, q, pos0, n, out, oh, ol};
   switch (s.hd) {
     case 64: return flash32_launch<64>(a, st);
     case 80: return flash32_launch<80>(a, st);

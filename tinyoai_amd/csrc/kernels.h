@@ -101,13 +101,25 @@ hipError_t launch_attention(const StableDims &s, const KVDev &kv, const float *q
 // Causal attention of n prefill queries on the matrix cores (head widths
 // 64, 80, 96, 128): q [n][heads*hd] at positions pos0 + j -> out.
 bool flash_prefill_supported(int hd);
+// out (fp32, may be null) and / or the bf16 operand planes oh, ol of the
+// matrix-core GEMM (null: none).
 hipError_t launch_flash_prefill(const StableDims &s, const KVDev &kv, const float *q, const int *pos0, int n,
-                                float *out, hipStream_t st);
+                                float *out, hipStream_t st, uint16_t *oh = nullptr, uint16_t *ol = nullptr);
 int attention_steps(int max_pos, int heads);
 // Floats per (query, head) in the partials buffer: max_splits records of
 // hd + 2, rounded to 256 bytes.
 __host__ __device__ inline int64_t partial_region(int max_splits, int hd) {
   return ((int64_t)max_splits * (hd + 2) + 63) / 64 * 64;
+}
+
+// The operand planes of the matrix-core GEMM for one value: bf16 hi (round
+// to nearest even) and lo = bf16(v - hi), as launch_split_bf16 forms them.
+// The empty asm keeps v one fp32 value for both conversions.
+__device__ __forceinline__ void store_bf16_split(uint16_t *hi, uint16_t *lo, int64_t i, float v) {
+  asm volatile("" : "+v"(v));
+  const __bf16 h = (__bf16)v;
+  hi[i] = __builtin_bit_cast(uint16_t, h);
+  lo[i] = __builtin_bit_cast(uint16_t, (__bf16)(v - (float)h));
 }
 int attention_splits(int max_pos, int steps);
 // out[rows] = W * norm(x) (skipped when ln_w is null; norm as StableDims),
@@ -156,8 +168,9 @@ int persistent_decode_grid(const PersistentDecode &a, const LayerDev &layer0);
 hipError_t launch_persistent_decode(const PersistentDecode &a, const LayerDev &layer0, int grid, hipStream_t st);
 
 // ---- prefill (n tokens) ----
+// out (fp32, may be null) and / or bf16 operand planes oh, ol (null: none).
 hipError_t launch_layer_norm_rows(const float *x, const float *w, const float *b, double eps, int n, int d,
-                                  float *out, hipStream_t st);
+                                  float *out, hipStream_t st, uint16_t *oh = nullptr, uint16_t *ol = nullptr);
 // out[n][rows] = x[n][cols] * W^T on the vector units (any format/shape).
 hipError_t launch_gemm(const MatDesc &w, const float *x, int n, float *out, hipStream_t st);
 // The matrix-core product: y[M][N] (row stride ldy) = X * W^T with X given
@@ -176,9 +189,11 @@ hipError_t launch_split_bf16(const float *x, int ldx, int k, int64_t rows, uint1
                              hipStream_t st);
 // Epilogue of the fused in-projection for n tokens: y [n][win rows] ->
 // RoPE'd q [n][heads*hd], K/V into the cache at positions pos0 + j, and
-// m [n][inter] = SiLU-gate(gate, up).
+// m [n][inter] = SiLU-gate(gate, up) (m may be null), and / or m as bf16
+// operand planes mh, ml (null: none).
 hipError_t launch_in_epilogue(const StableDims &s, const KVDev &kv, const float *y, int ldy, const float *rope,
-                              const int *pos0, int n, float *q, float *m, hipStream_t st);
+                              const int *pos0, int n, float *q, float *m, hipStream_t st, uint16_t *mh = nullptr,
+                              uint16_t *ml = nullptr);
 hipError_t launch_silu_gate(float *g, const float *u, int64_t n, hipStream_t st);
 // x = (x + p) + d elementwise (stablelm.go:375-377).
 // x = (x + sum_s p[s]) + sum_s d[s] over sp and sd partial products n

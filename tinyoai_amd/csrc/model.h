@@ -148,6 +148,8 @@ struct StableModel {
   // y = x * W^T; with `splits`, the product may come as *splits K-split
   // partials n * ldy floats apart (y holds kPrefillSplits of them).
   int project(const MatDesc &w, const float *x, int ldx, int n, float *y, int ldy, int *splits = nullptr);
+  // y = X * W^T with X already in the bf16 planes XH, XL (matrix-core formats).
+  int project_planes(const MatDesc &w, int n, float *y, int ldy, int *splits = nullptr);
   int prefill_chunk(const int32_t *ids, int n, int start, bool want_logits);
   int forward(int prefix, const int32_t *tokens, int n, bool want_logits, float *logits);
 };

@@ -9,14 +9,18 @@
 namespace {
 
 __global__ __launch_bounds__(256) void layer_norm_rows_kernel(const float *x, const float *w, const float *b,
-                                                               double eps, int d, float *out) {
+                                                               double eps, int d, float *out, uint16_t *oh,
+                                                               uint16_t *ol) {
   extern __shared__ __align__(16) float lds[];
   double *red = reinterpret_cast<double *>(lds + ((d + 3) & ~3));
   const int64_t row = blockIdx.x;
   for (int i = threadIdx.x; i < d; i += blockDim.x) lds[i] = x[row * d + i];
   __syncthreads();
   layer_norm_lds(lds, d, w, b, eps, red);
-  for (int i = threadIdx.x; i < d; i += blockDim.x) out[row * d + i] = lds[i];
+  for (int i = threadIdx.x; i < d; i += blockDim.x) {
+    if (out) out[row * d + i] = lds[i];
+    if (oh) store_bf16_split(oh, ol, row * d + i, lds[i]);
+  }
 }
 
 // out[n][N] = x[n][K] * W[N][K]^T, fp32 SIMT tiles of 64 tokens x 64 rows,
@@ -81,17 +85,26 @@ __global__ __launch_bounds__(256) void gemm_simt_kernel(MatDesc w, const float *
 
 // One block per token: the fused in-projection epilogue (RoPE on q and k,
 // storeKV at the token's absolute position, SiLU-gate), as prefill.go:60-96
-// applies it row by row.
+// applies it row by row. With mh, the SiLU-gate outputs (the units from
+// mu0 on) also go out as the down projection's bf16 operand planes, and to
+// m only when m is given.
 __global__ void in_epilogue_kernel(StableDims s, KVDev kv, const float *y, int ldy, const float *rope,
-                                   const int *pos0, int units, float *q, float *m) {
+                                   const int *pos0, int units, float *q, float *m, uint16_t *mh, uint16_t *ml) {
   const int j = blockIdx.x;
   const int pos = *pos0 + j;
   const float *yj = y + (int64_t)j * ldy;
   const float *rope_row = rope + (int64_t)pos * s.rot;
-  float *qj = q + (int64_t)j * s.heads * s.hd, *mj = m + (int64_t)j * s.inter;
+  const int mu0 = (s.win_q + 2 * s.win_kv) / 2;
+  float *qj = q + (int64_t)j * s.heads * s.hd, *mj = m ? m + (int64_t)j * s.inter : nullptr;
   for (int u = threadIdx.x; u < units; u += blockDim.x) {
     const float2 v = *reinterpret_cast<const float2 *>(yj + 2 * u);
-    in_pair_epilogue(s, kv, rope_row, pos, u, v.x, v.y, qj, mj);
+    if (mh && u >= mu0) {
+      const float g = s.silu ? silu_gate_llama(v.x, v.y) : silu_gate(v.x, v.y);
+      if (mj) mj[u - mu0] = g;
+      store_bf16_split(mh, ml, (int64_t)j * s.inter + (u - mu0), g);
+    } else {
+      in_pair_epilogue(s, kv, rope_row, pos, u, v.x, v.y, qj, mj);
+    }
   }
 }
 
@@ -118,9 +131,10 @@ int elementwise_grid(int64_t n) { return (int)std::min<int64_t>((n + 255) / 256,
 }  // namespace
 
 hipError_t launch_layer_norm_rows(const float *x, const float *w, const float *b, double eps, int n, int d,
-                                  float *out, hipStream_t st) {
+                                  float *out, hipStream_t st, uint16_t *oh, uint16_t *ol) {
+  if (!oh != !ol) return hipErrorInvalidValue;
   const size_t lds = (size_t)((d + 3) & ~3) * 4 + 8 * sizeof(double);
-  hipLaunchKernelGGL(layer_norm_rows_kernel, dim3(n), dim3(256), lds, st, x, w, b, eps, d, out);
+  hipLaunchKernelGGL(layer_norm_rows_kernel, dim3(n), dim3(256), lds, st, x, w, b, eps, d, out, oh, ol);
   return hipGetLastError();
 }
 
@@ -131,10 +145,12 @@ hipError_t launch_gemm(const MatDesc &w, const float *x, int n, float *out, hipS
 }
 
 hipError_t launch_in_epilogue(const StableDims &s, const KVDev &kv, const float *y, int ldy, const float *rope,
-                              const int *pos0, int n, float *q, float *m, hipStream_t st) {
-  if (ldy % 2) return hipErrorInvalidValue;
+                              const int *pos0, int n, float *q, float *m, hipStream_t st, uint16_t *mh,
+                              uint16_t *ml) {
+  if (ldy % 2 || !mh != !ml || (!m && !mh) || s.win_q % 2) return hipErrorInvalidValue;
   const int units = (s.d + 2 * s.kv_heads * s.hd + 2 * s.inter) / 2;
-  hipLaunchKernelGGL(in_epilogue_kernel, dim3(n), dim3(256), 0, st, s, kv, y, ldy, rope, pos0, units, q, m);
+  hipLaunchKernelGGL(in_epilogue_kernel, dim3(n), dim3(256), 0, st, s, kv, y, ldy, rope, pos0, units, q, m, mh,
+                     ml);
   return hipGetLastError();
 }
 
