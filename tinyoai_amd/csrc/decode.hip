@@ -51,10 +51,6 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttArgs a) {
   __shared__ int s_last;
   const StableDims &s = a.s;
   const int split = blockIdx.x, h = blockIdx.y, j = blockIdx.z;
-  const int pos = *a.pos0 + j;
-  const int npos = pos + 1;
-  const int nsplit = (npos + SPLIT - 1) / SPLIT;
-  if (split >= nsplit) return;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane & 3, pl = lane >> 2;
   const int kvh = h / (s.heads / s.kv_heads);
   const float *q = a.q + (int64_t)j * s.heads * HD + h * HD + g * DPL;
@@ -63,17 +59,23 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttArgs a) {
   for (int i = 0; i < DPL; i++) qr[i] = q[i];
   const int64_t head_base = (int64_t)kvh * a.kv.cap * HD;
   const int t0 = split * SPLIT + wave * STEPS * 16 + pl;
+  // The block's K (and V) entries are loaded before the query position
+  // arrives, so the loads do not wait for it: positions are clamped to the
+  // cache, and entries past the query's position are masked below.
   // Narrow blocks issue the V loads with the K loads (one memory round
   // trip); wide ones load V after the scores to bound register use.
   constexpr bool kEarlyV = STEPS <= 2;
   float kr[STEPS][DPL], vr[STEPS][DPL];
 #pragma unroll
-  for (int st = 0; st < STEPS; st++)
-    if (t0 + st * 16 < npos) {
-      load_kv<DPL, HALF>(a.kv.k, head_base + (int64_t)(t0 + st * 16) * HD + g * DPL, kr[st]);
-      if constexpr (kEarlyV)
-        load_kv<DPL, HALF>(a.kv.v, head_base + (int64_t)(t0 + st * 16) * HD + g * DPL, vr[st]);
-    }
+  for (int st = 0; st < STEPS; st++) {
+    const int64_t e = head_base + (int64_t)min(t0 + st * 16, a.kv.cap - 1) * HD + g * DPL;
+    load_kv<DPL, HALF>(a.kv.k, e, kr[st]);
+    if constexpr (kEarlyV) load_kv<DPL, HALF>(a.kv.v, e, vr[st]);
+  }
+  const int pos = *a.pos0 + j;
+  const int npos = pos + 1;
+  const int nsplit = (npos + SPLIT - 1) / SPLIT;
+  if (split >= nsplit) return;
   float score[STEPS];
   float mx = -INFINITY;
 #pragma unroll

@@ -74,7 +74,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h = blockIdx.y, kvh = h / (s.heads / s.kv_heads);
   const int p0 = *a.pos0;
-  const int qb = blockIdx.x * kQ32;                  // first query of the block
+  // Query tiles run in reverse order for the second half of the heads:
+  // workgroups k and k + grid / 2 share a CU when the grid fills two per
+  // CU, and the reversal pairs a long causal range with a short one there.
+  const int qt = blockIdx.y >= (gridDim.y + 1) / 2 ? gridDim.x - 1 - blockIdx.x : blockIdx.x;
+  const int qb = qt * kQ32;                          // first query of the block
   const int qw = qb + wave * 32;                     // first query of the wave
   const int col = lane & 31, g = lane >> 5;          // S^T column (query) / B row, lane group
   const int myq = qw + col;                          // this lane's query as an S^T column
