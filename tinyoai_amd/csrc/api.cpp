@@ -488,7 +488,8 @@ int StableModel::init(const tinyoai_stablelm_config &c, const tinyoai_tensor *te
       (rc = alloc((void **)&Y, B * win_rows * 4)) || (rc = alloc((void **)&Q, B * w_att * 4)) ||
       (rc = alloc((void **)&M, B * I * 4)) || (rc = alloc((void **)&A, B * w_att * 4)) ||
       (rc = alloc((void **)&P, kPrefillSplits * B * d * 4)) || (rc = alloc((void **)&D, kPrefillSplits * B * d * 4)) ||
-      (rc = alloc((void **)&XH, B * wide * 2)) || (rc = alloc((void **)&XL, B * wide * 2)))
+      (rc = alloc((void **)&XH, B * wide * 2)) || (rc = alloc((void **)&XL, B * wide * 2)) ||
+      (rc = alloc((void **)&MH, B * I * 2)) || (rc = alloc((void **)&ML, B * I * 2)))
     return rc;
   // Persistent decode state.
   const int L = c.num_hidden_layers;
@@ -781,10 +782,11 @@ int StableModel::project(const MatDesc &w, const float *x, int ldx, int n, float
   return TINYOAI_OK;
 }
 
-int StableModel::project_planes(const MatDesc &w, int n, float *y, int ldy, int *splits) {
+int StableModel::project_planes(const MatDesc &w, const uint16_t *xh, const uint16_t *xl, int n, float *y, int ldy,
+                                int *splits) {
   const int ks = splits ? gemm_splits(w, n, kPrefillSplits) : 1;
   if (splits) *splits = ks;
-  STAGE(ST_PREFILL_GEMM, launch_gemm_mfma(w, XH, XL, n, y, ldy, stream, ks), "projection");
+  STAGE(ST_PREFILL_GEMM, launch_gemm_mfma(w, xh, xl, n, y, ldy, stream, ks), "projection");
   return TINYOAI_OK;
 }
 
@@ -803,23 +805,31 @@ int StableModel::prefill_chunk(const int32_t *ids, int n, int start, bool want_l
     const int64_t vpc = values_per_chunk(w.wout.fmt), down0 = (d + vpc - 1) / vpc * vpc;
     const MatDesc wo = column_view(w.wout, 0, d), wd = column_view(w.wout, down0, I);
     int rc;
-    // Inputs of matrix-core projections leave their producers as the bf16
-    // planes XH, XL (no separate split pass); the fp32 copies are kept where
-    // another format or the trace needs them. The planes are reused in
-    // order: LayerNorm -> win, SiLU-gate -> down, attention -> o.
+    // Inputs of matrix-core projections leave their producers as bf16
+    // planes (no separate split pass); the fp32 copies are kept where
+    // another format or the trace needs them. LayerNorm -> XH, XL -> win;
+    // its epilogue (fused into the product when both win and down run on
+    // the matrix cores) -> MH, ML -> down; attention -> XH, XL -> o.
     const bool pin = gemm_mfma_supported(w.win), pd = gemm_mfma_supported(wd);
     const bool flash = flash_prefill_supported(dims.hd), po = flash && gemm_mfma_supported(wo);
     STAGE(ST_PREFILL_NORM,
           launch_layer_norm_rows(X, w.ln_w, w.ln_b, dims.eps, n, d, pin ? nullptr : H, stream, pin ? XH : nullptr,
                                  pin ? XL : nullptr),
           "layer_norm");
-    if ((rc = pin ? project_planes(w.win, n, Y, win_rows) : project(w.win, H, d, n, Y, win_rows))) return rc;
-    STAGE(ST_PREFILL_EPILOGUE,
-          launch_in_epilogue(dims, kv[l], Y, win_rows, rope, d_pos0, n, Q, pd && !tracing ? nullptr : M, stream,
-                             pd ? XH : nullptr, pd ? XL : nullptr),
-          "in_epilogue");
+    float *m32 = pd && !tracing ? nullptr : M;
+    if (pin && pd) {
+      const InEpilogue e{dims, kv[l], rope, d_pos0, Q, m32, MH, ML};
+      STAGE(ST_PREFILL_GEMM, launch_gemm_in_epilogue(w.win, XH, XL, n, e, stream), "projection + epilogue");
+    } else {
+      if ((rc = pin ? project_planes(w.win, XH, XL, n, Y, win_rows) : project(w.win, H, d, n, Y, win_rows)))
+        return rc;
+      STAGE(ST_PREFILL_EPILOGUE,
+            launch_in_epilogue(dims, kv[l], Y, win_rows, rope, d_pos0, n, Q, m32, stream, pd ? MH : nullptr,
+                               pd ? ML : nullptr),
+            "in_epilogue");
+    }
     int sp = 1, sd = 1;
-    if ((rc = pd ? project_planes(wd, n, D, d, &sd) : project(wd, M, I, n, D, d, &sd))) return rc;
+    if ((rc = pd ? project_planes(wd, MH, ML, n, D, d, &sd) : project(wd, M, I, n, D, d, &sd))) return rc;
     if (flash)
       STAGE(ST_PREFILL_ATTENTION,
             launch_flash_prefill(dims, kv[l], Q, d_pos0, n, po && !tracing ? nullptr : A, stream, po ? XH : nullptr,
@@ -828,7 +838,7 @@ int StableModel::prefill_chunk(const int32_t *ids, int n, int start, bool want_l
     else
       STAGE(ST_PREFILL_ATTENTION,
             launch_attention(dims, kv[l], Q, d_pos0, n, start + n - 1, partials, counters, A, stream), "attention");
-    if ((rc = po ? project_planes(wo, n, P, d, &sp) : project(wo, A, d, n, P, d, &sp))) return rc;
+    if ((rc = po ? project_planes(wo, XH, XL, n, P, d, &sp) : project(wo, A, d, n, P, d, &sp))) return rc;
     STAGE(ST_PREFILL_ELEMENTWISE, launch_residual(X, P, sp, D, sd, (int64_t)n * d, stream), "residual");
     if (tracing) {
       TRY_HIP(launch_copy_row(X + (size_t)(n - 1) * d, trace_dev + (size_t)l * d, d, stream), "trace");

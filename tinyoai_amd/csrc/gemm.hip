@@ -1,27 +1,26 @@
 // Prefill projections on the gfx950 matrix cores: Y[M][N] = X[M][K] * W^T
-// with v_mfma_f32_16x16x32_bf16 (fp32 accumulation).
+// with v_mfma_f32_32x32x16_bf16 (fp32 accumulation).
 //
-// Operands: X arrives as bf16 planes (split_bf16 below): with XS = 2 the
-// pair hi + lo carries 16 significant bits of every activation, with XS = 1
-// only hi. BF16 weights feed the cores as stored. Q8_0 quants (|q| <= 128)
-// are exact in bf16; each K step of 32 is one Q8_0 block, so the block
-// product is formed without scale and added as acc += d * block on the
-// fp32 accumulators, which keeps the weights exact.
+// Operands: X arrives as bf16 planes (split_bf16 below, or written so by the
+// producing kernel): with XS = 2 the pair hi + lo carries 16 significant
+// bits of every activation, with XS = 1 only hi. BF16 weights feed the
+// cores as stored. Q8_0 quants (|q| <= 128) are exact in bf16; each quant
+// block's product is formed without scale and added as acc += d * block on
+// the fp32 accumulators, which keeps the weights exact.
 //
-// Tiling: 128 x 128 output per 256-thread block, four waves of 64 x 64
-// (4 x 4 tiles of 16 x 16), K step 32, double-buffered LDS. LDS rows are
-// padded to 80 bytes so the 16-byte fragment reads of 16 consecutive rows
-// cover all 64 banks once.
+// The in-projection can finish in the kernel itself: with EPI the output
+// pairs of win go through the fused epilogue (RoPE, KV append, SiLU-gate)
+// instead of being stored.
 #include <algorithm>
 
-#include "kernels.h"
+#include "epilogue.h"
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 namespace {
 
-constexpr int kBM = 128, kBN = 128, kBK = 32, kRow = 40;  // LDS row: 40 bf16 = 80 B
+constexpr int kKAlign = 32;  // K of the matrix-core products: a multiple of 32 (one Q8_0 block)
 
 __device__ __forceinline__ uint32_t bf16_bits(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
 
@@ -44,176 +43,13 @@ struct GemmArgs {
   float *y;
   int ldy;
   int ksplit;                 // K ranges summed separately: split s writes y + s * M * ldy
+  InEpilogue e;               // the fused in-projection epilogue (EPI instances)
 };
 
 // The K steps of split s of `splits` (nk steps in all): [k_lo, k_hi).
 __device__ __forceinline__ void split_range(int nk, int splits, int s, int &k_lo, int &k_hi) {
   k_lo = (int)((int64_t)nk * s / splits);
   k_hi = (int)((int64_t)nk * (s + 1) / splits);
-}
-
-template <int WF, int XS>
-__global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
-  __shared__ __align__(16) uint16_t sa[2][XS][kBM * kRow];
-  __shared__ __align__(16) uint16_t sb[2][kBN * kRow];
-  __shared__ float ss[2][kBN];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-  const int K = g.w.cols, N = g.w.rows, nk = K / kBK;
-  // Tile order: workgroups are dispatched round-robin over the 8 XCDs, each
-  // with its own L2. Consecutive workgroups of one XCD take the M tiles of
-  // one N tile, so a weight tile is fetched from HBM once and re-read from
-  // that XCD's L2 by the other M tiles.
-  const int MT = (g.M + kBM - 1) / kBM, NT = (N + kBN - 1) / kBN;
-  const int per_split = (NT + 7) / 8 * 8 * MT, b = blockIdx.x % per_split, split = blockIdx.x / per_split;
-  const int xcd = b & 7, slot = b >> 3;
-  const int nt = xcd + 8 * (slot / MT), mt = slot % MT;
-  if (nt >= NT) return;  // the grid rounds NT up to a multiple of 8
-  const int m0 = mt * kBM, n0 = nt * kBN;
-  int k_lo, k_hi;
-  split_range(nk, g.ksplit, split, k_lo, k_hi);
-  float *y = g.y + (int64_t)split * g.M * g.ldy;
-  const int srow = tid >> 1, shalf = tid & 1;  // staging: one row half (16 K values) per thread
-
-  uint4 rah0, rah1, ral0, ral1, rb[2];
-  uint16_t rs = 0;
-  auto gload = [&](int kb) {
-    const int k = kb * kBK + shalf * 16;
-    const int m = m0 + srow;
-    if (m < g.M) {
-      const uint4 *p = reinterpret_cast<const uint4 *>(g.xh + (int64_t)m * K + k);
-      rah0 = p[0];
-      rah1 = p[1];
-      if constexpr (XS == 2) {
-        const uint4 *q = reinterpret_cast<const uint4 *>(g.xl + (int64_t)m * K + k);
-        ral0 = q[0];
-        ral1 = q[1];
-      }
-    } else {
-      rah0 = rah1 = ral0 = ral1 = make_uint4(0, 0, 0, 0);
-    }
-    const int n = n0 + srow;
-    if constexpr (WF == FMT_BF16) {
-      if (n < N) {
-        const uint4 *p = reinterpret_cast<const uint4 *>(g.w.vals + (int64_t)n * g.w.vstride + (int64_t)k * 2);
-        rb[0] = p[0];
-        rb[1] = p[1];
-      } else {
-        rb[0] = rb[1] = make_uint4(0, 0, 0, 0);
-      }
-    } else {
-      rb[0] = n < N ? *reinterpret_cast<const uint4 *>(g.w.vals + (int64_t)n * g.w.vstride + k)
-                    : make_uint4(0, 0, 0, 0);
-      if (tid < kBN)
-        rs = n0 + tid < N ? reinterpret_cast<const uint16_t *>(g.w.meta + (int64_t)(n0 + tid) * g.w.mstride)[kb] : 0;
-    }
-  };
-  auto lstore = [&](int buf) {
-    {
-      uint4 *d = reinterpret_cast<uint4 *>(&sa[buf][0][srow * kRow + shalf * 16]);
-      d[0] = rah0;
-      d[1] = rah1;
-      if constexpr (XS == 2) {
-        uint4 *e = reinterpret_cast<uint4 *>(&sa[buf][XS - 1][srow * kRow + shalf * 16]);
-        e[0] = ral0;
-        e[1] = ral1;
-      }
-    }
-    uint4 *d = reinterpret_cast<uint4 *>(&sb[buf][srow * kRow + shalf * 16]);
-    if constexpr (WF == FMT_BF16) {
-      d[0] = rb[0];
-      d[1] = rb[1];
-    } else {  // 16 int8 -> 16 bf16, exact
-      const uint32_t ws[4] = {rb[0].x, rb[0].y, rb[0].z, rb[0].w};
-      uint32_t o[8];
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const uint32_t v = ws[i];
-        o[2 * i] = bf16_bits((float)(int8_t)v) | bf16_bits((float)(int8_t)(v >> 8)) << 16;
-        o[2 * i + 1] = bf16_bits((float)(int8_t)(v >> 16)) | bf16_bits((float)(int8_t)(v >> 24)) << 16;
-      }
-      d[0] = make_uint4(o[0], o[1], o[2], o[3]);
-      d[1] = make_uint4(o[4], o[5], o[6], o[7]);
-      if (tid < kBN) ss[buf][tid] = hw_half(rs);
-    }
-  };
-
-  f32x4 acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; i++)
-#pragma unroll
-    for (int j = 0; j < 4; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-  if (k_lo < k_hi) {
-    gload(k_lo);
-    lstore(0);
-  }
-  __syncthreads();
-  const int frow = lane & 15, fk = (lane >> 4) * 8;
-  for (int kb = k_lo; kb < k_hi; kb++) {
-    const int cur = (kb - k_lo) & 1;
-    if (kb + 1 < k_hi) gload(kb + 1);
-    bf16x8 bfr[4];
-#pragma unroll
-    for (int ni = 0; ni < 4; ni++)
-      bfr[ni] = *reinterpret_cast<const bf16x8 *>(&sb[cur][(wn * 64 + ni * 16 + frow) * kRow + fk]);
-    float sc[4];
-    if constexpr (WF == FMT_Q8_0) {
-#pragma unroll
-      for (int ni = 0; ni < 4; ni++) sc[ni] = ss[cur][wn * 64 + ni * 16 + frow];
-    }
-    bf16x8 afr[XS][4];
-#pragma unroll
-    for (int p = 0; p < XS; p++)
-#pragma unroll
-      for (int mi = 0; mi < 4; mi++)
-        afr[p][mi] = *reinterpret_cast<const bf16x8 *>(&sa[cur][p][(wm * 64 + mi * 16 + frow) * kRow + fk]);
-    // One plane's 16 products before the other's (no MFMA waits for the
-    // previous one's result).
-    if constexpr (WF == FMT_Q8_0) {
-      f32x4 t[4][4];
-#pragma unroll
-      for (int mi = 0; mi < 4; mi++)
-#pragma unroll
-        for (int ni = 0; ni < 4; ni++)
-          t[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(afr[0][mi], bfr[ni], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-      if constexpr (XS == 2) {
-#pragma unroll
-        for (int mi = 0; mi < 4; mi++)
-#pragma unroll
-          for (int ni = 0; ni < 4; ni++)
-            t[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(afr[1][mi], bfr[ni], t[mi][ni], 0, 0, 0);
-      }
-#pragma unroll
-      for (int mi = 0; mi < 4; mi++)
-#pragma unroll
-        for (int ni = 0; ni < 4; ni++)
-#pragma unroll
-          for (int i = 0; i < 4; i++) acc[mi][ni][i] = fmaf(sc[ni], t[mi][ni][i], acc[mi][ni][i]);
-    } else {
-#pragma unroll
-      for (int p = 0; p < XS; p++)
-#pragma unroll
-        for (int mi = 0; mi < 4; mi++)
-#pragma unroll
-          for (int ni = 0; ni < 4; ni++)
-            acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(afr[p][mi], bfr[ni], acc[mi][ni], 0, 0, 0);
-    }
-    if (kb + 1 < k_hi) lstore(cur ^ 1);
-    __syncthreads();
-  }
-  // D fragment: lane holds rows 4 * (lane / 16) + i of column lane % 16.
-#pragma unroll
-  for (int mi = 0; mi < 4; mi++)
-#pragma unroll
-    for (int ni = 0; ni < 4; ni++) {
-      const int n = n0 + wn * 64 + ni * 16 + frow;
-      if (n >= N) continue;
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const int m = m0 + wm * 64 + mi * 16 + (lane >> 4) * 4 + i;
-        if (m < g.M) y[(int64_t)m * g.ldy + n] = acc[mi][ni][i];
-      }
-    }
 }
 
 // ------------------------------------------------------------ large tiles
@@ -232,6 +68,11 @@ constexpr int kLThreads = 512;
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 template <int WF, int XS>
+constexpr size_t gemm_large_lds() {
+  return (size_t)2 * (XS * kLM * kLRow + kLN * kLRow + (WF == FMT_Q8_0 ? 2 * kLN * 2 : 0)) * 2;
+}
+
+template <int WF, int XS, bool EPI>
 __global__ __launch_bounds__(kLThreads) void gemm_large_kernel(GemmArgs g) {
   extern __shared__ __align__(16) uint16_t lds16[];
   // per stage: A planes [XS][kLM][kLRow], B [kLN][kLRow], scales [2][kLN] floats (Q8_0)
@@ -440,6 +281,50 @@ __global__ __launch_bounds__(kLThreads) void gemm_large_kernel(GemmArgs g) {
     }
   }
   // D fragment: lane holds column lane % 32 of rows (v / 4) * 8 + (lane / 32) * 4 + v % 4.
+  if constexpr (EPI) {
+    // The block's output tile goes to LDS (free once every wave's last
+    // products are formed), then threads take (token, row pair of win)
+    // items in order through the in-projection epilogue, as
+    // in_epilogue_kernel does per token: neighbouring threads store
+    // neighbouring outputs.
+    constexpr int kPitch = kLN + 4;  // floats: the lane groups' rows fall on different banks
+    static_assert(kLM * kPitch * 4 <= gemm_large_lds<WF, XS>(), "output tile fits the staging LDS");
+    float *tile = reinterpret_cast<float *>(lds16);
+    __syncthreads();
+#pragma unroll
+    for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+      for (int ni = 0; ni < 2; ni++)
+#pragma unroll
+        for (int v = 0; v < 16; v++)
+          tile[(wm * 64 + mi * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3)) * kPitch + wn * 64 + ni * 32 + frow] =
+              acc[mi][ni][v];
+    __syncthreads();
+    // Values, not references into the kernel arguments (a reference makes
+    // the compiler copy the argument block to per-lane scratch).
+    const StableDims es = g.e.s;
+    const KVDev ekv = g.e.kv;
+    const float *rope = g.e.rope;
+    float *eq = g.e.q, *em = g.e.m;
+    uint16_t *emh = g.e.mh, *eml = g.e.ml;
+    const int p0 = *g.e.pos0, mu0 = (es.win_q + 2 * es.win_kv) / 2;
+    for (int it = tid; it < kLM * (kLN / 2); it += kLThreads) {
+      const int r = it / (kLN / 2), c = 2 * (it % (kLN / 2)), m = m0 + r, n = n0 + c, u = n >> 1;
+      if (m >= g.M || n >= N) continue;
+      const float2 pv = *reinterpret_cast<const float2 *>(tile + r * kPitch + c);
+      if (u >= mu0) {
+        const float gv = es.silu ? silu_gate_llama(pv.x, pv.y) : silu_gate(pv.x, pv.y);
+        const int64_t i = (int64_t)m * es.inter + (u - mu0);
+        if (em) em[i] = gv;
+        store_bf16_split(emh, eml, i, gv);
+      } else {
+        const int pos = p0 + m;
+        in_pair_epilogue(es, ekv, rope + (int64_t)pos * es.rot, pos, u, pv.x, pv.y,
+                         eq + (int64_t)m * es.heads * es.hd, nullptr);
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int mi = 0; mi < 2; mi++)
 #pragma unroll
@@ -454,35 +339,23 @@ __global__ __launch_bounds__(kLThreads) void gemm_large_kernel(GemmArgs g) {
     }
 }
 
-template <int WF, int XS>
-constexpr size_t gemm_large_lds() {
-  return (size_t)2 * (XS * kLM * kLRow + kLN * kLRow + (WF == FMT_Q8_0 ? 2 * kLN * 2 : 0)) * 2;
-}
-
-template <int WF, int XS>
+template <int WF, int XS, bool EPI = false>
 hipError_t gemm_large_launch(const GemmArgs &g, hipStream_t st) {
   constexpr size_t lds = gemm_large_lds<WF, XS>();
-  static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemm_large_kernel<WF, XS>),
-                                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  static const hipError_t attr = hipFuncSetAttribute(
+      reinterpret_cast<const void *>(&gemm_large_kernel<WF, XS, EPI>), hipFuncAttributeMaxDynamicSharedMemorySize,
+      (int)lds);
   if (attr != hipSuccess) return attr;
   const int NT = (g.w.rows + kLN - 1) / kLN, MT = (g.M + kLM - 1) / kLM;
   dim3 grid((NT + 7) / 8 * 8 * MT * g.ksplit);
-  hipLaunchKernelGGL((gemm_large_kernel<WF, XS>), grid, dim3(kLThreads), lds, st, g);
-  return hipGetLastError();
-}
-
-template <int WF, int XS>
-hipError_t gemm_launch(const GemmArgs &g, hipStream_t st) {
-  const int NT = (g.w.rows + kBN - 1) / kBN, MT = (g.M + kBM - 1) / kBM;
-  dim3 grid((NT + 7) / 8 * 8 * MT * g.ksplit);
-  hipLaunchKernelGGL((gemm_kernel<WF, XS>), grid, dim3(256), 0, st, g);
+  hipLaunchKernelGGL((gemm_large_kernel<WF, XS, EPI>), grid, dim3(kLThreads), lds, st, g);
   return hipGetLastError();
 }
 
 }  // namespace
 
 bool gemm_mfma_supported(const MatDesc &w) {
-  return (w.fmt == FMT_Q8_0 || w.fmt == FMT_BF16) && w.cols % kBK == 0 && w.vstride % 16 == 0;
+  return (w.fmt == FMT_Q8_0 || w.fmt == FMT_BF16) && w.cols % kKAlign == 0 && w.vstride % 16 == 0;
 }
 
 int gemm_planes(const MatDesc &) { return 2; }
@@ -496,10 +369,7 @@ hipError_t launch_split_bf16(const float *x, int ldx, int k, int64_t rows, uint1
 }
 
 int gemm_splits(const MatDesc &w, int M, int max_splits) {
-  const bool large = true;
-  const int NT = (w.rows + (large ? kLN : kBN) - 1) / (large ? kLN : kBN);
-  const int MT = (M + (large ? kLM : kBM) - 1) / (large ? kLM : kBM);
-  const int nk = (w.cols + (large ? kLK : kBK) - 1) / (large ? kLK : kBK);
+  const int NT = (w.rows + kLN - 1) / kLN, MT = (M + kLM - 1) / kLM, nk = (w.cols + kLK - 1) / kLK;
   // about one block per CU, at least 4 K steps per split
   int s = std::max(1, 256 / std::max(1, NT * MT));
   s = std::min({s, max_splits, std::max(1, nk / 4)});
@@ -509,7 +379,16 @@ int gemm_splits(const MatDesc &w, int M, int max_splits) {
 hipError_t launch_gemm_mfma(const MatDesc &w, const uint16_t *xh, const uint16_t *xl, int M, float *y, int ldy,
                             hipStream_t st, int ksplit) {
   if (!gemm_mfma_supported(w) || ksplit < 1) return hipErrorInvalidValue;
-  GemmArgs g{w, xh, xl, M, y, ldy, ksplit};
+  GemmArgs g{w, xh, xl, M, y, ldy, ksplit, {}};
   if (w.fmt == FMT_Q8_0) return xl ? gemm_large_launch<FMT_Q8_0, 2>(g, st) : gemm_large_launch<FMT_Q8_0, 1>(g, st);
   return xl ? gemm_large_launch<FMT_BF16, 2>(g, st) : gemm_large_launch<FMT_BF16, 1>(g, st);
+}
+
+hipError_t launch_gemm_in_epilogue(const MatDesc &w, const uint16_t *xh, const uint16_t *xl, int M,
+                                   const InEpilogue &e, hipStream_t st) {
+  if (!gemm_mfma_supported(w) || !xl || !e.mh || !e.ml || !e.q || !e.rope || !e.pos0 || w.rows % 2 ||
+      e.s.win_q % 2)
+    return hipErrorInvalidValue;
+  GemmArgs g{w, xh, xl, M, nullptr, 0, 1, e};
+  return w.fmt == FMT_Q8_0 ? gemm_large_launch<FMT_Q8_0, 2, true>(g, st) : gemm_large_launch<FMT_BF16, 2, true>(g, st);
 }

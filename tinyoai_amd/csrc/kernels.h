@@ -184,6 +184,22 @@ int gemm_planes(const MatDesc &w);
 int gemm_splits(const MatDesc &w, int M, int max_splits);
 hipError_t launch_gemm_mfma(const MatDesc &w, const uint16_t *xh, const uint16_t *xl, int M, float *y, int ldy,
                             hipStream_t st, int ksplit = 1);
+// The fused in-projection epilogue of a matrix-core win product for M
+// tokens at positions *pos0 + j: RoPE'd q [M][heads*hd], K/V into the
+// cache, and the SiLU-gate outputs as bf16 planes mh, ml [M][inter] (and
+// fp32 m [M][inter] when m is not null), as launch_in_epilogue forms them
+// from y.
+struct InEpilogue {
+  StableDims s;
+  KVDev kv;
+  const float *rope;
+  const int *pos0;
+  float *q;
+  float *m;
+  uint16_t *mh, *ml;
+};
+hipError_t launch_gemm_in_epilogue(const MatDesc &w, const uint16_t *xh, const uint16_t *xl, int M,
+                                   const InEpilogue &e, hipStream_t st);
 // x fp32 [rows][k] (row stride ldx) -> bf16 hi [rows][k] and lo = x - hi.
 hipError_t launch_split_bf16(const float *x, int ldx, int k, int64_t rows, uint16_t *hi, uint16_t *lo,
                              hipStream_t st);

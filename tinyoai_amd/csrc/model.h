@@ -102,6 +102,7 @@ struct StableModel {
   float *X = nullptr, *H = nullptr, *Y = nullptr, *Q = nullptr, *M = nullptr, *A = nullptr, *P = nullptr,
         *D = nullptr;
   uint16_t *XH = nullptr, *XL = nullptr;
+  uint16_t *MH = nullptr, *ML = nullptr;  // the SiLU-gate outputs as bf16 planes (down projection operand)
   void *h_pinned = nullptr;
   hipEvent_t params_copied = nullptr;  // last H2D copy out of h_pinned's parameter slot
   bool tracing = false;
@@ -148,8 +149,9 @@ struct StableModel {
   // y = x * W^T; with `splits`, the product may come as *splits K-split
   // partials n * ldy floats apart (y holds kPrefillSplits of them).
   int project(const MatDesc &w, const float *x, int ldx, int n, float *y, int ldy, int *splits = nullptr);
-  // y = X * W^T with X already in the bf16 planes XH, XL (matrix-core formats).
-  int project_planes(const MatDesc &w, int n, float *y, int ldy, int *splits = nullptr);
+  // y = X * W^T with X already in bf16 planes xh, xl (matrix-core formats).
+  int project_planes(const MatDesc &w, const uint16_t *xh, const uint16_t *xl, int n, float *y, int ldy,
+                     int *splits = nullptr);
   int prefill_chunk(const int32_t *ids, int n, int start, bool want_logits);
   int forward(int prefix, const int32_t *tokens, int n, bool want_logits, float *logits);
 };
