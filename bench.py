@@ -133,6 +133,8 @@ def main():
     ap.add_argument("--dtype", choices=["q8_0", "bf16"], default="q8_0",
                     help="weight format (bf16 with --prompt 8129 --generate 64 --kv 16: the long-context workload)")
     ap.add_argument("--kv", type=int, choices=[16, 32], default=32, help="KV cache bits")
+    ap.add_argument("--att-steps", type=int, choices=[0, 1, 2, 4, 8, 16], default=0,
+                    help="decode attention positions per block / 64 (0 = chosen from the position)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the path would shard by "
@@ -154,6 +156,7 @@ def main():
     print(f"[bench] synthetic weights in {gen_s:.1f}s", file=sys.stderr, flush=True)
     fwd = hip.StableLMForwarder(config, tensors)
     fwd.set_kv_bits(args.kv)
+    fwd.set_launch("attention", args.att_steps, 0)
     print("[bench] weights resident in HBM", file=sys.stderr, flush=True)
     rng = np.random.default_rng(args.seed + 1)
     prompt = rng.integers(0, config["vocab_size"], args.prompt).astype(np.int32)

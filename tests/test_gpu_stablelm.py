@@ -173,6 +173,42 @@ def test_three_b_shapes_two_layers(hip, oracle):
     assert toks_gpu == toks_ref
 
 
+@pytest.mark.parametrize("kv_bits", [32, 16])
+def test_decode_attention_shapes_agree(hip, kv_bits):
+    """Every decode attention shape (64, 128 and 256 positions per 4-wave
+    block; 512 and 1024 per 16-wave block) against the shape chosen from the
+    position, at the 3B head layout: 40 decode tokens from position 1000
+    cross the 1024-position block boundary (one split, then two). Logits and
+    per-layer residuals within 2e-5 of their range (only the order of the
+    softmax sums differs), identical greedy tokens."""
+    config = W.validate_stablelm_config(dict(W.STABLELM_3B, num_hidden_layers=3, max_position_embeddings=2048))
+    tensors = W.synthetic_stablelm(config, W.Q8_0, seed=9)
+    prompt = np.random.default_rng(13).integers(0, 65536, 1000).astype(np.int32)
+    shapes = [0, 1, 4, 8, 16]
+    fwds = {}
+    for steps in shapes:
+        f = hip.StableLMForwarder(config, tensors)
+        f.set_kv_bits(kv_bits)
+        f.set_launch("attention", steps, 0)
+        f.trace(True)
+        fwds[steps] = f
+    logits = {k: f.forward(0, prompt) for k, f in fwds.items()}
+    for step in range(40):
+        tok = int(np.argmax(logits[0]))
+        for k in shapes[1:]:
+            assert int(np.argmax(logits[k])) == tok, (k, step)
+        logits = {k: f.forward(1000 + step, [tok]) for k, f in fwds.items()}
+        span = float(np.ptp(logits[0]))
+        tr = fwds[0].trace_read()
+        for k in shapes[1:]:
+            assert np.max(np.abs(logits[k] - logits[0])) <= 2e-5 * span, (k, step)
+            assert np.max(np.abs(fwds[k].trace_read() - tr)) <= 2e-5 * float(np.ptp(tr)), (k, step)
+    with pytest.raises(RuntimeError):
+        fwds[0].set_launch("attention", 3, 0)
+    for f in fwds.values():
+        f.close()
+
+
 @pytest.mark.parametrize("dtype,kv_bits", [(W.Q8_0, 32), (W.Q8_0, 16), (W.BF16, 32)])
 def test_persistent_decode_matches_per_kernel_path(hip, dtype, kv_bits):
     """The single-launch decode (one cooperative kernel per token) against

@@ -737,7 +737,8 @@ int StableModel::decode_step(int token, int pos, bool want_logits) {
     }
     return TINYOAI_OK;
   }
-  const int steps = attention_steps(pos, dims.heads), splits = attention_splits(pos, steps);
+  const int steps = att_steps > 0 ? att_steps : attention_steps(pos, dims.heads);
+  const int splits = attention_splits(pos, steps);
   if (prof.on || !use_graphs) return enqueue_decode(steps, splits, want_logits);
   const int64_t key = ((int64_t)steps << 40) | ((int64_t)splits << 8) | (want_logits ? 2 : 0) | (tracing ? 1 : 0);
   auto it = graphs.find(key);
@@ -1052,9 +1053,16 @@ int tinyoai_stablelm_set_persistent(tinyoai_model *m, int32_t enable) {
 
 int tinyoai_stablelm_set_launch(tinyoai_model *m, int32_t stage, int32_t grid, int32_t threads) {
   if (!m || !m->stable) return fail(TINYOAI_EINVAL, "not a StableLM handle");
+  StableModel &s = *m->stable;
+  if (stage == 3) {  // decode attention: grid = positions per block / 64 (0 = by position)
+    if (grid != 0 && grid != 1 && grid != 2 && grid != 4 && grid != 8 && grid != 16)
+      return fail(TINYOAI_EINVAL, "attention steps %d", grid);
+    s.att_steps = grid;
+    s.drop_graphs();
+    return TINYOAI_OK;
+  }
   if (grid <= 0 || grid > (1 << 20) || (threads != 256 && threads != 512))
     return fail(TINYOAI_EINVAL, "launch shape %d x %d", grid, threads);
-  StableModel &s = *m->stable;
   switch (stage) {
     case 0: s.grid_in = grid; s.threads_in = threads; break;
     case 1: s.grid_out = grid; s.threads_out = threads; break;

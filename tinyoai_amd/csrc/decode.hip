@@ -37,13 +37,37 @@ __device__ __forceinline__ void publish(float *p, float v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// One block of 4 waves per (split, head, query); a split covers
-// 4 * STEPS * 16 positions. Lane = 4 * position-in-step + dim group: four
-// lanes share a position, each holding hd/4 dimensions. Online-softmax
+// Dimension held in register r by lane group g of a position's four lanes.
+// When hd/4 is a multiple of 4, the lanes interleave 4-value chunks
+// (group g holds chunks g, g + 4, ...), so one load instruction reads 4
+// adjacent chunks of each position: 64 contiguous bytes of an fp32 row
+// (32 of an fp16 row) instead of four pieces a quarter-row apart.
+template <int DPL>
+__device__ __forceinline__ constexpr int att_dim(int g, int r) {
+  return DPL % 4 == 0 ? ((r >> 2) * 4 + g) * 4 + (r & 3) : g * DPL + r;
+}
+
+// Loads the DPL values of lane group g from the row at element e.
+template <int DPL, bool HALF>
+__device__ __forceinline__ void load_kv_lanes(const void *base, int64_t e, int g, float *r) {
+  if constexpr (DPL % 4 == 0) {
+#pragma unroll
+    for (int c = 0; c < DPL / 4; c++) load_kv<4, HALF>(base, e + att_dim<DPL>(g, 4 * c), r + 4 * c);
+  } else {
+    load_kv<DPL, HALF>(base, e + g * DPL, r);
+  }
+}
+
+// One block of WAVES waves per (split, head, query); a split covers
+// WAVES * STEPS * 16 positions. Lane = 4 * position-in-step + dim group:
+// four lanes share a position, each holding hd/4 dimensions. Online-softmax
 // partials combine across the waves in LDS, then across the splits of a
-// (query, head) in the last block to finish (the others exit).
-template <int HD, bool HALF, int STEPS>
-__global__ __launch_bounds__(kThreads) void attention_kernel(AttArgs a) {
+// (query, head) in the last block to finish (the others exit). With 16
+// waves a block covers up to 1024 positions, so a short context needs one
+// block per head and no cross-block combine at all.
+template <int HD, bool HALF, int STEPS, int WAVES = kWaves>
+__global__ __launch_bounds__(WAVES * 64) void attention_kernel(AttArgs a) {
+  constexpr int kWaves = WAVES, kThreads = WAVES * 64;
   constexpr int DPL = HD / 4;
   constexpr int SPLIT = kWaves * STEPS * 16;
   __shared__ float s_m[kWaves], s_l[kWaves], s_o[kWaves][HD];
@@ -53,10 +77,10 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttArgs a) {
   const int split = blockIdx.x, h = blockIdx.y, j = blockIdx.z;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane & 3, pl = lane >> 2;
   const int kvh = h / (s.heads / s.kv_heads);
-  const float *q = a.q + (int64_t)j * s.heads * HD + h * HD + g * DPL;
+  const float *q = a.q + (int64_t)j * s.heads * HD + h * HD;
   float qr[DPL];
 #pragma unroll
-  for (int i = 0; i < DPL; i++) qr[i] = q[i];
+  for (int i = 0; i < DPL; i++) qr[i] = q[att_dim<DPL>(g, i)];
   const int64_t head_base = (int64_t)kvh * a.kv.cap * HD;
   const int t0 = split * SPLIT + wave * STEPS * 16 + pl;
   // The block's K (and V) entries are loaded before the query position
@@ -68,9 +92,9 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttArgs a) {
   float kr[STEPS][DPL], vr[STEPS][DPL];
 #pragma unroll
   for (int st = 0; st < STEPS; st++) {
-    const int64_t e = head_base + (int64_t)min(t0 + st * 16, a.kv.cap - 1) * HD + g * DPL;
-    load_kv<DPL, HALF>(a.kv.k, e, kr[st]);
-    if constexpr (kEarlyV) load_kv<DPL, HALF>(a.kv.v, e, vr[st]);
+    const int64_t e = head_base + (int64_t)min(t0 + st * 16, a.kv.cap - 1) * HD;
+    load_kv_lanes<DPL, HALF>(a.kv.k, e, g, kr[st]);
+    if constexpr (kEarlyV) load_kv_lanes<DPL, HALF>(a.kv.v, e, g, vr[st]);
   }
   const int pos = *a.pos0 + j;
   const int npos = pos + 1;
@@ -95,7 +119,7 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttArgs a) {
   if constexpr (!kEarlyV) {
 #pragma unroll
     for (int st = 0; st < STEPS; st++)
-      if (t0 + st * 16 < npos) load_kv<DPL, HALF>(a.kv.v, head_base + (int64_t)(t0 + st * 16) * HD + g * DPL, vr[st]);
+      if (t0 + st * 16 < npos) load_kv_lanes<DPL, HALF>(a.kv.v, head_base + (int64_t)(t0 + st * 16) * HD, g, vr[st]);
   }
   float o[DPL];
 #pragma unroll
@@ -123,7 +147,7 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttArgs a) {
   if (lane == 0) { s_m[wave] = mx; s_l[wave] = l; }
   if (pl == 0) {
 #pragma unroll
-    for (int i = 0; i < DPL; i++) s_o[wave][g * DPL + i] = o[i];
+    for (int i = 0; i < DPL; i++) s_o[wave][att_dim<DPL>(g, i)] = o[i];
   }
   __syncthreads();
   // combine the waves (a wave with no valid position has m = -inf, l = 0)
@@ -180,7 +204,9 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttArgs a) {
   m = wave_max(m);
   if (lane == 0) s_m[wave] = m;
   __syncthreads();
-  m = fmaxf(fmaxf(s_m[0], s_m[1]), fmaxf(s_m[2], s_m[3]));
+  m = s_m[0];
+#pragma unroll
+  for (int w = 1; w < kWaves; w++) m = fmaxf(m, s_m[w]);
   float lsum = 0.f;
   for (int sp = tid; sp < nsplit; sp += kThreads) {
     const float e = expf(base[sp * (HD + 2)] - m);
@@ -191,7 +217,13 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttArgs a) {
   __syncthreads();
   if (lane == 0) s_l[wave] = lsum;
   __syncthreads();
-  const float Ltot = (s_l[0] + s_l[1]) + (s_l[2] + s_l[3]);
+  float Ltot = 0.f;
+  if constexpr (kWaves == 4) {
+    Ltot = (s_l[0] + s_l[1]) + (s_l[2] + s_l[3]);
+  } else {
+#pragma unroll
+    for (int w = 0; w < kWaves; w++) Ltot += s_l[w];
+  }
   for (int d = tid; d < HD; d += kThreads) {
     float acc = 0.f;
 #pragma unroll 8
@@ -203,11 +235,22 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttArgs a) {
 
 template <int HD, bool HALF>
 hipError_t launch_attention_hd(const AttArgs &a, int nq, int splits, int steps, hipStream_t st) {
+  // `steps` = positions per block / 64: 1, 2 and 4 on 4-wave blocks, 8 and
+  // 16 on 16-wave blocks (2 and 4 positions of 16 per wave).
   dim3 grid(splits, a.s.heads, nq);
   switch (steps) {
     case 1: TINYOAI_TIMED_LAUNCH((attention_kernel<HD, HALF, 1>), grid, dim3(kThreads), 0, st, a); break;
     case 2: TINYOAI_TIMED_LAUNCH((attention_kernel<HD, HALF, 2>), grid, dim3(kThreads), 0, st, a); break;
     case 4: TINYOAI_TIMED_LAUNCH((attention_kernel<HD, HALF, 4>), grid, dim3(kThreads), 0, st, a); break;
+    case 8:
+    case 16:
+      // 16-wave blocks hold at most 128 VGPRs per lane: wider heads would spill.
+      if constexpr (HD <= 80) {
+        if (steps == 8) TINYOAI_TIMED_LAUNCH((attention_kernel<HD, HALF, 2, 16>), grid, dim3(1024), 0, st, a);
+        else TINYOAI_TIMED_LAUNCH((attention_kernel<HD, HALF, 4, 16>), grid, dim3(1024), 0, st, a);
+        break;
+      }
+      return hipErrorInvalidValue;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

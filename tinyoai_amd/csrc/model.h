@@ -109,6 +109,7 @@ struct StableModel {
   float *trace_dev = nullptr, *trace_att = nullptr, *trace_gate = nullptr;  // [L][d], [L][heads*hd], [L][inter]
   int grid_in = 0, grid_out = 0, grid_head = 0;
   int threads_in = 256, threads_out = 256, threads_head = 256;
+  int att_steps = 0;  // decode attention positions per block / 64; 0 = chosen by position
 
   // Persistent decode (one cooperative launch per token): device copies of
   // the layer and KV descriptors, per-layer handoff buffers, counters.
