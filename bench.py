@@ -93,6 +93,63 @@ def llama_stories(prompt_len=32, generate=256, seed=260):
             "ms_per_token": round(dt / generate * 1e3, 4), "first_tokens": toks[:8]}
 
 
+def q8_0_kernel(seed=2, reps=192, copies=16):
+    """The isolated Q8_0 product on a 6912 x 2560 weight (int8 uniform in
+    [-127, 127], fp16 d = RNE(|N(0, 0.02)| / 127), x ~ N(0, 1)): the decode
+    matvec (M = 1) and the batched product (M = 128: bf16 operand planes of
+    x, then the matrix-core GEMM) through tinyoai_weight_mul_device, timed
+    back to back with events on the stream the kernels run on. The launches
+    cycle through `copies` device copies of the weight (16 x 18.8 MB, more
+    than the 256 MB last-level cache), so each reads its weight from HBM as
+    a decode step does, not from the cache that holds a repeated one. Algorithmic
+    bytes count W once plus x and y; flops are 2 * M * 6912 * 2560. Results
+    are checked against a float64 dequant-dot (every row at M = 1, the
+    first 256 rows at M = 128), relative to sum |x * w| of each output."""
+    import numpy as np
+    import torch
+    from tinyoai_amd import hip, weights as W
+    rows, cols = 6912, 2560
+    rng = np.random.default_rng(seed)
+    t = W.synthetic_q8_0(rows, cols, rng)
+    raw = np.frombuffer(t.data, np.uint8).reshape(-1, 34)
+    d = raw[:, :2].copy().view(np.float16).ravel().astype(np.float64)
+    wref = (raw[:, 2:].view(np.int8).astype(np.float64) * d[:, None]).reshape(rows, cols)
+    ws = [hip.Weight(t) for _ in range(copies)]
+    w = ws[0]
+    st = torch.cuda.current_stream()
+    out = {}
+    for m in (1, 128):
+        x = torch.randn(m, cols, generator=torch.Generator().manual_seed(seed + m)).cuda()
+        y = torch.empty(m, rows, device="cuda")
+        for c in ws:  # also sizes each copy's bf16 operand-plane buffer outside the timed loop
+            c.mul_device(x.data_ptr(), m, y.data_ptr(), st.cuda_stream)
+        torch.cuda.synchronize()
+        xr = x.cpu().double().numpy()
+        nr = rows if m == 1 else 256
+        yref = xr @ wref[:nr].T
+        bound = np.abs(xr) @ np.abs(wref[:nr]).T
+        err = float(np.max(np.abs(y.cpu().double().numpy()[:, :nr] - yref) / bound))
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(st)
+        for i in range(reps):
+            ws[i % copies].mul_device(x.data_ptr(), m, y.data_ptr(), st.cuda_stream)
+        e1.record(st)
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / reps
+        nbytes = rows * cols // 32 * 34 + 4 * m * (cols + rows)
+        flops = 2.0 * m * rows * cols
+        out[f"m{m}"] = {"us_per_product": round(us, 3), "hbm_gbs": round(nbytes / us / 1e3, 1),
+                        "hbm_frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4),
+                        "tflops": round(flops / us / 1e6, 2),
+                        "mfma_frac_bf16": round(flops / us / 1e6 / 2500.0, 4),
+                        "algorithmic_bytes": nbytes, "flops": int(flops), "max_rel_err": err}
+    for c in ws:
+        c.close()
+    out["workload"] = (f"Q8_0 6912x2560 (GGUF 34-byte blocks), fp32 x ~ N(0,1); M=1 matvec, M=128 product; "
+                       f"launches cycle through {copies} device copies of the weight")
+    return out
+
+
 def cpu_baseline(config, tensors, threads, prompt_len):
     """The oracle (C restatement of the Go scalar engine) on the host cores:
     a 128-token batched prefill chunk (prefillBatch) and 2 decode forwards
@@ -243,6 +300,7 @@ def main():
     }
     fwd.close()
     out["llama"] = llama_stories()
+    out["kernel_q8_0"] = q8_0_kernel()
     if not args.no_cpu:
         print("[bench] timing the CPU oracle", file=sys.stderr, flush=True)
         out["cpu_baseline"] = cpu_baseline(config, tensors, args.cpu_threads, args.prompt)
