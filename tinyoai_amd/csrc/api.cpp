@@ -403,7 +403,7 @@ int StableModel::init(const tinyoai_stablelm_config &c, const tinyoai_tensor *te
   if ((rc = load("lm_head.weight", c.vocab_size, d, head))) return rc;
   if ((rc = load_vec("model.norm.weight", &norm_w))) return rc;
   if ((rc = load_vec("model.norm.bias", &norm_b))) return rc;
-  mats.resize((size_t)c.num_hidden_layers * 2);
+  mats.resize((size_t)c.num_hidden_layers * 4);
   layers.resize(c.num_hidden_layers);
   win_rows = d + 2 * kvw + 2 * I;
   auto find = [&](const std::string &name, int64_t rows, int64_t cols, const tinyoai_tensor **t) -> int {
@@ -430,28 +430,39 @@ int StableModel::init(const tinyoai_stablelm_config &c, const tinyoai_tensor *te
     const tinyoai_tensor *t[7];
     for (int i = 0; i < 7; i++)
       if ((rc = find(p + names[i], shape[i][0], shape[i][1], &t[i]))) return rc;
-    const int32_t fin = t[0]->dtype, fout = t[3]->dtype;
-    if (t[1]->dtype != fin || t[2]->dtype != fin || t[4]->dtype != fin || t[5]->dtype != fin || t[6]->dtype != fout)
-      return fail(TINYOAI_EINVAL,
-                  "layer %d: q/k/v/gate/up must share one storage format, and o/down another", l);
-    // win: [q | k | v | gate/up interleaved], rotary pairs adjacent in q and k.
-    DevMatrix &win = mats[(size_t)l * 2], &wout = mats[(size_t)l * 2 + 1];
-    if ((rc = win.create(fin, win_rows, d, stream))) return rc;
+    const int32_t fin = t[0]->dtype, fmlp = t[4]->dtype, fout = t[3]->dtype, fdown = t[6]->dtype;
+    if (t[1]->dtype != fin || t[2]->dtype != fin || t[5]->dtype != fmlp)
+      return fail(TINYOAI_EINVAL, "layer %d: q/k/v must share one storage format, and gate/up another", l);
+    DevMatrix &win = mats[(size_t)l * 4], &wout = mats[(size_t)l * 4 + 1];
+    DevMatrix &win2 = mats[(size_t)l * 4 + 2], &wout2 = mats[(size_t)l * 4 + 3];
+    // win: [q | k | v | gate/up interleaved], rotary pairs adjacent in q and
+    // k; the gate/up pairs in a section of their own when their format differs.
+    const bool split_in = fmlp != fin, split_out = fdown != fout;
+    if ((rc = win.create(fin, split_in ? d + 2 * kvw : win_rows, d, stream))) return rc;
+    DevMatrix &mlp = split_in ? win2 : win;
+    const int64_t mlp0 = split_in ? 0 : d + 2 * kvw;
+    if (split_in && (rc = win2.create(fmlp, 2 * I, d, stream))) return rc;
     if ((rc = place(win, p + names[0], t[0], RowMap{ROWMAP_HEADS, 0, hd, dims.rot, 0}, 0)) ||
         (rc = place(win, p + names[1], t[1], RowMap{ROWMAP_HEADS, d, hd, dims.rot, 0}, 0)) ||
         (rc = place(win, p + names[2], t[2], RowMap{ROWMAP_IDENTITY, d + kvw, 0, 0, 0}, 0)) ||
-        (rc = place(win, p + names[4], t[4], RowMap{ROWMAP_INTERLEAVE, d + 2 * kvw, 0, 0, 0}, 0)) ||
-        (rc = place(win, p + names[5], t[5], RowMap{ROWMAP_INTERLEAVE, d + 2 * kvw, 0, 0, 1}, 0)))
+        (rc = place(mlp, p + names[4], t[4], RowMap{ROWMAP_INTERLEAVE, mlp0, 0, 0, 0}, 0)) ||
+        (rc = place(mlp, p + names[5], t[5], RowMap{ROWMAP_INTERLEAVE, mlp0, 0, 0, 1}, 0)))
       return rc;
-    // wout: [o | down] per output row, down starting on a chunk boundary.
-    const int64_t vpc = values_per_chunk(fout), down0 = (d + vpc - 1) / vpc * vpc;
-    if ((rc = wout.create(fout, d, down0 + I, stream))) return rc;
+    // wout: [o | down] per output row, down starting on a chunk boundary;
+    // o and down as matrices of their own when their formats differ.
+    const int64_t vpc = values_per_chunk(fout), down0 = split_out ? 0 : (d + vpc - 1) / vpc * vpc;
+    if ((rc = wout.create(fout, d, split_out ? d : down0 + I, stream))) return rc;
+    DevMatrix &down = split_out ? wout2 : wout;
+    if (split_out && (rc = wout2.create(fdown, d, I, stream))) return rc;
     if ((rc = place(wout, p + names[3], t[3], RowMap{ROWMAP_IDENTITY, 0, 0, 0, 0}, 0)) ||
-        (rc = place(wout, p + names[6], t[6], RowMap{ROWMAP_IDENTITY, 0, 0, 0, 0}, down0)))
+        (rc = place(down, p + names[6], t[6], RowMap{ROWMAP_IDENTITY, 0, 0, 0, 0}, down0)))
       return rc;
     LayerDev &L = layers[l];
     L.win = win.desc;
     L.wout = wout.desc;
+    L.win2 = split_in ? win2.desc : MatDesc{};
+    L.wout2 = split_out ? wout2.desc : MatDesc{};
+    mixed_layers |= split_in || split_out;
     if ((rc = load_vec(p + "input_layernorm.weight", &L.ln_w))) return rc;
     if ((rc = load_vec(p + "input_layernorm.bias", &L.ln_b))) return rc;
   }
@@ -524,7 +535,8 @@ int StableModel::init(const tinyoai_stablelm_config &c, const tinyoai_tensor *te
   threads_out = 256;
   grid_head = cus * 2;
   threads_head = 512;
-  pgrid = persistent_decode_grid(persistent_args(true), layers[0]);
+  // The single-launch decode streams fused layer matrices only.
+  pgrid = mixed_layers ? 0 : persistent_decode_grid(persistent_args(true), layers[0]);
   return TINYOAI_OK;
 }
 
@@ -681,15 +693,35 @@ int StableModel::upload_params(const int *head_vals, int nh, const int32_t *ids,
 // sequence can be captured once per shape.
 int StableModel::enqueue_decode(int steps, int splits, bool want_logits) {
   for (int l = 0; l < cfg.num_hidden_layers; l++) {
+    const LayerDev &w = layers[l];
+    const float *rope_row = reinterpret_cast<const float *>(params + 16);
     STAGE(ST_DECODE_IN,
-          launch_decode_in(layers[l], dims, kv[l], x, l == 0 ? &embed.desc : nullptr, params,
-                           reinterpret_cast<const float *>(params + 16), params + 1, qbuf, mbuf, grid_in, threads_in,
-                           stream),
+          launch_decode_in(w, dims, kv[l], x, l == 0 ? &embed.desc : nullptr, params, rope_row, params + 1, qbuf,
+                           mbuf, grid_in, threads_in, stream),
           "decode_in");
+    if (w.win2.rows) {  // the gate/up section in a format of its own: every row pair is a SiLU-gate pair
+      LayerDev wm = w;
+      wm.win = w.win2;
+      StableDims dm = dims;
+      dm.win_q = dm.win_kv = 0;
+      STAGE(ST_DECODE_IN,
+            launch_decode_in(wm, dm, kv[l], x, nullptr, params, rope_row, params + 1, qbuf, mbuf, grid_in, threads_in,
+                             stream),
+            "decode_in");
+    }
     STAGE(ST_ATTENTION,
           launch_attention(dims, kv[l], qbuf, params + 1, 1, 0, partials, counters, abuf, stream, steps, splits),
           "attention");
-    STAGE(ST_DECODE_OUT, launch_decode_out(layers[l].wout, dims.d, dims.inter, abuf, mbuf, x, grid_out, threads_out, stream), "decode_out");
+    if (w.wout2.rows) {  // o and down in formats of their own: x = (x + o*a) + down*m in two products
+      STAGE(ST_DECODE_OUT, launch_decode_out(w.wout, dims.d, 0, abuf, nullptr, x, grid_out, threads_out, stream),
+            "decode_out");
+      STAGE(ST_DECODE_OUT, launch_decode_out(w.wout2, dims.inter, 0, mbuf, nullptr, x, grid_out, threads_out, stream),
+            "decode_out");
+    } else {
+      STAGE(ST_DECODE_OUT,
+            launch_decode_out(w.wout, dims.d, dims.inter, abuf, mbuf, x, grid_out, threads_out, stream),
+            "decode_out");
+    }
     if (tracing) {
       const int hq = dims.heads * dims.hd;
       TRY_HIP(launch_copy_row(x, trace_dev + (size_t)l * dims.d, dims.d, stream), "trace");
@@ -803,22 +835,40 @@ int StableModel::prefill_chunk(const int32_t *ids, int n, int start, bool want_l
   STAGE(ST_EMBED, launch_embed(embed.desc, d_ids, n, X, stream), "embed");
   for (int l = 0; l < cfg.num_hidden_layers; l++) {
     const LayerDev &w = layers[l];
+    const bool split_in = w.win2.rows > 0, split_out = w.wout2.rows > 0;
     const int64_t vpc = values_per_chunk(w.wout.fmt), down0 = (d + vpc - 1) / vpc * vpc;
-    const MatDesc wo = column_view(w.wout, 0, d), wd = column_view(w.wout, down0, I);
+    const MatDesc wo = split_out ? w.wout : column_view(w.wout, 0, d);
+    const MatDesc wd = split_out ? w.wout2 : column_view(w.wout, down0, I);
     int rc;
     // Inputs of matrix-core projections leave their producers as bf16
     // planes (no separate split pass); the fp32 copies are kept where
     // another format or the trace needs them. LayerNorm -> XH, XL -> win;
     // its epilogue (fused into the product when both win and down run on
     // the matrix cores) -> MH, ML -> down; attention -> XH, XL -> o.
-    const bool pin = gemm_mfma_supported(w.win), pd = gemm_mfma_supported(wd);
+    const bool pin = !split_in && gemm_mfma_supported(w.win), pd = gemm_mfma_supported(wd);
     const bool flash = flash_prefill_supported(dims.hd), po = flash && gemm_mfma_supported(wo);
     STAGE(ST_PREFILL_NORM,
           launch_layer_norm_rows(X, w.ln_w, w.ln_b, dims.eps, n, d, pin ? nullptr : H, stream, pin ? XH : nullptr,
                                  pin ? XL : nullptr),
           "layer_norm");
     float *m32 = pd && !tracing ? nullptr : M;
-    if (pin && pd) {
+    if (split_in) {
+      // [q | k | v] and the gate/up pairs in formats of their own: two
+      // products from the fp32 LayerNorm output, then the epilogue of each
+      // section (q/k/v rows only, then gate/up pairs only).
+      StableDims da = dims, dm = dims;
+      da.inter = 0;
+      dm.win_q = dm.win_kv = 0;
+      const int ra = w.win.rows, rm = w.win2.rows;
+      float *Ya = Y, *Ym = Y + (size_t)n * ra;
+      if ((rc = project(w.win, H, d, n, Ya, ra)) || (rc = project(w.win2, H, d, n, Ym, rm))) return rc;
+      STAGE(ST_PREFILL_EPILOGUE,
+            launch_in_epilogue(da, kv[l], Ya, ra, rope, d_pos0, n, Q, M, stream, nullptr, nullptr), "in_epilogue");
+      STAGE(ST_PREFILL_EPILOGUE,
+            launch_in_epilogue(dm, kv[l], Ym, rm, rope, d_pos0, n, Q, m32, stream, pd ? MH : nullptr,
+                               pd ? ML : nullptr),
+            "in_epilogue");
+    } else if (pin && pd) {
       const InEpilogue e{dims, kv[l], rope, d_pos0, Q, m32, MH, ML};
       STAGE(ST_PREFILL_GEMM, launch_gemm_in_epilogue(w.win, XH, XL, n, e, stream), "projection + epilogue");
     } else {

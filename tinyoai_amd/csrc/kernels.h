@@ -41,6 +41,11 @@ LaunchTiming &launch_timing();  // the calling thread's
 struct LayerDev {
   MatDesc win, wout;
   const float *ln_w, *ln_b;
+  // A layer whose attention and MLP matrices differ in storage format (as
+  // in GGUF K-quant mixes) keeps them as sections of their own: then win
+  // holds only [q | k | v] and win2 the gate/up pairs; wout holds only o
+  // and wout2 down. rows == 0 when the layer is fused.
+  MatDesc win2, wout2;
 };
 
 // Shapes and constants of a decoder layer, with the choices that tell

@@ -78,7 +78,8 @@ struct StableModel {
   StableDims dims{};
   hipStream_t stream = nullptr;
   DevMatrix embed, head;
-  std::vector<DevMatrix> mats;  // win, wout of each layer
+  std::vector<DevMatrix> mats;  // win, wout, win2, wout2 of each layer
+  bool mixed_layers = false;    // some layer keeps its MLP (or down) matrices as sections of their own
   std::vector<LayerDev> layers;
   const float *norm_w = nullptr, *norm_b = nullptr;
   float *rope = nullptr;

@@ -148,7 +148,7 @@ hipError_t launch_in_epilogue(const StableDims &s, const KVDev &kv, const float 
                               const int *pos0, int n, float *q, float *m, hipStream_t st, uint16_t *mh,
                               uint16_t *ml) {
   if (ldy % 2 || !mh != !ml || (!m && !mh) || s.win_q % 2) return hipErrorInvalidValue;
-  const int units = (s.d + 2 * s.kv_heads * s.hd + 2 * s.inter) / 2;
+  const int units = (s.win_q + 2 * s.win_kv + 2 * s.inter) / 2;
   hipLaunchKernelGGL(in_epilogue_kernel, dim3(n), dim3(256), 0, st, s, kv, y, ldy, rope, pos0, units, q, m, mh,
                      ml);
   return hipGetLastError();
