@@ -43,6 +43,7 @@ extern "C" {
 
 typedef struct tinyoai_model tinyoai_model;
 typedef struct tinyoai_weight tinyoai_weight;
+typedef struct tinyoai_branches tinyoai_branches;
 
 /* One tensor in its on-disk encoding, row-major [rows, cols] (vectors:
  * rows = 1), named as in the Hugging Face checkpoint
@@ -107,6 +108,29 @@ int tinyoai_stablelm_offset(const tinyoai_model *m);
 
 /* Releases weights, KV and the stream (mlx_native.go:247-259). */
 int tinyoai_stablelm_close(tinyoai_model *m);
+
+/* NewBranches (mlx_branches.go:25-33; mlxBrancher, branches.go:55-59): opens
+ * `count` independent suffixes that borrow the resident prefix [0, prefix)
+ * (0 <= prefix <= offset) read-only. Each branch owns up to `max_steps`
+ * positions of suffix KV, allocated here (the reference grows its arrays
+ * per step); the KV format is the model's at opening. Head widths 8, 64 and
+ * 80; count * vocab <= the prefill chunk's product buffer. While branches
+ * are open the caller must not rewind, reset or change the KV format of
+ * the model (the reference holds the model gate), and must close them
+ * before the model. */
+int tinyoai_stablelm_branches_open(tinyoai_model *m, int32_t prefix, int32_t count, int32_t max_steps,
+                                   tinyoai_branches **out);
+/* nativeBranches.Forward (mlx_branches.go:120-182): one token per branch,
+ * all at absolute position prefix + step; writes `count` rows of fp32
+ * logits [count][vocab]. Attention combines the shared prefix with the
+ * branch's own suffix under one softmax (branchAttention,
+ * mlx_branches.go:98-114). TINYOAI_EINVAL for a wrong count, an invalid id,
+ * or a step past max_steps or the context; a native failure closes the
+ * branches' storage (later calls fail), as Forward closes them on error. */
+int tinyoai_stablelm_branches_forward(tinyoai_branches *b, const int32_t *tokens, int32_t count, float *logits);
+/* nativeBranches.Close (mlx_branches.go:36-47): frees the suffix KV; the
+ * shared prefix stays. NULL is accepted. */
+int tinyoai_stablelm_branches_close(tinyoai_branches *b);
 
 /* Debug hooks for parity checks: copy KV head `kv_head` of `layer` for
  * positions [0, n) as fp32 [n][head_dim] (stableState keys/values,

@@ -905,6 +905,65 @@ int StableModel::prefill_chunk(const int32_t *ids, int n, int start, bool want_l
   return TINYOAI_OK;
 }
 
+Branches::~Branches() {
+  if (m && m->stream) hipStreamSynchronize(m->stream);
+  for (void *p : buffers) hipFree(p);
+}
+
+// One token per branch at position prefix + step (nativeBranches.Forward,
+// mlx_branches.go:120-182): the rows go through the prefill products; their
+// K and V land in the branch slots; attention reads the shared prefix and
+// the branch's own suffix; every row's logits come back.
+int StableModel::branch_step(Branches &b, const int32_t *tokens, float *logits) {
+  const int n = b.count, pos = b.prefix + b.step, d = dims.d, I = dims.inter, V = cfg.vocab_size;
+  const int vals[1] = {pos};
+  if (int rc = upload_params(vals, 1, tokens, n)) return rc;
+  const int *d_pos0 = params, *d_ids = params + 16;
+  TRY_HIP(launch_embed(embed.desc, d_ids, n, X, stream), "embed");
+  for (int l = 0; l < cfg.num_hidden_layers; l++) {
+    const LayerDev &w = layers[l];
+    const bool split_in = w.win2.rows > 0, split_out = w.wout2.rows > 0;
+    const int64_t vpc = values_per_chunk(w.wout.fmt), down0 = (d + vpc - 1) / vpc * vpc;
+    const MatDesc wo = split_out ? w.wout : column_view(w.wout, 0, d);
+    const MatDesc wd = split_out ? w.wout2 : column_view(w.wout, down0, I);
+    int rc;
+    TRY_HIP(launch_layer_norm_rows(X, w.ln_w, w.ln_b, dims.eps, n, d, H, stream), "layer_norm");
+    if (split_in) {
+      StableDims da = dims, dm = dims;
+      da.inter = 0;
+      dm.win_q = dm.win_kv = 0;
+      const int ra = w.win.rows, rm = w.win2.rows;
+      float *Ya = Y, *Ym = Y + (size_t)n * ra;
+      if ((rc = project(w.win, H, d, n, Ya, ra)) || (rc = project(w.win2, H, d, n, Ym, rm))) return rc;
+      TRY_HIP(launch_in_epilogue(da, b.kv[l], Ya, ra, rope, d_pos0, n, Q, M, stream, nullptr, nullptr, b.slots,
+                                 b.prefix),
+              "in_epilogue");
+      TRY_HIP(launch_in_epilogue(dm, b.kv[l], Ym, rm, rope, d_pos0, n, Q, M, stream, nullptr, nullptr, b.slots,
+                                 b.prefix),
+              "in_epilogue");
+    } else {
+      if ((rc = project(w.win, H, d, n, Y, win_rows))) return rc;
+      TRY_HIP(launch_in_epilogue(dims, b.kv[l], Y, win_rows, rope, d_pos0, n, Q, M, stream, nullptr, nullptr,
+                                 b.slots, b.prefix),
+              "in_epilogue");
+    }
+    int sp = 1, sd = 1;
+    if ((rc = project(wd, M, I, n, D, d, &sd))) return rc;
+    TRY_HIP(launch_branch_attention(dims, kv[l], b.kv[l], b.prefix, b.slots, Q, d_pos0, n, pos, b.partials,
+                                    b.counters, A, b.max_splits, stream),
+            "branch attention");
+    if ((rc = project(wo, A, d, n, P, d, &sp))) return rc;
+    TRY_HIP(launch_residual(X, P, sp, D, sd, (int64_t)n * d, stream), "residual");
+  }
+  // Final LayerNorm of every row, then the classifier over all rows.
+  TRY_HIP(launch_layer_norm_rows(X, norm_w, norm_b, dims.eps, n, d, H, stream), "final norm");
+  if (int rc = project(head.desc, H, d, n, Y, V)) return rc;
+  TRY_HIP(hipMemcpyAsync(logits, Y, (size_t)n * V * 4, hipMemcpyDeviceToHost, stream), "logits");
+  TRY_HIP(hipStreamSynchronize(stream), "branch step");
+  b.step++;
+  return TINYOAI_OK;
+}
+
 int StableModel::forward(int prefix, const int32_t *tokens, int n, bool want_logits, float *logits) {
   if (prefix < 0 || prefix > offset || n <= 0 || !tokens || prefix + n > cfg.max_position_embeddings)
     return fail(TINYOAI_EINVAL, "invalid cached prefix or context length (prefix %d, offset %d, n %d)", prefix,
@@ -1038,6 +1097,76 @@ int tinyoai_stablelm_close(tinyoai_model *m) {
   if (!m) return TINYOAI_OK;
   if (m->stable) hipStreamSynchronize(m->stable->stream);
   delete m;
+  return TINYOAI_OK;
+}
+
+}  // extern "C"
+
+struct tinyoai_branches {
+  std::unique_ptr<tinyoai::Branches> b;
+};
+
+extern "C" {
+
+int tinyoai_stablelm_branches_open(tinyoai_model *m, int32_t prefix, int32_t count, int32_t max_steps,
+                                   tinyoai_branches **out) {
+  if (!m || !m->stable || !out) return fail(TINYOAI_EINVAL, "not a StableLM handle");
+  *out = nullptr;
+  StableModel &s = *m->stable;
+  const int hd = s.dims.hd;
+  if (prefix < 0 || prefix > s.offset || count < 1 || max_steps < 1 || count > s.chunk ||
+      (int64_t)count * s.cfg.vocab_size > (int64_t)s.chunk * s.win_rows ||
+      (int64_t)prefix + max_steps > s.cfg.max_position_embeddings)
+    return fail(TINYOAI_EINVAL, "invalid branch prefix or batch size (prefix %d, offset %d, count %d, steps %d)",
+                prefix, s.offset, count, max_steps);
+  if (hd != 8 && hd != 64 && hd != 80) return fail(TINYOAI_EINVAL, "branch attention: head width %d", hd);
+  if (int rc = s.ensure_kv(std::max(prefix, 1))) return rc;
+  auto h = std::make_unique<tinyoai_branches>();
+  h->b = std::make_unique<Branches>();
+  Branches &b = *h->b;
+  b.m = &s;
+  b.prefix = prefix;
+  b.count = count;
+  b.slots = max_steps;
+  b.max_splits = (prefix + max_steps) / 64 + 1;
+  auto balloc = [&](void **p, size_t bytes) -> int {
+    hipError_t e = hipMalloc(p, std::max<size_t>(bytes, 256));
+    if (e != hipSuccess) return fail(TINYOAI_ENOMEM, "hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
+    b.buffers.push_back(*p);
+    return TINYOAI_OK;
+  };
+  const size_t kvb = (size_t)s.dims.kv_heads * count * max_steps * hd * (s.kv_half ? 2 : 4);
+  for (int l = 0; l < s.cfg.num_hidden_layers; l++) {
+    KVDev k{nullptr, nullptr, count * max_steps, s.kv_half};
+    if (int rc = balloc(&k.k, kvb)) return rc;
+    if (int rc = balloc(&k.v, kvb)) return rc;
+    b.kv.push_back(k);
+  }
+  const size_t qh = (size_t)count * s.dims.heads;
+  if (int rc = balloc((void **)&b.partials, qh * partial_region(b.max_splits, hd) * 4)) return rc;
+  if (int rc = balloc((void **)&b.counters, qh * 4)) return rc;
+  TRY_HIP(hipMemsetAsync(b.counters, 0, qh * 4, s.stream), "branch counters");
+  TRY_HIP(hipStreamSynchronize(s.stream), "branch open");
+  *out = h.release();
+  return TINYOAI_OK;
+}
+
+int tinyoai_stablelm_branches_forward(tinyoai_branches *h, const int32_t *tokens, int32_t count, float *logits) {
+  if (!h || !h->b) return fail(TINYOAI_EINVAL, "branches are closed");
+  Branches &b = *h->b;
+  StableModel &s = *b.m;
+  if (!tokens || !logits || count != b.count || b.step >= b.slots ||
+      b.prefix + b.step >= s.cfg.max_position_embeddings)
+    return fail(TINYOAI_EINVAL, "invalid branch batch or context length");
+  for (int i = 0; i < count; i++)
+    if (tokens[i] < 0 || tokens[i] >= s.cfg.vocab_size) return fail(TINYOAI_EINVAL, "invalid branch token %d", tokens[i]);
+  const int rc = s.branch_step(b, tokens, logits);
+  if (rc) h->b.reset();  // Forward closes the suffix caches on an evaluation error
+  return rc;
+}
+
+int tinyoai_stablelm_branches_close(tinyoai_branches *h) {
+  delete h;
   return TINYOAI_OK;
 }
 

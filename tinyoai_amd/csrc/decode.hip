@@ -30,6 +30,11 @@ struct AttArgs {
   float *partials;
   unsigned *counters;
   float *out;
+  // Branches (BR): query j is branch j at position *pos0; positions below
+  // `prefix` come from kv (the shared prefix), the others from slots
+  // j * slots + (t - prefix) of the branch cache sfx.
+  KVDev sfx;
+  int prefix, slots;
 };
 
 // Agent-scope relaxed atomic store of a partial result.
@@ -65,7 +70,7 @@ __device__ __forceinline__ void load_kv_lanes(const void *base, int64_t e, int g
 // (query, head) in the last block to finish (the others exit). With 16
 // waves a block covers up to 1024 positions, so a short context needs one
 // block per head and no cross-block combine at all.
-template <int HD, bool HALF, int STEPS, int WAVES = kWaves>
+template <int HD, bool HALF, int STEPS, int WAVES = kWaves, bool BR = false>
 __global__ __launch_bounds__(WAVES * 64) void attention_kernel(AttArgs a) {
   constexpr int kWaves = WAVES, kThreads = WAVES * 64;
   constexpr int DPL = HD / 4;
@@ -82,7 +87,27 @@ __global__ __launch_bounds__(WAVES * 64) void attention_kernel(AttArgs a) {
 #pragma unroll
   for (int i = 0; i < DPL; i++) qr[i] = q[att_dim<DPL>(g, i)];
   const int64_t head_base = (int64_t)kvh * a.kv.cap * HD;
+  const int64_t sfx_base = BR ? (int64_t)kvh * a.sfx.cap * HD + (int64_t)j * a.slots * HD : 0;
   const int t0 = split * SPLIT + wave * STEPS * 16 + pl;
+  // Element offset of position t (clamped into its region) and whether it
+  // lies in the branch cache. The base is chosen by address arithmetic on
+  // the two caches (as in_pair_outputs does), not by a pointer select.
+  auto where = [&](int t, int64_t &e) -> bool {
+    if constexpr (BR) {
+      if (t >= a.prefix) {
+        e = sfx_base + (int64_t)min(t - a.prefix, a.slots - 1) * HD;
+        return true;
+      }
+      e = head_base + (int64_t)t * HD;
+      return false;
+    } else {
+      e = head_base + (int64_t)min(t, a.kv.cap - 1) * HD;
+      return false;
+    }
+  };
+  const uintptr_t kbase = reinterpret_cast<uintptr_t>(a.kv.k), vbase = reinterpret_cast<uintptr_t>(a.kv.v);
+  const uintptr_t kdelta = BR ? reinterpret_cast<uintptr_t>(a.sfx.k) - kbase : 0;
+  const uintptr_t vdelta = BR ? reinterpret_cast<uintptr_t>(a.sfx.v) - vbase : 0;
   // The block's K (and V) entries are loaded before the query position
   // arrives, so the loads do not wait for it: positions are clamped to the
   // cache, and entries past the query's position are masked below.
@@ -92,11 +117,12 @@ __global__ __launch_bounds__(WAVES * 64) void attention_kernel(AttArgs a) {
   float kr[STEPS][DPL], vr[STEPS][DPL];
 #pragma unroll
   for (int st = 0; st < STEPS; st++) {
-    const int64_t e = head_base + (int64_t)min(t0 + st * 16, a.kv.cap - 1) * HD;
-    load_kv_lanes<DPL, HALF>(a.kv.k, e, g, kr[st]);
-    if constexpr (kEarlyV) load_kv_lanes<DPL, HALF>(a.kv.v, e, g, vr[st]);
+    int64_t e;
+    const bool b = where(t0 + st * 16, e);
+    load_kv_lanes<DPL, HALF>(reinterpret_cast<const void *>(kbase + (b ? kdelta : 0)), e, g, kr[st]);
+    if constexpr (kEarlyV) load_kv_lanes<DPL, HALF>(reinterpret_cast<const void *>(vbase + (b ? vdelta : 0)), e, g, vr[st]);
   }
-  const int pos = *a.pos0 + j;
+  const int pos = *a.pos0 + (BR ? 0 : j);
   const int npos = pos + 1;
   const int nsplit = (npos + SPLIT - 1) / SPLIT;
   if (split >= nsplit) return;
@@ -119,7 +145,11 @@ __global__ __launch_bounds__(WAVES * 64) void attention_kernel(AttArgs a) {
   if constexpr (!kEarlyV) {
 #pragma unroll
     for (int st = 0; st < STEPS; st++)
-      if (t0 + st * 16 < npos) load_kv_lanes<DPL, HALF>(a.kv.v, head_base + (int64_t)(t0 + st * 16) * HD, g, vr[st]);
+      if (t0 + st * 16 < npos) {
+        int64_t e;
+        const bool b = where(t0 + st * 16, e);
+        load_kv_lanes<DPL, HALF>(reinterpret_cast<const void *>(vbase + (b ? vdelta : 0)), e, g, vr[st]);
+      }
   }
   float o[DPL];
 #pragma unroll
@@ -256,6 +286,18 @@ hipError_t launch_attention_hd(const AttArgs &a, int nq, int splits, int steps, 
   return hipGetLastError();
 }
 
+template <int HD, bool HALF>
+hipError_t launch_branch_attention_hd(const AttArgs &a, int nq, int splits, int steps, hipStream_t st) {
+  dim3 grid(splits, a.s.heads, nq);
+  switch (steps) {
+    case 1: hipLaunchKernelGGL((attention_kernel<HD, HALF, 1, kWaves, true>), grid, dim3(kThreads), 0, st, a); break;
+    case 2: hipLaunchKernelGGL((attention_kernel<HD, HALF, 2, kWaves, true>), grid, dim3(kThreads), 0, st, a); break;
+    case 4: hipLaunchKernelGGL((attention_kernel<HD, HALF, 4, kWaves, true>), grid, dim3(kThreads), 0, st, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
 template <int HD>
 hipError_t launch_attention_kv(const AttArgs &a, int nq, int splits, int steps, hipStream_t st) {
   return a.kv.half ? launch_attention_hd<HD, true>(a, nq, splits, steps, st)
@@ -337,6 +379,25 @@ hipError_t launch_attention(const StableDims &s, const KVDev &kv, const float *q
     case 80: return launch_attention_kv<80>(a, nq, splits, steps, st);
     case 96: return launch_attention_kv<96>(a, nq, splits, steps, st);
     case 128: return launch_attention_kv<128>(a, nq, splits, steps, st);
+  }
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_branch_attention(const StableDims &s, const KVDev &kv, const KVDev &sfx, int prefix, int slots,
+                                   const float *q, const int *pos0, int nq, int max_pos, float *partials,
+                                   unsigned *counters, float *out, int max_splits, hipStream_t st) {
+  const int steps = std::min(attention_steps(max_pos, s.heads), 4), splits = attention_splits(max_pos, steps);
+  if (splits > 512 || splits > max_splits || prefix < 0 || prefix > kv.cap || slots <= 0 ||
+      (int64_t)nq * slots > sfx.cap || max_pos - prefix >= slots || kv.half != sfx.half)
+    return hipErrorInvalidValue;
+  AttArgs a{s, kv, q, pos0, max_splits, partials, counters, out, sfx, prefix, slots};
+  switch (s.hd) {
+    case 64: return kv.half ? launch_branch_attention_hd<64, true>(a, nq, splits, steps, st)
+                            : launch_branch_attention_hd<64, false>(a, nq, splits, steps, st);
+    case 80: return kv.half ? launch_branch_attention_hd<80, true>(a, nq, splits, steps, st)
+                            : launch_branch_attention_hd<80, false>(a, nq, splits, steps, st);
+    case 8: return kv.half ? launch_branch_attention_hd<8, true>(a, nq, splits, steps, st)
+                           : launch_branch_attention_hd<8, false>(a, nq, splits, steps, st);
   }
   return hipErrorInvalidValue;
 }

@@ -103,6 +103,13 @@ hipError_t launch_decode_out(const MatDesc &wout, int ka, int km, const float *a
 hipError_t launch_attention(const StableDims &s, const KVDev &kv, const float *q, const int *pos0, int nq,
                             int max_pos, float *partials, unsigned *counters, float *out, hipStream_t st,
                             int steps = 0, int splits = 0);
+// Branch attention (query j = branch j at position *pos0 = max_pos):
+// positions below `prefix` from kv, the rest from slots j * slots + (t -
+// prefix) of sfx. partials holds nq * heads * partial_region(max_splits, hd)
+// floats. Head widths 8, 64 and 80.
+hipError_t launch_branch_attention(const StableDims &s, const KVDev &kv, const KVDev &sfx, int prefix, int slots,
+                                   const float *q, const int *pos0, int nq, int max_pos, float *partials,
+                                   unsigned *counters, float *out, int max_splits, hipStream_t st);
 // Causal attention of n prefill queries on the matrix cores (head widths
 // 64, 80, 96, 128): q [n][heads*hd] at positions pos0 + j -> out.
 bool flash_prefill_supported(int hd);
@@ -214,7 +221,7 @@ hipError_t launch_split_bf16(const float *x, int ldx, int k, int64_t rows, uint1
 // operand planes mh, ml (null: none).
 hipError_t launch_in_epilogue(const StableDims &s, const KVDev &kv, const float *y, int ldy, const float *rope,
                               const int *pos0, int n, float *q, float *m, hipStream_t st, uint16_t *mh = nullptr,
-                              uint16_t *ml = nullptr);
+                              uint16_t *ml = nullptr, int slots = 0, int prefix = 0);
 hipError_t launch_silu_gate(float *g, const float *u, int64_t n, hipStream_t st);
 // x = (x + p) + d elementwise (stablelm.go:375-377).
 // x = (x + sum_s p[s]) + sum_s d[s] over sp and sd partial products n

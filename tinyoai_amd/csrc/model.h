@@ -156,6 +156,23 @@ struct StableModel {
                      int *splits = nullptr);
   int prefill_chunk(const int32_t *ids, int n, int start, bool want_logits);
   int forward(int prefix, const int32_t *tokens, int n, bool want_logits, float *logits);
+  int branch_step(struct Branches &b, const int32_t *tokens, float *logits);
+};
+
+// Independent suffixes of a resident prefix (nativeBranches,
+// mlx_branches.go:14-20): the prefix KV [0, prefix) of the model is read,
+// never written; each branch owns `slots` positions of suffix KV per layer,
+// laid out [kv_heads][count * slots][hd] so that branch j's step s is slot
+// j * slots + s.
+struct Branches {
+  StableModel *m = nullptr;
+  int prefix = 0, count = 0, slots = 0, step = 0;
+  std::vector<KVDev> kv;
+  float *partials = nullptr;
+  unsigned *counters = nullptr;
+  int max_splits = 0;
+  std::vector<void *> buffers;
+  ~Branches();
 };
 
 // The legacy Llama of llama2.c checkpoints (Model.transformer,

@@ -88,10 +88,14 @@ __global__ __launch_bounds__(256) void gemm_simt_kernel(MatDesc w, const float *
 // applies it row by row. With mh, the SiLU-gate outputs (the units from
 // mu0 on) also go out as the down projection's bf16 operand planes, and to
 // m only when m is given.
+// With slots > 0 the rows are branches at one position (*pos0): row j's K
+// and V go to slot j * slots + (pos - prefix) of the branch cache kv.
 __global__ void in_epilogue_kernel(StableDims s, KVDev kv, const float *y, int ldy, const float *rope,
-                                   const int *pos0, int units, float *q, float *m, uint16_t *mh, uint16_t *ml) {
+                                   const int *pos0, int units, float *q, float *m, uint16_t *mh, uint16_t *ml,
+                                   int slots, int prefix) {
   const int j = blockIdx.x;
-  const int pos = *pos0 + j;
+  const int pos = *pos0 + (slots ? 0 : j);
+  const int slot = slots ? j * slots + (pos - prefix) : pos;
   const float *yj = y + (int64_t)j * ldy;
   const float *rope_row = rope + (int64_t)pos * s.rot;
   const int mu0 = (s.win_q + 2 * s.win_kv) / 2;
@@ -103,7 +107,7 @@ __global__ void in_epilogue_kernel(StableDims s, KVDev kv, const float *y, int l
       if (mj) mj[u - mu0] = g;
       store_bf16_split(mh, ml, (int64_t)j * s.inter + (u - mu0), g);
     } else {
-      in_pair_epilogue(s, kv, rope_row, pos, u, v.x, v.y, qj, mj);
+      in_pair_epilogue(s, kv, rope_row, slot, u, v.x, v.y, qj, mj);
     }
   }
 }
@@ -146,11 +150,12 @@ hipError_t launch_gemm(const MatDesc &w, const float *x, int n, float *out, hipS
 
 hipError_t launch_in_epilogue(const StableDims &s, const KVDev &kv, const float *y, int ldy, const float *rope,
                               const int *pos0, int n, float *q, float *m, hipStream_t st, uint16_t *mh,
-                              uint16_t *ml) {
-  if (ldy % 2 || !mh != !ml || (!m && !mh) || s.win_q % 2) return hipErrorInvalidValue;
+                              uint16_t *ml, int slots, int prefix) {
+  if (ldy % 2 || !mh != !ml || (!m && !mh) || s.win_q % 2 || slots < 0 || (slots && (int64_t)n * slots > kv.cap))
+    return hipErrorInvalidValue;
   const int units = (s.win_q + 2 * s.win_kv + 2 * s.inter) / 2;
   hipLaunchKernelGGL(in_epilogue_kernel, dim3(n), dim3(256), 0, st, s, kv, y, ldy, rope, pos0, units, q, m, mh,
-                     ml);
+                     ml, slots, prefix);
   return hipGetLastError();
 }
 

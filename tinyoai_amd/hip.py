@@ -20,7 +20,8 @@ EXPORTS = [
     "tinyoai_stablelm_limit_cache", "tinyoai_stablelm_reset", "tinyoai_stablelm_offset", "tinyoai_stablelm_close",
     "tinyoai_stablelm_read_kv", "tinyoai_stablelm_trace", "tinyoai_stablelm_trace_read",
     "tinyoai_stablelm_trace_read_stages", "tinyoai_stablelm_decode_timeline", "tinyoai_stablelm_set_persistent",
-    "tinyoai_stablelm_set_launch",
+    "tinyoai_stablelm_set_launch", "tinyoai_stablelm_branches_open", "tinyoai_stablelm_branches_forward",
+    "tinyoai_stablelm_branches_close",
     "tinyoai_stablelm_profile", "tinyoai_stablelm_profile_read", "tinyoai_llama_load",
     "tinyoai_llama_forward", "tinyoai_llama_reset", "tinyoai_llama_close", "tinyoai_weight_upload",
     "tinyoai_weight_read_values", "tinyoai_weight_mul", "tinyoai_weight_mul_device", "tinyoai_weight_free",
@@ -76,6 +77,9 @@ def lib():
         L.tinyoai_stablelm_decode_timeline.restype = C.c_int64
         L.tinyoai_stablelm_set_persistent.argtypes = [P, C.c_int32]
         L.tinyoai_stablelm_set_launch.argtypes = [P, C.c_int32, C.c_int32, C.c_int32]
+        L.tinyoai_stablelm_branches_open.argtypes = [P, C.c_int32, C.c_int32, C.c_int32, C.POINTER(P)]
+        L.tinyoai_stablelm_branches_forward.argtypes = [P, ip, C.c_int32, fp]
+        L.tinyoai_stablelm_branches_close.argtypes = [P]
         L.tinyoai_stablelm_profile.argtypes = [P, C.c_int32]
         L.tinyoai_stablelm_profile_read.argtypes = [P, C.POINTER(C.c_double), C.POINTER(C.c_int64), C.c_int32]
         L.tinyoai_llama_load.argtypes = [C.POINTER(LlamaConfig), fp, C.c_uint64, C.POINTER(P)]
@@ -149,6 +153,35 @@ LAYER_TENSORS = ("input_layernorm.weight", "input_layernorm.bias", "self_attn.q_
                  "mlp.gate_proj.weight", "mlp.up_proj.weight", "mlp.down_proj.weight")
 
 
+class Branches:
+    """nativeBranches (mlx_branches.go:14-182) over the C ABI: forward() takes
+    one token per branch, all at position prefix + step, and returns the
+    logits rows [count][vocab]."""
+
+    def __init__(self, fwd, prefix: int, count: int, max_steps: int):
+        self.h = C.c_void_p()
+        self.count = count
+        self.vocab = fwd.config["vocab_size"]
+        check(lib().tinyoai_stablelm_branches_open(fwd.h, prefix, count, max_steps, C.byref(self.h)))
+        self._logits = np.empty((count, self.vocab), np.float32)
+
+    def forward(self, tokens) -> np.ndarray:
+        toks = np.ascontiguousarray(tokens, np.int32)
+        check(lib().tinyoai_stablelm_branches_forward(self.h, _ip(toks), toks.size, _fp(self._logits)))
+        return self._logits.copy()
+
+    def close(self):
+        if self.h:
+            lib().tinyoai_stablelm_branches_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 class StableLMForwarder:
     """The HIP StableLM forwarder: the mlxForwarder contract (mlx.go:45-51)
     plus SetKVBits / LimitCache (mlx_kv.go:78-91, mlx_native.go:231-244)."""
@@ -180,6 +213,12 @@ class StableLMForwarder:
         check(lib().tinyoai_stablelm_forward(self.h, prefix, _ip(toks), toks.size, int(want_logits),
                                              _fp(self._logits)))
         return self._logits.copy() if want_logits else None
+
+    def new_branches(self, prefix: int, count: int, max_steps: int) -> "Branches":
+        """NewBranches (mlx_branches.go:25-33): `count` suffixes borrowing
+        the resident prefix [0, prefix), each with room for `max_steps`
+        tokens. Close them before this forwarder."""
+        return Branches(self, prefix, count, max_steps)
 
     def set_kv_bits(self, bits: int) -> bool:
         cleared = C.c_int32()
