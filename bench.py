@@ -150,6 +150,63 @@ def q8_0_kernel(seed=2, reps=192, copies=16):
     return out
 
 
+def branches_workload(args):
+    """The K-quant branch workload: StableLM-3B shapes with Q6_K attention
+    matrices and classifier, Q4_K MLP, fp16 KV; a 4096-token uniform-random
+    prefix is prefilled, then 16 branches (seeded first tokens) borrow it
+    and take 64 greedy tokens each in lockstep (one batched step = one token
+    for every branch, all logits rows back to the host for argmax). The
+    branches share one position, as nativeBranches does; ragged private
+    suffixes are not part of that interface. Roofline bytes per step: every
+    weight byte once plus the shared prefix KV once plus the suffix KV."""
+    import numpy as np
+    import torch
+    from tinyoai_amd import hip, weights as W
+    torch.cuda.set_device(0)
+    P, B, T = 4096, 16, 64
+    config = W.validate_stablelm_config(dict(W.STABLELM_3B, num_hidden_layers=args.layers,
+                                             max_position_embeddings=8192))
+    tensors = W.synthetic_stablelm(config, W.Q4_K, seed=args.seed, attn_dtype=W.Q6_K, head_dtype=W.Q6_K)
+    weight_bytes = sum(t.data.nbytes for name, t in tensors.items()
+                       if name.endswith("proj.weight") or name == "lm_head.weight")
+    fwd = hip.StableLMForwarder(config, tensors)
+    fwd.set_kv_bits(16)
+    rng = np.random.default_rng(args.seed + 2)
+    prompt = rng.integers(0, config["vocab_size"], P).astype(np.int32)
+    seeds = rng.integers(0, config["vocab_size"], B).astype(np.int32)
+    fwd.forward(0, prompt[:64])  # warm-up of the prefill kernels
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    fwd.forward(0, prompt)
+    prefill_s = time.perf_counter() - t0
+    step_s = []
+    for rep in range(2):  # the first pass is the warm-up
+        br = fwd.new_branches(P, B, T)
+        toks, t0 = seeds, time.perf_counter()
+        for s in range(T):
+            rows = br.forward(toks)
+            toks = rows.argmax(axis=1).astype(np.int32)
+        step_s.append((time.perf_counter() - t0) / T)
+        br.close()
+    fwd.close()
+    L, kvw = config["num_hidden_layers"], config["hidden_size"] // config["num_attention_heads"] * config["num_key_value_heads"]
+    kv_pos = L * 2 * kvw * 2
+    mean_suffix = (T - 1) / 2 + 1
+    step_bytes = weight_bytes + P * kv_pos + B * mean_suffix * kv_pos
+    per_step = step_s[-1]
+    achieved = step_bytes / per_step / 1e9
+    return {"metric": "branch decode tok/s, 3B StableLM Q6_K attention / Q4_K MLP, 16 branches on a 4096-token prefix",
+            "value": round(B / per_step, 1), "unit": "tok/s", "n_gpus": 1, "ms_per_step": round(per_step * 1e3, 3),
+            "higher_is_better": True, "dtype": "f32", "data": "synthetic",
+            "config": {"workload": "StableLM-3B-shape GGUF Q6_K attention + classifier / Q4_K MLP, fp16 KV, "
+                                   f"{P}-token prefix, {B} lockstep branches x {T} greedy tokens",
+                       "layers": L, "prefix": P, "branches": B, "tokens_per_branch": T},
+            "prefill_s": round(prefill_s, 4),
+            "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(achieved / HBM_PEAK_GBS, 4), "algorithmic_bytes_per_step": int(step_bytes),
+                         "weight_bytes": int(weight_bytes)}}
+
+
 def cpu_baseline(config, tensors, threads, prompt_len):
     """The oracle (C restatement of the Go scalar engine) on the host cores:
     a 128-token batched prefill chunk (prefillBatch) and 2 decode forwards
@@ -187,6 +244,8 @@ def main():
     ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--seed", type=int, default=1234)
+    ap.add_argument("--workload", choices=["decode", "branches"], default="decode",
+                    help="branches: the K-quant 16-branch workload instead of the Q8_0 decode one")
     ap.add_argument("--dtype", choices=["q8_0", "bf16"], default="q8_0",
                     help="weight format (bf16 with --prompt 8129 --generate 64 --kv 16: the long-context workload)")
     ap.add_argument("--kv", type=int, choices=[16, 32], default=32, help="KV cache bits")
@@ -197,6 +256,10 @@ def main():
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the path would shard by "
               f"attention head / MLP column with one all-reduce per layer; see DESIGN.md).", file=sys.stderr)
         sys.exit(2)
+
+    if args.workload == "branches":
+        print(json.dumps(branches_workload(args)))
+        return
 
     import numpy as np
     import torch

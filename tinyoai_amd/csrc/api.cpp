@@ -808,6 +808,17 @@ int StableModel::project(const MatDesc &w, const float *x, int ldx, int n, float
     if (splits) *splits = ks;
     STAGE(ST_PREFILL_GEMM, launch_split_bf16(x, ldx, w.cols, n, XH, two ? XL : nullptr, stream), "bf16 split");
     STAGE(ST_PREFILL_GEMM, launch_gemm_mfma(w, XH, two ? XL : nullptr, n, y, ldy, stream, ks), "projection");
+  } else if (n <= kRowStreamMax) {
+    // A few rows (branch steps, short suffixes): one row-streaming matvec
+    // per row. The vector-unit GEMM costs about as much for 16 rows as for
+    // 64 (677 us for a 16-row K-quant product at the 3B shapes); the row
+    // kernels stream the matrix per row, from the last-level cache after
+    // the first row.
+    for (int j = 0; j < n; j++)
+      STAGE(ST_PREFILL_GEMM,
+            launch_ln_matvec(w, nullptr, nullptr, 0.0, 0, x + (size_t)j * ldx, y + (size_t)j * ldy, grid_out,
+                             threads_out, stream),
+            "projection");
   } else {
     if (ldx != w.cols || ldy != w.rows) return fail(TINYOAI_EINVAL, "vector-unit GEMM needs dense operands");
     STAGE(ST_PREFILL_GEMM, launch_gemm(w, x, n, y, stream), "projection");

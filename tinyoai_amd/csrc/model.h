@@ -96,6 +96,7 @@ struct StableModel {
   unsigned *counters = nullptr;
   int max_splits = 0;
   static constexpr int kPrefillSplits = 8;  // K-split partial products P and D can hold
+  static constexpr int kRowStreamMax = 32;  // non-matrix-core products of at most this many rows run per row
   // prefill workspaces, `chunk` tokens each: residual X, LayerNorm H, win
   // products Y, RoPE'd queries Q, SiLU-gate M, attention A, o and down
   // products P and D, bf16 planes XH/XL of the current GEMM operand
