@@ -362,3 +362,103 @@ def test_llama_rmsnorm_rope_closed_form(oracle):
     x = x + w2 @ (g / (1 + np.exp(-g)) * u)
     want = emb @ rms(x, rms_f)
     assert np.max(np.abs(got - want)) <= 1e-5 * max(1, np.max(np.abs(want)))
+
+
+def llama_float64(c: dict, w: np.ndarray, tokens, planted: str | None = None) -> np.ndarray:
+    """An independent float64 statement of Model.transformer
+    (model.go:407-481) over a whole token sequence, written from the
+    mathematics rather than the Go loops: RMSNorm as g * x / rms(x); RoPE as
+    the complex product (v0 + i v1)(cos + i sin) with the checkpoint's
+    freq_cis rows (rotateHead, model.go:611-618); grouped-query attention
+    where query head h reads kv head h // (heads / kv_heads); softmax over
+    positions 0..pos; SwiGLU; logits through the tied embedding. Returns
+    the logits of every position [n][vocab]. `planted` swaps in a plausible
+    mistake (so the test below shows the comparison would catch it)."""
+    dim, hid, L, V, S = c["dim"], c["hidden_dim"], c["n_layers"], c["vocab_size"], c["seq_len"]
+    H, KVH = c["n_heads"], c["n_kv_heads"]
+    hs = dim // H
+    kvd = hs * KVH
+    p = w.astype(np.float64)
+    o = 0
+
+    def take(n, shape):
+        nonlocal o
+        t = p[o:o + n].reshape(shape)
+        o += n
+        return t
+
+    emb = take(V * dim, (V, dim))
+    rms_att = take(L * dim, (L, dim))
+    wq = take(L * dim * dim, (L, dim, dim))
+    wk = take(L * dim * kvd, (L, kvd, dim))
+    wv = take(L * dim * kvd, (L, kvd, dim))
+    wo = take(L * dim * dim, (L, dim, dim))
+    rms_ffn = take(L * dim, (L, dim))
+    w1 = take(L * hid * dim, (L, hid, dim))
+    w2 = take(L * dim * hid, (L, dim, hid))
+    w3 = take(L * hid * dim, (L, hid, dim))
+    rms_f = take(dim, (dim,))
+    fcr = take(S * hs // 2, (S, hs // 2))
+    fci = take(S * hs // 2, (S, hs // 2))
+    if planted == "swap_cos_sin":
+        fcr, fci = fci, fcr
+
+    def rms(x, g):
+        return g * (x / math.sqrt(float(np.mean(x * x)) + 1e-5))
+
+    def rope(vec, pos):
+        z = vec.reshape(-1, hs // 2, 2)
+        zc = (z[..., 0] + 1j * z[..., 1]) * (fcr[pos] + 1j * fci[pos])
+        return np.stack([zc.real, zc.imag], axis=-1).reshape(vec.shape)
+
+    kv_of = (lambda h: h % KVH) if planted == "gqa_modulo" else (lambda h: h // (H // KVH))
+    keys = np.zeros((L, len(tokens), KVH, hs))
+    vals = np.zeros((L, len(tokens), KVH, hs))
+    out = []
+    for pos, tok in enumerate(tokens):
+        x = emb[tok].copy()
+        for l in range(L):
+            h = rms(x, rms_att[l])
+            q = rope((wq[l] @ h).reshape(H, hs), pos)
+            keys[l, pos] = rope((wk[l] @ h).reshape(KVH, hs), pos)
+            vals[l, pos] = (wv[l] @ h).reshape(KVH, hs)
+            att = np.zeros((H, hs))
+            last = pos + 1 if planted != "drop_last_key" else max(pos, 1)
+            for hh in range(H):
+                kh = kv_of(hh)
+                s = keys[l, :last, kh] @ q[hh] / math.sqrt(hs)
+                e = np.exp(s - s.max())
+                att[hh] = (e / e.sum()) @ vals[l, :last, kh]
+            x = x + wo[l] @ att.reshape(dim)
+            h = rms(x, rms_ffn[l])
+            g, u = w1[l] @ h, w3[l] @ h
+            x = x + w2[l] @ (g / (1 + np.exp(-g)) * u)
+        out.append(emb @ rms(x, rms_f))
+    return np.array(out)
+
+
+LLAMA_SEQ = [1, 365, 301, 259, 377, 263, 407, 270, 433]  # BOS, then ids of stories260K's vocabulary
+
+
+@pytest.mark.parametrize("planted", [None, "swap_cos_sin", "gqa_modulo", "drop_last_key"])
+def test_llama_float64_brute_force(oracle, planted):
+    """Pins or_llama_transformer (model.go:407-481) on stories260K at
+    positions 0..8, where the RoPE rotation is not the identity
+    (freq_cis rows 1..8 of the checkpoint), softmax has up to 9 terms and
+    the 8 query heads share 4 kv heads: every position's logits within
+    5e-6 of their range of a float64 statement of the same model. The
+    float64 side with a planted mistake (cos/sin swapped in the complex
+    product, query head h reading kv head h % 4, the newest key left out
+    of the softmax) must disagree by far more than that bound, so the
+    bound is tight enough to see each of them."""
+    c, w = W.read_llama2c(os.path.join(GOLDEN, "stories260K.bin"))
+    m = oracle.Llama(c, w)
+    got = np.array([m.transformer(tok, pos) for pos, tok in enumerate(LLAMA_SEQ)], np.float64)
+    want = llama_float64(c, w, LLAMA_SEQ, planted)
+    err = np.max(np.abs(got - want), axis=1) / np.ptp(want, axis=1)
+    if planted is None:
+        assert np.all(err <= 5e-6), err
+        # position 0 is the identity rotation; the later rows carry the pin
+        assert np.all(np.ptp(want, axis=1) > 1.0)
+    else:
+        assert np.max(err[1:]) > 1e-2, (planted, err)
