@@ -1,18 +1,26 @@
 #!/usr/bin/env python3
 """Decode/prefill benchmark of the HIP StableLM forwarder on one MI355X.
 
-Workload (one "step"): StableLM-3B shapes (32 layers, hidden 2560, 32 x 80
-heads, 25% rotary, SiLU MLP 6912, vocab 65536) with seeded synthetic GGUF
-Q8_0 weights, fp32 KV; a 512-token uniform-random prompt is prefilled, then
-256 greedy tokens are chosen (255 one-token decode forwards, the logits of
-each copied to the host and argmax'd there, as the Go host does).
+Headline workload (one "step"): StableLM-3B shapes (32 layers, hidden 2560,
+32 x 80 heads, 25% rotary, SiLU MLP 6912, vocab 65536) with seeded synthetic
+GGUF Q8_0 weights, fp32 KV; a 512-token uniform-random prompt is prefilled,
+then 256 greedy tokens are chosen (255 one-token decode forwards, the logits
+of each copied to the host and argmax'd there, as the Go host does).
 
 Prints one JSON line: value = decode tokens/s over the timed steps, plus the
 prefill seconds, the roofline fraction of the dominant decode kernel
 (HIP-event durations on the library's stream) and the CPU oracle timed on
-the host cores.
+the host cores. Beside the headline it reports, under their own keys:
+  long_context  BF16 weights, an 8129-token prefill (fp16 KV) and 64 greedy
+                decode tokens at ~8.2K positions;
+  branches      K-quant weights (Q6_K attention and classifier, Q4_K MLP),
+                fp16 KV: a 4096-token prefix, 16 branches given private
+                suffixes of 1-256 tokens, then 64 lockstep greedy tokens;
+  llama         the stories260K Llama-2 checkpoint, 32 + 256 tokens;
+  kernel_q8_0   the isolated 6912 x 2560 Q8_0 product at M = 1 and 128.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+       [--workload all|decode|long_context|branches]
 """
 import argparse
 import json
@@ -150,15 +158,84 @@ def q8_0_kernel(seed=2, reps=192, copies=16):
     return out
 
 
+def token_bytes_fmt(c, pos, weight_bytes, kv_bytes):
+    """Algorithmic bytes of one decode forward at position pos given the
+    layers' and head's weight bytes: the weights once, one embedding row,
+    the KV read (positions 0..pos) and the new entry's write."""
+    d, L = c["hidden_size"], c["num_hidden_layers"]
+    kv = d // c["num_attention_heads"] * c["num_key_value_heads"]
+    return weight_bytes + 2 * d + L * 2 * kv * kv_bytes * (pos + 2)
+
+
+def matrix_bytes(tensors):
+    """Bytes of every projection matrix and the classifier (what a decode
+    forward streams once)."""
+    return sum(t.data.nbytes for name, t in tensors.items()
+               if name.endswith("proj.weight") or name == "lm_head.weight")
+
+
+def long_context_workload(args):
+    """BF16 weights (N(0, 0.02)), fp16 KV: an 8129-token uniform-random
+    prompt (prefilled in the library's 2048-token chunks), then 64 greedy
+    tokens. Prefill is reported against the MFMA roofline with its useful
+    flops (linear 2 * n * params + causal attention 4 * hd * n(n+1)/2 per
+    head and layer); decode against the HBM roofline at the mean position."""
+    import numpy as np
+    import torch
+    from tinyoai_amd import hip, weights as W
+    n, T = 8129, 64
+    config = W.validate_stablelm_config(dict(W.STABLELM_3B, num_hidden_layers=args.layers,
+                                             max_position_embeddings=8192))
+    t0 = time.perf_counter()
+    tensors = W.synthetic_stablelm(config, W.BF16, seed=args.seed + 10)
+    print(f"[bench] long context: bf16 weights in {time.perf_counter() - t0:.1f}s", file=sys.stderr, flush=True)
+    fwd = hip.StableLMForwarder(config, tensors)
+    wbytes = matrix_bytes(tensors)
+    del tensors
+    fwd.set_kv_bits(16)
+    prompt = np.random.default_rng(args.seed + 11).integers(0, config["vocab_size"], n).astype(np.int32)
+    fwd.forward(0, prompt[:2048], want_logits=False)  # warm-up of the prefill kernels
+    torch.cuda.synchronize()
+    runs = []
+    for _ in range(2):
+        t0 = time.perf_counter()
+        logits = fwd.forward(0, prompt)
+        runs.append(time.perf_counter() - t0)
+    prefill_s = min(runs)
+    toks, t0 = [], time.perf_counter()
+    for i in range(T):
+        toks.append(int(np.argmax(logits)))
+        if i + 1 < T:
+            logits = fwd.forward(n + i, [toks[-1]])
+    decode_s = time.perf_counter() - t0
+    fwd.close()
+    d, I, L = config["hidden_size"], config["intermediate_size"], config["num_hidden_layers"]
+    hd, H = d // config["num_attention_heads"], config["num_attention_heads"]
+    kvw = hd * config["num_key_value_heads"]
+    linear = 2.0 * n * L * (d * (d + 2 * kvw) + d * d + 3 * d * I)
+    attention = 4.0 * hd * (n * (n + 1) / 2) * H * L
+    flops = linear + attention
+    tflops = flops / prefill_s / 1e12
+    dec_tok_s = (T - 1) / decode_s
+    mean_pos = n + (T - 2) / 2
+    roof_tok_s = HBM_PEAK_GBS * 1e9 / token_bytes_fmt(config, mean_pos, wbytes, 2)
+    return {"workload": f"StableLM-3B-shape BF16, {n}-token prompt (2048-token chunks) + {T} greedy tokens, fp16 KV",
+            "layers": L, "prefill_s": round(prefill_s, 4), "prefill_tok_s": round(n / prefill_s, 1),
+            "prefill_useful_tflops": round(tflops, 1), "prefill_flops": flops,
+            "prefill_mfma_frac_bf16": round(tflops / 2500.0, 4),
+            "decode_tok_s": round(dec_tok_s, 2), "decode_roofline_tok_s": round(roof_tok_s, 1),
+            "decode_frac_of_hbm_roofline": round(dec_tok_s / roof_tok_s, 4), "first_tokens": toks[:8]}
+
+
 def branches_workload(args):
-    """The K-quant branch workload: StableLM-3B shapes with Q6_K attention
-    matrices and classifier, Q4_K MLP, fp16 KV; a 4096-token uniform-random
-    prefix is prefilled, then 16 branches (seeded first tokens) borrow it
-    and take 64 greedy tokens each in lockstep (one batched step = one token
-    for every branch, all logits rows back to the host for argmax). The
-    branches share one position, as nativeBranches does; ragged private
-    suffixes are not part of that interface. Roofline bytes per step: every
-    weight byte once plus the shared prefix KV once plus the suffix KV."""
+    """The K-quant branch workload: Q6_K attention matrices and classifier,
+    Q4_K MLP, fp16 KV; a 4096-token uniform-random prefix is prefilled, 16
+    branches borrow it, each is given a private suffix of 1-256 random
+    tokens (seeded lengths; one append call), then every branch takes 64
+    greedy tokens in lockstep (one batched step = one token for every
+    branch, at its own position; all logits rows back to the host for
+    argmax). Roofline bytes per step: every weight byte once, the shared
+    prefix KV once, and each branch's suffix KV."""
     import numpy as np
     import torch
     from tinyoai_amd import hip, weights as W
@@ -166,71 +243,85 @@ def branches_workload(args):
     P, B, T = 4096, 16, 64
     config = W.validate_stablelm_config(dict(W.STABLELM_3B, num_hidden_layers=args.layers,
                                              max_position_embeddings=8192))
+    t0 = time.perf_counter()
     tensors = W.synthetic_stablelm(config, W.Q4_K, seed=args.seed, attn_dtype=W.Q6_K, head_dtype=W.Q6_K)
-    weight_bytes = sum(t.data.nbytes for name, t in tensors.items()
-                       if name.endswith("proj.weight") or name == "lm_head.weight")
+    print(f"[bench] branches: k-quant weights in {time.perf_counter() - t0:.1f}s", file=sys.stderr, flush=True)
+    weight_bytes = matrix_bytes(tensors)
     fwd = hip.StableLMForwarder(config, tensors)
+    del tensors
     fwd.set_kv_bits(16)
     rng = np.random.default_rng(args.seed + 2)
     prompt = rng.integers(0, config["vocab_size"], P).astype(np.int32)
-    seeds = rng.integers(0, config["vocab_size"], B).astype(np.int32)
-    fwd.forward(0, prompt[:64])  # warm-up of the prefill kernels
+    lengths = rng.integers(1, 257, B)
+    suffixes = [rng.integers(0, config["vocab_size"], k).astype(np.int32) for k in lengths]
+    fwd.forward(0, prompt[:64], want_logits=False)  # warm-up of the prefill kernels
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    fwd.forward(0, prompt)
+    fwd.forward(0, prompt, want_logits=False)
     prefill_s = time.perf_counter() - t0
-    step_s = []
+    step_s, append_s = [], []
     for rep in range(2):  # the first pass is the warm-up
-        br = fwd.new_branches(P, B, T)
-        toks, t0 = seeds, time.perf_counter()
-        for s in range(T):
+        br = fwd.new_branches(P, B)
+        t0 = time.perf_counter()
+        rows = br.append(suffixes)
+        append_s.append(time.perf_counter() - t0)
+        toks, t0 = rows.argmax(axis=1).astype(np.int32), time.perf_counter()
+        for s in range(T - 1):
             rows = br.forward(toks)
             toks = rows.argmax(axis=1).astype(np.int32)
-        step_s.append((time.perf_counter() - t0) / T)
+        step_s.append((time.perf_counter() - t0) / (T - 1))
         br.close()
     fwd.close()
     L, kvw = config["num_hidden_layers"], config["hidden_size"] // config["num_attention_heads"] * config["num_key_value_heads"]
     kv_pos = L * 2 * kvw * 2
-    mean_suffix = (T - 1) / 2 + 1
+    mean_suffix = float(np.mean(lengths)) + T / 2
     step_bytes = weight_bytes + P * kv_pos + B * mean_suffix * kv_pos
     per_step = step_s[-1]
     achieved = step_bytes / per_step / 1e9
-    return {"metric": "branch decode tok/s, 3B StableLM Q6_K attention / Q4_K MLP, 16 branches on a 4096-token prefix",
-            "value": round(B / per_step, 1), "unit": "tok/s", "n_gpus": 1, "ms_per_step": round(per_step * 1e3, 3),
-            "higher_is_better": True, "dtype": "f32", "data": "synthetic",
-            "config": {"workload": "StableLM-3B-shape GGUF Q6_K attention + classifier / Q4_K MLP, fp16 KV, "
-                                   f"{P}-token prefix, {B} lockstep branches x {T} greedy tokens",
-                       "layers": L, "prefix": P, "branches": B, "tokens_per_branch": T},
-            "prefill_s": round(prefill_s, 4),
+    return {"workload": "StableLM-3B-shape GGUF Q6_K attention + classifier / Q4_K MLP, fp16 KV, "
+                        f"{P}-token prefix, {B} branches with private suffixes of 1-256 tokens, {T} lockstep "
+                        "greedy tokens each", "layers": L, "prefix": P, "branches": B, "tokens_per_branch": T,
+            "suffix_lengths": [int(k) for k in lengths], "prefix_prefill_s": round(prefill_s, 4),
+            "suffix_append_s": round(append_s[-1], 4), "ms_per_step": round(per_step * 1e3, 3),
+            "tok_s": round(B / per_step, 1),
             "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(achieved / HBM_PEAK_GBS, 4), "algorithmic_bytes_per_step": int(step_bytes),
                          "weight_bytes": int(weight_bytes)}}
 
 
-def cpu_baseline(config, tensors, threads, prompt_len):
-    """The oracle (C restatement of the Go scalar engine) on the host cores:
-    a 128-token batched prefill chunk (prefillBatch) and 2 decode forwards
-    at positions prompt_len, prompt_len + 1 on a zero-initialised KV."""
+def cpu_baseline(config, tensors, threads, prompt_len, decode_tokens=6, prefill_tokens=128):
+    """The oracle (C restatement of the Go scalar engine) on the host cores,
+    at each thread count of `threads`: a batched prefill of 128 tokens
+    (prefillBatch, timed), then `decode_tokens` greedy decode forwards with
+    logits at the positions that follow (timed). The headline figure is the
+    last thread count's decode rate."""
     import numpy as np
     from oracle import pyoracle
-    pyoracle.set_threads(threads)
-    m = pyoracle.StableLM(config, tensors, capacity=1024)
     rng = np.random.default_rng(5)
-    ids = rng.integers(0, config["vocab_size"], 128).astype(np.int32)
-    t0 = time.perf_counter()
-    m.prefill(ids, 0)
-    prefill_tok_s = 128 / (time.perf_counter() - t0)
-    t0 = time.perf_counter()
-    for i in range(2):
-        m.forward(int(ids[i]), prompt_len + i)
-    decode_tok_s = 2 / (time.perf_counter() - t0)
-    m.close()
-    return {"value": round(decode_tok_s, 4), "unit": "tok/s", "cores": threads, "kind": "port",
-            "prefill_tok_s": round(prefill_tok_s, 3),
-            "prefill_s_extrapolated": round(prompt_len / prefill_tok_s, 2),
-            "sample": f"oracle (C restatement of tinyoai's Go scalar-float64 engine, -ffp-contract=off, "
-                      f"{threads} OpenMP threads): one 128-token batched prefill chunk and 2 decode forwards "
-                      f"at positions {prompt_len}-{prompt_len + 1} with zero-initialised fp32 KV, same weights"}
+    ids = rng.integers(0, config["vocab_size"], prefill_tokens).astype(np.int32)
+    runs = {}
+    for th in threads:
+        pyoracle.set_threads(th)
+        m = pyoracle.StableLM(config, tensors, capacity=1024)
+        t0 = time.perf_counter()
+        logits = m.prefill(ids, 0)
+        prefill_tok_s = prefill_tokens / (time.perf_counter() - t0)
+        t0 = time.perf_counter()
+        for i in range(decode_tokens):
+            logits = m.forward(int(np.argmax(logits)), prefill_tokens + i)
+        decode_tok_s = decode_tokens / (time.perf_counter() - t0)
+        m.close()
+        runs[th] = {"decode_tok_s": round(decode_tok_s, 4), "prefill_tok_s": round(prefill_tok_s, 3),
+                    "prefill_s_extrapolated": round(prompt_len / prefill_tok_s, 2)}
+        print(f"[bench] cpu oracle at {th} threads: {runs[th]}", file=sys.stderr, flush=True)
+    top = threads[-1]
+    return {"value": runs[top]["decode_tok_s"], "unit": "tok/s", "cores": top, "kind": "port",
+            "prefill_tok_s": runs[top]["prefill_tok_s"], "prefill_s_extrapolated": runs[top]["prefill_s_extrapolated"],
+            "by_threads": {str(k): v for k, v in runs.items()},
+            "sample": f"oracle (C restatement of tinyoai's Go scalar-float64 engine, -ffp-contract=off, OpenMP "
+                      f"threads {list(threads)}; {top} = the host cores given to one GPU): a {prefill_tokens}-token "
+                      f"batched prefill, then {decode_tokens} greedy decode forwards with logits at positions "
+                      f"{prefill_tokens}-{prefill_tokens + decode_tokens - 1}, same weights"}
 
 
 def main():
@@ -241,11 +332,12 @@ def main():
     ap.add_argument("--prompt", type=int, default=512)
     ap.add_argument("--generate", type=int, default=256)
     ap.add_argument("--layers", type=int, default=32)
-    ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
+    ap.add_argument("--cpu-threads", type=str, default="8,16",
+                    help="oracle thread counts for the CPU baseline (16: the host cores given to one GPU)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--seed", type=int, default=1234)
-    ap.add_argument("--workload", choices=["decode", "branches"], default="decode",
-                    help="branches: the K-quant 16-branch workload instead of the Q8_0 decode one")
+    ap.add_argument("--workload", choices=["all", "decode", "long_context", "branches"], default="all",
+                    help="all: the Q8_0 decode headline plus every other workload under its own key")
     ap.add_argument("--dtype", choices=["q8_0", "bf16"], default="q8_0",
                     help="weight format (bf16 with --prompt 8129 --generate 64 --kv 16: the long-context workload)")
     ap.add_argument("--kv", type=int, choices=[16, 32], default=32, help="KV cache bits")
@@ -257,8 +349,9 @@ def main():
               f"attention head / MLP column with one all-reduce per layer; see DESIGN.md).", file=sys.stderr)
         sys.exit(2)
 
-    if args.workload == "branches":
-        print(json.dumps(branches_workload(args)))
+    if args.workload in ("branches", "long_context"):
+        fn = branches_workload if args.workload == "branches" else long_context_workload
+        print(json.dumps({args.workload: fn(args)}))
         return
 
     import numpy as np
@@ -366,9 +459,16 @@ def main():
     out["kernel_q8_0"] = q8_0_kernel()
     if not args.no_cpu:
         print("[bench] timing the CPU oracle", file=sys.stderr, flush=True)
-        out["cpu_baseline"] = cpu_baseline(config, tensors, args.cpu_threads, args.prompt)
+        threads = [int(t) for t in args.cpu_threads.split(",") if t]
+        out["cpu_baseline"] = cpu_baseline(config, tensors, threads, args.prompt)
     else:
         out["cpu_baseline"] = None
+    del tensors
+    if args.workload == "all":
+        print("[bench] long-context workload", file=sys.stderr, flush=True)
+        out["long_context"] = long_context_workload(args)
+        print("[bench] branch workload", file=sys.stderr, flush=True)
+        out["branches"] = branches_workload(args)
     print(json.dumps(out))
 
 

@@ -76,9 +76,11 @@ const char *tinyoai_last_error(void);
 
 /* Uploads every tensor named by loadStableWeights (stablelm.go:178-191) to
  * HBM and prepares fp32 KV storage (StableLMOptions{KVCache: "f32"}).
- * Layer matrices are regrouped per layer into one input-side matrix
- * (q, k, v, gate, up: one storage format) and one output-side matrix
- * (o, down: one storage format); other combinations return TINYOAI_EINVAL. */
+ * Layer matrices are regrouped per layer into an input-side matrix (q, k,
+ * v, gate, up) and an output-side matrix (o, down). q, k and v must share
+ * one storage format and gate and up one format; the attention and MLP
+ * sections may differ (as GGUF K-quant mixes store them), and then each is
+ * kept as a matrix of its own. Other combinations return TINYOAI_EINVAL. */
 int tinyoai_stablelm_load(const tinyoai_stablelm_config *config, const tinyoai_tensor *tensors,
                           int32_t n_tensors, tinyoai_model **out);
 
@@ -91,9 +93,11 @@ int tinyoai_stablelm_load(const tinyoai_stablelm_config *config, const tinyoai_t
 int tinyoai_stablelm_forward(tinyoai_model *m, int32_t prefix, const int32_t *tokens, int32_t n,
                              int32_t want_logits, float *logits);
 
-/* SetKVBits (mlx_kv.go:78-91): 32 = fp32 KV, 16 = fp16 KV rounded with
- * floatHalf (kv_cache.go:27-65). A change discards the resident prefix and
- * sets *cleared = 1. */
+/* SetKVBits (mlx_kv.go:78-91): 16 = fp16 KV rounded with floatHalf
+ * (kv_cache.go:27-65), 32 = fp32 KV (the CPU engine's StableLMOptions{KVCache:
+ * "f32"}). The MLX forwarder's 8 (affine 8-bit KV in groups of 64,
+ * mlx_kv.go:46-73) is rejected with TINYOAI_EINVAL. A change discards the
+ * resident prefix and sets *cleared = 1. */
 int tinyoai_stablelm_set_kv_bits(tinyoai_model *m, int32_t bits, int32_t *cleared);
 
 /* LimitCache (mlx_native.go:231-244): reserves `limit` KV positions; a
@@ -106,28 +110,39 @@ int tinyoai_stablelm_reset(tinyoai_model *m);
 /* Resident prefix length (nativeMLX.offset), or a negative code. */
 int tinyoai_stablelm_offset(const tinyoai_model *m);
 
-/* Releases weights, KV and the stream (mlx_native.go:247-259). */
+/* Releases weights, KV and the stream (mlx_native.go:247-259); refused
+ * (TINYOAI_EINVAL, nothing released) while branches are open. */
 int tinyoai_stablelm_close(tinyoai_model *m);
 
 /* NewBranches (mlx_branches.go:25-33; mlxBrancher, branches.go:55-59): opens
  * `count` independent suffixes that borrow the resident prefix [0, prefix)
- * (0 <= prefix <= offset) read-only. Each branch owns up to `max_steps`
- * positions of suffix KV, allocated here (the reference grows its arrays
- * per step); the KV format is the model's at opening. Head widths 8, 64 and
- * 80; count * vocab <= the prefill chunk's product buffer. While branches
- * are open the caller must not rewind, reset or change the KV format of
- * the model (the reference holds the model gate), and must close them
- * before the model. */
-int tinyoai_stablelm_branches_open(tinyoai_model *m, int32_t prefix, int32_t count, int32_t max_steps,
+ * (0 <= prefix <= offset) read-only. Branch j holds the suffix positions
+ * prefix + [0, length(j)); the suffix KV grows with use (in powers of two,
+ * at most max_len positions per branch; 0 = up to the context), in the
+ * model's KV format at opening. Head widths 8, 64 and 80; count * vocab <=
+ * the prefill chunk's product buffer. While branches are open the model
+ * refuses forward, reset, set_kv_bits, limit_cache and close with
+ * TINYOAI_EINVAL (the reference's session holds the model gate,
+ * branches.go:16-22). */
+int tinyoai_stablelm_branches_open(tinyoai_model *m, int32_t prefix, int32_t count, int32_t max_len,
                                    tinyoai_branches **out);
 /* nativeBranches.Forward (mlx_branches.go:120-182): one token per branch,
- * all at absolute position prefix + step; writes `count` rows of fp32
+ * branch j at position prefix + length(j); writes `count` rows of fp32
  * logits [count][vocab]. Attention combines the shared prefix with the
  * branch's own suffix under one softmax (branchAttention,
  * mlx_branches.go:98-114). TINYOAI_EINVAL for a wrong count, an invalid id,
- * or a step past max_steps or the context; a native failure closes the
+ * or a suffix past max_len or the context; a native failure closes the
  * branches' storage (later calls fail), as Forward closes them on error. */
 int tinyoai_stablelm_branches_forward(tinyoai_branches *b, const int32_t *tokens, int32_t count, float *logits);
+/* Private suffixes of different lengths (no counterpart in the reference,
+ * whose branches all advance one token per step): appends lengths[j] >= 1
+ * tokens to branch j, the tokens given branch after branch (sum of lengths
+ * ids), evaluated causally within each branch against the shared prefix;
+ * writes each branch's last-row logits [count][vocab]. Errors as forward. */
+int tinyoai_stablelm_branches_append(tinyoai_branches *b, const int32_t *tokens, const int32_t *lengths,
+                                     int32_t count, float *logits);
+/* Suffix tokens branch `branch` holds, or a negative code. */
+int tinyoai_stablelm_branches_length(const tinyoai_branches *b, int32_t branch);
 /* nativeBranches.Close (mlx_branches.go:36-47): frees the suffix KV; the
  * shared prefix stays. NULL is accepted. */
 int tinyoai_stablelm_branches_close(tinyoai_branches *b);

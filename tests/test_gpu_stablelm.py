@@ -331,63 +331,6 @@ def test_mixed_format_layers_against_oracle(hip, oracle, mlp, attn):
     f.close()
 
 
-def _branch_case(hip, oracle, config, tensors, prompt, seeds, steps, kv_bits):
-    """Branches of a resident prompt against one oracle per branch (the
-    prompt prefilled, then the branch's tokens one by one): logits within
-    1e-3 of their range, identical greedy ids; afterwards the resident
-    model continues as if no branch had run."""
-    P, B = len(prompt), len(seeds)
-    half = kv_bits == 16
-    f = hip.StableLMForwarder(config, tensors)
-    f.set_kv_bits(kv_bits)
-    f.forward(0, prompt)
-    refs = [oracle.StableLM(config, tensors, half_kv=half, capacity=P + steps + 1) for _ in range(B)]
-    for r in refs:
-        r.prefill(prompt, 0)
-    br = f.new_branches(P, B, steps)
-    toks = list(seeds)
-    for s in range(steps):
-        got = br.forward(toks)
-        assert got.shape == (B, config["vocab_size"])
-        for j in range(B):
-            want = refs[j].forward(toks[j], P + s)
-            assert np.max(np.abs(got[j] - want)) <= 1e-3 * float(np.ptp(want)), (s, j)
-            assert int(np.argmax(got[j])) == int(np.argmax(want)), (s, j)
-        toks = [int(np.argmax(got[j])) for j in range(B)]
-    with pytest.raises(RuntimeError):
-        br.forward(toks)  # past max_steps
-    br.close()
-    with pytest.raises(RuntimeError):
-        f.new_branches(P + 1, B, 4)  # beyond the resident prefix
-    ref = oracle.StableLM(config, tensors, half_kv=half, capacity=P + 2)
-    ref.prefill(prompt, 0)
-    want = ref.forward(int(seeds[0]), P)
-    got = f.forward(P, [int(seeds[0])])
-    assert np.max(np.abs(got - want)) <= 1e-3 * float(np.ptp(want))
-    f.close()
-
-
-@pytest.mark.parametrize("kv_bits", [32, 16])
-def test_branches_reference_model(hip, oracle, tiny_stablelm, kv_bits):
-    """nativeBranches semantics (mlx_branches.go:25-182) on the reference's
-    tiny StableLM (head width 8): five branches of the "Hello abc" prompt,
-    six lockstep tokens each."""
-    config, tensors = tiny_stablelm
-    _branch_case(hip, oracle, config, tensors, np.array(HELLO_ABC, np.int32), [264, 285, 199, 5, 300], 6, kv_bits)
-
-
-def test_branches_kquant_mix_3b_shapes(hip, oracle):
-    """The K-quant branch workload's layer shapes and formats (Q6_K
-    attention and classifier, Q4_K MLP, fp16 KV), two layers: four branches
-    of a 70-token prompt (two 64-position attention splits of shared prefix
-    plus the suffix), five tokens each."""
-    config = W.validate_stablelm_config(dict(W.STABLELM_3B, num_hidden_layers=2, max_position_embeddings=256))
-    tensors = W.synthetic_stablelm(config, W.Q4_K, seed=31, attn_dtype=W.Q6_K, head_dtype=W.Q6_K)
-    prompt = np.random.default_rng(37).integers(0, 65536, 70).astype(np.int32)
-    oracle.set_threads(8)
-    _branch_case(hip, oracle, config, tensors, prompt, [11, 4093, 60000, 777], 5, 16)
-
-
 @pytest.mark.parametrize("kv_bits", [32, 16])
 def test_prefill_after_prefix_against_oracle(hip, oracle, kv_bits):
     """Matrix-core prefill attention at a nonzero start: a 100-token prefix,

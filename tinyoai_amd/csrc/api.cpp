@@ -483,7 +483,7 @@ int StableModel::init(const tinyoai_stablelm_config &c, const tinyoai_tensor *te
   if ((rc = alloc((void **)&x, (size_t)d * 4)) || (rc = alloc((void **)&qbuf, w_att * 4)) ||
       (rc = alloc((void **)&mbuf, (size_t)I * 4)) || (rc = alloc((void **)&abuf, w_att * 4)) ||
       (rc = alloc((void **)&logits_dev, (size_t)c.vocab_size * 4 + 256)) ||
-      (rc = alloc((void **)&params, (size_t)(16 + std::max(chunk, dims.rot)) * 4)) ||
+      (rc = alloc((void **)&params, (size_t)(16 + std::max(chunk, dims.rot) + 2 * chunk) * 4)) ||
       (rc = alloc((void **)&trace_dev, (size_t)c.num_hidden_layers * d * 4)) ||
       (rc = alloc((void **)&trace_att, (size_t)c.num_hidden_layers * w_att * 4)) ||
       (rc = alloc((void **)&trace_gate, (size_t)c.num_hidden_layers * I * 4)))
@@ -520,7 +520,8 @@ int StableModel::init(const tinyoai_stablelm_config &c, const tinyoai_tensor *te
   if (e != hipSuccess) return hip_fail(e, "persistent decode state");
   e = hipEventCreateWithFlags(&params_copied, hipEventDisableTiming);
   if (e != hipSuccess) return hip_fail(e, "hipEventCreate");
-  e = hipHostMalloc(&h_pinned, (size_t)c.vocab_size * 4 + 4096 + (size_t)std::max(chunk, dims.rot) * 4 + 64,
+  e = hipHostMalloc(&h_pinned,
+                    (size_t)c.vocab_size * 4 + 4096 + (size_t)(std::max(chunk, dims.rot) + 2 * chunk) * 4 + 64,
                     hipHostMallocDefault);
   if (e != hipSuccess) return fail(TINYOAI_ENOMEM, "hipHostMalloc: %s", hipGetErrorString(e));
   e = hipStreamSynchronize(stream);
@@ -673,16 +674,23 @@ int StableModel::ensure_kv(int needed) {
     prof.end(stream);                  \
   } while (0)
 
-// Copies head[0..nh), then from int 16 on the ids or the float row, into
-// the device parameter block through the pinned slot, first waiting for the
-// slot's previous copy.
-int StableModel::upload_params(const int *head_vals, int nh, const int32_t *ids, int n, const float *row, int nrow) {
+// Copies head[0..nh), then from int 16 on the ids or the float row, and
+// the n (position, slot) pairs of `rows` into the device parameter block
+// (see rows_dev) through the pinned slot, first waiting for the slot's
+// previous copy.
+int StableModel::upload_params(const int *head_vals, int nh, const int32_t *ids, int n, const float *row, int nrow,
+                               const int *rows) {
   int *hp = (int *)((char *)h_pinned + (size_t)cfg.vocab_size * 4 + 64);  // after the logits and error word
   if (params_copied) TRY_HIP(hipEventSynchronize(params_copied), "parameter slot");
   for (int i = 0; i < nh; i++) hp[i] = head_vals[i];
   if (n) memcpy(hp + 16, ids, (size_t)n * 4);
   if (nrow) memcpy(hp + 16, row, (size_t)nrow * 4);
-  const int count = n ? 16 + n : (nrow ? 16 + nrow : nh);
+  int count = n ? 16 + n : (nrow ? 16 + nrow : nh);
+  if (rows) {
+    const int off = 16 + std::max(chunk, dims.rot);
+    memcpy(hp + off, rows, (size_t)n * 8);
+    count = off + 2 * n;
+  }
   TRY_HIP(hipMemcpyAsync(params, hp, (size_t)count * 4, hipMemcpyHostToDevice, stream), "parameters");
   TRY_HIP(hipEventRecord(params_copied, stream), "parameter event");
   return TINYOAI_OK;
@@ -796,9 +804,11 @@ int StableModel::decode_step(int token, int pos, bool want_logits) {
 
 // y[n][ldy] = x[n][ldx] * W^T: on the matrix cores when the format allows
 // (activations split into bf16 hi/lo planes first), else the vector-unit
-// GEMM. Every output row depends only on its own input row, whatever the
-// chunk size (a prefix reused from the cache gives the same results).
-int StableModel::project(const MatDesc &w, const float *x, int ldx, int n, float *y, int ldy, int *splits) {
+// GEMM. Without rowstream every output row depends only on its own input
+// row, whatever the chunk size (a prefix reused from the cache gives the
+// same results).
+int StableModel::project(const MatDesc &w, const float *x, int ldx, int n, float *y, int ldy, int *splits,
+                         bool rowstream) {
   if (splits) *splits = 1;
   if (gemm_mfma_supported(w)) {
     const bool two = gemm_planes(w) == 2;
@@ -808,12 +818,11 @@ int StableModel::project(const MatDesc &w, const float *x, int ldx, int n, float
     if (splits) *splits = ks;
     STAGE(ST_PREFILL_GEMM, launch_split_bf16(x, ldx, w.cols, n, XH, two ? XL : nullptr, stream), "bf16 split");
     STAGE(ST_PREFILL_GEMM, launch_gemm_mfma(w, XH, two ? XL : nullptr, n, y, ldy, stream, ks), "projection");
-  } else if (n <= kRowStreamMax) {
-    // A few rows (branch steps, short suffixes): one row-streaming matvec
-    // per row. The vector-unit GEMM costs about as much for 16 rows as for
-    // 64 (677 us for a 16-row K-quant product at the 3B shapes); the row
-    // kernels stream the matrix per row, from the last-level cache after
-    // the first row.
+  } else if (rowstream && n <= kRowStreamMax) {
+    // A few branch rows: one row-streaming matvec per row. The vector-unit
+    // GEMM costs about as much for 16 rows as for 64 (677 us for a 16-row
+    // K-quant product at the 3B shapes); the row kernels stream the matrix
+    // per row, from the last-level cache after the first row.
     for (int j = 0; j < n; j++)
       STAGE(ST_PREFILL_GEMM,
             launch_ln_matvec(w, nullptr, nullptr, 0.0, 0, x + (size_t)j * ldx, y + (size_t)j * ldy, grid_out,
@@ -916,66 +925,209 @@ int StableModel::prefill_chunk(const int32_t *ids, int n, int start, bool want_l
   return TINYOAI_OK;
 }
 
-Branches::~Branches() {
-  if (m && m->stream) hipStreamSynchronize(m->stream);
-  for (void *p : buffers) hipFree(p);
+int StableModel::busy_with_branches() const {
+  return open_branches > 0 ? fail(TINYOAI_EINVAL, "%d branch session(s) borrow this model's prefix: close them first",
+                                  open_branches)
+                           : TINYOAI_OK;
 }
 
-// One token per branch at position prefix + step (nativeBranches.Forward,
-// mlx_branches.go:120-182): the rows go through the prefill products; their
-// K and V land in the branch slots; attention reads the shared prefix and
-// the branch's own suffix; every row's logits come back.
-int StableModel::branch_step(Branches &b, const int32_t *tokens, float *logits) {
-  const int n = b.count, pos = b.prefix + b.step, d = dims.d, I = dims.inter, V = cfg.vocab_size;
-  const int vals[1] = {pos};
-  if (int rc = upload_params(vals, 1, tokens, n)) return rc;
-  const int *d_pos0 = params, *d_ids = params + 16;
-  TRY_HIP(launch_embed(embed.desc, d_ids, n, X, stream), "embed");
-  for (int l = 0; l < cfg.num_hidden_layers; l++) {
-    const LayerDev &w = layers[l];
-    const bool split_in = w.win2.rows > 0, split_out = w.wout2.rows > 0;
-    const int64_t vpc = values_per_chunk(w.wout.fmt), down0 = (d + vpc - 1) / vpc * vpc;
-    const MatDesc wo = split_out ? w.wout : column_view(w.wout, 0, d);
-    const MatDesc wd = split_out ? w.wout2 : column_view(w.wout, down0, I);
-    int rc;
-    TRY_HIP(launch_layer_norm_rows(X, w.ln_w, w.ln_b, dims.eps, n, d, H, stream), "layer_norm");
-    if (split_in) {
-      StableDims da = dims, dm = dims;
-      da.inter = 0;
-      dm.win_q = dm.win_kv = 0;
-      const int ra = w.win.rows, rm = w.win2.rows;
-      float *Ya = Y, *Ym = Y + (size_t)n * ra;
-      if ((rc = project(w.win, H, d, n, Ya, ra)) || (rc = project(w.win2, H, d, n, Ym, rm))) return rc;
-      TRY_HIP(launch_in_epilogue(da, b.kv[l], Ya, ra, rope, d_pos0, n, Q, M, stream, nullptr, nullptr, b.slots,
-                                 b.prefix),
-              "in_epilogue");
-      TRY_HIP(launch_in_epilogue(dm, b.kv[l], Ym, rm, rope, d_pos0, n, Q, M, stream, nullptr, nullptr, b.slots,
-                                 b.prefix),
-              "in_epilogue");
-    } else {
-      if ((rc = project(w.win, H, d, n, Y, win_rows))) return rc;
-      TRY_HIP(launch_in_epilogue(dims, b.kv[l], Y, win_rows, rope, d_pos0, n, Q, M, stream, nullptr, nullptr,
-                                 b.slots, b.prefix),
-              "in_epilogue");
-    }
-    int sp = 1, sd = 1;
-    if ((rc = project(wd, M, I, n, D, d, &sd))) return rc;
-    TRY_HIP(launch_branch_attention(dims, kv[l], b.kv[l], b.prefix, b.slots, Q, d_pos0, n, pos, b.partials,
-                                    b.counters, A, b.max_splits, stream),
-            "branch attention");
-    if ((rc = project(wo, A, d, n, P, d, &sp))) return rc;
-    TRY_HIP(launch_residual(X, P, sp, D, sd, (int64_t)n * d, stream), "residual");
+void Branches::free_kv() {
+  for (auto &l : kv) {
+    if (l.k) hipFree(l.k);
+    if (l.v) hipFree(l.v);
   }
-  // Final LayerNorm of every row, then the classifier over all rows.
-  TRY_HIP(launch_layer_norm_rows(X, norm_w, norm_b, dims.eps, n, d, H, stream), "final norm");
-  if (int rc = project(head.desc, H, d, n, Y, V)) return rc;
-  TRY_HIP(hipMemcpyAsync(logits, Y, (size_t)n * V * 4, hipMemcpyDeviceToHost, stream), "logits");
+  kv.clear();
+  scap = 0;
+}
+
+Branches::~Branches() {
+  if (m && m->stream) hipStreamSynchronize(m->stream);
+  free_kv();
+  if (partials) hipFree(partials);
+  if (counters) hipFree(counters);
+  if (last) hipFree(last);
+  if (m) m->open_branches--;
+}
+
+int Branches::grow(int need) {
+  if (need <= scap) return TINYOAI_OK;
+  int want = 16;
+  while (want < need) want *= 2;
+  want = std::min(want, max_len);
+  if (want < need) return fail(TINYOAI_EINVAL, "branch suffix of %d positions exceeds its limit %d", need, max_len);
+  const StableDims &s = m->dims;
+  const size_t esz = m->kv_half ? 2 : 4, row = (size_t)s.hd * esz;
+  const size_t bytes = (size_t)s.kv_heads * count * want * row;
+  std::vector<KVDev> grown(m->cfg.num_hidden_layers);
+  for (auto &l : grown) {
+    hipError_t e = hipMalloc(&l.k, bytes);
+    if (e == hipSuccess) e = hipMalloc(&l.v, bytes);
+    if (e != hipSuccess) {
+      for (auto &g : grown) { if (g.k) hipFree(g.k); if (g.v) hipFree(g.v); }
+      return fail(TINYOAI_ENOMEM, "branch KV of %d positions: %s", want, hipGetErrorString(e));
+    }
+    l.cap = count * want;
+    l.half = m->kv_half;
+  }
+  // Existing entries: rows of scap * hd values (one per kv head and branch)
+  // move to rows of want * hd.
+  if (scap > 0) {
+    for (size_t l = 0; l < kv.size(); l++)
+      for (int which = 0; which < 2; which++) {
+        hipError_t e = hipMemcpy2DAsync(which ? grown[l].v : grown[l].k, want * row, which ? kv[l].v : kv[l].k,
+                                        scap * row, scap * row, (size_t)s.kv_heads * count, hipMemcpyDeviceToDevice,
+                                        m->stream);
+        if (e != hipSuccess) {
+          hipStreamSynchronize(m->stream);
+          for (auto &g : grown) { hipFree(g.k); hipFree(g.v); }
+          return hip_fail(e, "branch KV growth");
+        }
+      }
+  }
+  hipError_t e = hipStreamSynchronize(m->stream);
+  free_kv();
+  kv = grown;
+  scap = want;
+  return e == hipSuccess ? TINYOAI_OK : hip_fail(e, "branch KV growth");
+}
+
+int Branches::ensure_partials(int nq, int splits) {
+  const size_t need = (size_t)nq * m->dims.heads * partial_region(splits, m->dims.hd);
+  const size_t words = (size_t)nq * m->dims.heads;
+  if (need > partial_floats) {
+    hipStreamSynchronize(m->stream);
+    if (partials) hipFree(partials);
+    partials = nullptr;
+    partial_floats = 0;
+    hipError_t e = hipMalloc(&partials, need * 4);
+    if (e != hipSuccess) return fail(TINYOAI_ENOMEM, "branch attention scratch (%zu floats): %s", need, hipGetErrorString(e));
+    partial_floats = need;
+  }
+  if (words > counter_words) {
+    hipStreamSynchronize(m->stream);
+    if (counters) hipFree(counters);
+    counters = nullptr;
+    counter_words = 0;
+    hipError_t e = hipMalloc(&counters, words * 4);
+    if (e == hipSuccess) e = hipMemsetAsync(counters, 0, words * 4, m->stream);
+    if (e != hipSuccess) return fail(TINYOAI_ENOMEM, "branch attention counters: %s", hipGetErrorString(e));
+    counter_words = words;
+  }
+  return TINYOAI_OK;
+}
+
+// Branch rows (nativeBranches.Forward, mlx_branches.go:120-182, extended to
+// several rows per branch): the rows go through the prefill products; each
+// row's K and V land in its branch's suffix slots; attention reads the
+// shared prefix and the row's own branch suffix under one softmax
+// (branchAttention, mlx_branches.go:98-114). A branch's run of rows is
+// causal within itself, like a prefill chunk.
+int StableModel::branch_rows(Branches &b, const int32_t *ids, const int32_t *br, int n, float *logits) {
+  const int d = dims.d, I = dims.inter, V = cfg.vocab_size, pfx = b.prefix;
+  std::vector<int> add(b.count, 0), rows((size_t)2 * n);
+  int need = 0, run = 0;  // suffix positions needed; most rows of one branch in this call
+  for (int i = 0; i < n; i++) {
+    need = std::max(need, b.len[br[i]] + ++add[br[i]]);
+    run = std::max(run, add[br[i]]);
+  }
+  if (int rc = b.grow(need)) return rc;
+  for (int i = 0, k = 0; i < n; i++) {
+    const int j = br[i], s = b.len[j] + (k = (i > 0 && br[i - 1] == j) ? k + 1 : 0);
+    rows[2 * i] = pfx + s;
+    rows[2 * i + 1] = j * b.scap + s;
+  }
+  const bool flash = flash_prefill_supported(dims.hd);
+  // Rows per chunk: the prefill workspaces hold `chunk`; one row per branch
+  // (count <= chunk, checked at opening) runs as one chunk on the split-K
+  // attention; longer runs take the matrix-core attention per branch, or
+  // the split-K one in chunks whose partials stay within 64 MB.
+  int per = chunk;
+  if (run > 1 && !flash) {
+    const size_t region = (size_t)dims.heads * partial_region(attention_splits(pfx + need, 1), dims.hd) * 4;
+    per = (int)std::min<size_t>(per, std::max<size_t>(1, ((size_t)64 << 20) / region));
+  }
+  const int hq = dims.heads * dims.hd;
+  for (int r0 = 0; r0 < n; r0 += per) {
+    const int nc = std::min(per, n - r0);
+    const int32_t *cid = ids + r0;
+    const int *crow = rows.data() + 2 * r0;
+    if (int rc = upload_params(nullptr, 0, cid, nc, nullptr, 0, crow)) return rc;
+    const int *d_ids = params + 16, *d_rows = rows_dev();
+    // runs of one branch within the chunk: [seg[k], seg[k + 1])
+    std::vector<int> seg{0};
+    for (int i = 1; i < nc; i++)
+      if (br[r0 + i] != br[r0 + i - 1]) seg.push_back(i);
+    seg.push_back(nc);
+    int max_pos = 0;
+    for (int i = 0; i < nc; i++) max_pos = std::max(max_pos, crow[2 * i]);
+    const bool use_flash = flash && run > 1;
+    int max_splits = 0;
+    if (!use_flash) {
+      max_splits = attention_splits(max_pos, std::min(attention_steps(max_pos, dims.heads), 4));
+      if (int rc = b.ensure_partials(nc, max_splits)) return rc;
+    }
+    TRY_HIP(launch_embed(embed.desc, d_ids, nc, X, stream), "embed");
+    for (int l = 0; l < cfg.num_hidden_layers; l++) {
+      const LayerDev &w = layers[l];
+      const bool split_in = w.win2.rows > 0, split_out = w.wout2.rows > 0;
+      const int64_t vpc = values_per_chunk(w.wout.fmt), down0 = (d + vpc - 1) / vpc * vpc;
+      const MatDesc wo = split_out ? w.wout : column_view(w.wout, 0, d);
+      const MatDesc wd = split_out ? w.wout2 : column_view(w.wout, down0, I);
+      int rc;
+      TRY_HIP(launch_layer_norm_rows(X, w.ln_w, w.ln_b, dims.eps, nc, d, H, stream), "layer_norm");
+      if (split_in) {
+        StableDims da = dims, dm = dims;
+        da.inter = 0;
+        dm.win_q = dm.win_kv = 0;
+        const int ra = w.win.rows, rm = w.win2.rows;
+        float *Ya = Y, *Ym = Y + (size_t)nc * ra;
+        if ((rc = project(w.win, H, d, nc, Ya, ra, nullptr, true)) ||
+            (rc = project(w.win2, H, d, nc, Ym, rm, nullptr, true)))
+          return rc;
+        TRY_HIP(launch_in_epilogue(da, b.kv[l], Ya, ra, rope, nullptr, nc, Q, M, stream, nullptr, nullptr, d_rows),
+                "in_epilogue");
+        TRY_HIP(launch_in_epilogue(dm, b.kv[l], Ym, rm, rope, nullptr, nc, Q, M, stream, nullptr, nullptr, d_rows),
+                "in_epilogue");
+      } else {
+        if ((rc = project(w.win, H, d, nc, Y, win_rows, nullptr, true))) return rc;
+        TRY_HIP(launch_in_epilogue(dims, b.kv[l], Y, win_rows, rope, nullptr, nc, Q, M, stream, nullptr, nullptr,
+                                   d_rows),
+                "in_epilogue");
+      }
+      int sp = 1, sd = 1;
+      if ((rc = project(wd, M, I, nc, D, d, &sd, true))) return rc;
+      if (use_flash) {
+        for (size_t k = 0; k + 1 < seg.size(); k++) {
+          const int a0 = seg[k], cnt = seg[k + 1] - seg[k], j = br[r0 + a0];
+          TRY_HIP(launch_flash_prefill(dims, kv[l], Q + (size_t)a0 * hq, d_rows + 2 * a0, cnt, A + (size_t)a0 * hq,
+                                       stream, nullptr, nullptr, &b.kv[l], pfx, j * b.scap),
+                  "branch attention");
+        }
+      } else {
+        TRY_HIP(launch_branch_attention(dims, kv[l], b.kv[l], pfx, Q, d_rows, nc, max_pos, b.partials, b.counters,
+                                        A, max_splits, stream),
+                "branch attention");
+      }
+      if ((rc = project(wo, A, d, nc, P, d, &sp, true))) return rc;
+      TRY_HIP(launch_residual(X, P, sp, D, sd, (int64_t)nc * d, stream), "residual");
+    }
+    // each branch's newest row of this chunk
+    for (size_t k = 0; k + 1 < seg.size(); k++) {
+      const int last_row = seg[k + 1] - 1, j = br[r0 + last_row];
+      TRY_HIP(launch_copy_row(X + (size_t)last_row * d, b.last + (size_t)j * d, d, stream), "branch row");
+    }
+  }
+  // Final LayerNorm of every branch's newest row, then the classifier.
+  TRY_HIP(launch_layer_norm_rows(b.last, norm_w, norm_b, dims.eps, b.count, d, H, stream), "final norm");
+  if (int rc = project(head.desc, H, d, b.count, Y, V, nullptr, true)) return rc;
+  TRY_HIP(hipMemcpyAsync(logits, Y, (size_t)b.count * V * 4, hipMemcpyDeviceToHost, stream), "logits");
   TRY_HIP(hipStreamSynchronize(stream), "branch step");
-  b.step++;
+  for (int j = 0; j < b.count; j++) b.len[j] += add[j];
   return TINYOAI_OK;
 }
 
 int StableModel::forward(int prefix, const int32_t *tokens, int n, bool want_logits, float *logits) {
+  if (int rc = busy_with_branches()) return rc;
   if (prefix < 0 || prefix > offset || n <= 0 || !tokens || prefix + n > cfg.max_position_embeddings)
     return fail(TINYOAI_EINVAL, "invalid cached prefix or context length (prefix %d, offset %d, n %d)", prefix,
                 offset, n);
@@ -1063,8 +1215,10 @@ int tinyoai_stablelm_forward(tinyoai_model *m, int32_t prefix, const int32_t *to
 
 int tinyoai_stablelm_set_kv_bits(tinyoai_model *m, int32_t bits, int32_t *cleared) {
   if (!m || !m->stable) return fail(TINYOAI_EINVAL, "not a StableLM handle");
-  if (bits != 16 && bits != 32) return fail(TINYOAI_EINVAL, "KV bits must be 16 or 32");
+  if (bits != 16 && bits != 32)
+    return fail(TINYOAI_EINVAL, "KV bits must be 16 (fp16) or 32 (fp32); affine 8-bit KV is not supported");
   StableModel &s = *m->stable;
+  if (int rc = s.busy_with_branches()) return rc;
   const int half = bits == 16;
   int c = 0;
   if (half != s.kv_half) {
@@ -1080,6 +1234,7 @@ int tinyoai_stablelm_set_kv_bits(tinyoai_model *m, int32_t bits, int32_t *cleare
 int tinyoai_stablelm_limit_cache(tinyoai_model *m, int32_t limit, int32_t *cleared) {
   if (!m || !m->stable) return fail(TINYOAI_EINVAL, "not a StableLM handle");
   StableModel &s = *m->stable;
+  if (int rc = s.busy_with_branches()) return rc;
   if (limit <= 0 || limit > s.cfg.max_position_embeddings) return fail(TINYOAI_EINVAL, "invalid cache limit %d", limit);
   int c = 0;
   s.reserve = limit;
@@ -1094,6 +1249,7 @@ int tinyoai_stablelm_limit_cache(tinyoai_model *m, int32_t limit, int32_t *clear
 
 int tinyoai_stablelm_reset(tinyoai_model *m) {
   if (!m || !m->stable) return fail(TINYOAI_EINVAL, "not a StableLM handle");
+  if (int rc = m->stable->busy_with_branches()) return rc;
   hipStreamSynchronize(m->stable->stream);
   m->stable->free_kv();
   return TINYOAI_OK;
@@ -1106,7 +1262,10 @@ int tinyoai_stablelm_offset(const tinyoai_model *m) {
 
 int tinyoai_stablelm_close(tinyoai_model *m) {
   if (!m) return TINYOAI_OK;
-  if (m->stable) hipStreamSynchronize(m->stable->stream);
+  if (m->stable) {
+    if (int rc = m->stable->busy_with_branches()) return rc;
+    hipStreamSynchronize(m->stable->stream);
+  }
   delete m;
   return TINYOAI_OK;
 }
@@ -1119,61 +1278,78 @@ struct tinyoai_branches {
 
 extern "C" {
 
-int tinyoai_stablelm_branches_open(tinyoai_model *m, int32_t prefix, int32_t count, int32_t max_steps,
+int tinyoai_stablelm_branches_open(tinyoai_model *m, int32_t prefix, int32_t count, int32_t max_len,
                                    tinyoai_branches **out) {
   if (!m || !m->stable || !out) return fail(TINYOAI_EINVAL, "not a StableLM handle");
   *out = nullptr;
   StableModel &s = *m->stable;
-  const int hd = s.dims.hd;
-  if (prefix < 0 || prefix > s.offset || count < 1 || max_steps < 1 || count > s.chunk ||
-      (int64_t)count * s.cfg.vocab_size > (int64_t)s.chunk * s.win_rows ||
-      (int64_t)prefix + max_steps > s.cfg.max_position_embeddings)
-    return fail(TINYOAI_EINVAL, "invalid branch prefix or batch size (prefix %d, offset %d, count %d, steps %d)",
-                prefix, s.offset, count, max_steps);
+  const int hd = s.dims.hd, room = s.cfg.max_position_embeddings - prefix;
+  if (prefix < 0 || prefix > s.offset || count < 1 || max_len < 0 || count > s.chunk ||
+      (int64_t)count * s.cfg.vocab_size > (int64_t)s.chunk * s.win_rows || room < 1)
+    return fail(TINYOAI_EINVAL, "invalid branch prefix or batch size (prefix %d, offset %d, count %d)", prefix,
+                s.offset, count);
   if (hd != 8 && hd != 64 && hd != 80) return fail(TINYOAI_EINVAL, "branch attention: head width %d", hd);
   if (int rc = s.ensure_kv(std::max(prefix, 1))) return rc;
   auto h = std::make_unique<tinyoai_branches>();
   h->b = std::make_unique<Branches>();
   Branches &b = *h->b;
   b.m = &s;
+  s.open_branches++;
   b.prefix = prefix;
   b.count = count;
-  b.slots = max_steps;
-  b.max_splits = (prefix + max_steps) / 64 + 1;
-  auto balloc = [&](void **p, size_t bytes) -> int {
-    hipError_t e = hipMalloc(p, std::max<size_t>(bytes, 256));
-    if (e != hipSuccess) return fail(TINYOAI_ENOMEM, "hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
-    b.buffers.push_back(*p);
-    return TINYOAI_OK;
-  };
-  const size_t kvb = (size_t)s.dims.kv_heads * count * max_steps * hd * (s.kv_half ? 2 : 4);
-  for (int l = 0; l < s.cfg.num_hidden_layers; l++) {
-    KVDev k{nullptr, nullptr, count * max_steps, s.kv_half};
-    if (int rc = balloc(&k.k, kvb)) return rc;
-    if (int rc = balloc(&k.v, kvb)) return rc;
-    b.kv.push_back(k);
-  }
-  const size_t qh = (size_t)count * s.dims.heads;
-  if (int rc = balloc((void **)&b.partials, qh * partial_region(b.max_splits, hd) * 4)) return rc;
-  if (int rc = balloc((void **)&b.counters, qh * 4)) return rc;
-  TRY_HIP(hipMemsetAsync(b.counters, 0, qh * 4, s.stream), "branch counters");
-  TRY_HIP(hipStreamSynchronize(s.stream), "branch open");
+  b.max_len = max_len > 0 ? std::min(max_len, room) : room;
+  b.len.assign(count, 0);
+  hipError_t e = hipMalloc(&b.last, (size_t)count * s.dims.d * 4);
+  if (e != hipSuccess) return fail(TINYOAI_ENOMEM, "branch rows: %s", hipGetErrorString(e));
   *out = h.release();
   return TINYOAI_OK;
+}
+
+// Validates and runs `n` rows; a native failure closes the branches'
+// storage, as nativeBranches.Forward closes its caches on an evaluation
+// error (mlx_branches.go:172-175).
+static int branches_run(tinyoai_branches *h, const int32_t *tokens, const int32_t *br, int n, float *logits) {
+  Branches &b = *h->b;
+  StableModel &s = *b.m;
+  std::vector<int> add(b.count, 0);
+  for (int i = 0; i < n; i++) {
+    if (tokens[i] < 0 || tokens[i] >= s.cfg.vocab_size) return fail(TINYOAI_EINVAL, "invalid branch token %d", tokens[i]);
+    const int j = br[i];
+    if (++add[j] + b.len[j] > b.max_len)
+      return fail(TINYOAI_EINVAL, "branch %d: suffix of %d tokens exceeds the context (%d positions after prefix %d)",
+                  j, add[j] + b.len[j], b.max_len, b.prefix);
+  }
+  const int rc = s.branch_rows(b, tokens, br, n, logits);
+  if (rc) h->b.reset();
+  return rc;
 }
 
 int tinyoai_stablelm_branches_forward(tinyoai_branches *h, const int32_t *tokens, int32_t count, float *logits) {
   if (!h || !h->b) return fail(TINYOAI_EINVAL, "branches are closed");
   Branches &b = *h->b;
-  StableModel &s = *b.m;
-  if (!tokens || !logits || count != b.count || b.step >= b.slots ||
-      b.prefix + b.step >= s.cfg.max_position_embeddings)
-    return fail(TINYOAI_EINVAL, "invalid branch batch or context length");
-  for (int i = 0; i < count; i++)
-    if (tokens[i] < 0 || tokens[i] >= s.cfg.vocab_size) return fail(TINYOAI_EINVAL, "invalid branch token %d", tokens[i]);
-  const int rc = s.branch_step(b, tokens, logits);
-  if (rc) h->b.reset();  // Forward closes the suffix caches on an evaluation error
-  return rc;
+  if (!tokens || !logits || count != b.count) return fail(TINYOAI_EINVAL, "invalid branch batch or context length");
+  std::vector<int32_t> br(count);
+  for (int j = 0; j < count; j++) br[j] = j;
+  return branches_run(h, tokens, br.data(), count, logits);
+}
+
+int tinyoai_stablelm_branches_append(tinyoai_branches *h, const int32_t *tokens, const int32_t *lengths,
+                                     int32_t count, float *logits) {
+  if (!h || !h->b) return fail(TINYOAI_EINVAL, "branches are closed");
+  Branches &b = *h->b;
+  if (!tokens || !lengths || !logits || count != b.count) return fail(TINYOAI_EINVAL, "invalid branch batch");
+  std::vector<int32_t> br;
+  for (int j = 0; j < count; j++) {
+    if (lengths[j] < 1 || lengths[j] > b.max_len) return fail(TINYOAI_EINVAL, "branch %d: invalid length %d", j, lengths[j]);
+    br.insert(br.end(), lengths[j], j);
+  }
+  return branches_run(h, tokens, br.data(), (int)br.size(), logits);
+}
+
+int tinyoai_stablelm_branches_length(const tinyoai_branches *h, int32_t branch) {
+  if (!h || !h->b) return fail(TINYOAI_EINVAL, "branches are closed");
+  if (branch < 0 || branch >= h->b->count) return fail(TINYOAI_EINVAL, "invalid branch %d", branch);
+  return h->b->len[branch];
 }
 
 int tinyoai_stablelm_branches_close(tinyoai_branches *h) {

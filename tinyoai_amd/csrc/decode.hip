@@ -30,16 +30,22 @@ struct AttArgs {
   float *partials;
   unsigned *counters;
   float *out;
-  // Branches (BR): query j is branch j at position *pos0; positions below
-  // `prefix` come from kv (the shared prefix), the others from slots
-  // j * slots + (t - prefix) of the branch cache sfx.
+  // Branches (BR): query j sits at position rows[2j] with its own K/V at
+  // slot rows[2j + 1] of the branch cache sfx; positions below `prefix`
+  // come from kv (the shared prefix), position t >= prefix from slot
+  // rows[2j + 1] - rows[2j] + t of sfx.
   KVDev sfx;
-  int prefix, slots;
+  int prefix;
+  const int *rows;
 };
 
-// Agent-scope relaxed atomic store of a partial result.
+// Agent-scope relaxed atomic store of a partial result, and the matching
+// load: both go to the device's coherence point, past the XCDs' L2 caches.
 __device__ __forceinline__ void publish(float *p, float v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float collect(const float *p) {
+  return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Dimension held in register r by lane group g of a position's four lanes.
@@ -87,7 +93,10 @@ __global__ __launch_bounds__(WAVES * 64) void attention_kernel(AttArgs a) {
 #pragma unroll
   for (int i = 0; i < DPL; i++) qr[i] = q[att_dim<DPL>(g, i)];
   const int64_t head_base = (int64_t)kvh * a.kv.cap * HD;
-  const int64_t sfx_base = BR ? (int64_t)kvh * a.sfx.cap * HD + (int64_t)j * a.slots * HD : 0;
+  // BR: the query's position, and its suffix as element offsets: position
+  // t >= prefix at sfx_base + t * HD (t clamped to the query's position).
+  const int qpos = BR ? a.rows[2 * j] : 0;
+  const int64_t sfx_base = BR ? ((int64_t)kvh * a.sfx.cap + a.rows[2 * j + 1] - qpos) * HD : 0;
   const int t0 = split * SPLIT + wave * STEPS * 16 + pl;
   // Element offset of position t (clamped into its region) and whether it
   // lies in the branch cache. The base is chosen by address arithmetic on
@@ -95,7 +104,7 @@ __global__ __launch_bounds__(WAVES * 64) void attention_kernel(AttArgs a) {
   auto where = [&](int t, int64_t &e) -> bool {
     if constexpr (BR) {
       if (t >= a.prefix) {
-        e = sfx_base + (int64_t)min(t - a.prefix, a.slots - 1) * HD;
+        e = sfx_base + (int64_t)min(t, qpos) * HD;
         return true;
       }
       e = head_base + (int64_t)t * HD;
@@ -122,7 +131,7 @@ __global__ __launch_bounds__(WAVES * 64) void attention_kernel(AttArgs a) {
     load_kv_lanes<DPL, HALF>(reinterpret_cast<const void *>(kbase + (b ? kdelta : 0)), e, g, kr[st]);
     if constexpr (kEarlyV) load_kv_lanes<DPL, HALF>(reinterpret_cast<const void *>(vbase + (b ? vdelta : 0)), e, g, vr[st]);
   }
-  const int pos = *a.pos0 + (BR ? 0 : j);
+  const int pos = BR ? qpos : *a.pos0 + j;
   const int npos = pos + 1;
   const int nsplit = (npos + SPLIT - 1) / SPLIT;
   if (split >= nsplit) return;
@@ -202,12 +211,13 @@ __global__ __launch_bounds__(WAVES * 64) void attention_kernel(AttArgs a) {
     return;
   }
   // Cross-block combine. Partials are written with agent-scope relaxed
-  // atomic stores (write-through, visible across the XCDs' L2 caches) and
-  // ordered before the arrival increment by waiting for the stores; an
-  // agent-scope fence would write back and invalidate the whole L2 instead.
-  // Each (query, head) owns a 256-byte aligned region that only its last
-  // block reads, once, after every store to it: no cache holds a stale copy
-  // of those lines, so plain (pipelined) loads are safe there.
+  // atomic stores, and each thread waits for its stores to complete
+  // (vmcnt(0)) before the block's arrival increment; an agent-scope
+  // release fence would write back the whole L2 instead. The last block
+  // learns that it is last from the value its increment returns, so its
+  // loads of the partials issue after every other block's stores have
+  // completed; they are agent-scope atomic loads, which read the coherence
+  // point rather than a line an XCD's L2 may hold from earlier.
   float *region = a.partials + qh * partial_region(a.max_splits, HD);
   float *part = region + split * (HD + 2);
   if (tid == 0) {
@@ -230,7 +240,7 @@ __global__ __launch_bounds__(WAVES * 64) void attention_kernel(AttArgs a) {
   // Last block of this (query, head): every other split has published.
   const float *base = region;
   float m = -INFINITY;
-  for (int sp = tid; sp < nsplit; sp += kThreads) m = fmaxf(m, base[sp * (HD + 2)]);
+  for (int sp = tid; sp < nsplit; sp += kThreads) m = fmaxf(m, collect(base + sp * (HD + 2)));
   m = wave_max(m);
   if (lane == 0) s_m[wave] = m;
   __syncthreads();
@@ -239,9 +249,9 @@ __global__ __launch_bounds__(WAVES * 64) void attention_kernel(AttArgs a) {
   for (int w = 1; w < kWaves; w++) m = fmaxf(m, s_m[w]);
   float lsum = 0.f;
   for (int sp = tid; sp < nsplit; sp += kThreads) {
-    const float e = expf(base[sp * (HD + 2)] - m);
+    const float e = expf(collect(base + sp * (HD + 2)) - m);
     s_e[sp] = e;
-    lsum = fmaf(base[sp * (HD + 2) + 1], e, lsum);
+    lsum = fmaf(collect(base + sp * (HD + 2) + 1), e, lsum);
   }
   lsum = wave_sum(lsum);
   __syncthreads();
@@ -257,7 +267,7 @@ __global__ __launch_bounds__(WAVES * 64) void attention_kernel(AttArgs a) {
   for (int d = tid; d < HD; d += kThreads) {
     float acc = 0.f;
 #pragma unroll 8
-    for (int sp = 0; sp < nsplit; sp++) acc = fmaf(base[sp * (HD + 2) + 2 + d], s_e[sp], acc);
+    for (int sp = 0; sp < nsplit; sp++) acc = fmaf(collect(base + sp * (HD + 2) + 2 + d), s_e[sp], acc);
     outp[d] = acc / Ltot;
   }
   if (tid == 0) __hip_atomic_store(&a.counters[qh], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -383,14 +393,14 @@ hipError_t launch_attention(const StableDims &s, const KVDev &kv, const float *q
   return hipErrorInvalidValue;
 }
 
-hipError_t launch_branch_attention(const StableDims &s, const KVDev &kv, const KVDev &sfx, int prefix, int slots,
-                                   const float *q, const int *pos0, int nq, int max_pos, float *partials,
+hipError_t launch_branch_attention(const StableDims &s, const KVDev &kv, const KVDev &sfx, int prefix,
+                                   const float *q, const int *rows, int nq, int max_pos, float *partials,
                                    unsigned *counters, float *out, int max_splits, hipStream_t st) {
   const int steps = std::min(attention_steps(max_pos, s.heads), 4), splits = attention_splits(max_pos, steps);
-  if (splits > 512 || splits > max_splits || prefix < 0 || prefix > kv.cap || slots <= 0 ||
-      (int64_t)nq * slots > sfx.cap || max_pos - prefix >= slots || kv.half != sfx.half)
+  if (splits > 512 || splits > max_splits || prefix < 0 || prefix > kv.cap || nq < 1 || !rows ||
+      kv.half != sfx.half)
     return hipErrorInvalidValue;
-  AttArgs a{s, kv, q, pos0, max_splits, partials, counters, out, sfx, prefix, slots};
+  AttArgs a{s, kv, q, nullptr, max_splits, partials, counters, out, sfx, prefix, rows};
   switch (s.hd) {
     case 64: return kv.half ? launch_branch_attention_hd<64, true>(a, nq, splits, steps, st)
                             : launch_branch_attention_hd<64, false>(a, nq, splits, steps, st);

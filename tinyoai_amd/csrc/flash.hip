@@ -25,6 +25,10 @@ struct FlashArgs {
   int n;
   float *out;      // [n][heads][hd] (may be null)
   uint16_t *oh, *ol;  // the same as bf16 operand planes (null: none)
+  // Branch rows (BR instances): cache positions t >= prefix come from slot
+  // sfx_slot0 + (t - prefix) of the branch cache sfx.
+  KVDev sfx;
+  int prefix, sfx_slot0;
 };
 
 // x = hi + lo to about 2^-22. The empty asm pins x as one fp32 value: when x
@@ -53,7 +57,7 @@ constexpr int kQ32 = 128;  // queries per block
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-template <int HD, bool HALF>
+template <int HD, bool HALF, bool BR>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void flash32_kernel(FlashArgs a) {
   static_assert(HD % 16 == 0, "head width in 16-dim k-steps");
   constexpr int KS = HD / 16;         // k-steps over head dims
@@ -118,6 +122,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
       vt[e / PAD][HD * VP + e % PAD] = (_Float16)(e < VP ? 1.f : 0.f);
   }
   const int64_t head_base = (int64_t)kvh * a.kv.cap * HD;
+  // BR: the branch's suffix, position t >= prefix at element sfx_base + (t - prefix) * HD.
+  const int64_t sfx_base = BR ? ((int64_t)kvh * a.sfx.cap + a.sfx_slot0) * HD : 0;
   const int ntiles = last_pos / kTile + 1;
   // fp16 cache: a tile is loaded into registers while the previous one is
   // computed. Buffer loads read zeros past the block's last position.
@@ -128,24 +134,44 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
   static_assert(VB <= 256, "one V block per thread");
   constexpr uint32_t kNone = 0x80000000u;
   uint4 kreg[KPT], vreg[4];
+  // The model cache holds positions [0, min(last_pos + 1, prefix)) (all of
+  // them without BR); with BR the branch cache the rest. A piece whose key
+  // lies in the other region reads at kNone (zeros, no memory request) from
+  // this one, so OR-ing the two loads gives the piece.
+  const int n_model = BR ? min(last_pos + 1, a.prefix) : last_pos + 1;
   const __amdgpu_buffer_rsrc_t rk = plane_rsrc(
-      reinterpret_cast<const uint8_t *>(a.kv.k) + head_base * 2, (int64_t)(last_pos + 1) * HD * 2);
+      reinterpret_cast<const uint8_t *>(a.kv.k) + head_base * 2, (int64_t)n_model * HD * 2);
   const __amdgpu_buffer_rsrc_t rv = plane_rsrc(
-      reinterpret_cast<const uint8_t *>(a.kv.v) + head_base * 2, (int64_t)(last_pos + 1) * HD * 2);
+      reinterpret_cast<const uint8_t *>(a.kv.v) + head_base * 2, (int64_t)n_model * HD * 2);
+  const int n_sfx = BR ? max(last_pos + 1 - a.prefix, 0) : 0;
+  const __amdgpu_buffer_rsrc_t rk2 = plane_rsrc(
+      reinterpret_cast<const uint8_t *>(BR ? a.sfx.k : a.kv.k) + sfx_base * 2, (int64_t)n_sfx * HD * 2);
+  const __amdgpu_buffer_rsrc_t rv2 = plane_rsrc(
+      reinterpret_cast<const uint8_t *>(BR ? a.sfx.v : a.kv.v) + sfx_base * 2, (int64_t)n_sfx * HD * 2);
   auto ld16 = [](__amdgpu_buffer_rsrc_t r, uint32_t off) {
     const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
     return make_uint4(v.x, v.y, v.z, v.w);
+  };
+  // The 16-byte piece at dims [c8, c8 + 8) of key t (t < kNone / 2 / HD).
+  auto piece = [&](__amdgpu_buffer_rsrc_t r, __amdgpu_buffer_rsrc_t r2, bool ok, int t, int c8) {
+    if constexpr (BR) {
+      const uint32_t o1 = ok && t < a.prefix ? (uint32_t)((t * HD + c8) * 2) : kNone;
+      const uint32_t o2 = ok && t >= a.prefix ? (uint32_t)(((t - a.prefix) * HD + c8) * 2) : kNone;
+      const uint4 x = ld16(r, o1), y = ld16(r2, o2);
+      return make_uint4(x.x | y.x, x.y | y.y, x.z | y.z, x.w | y.w);
+    } else {
+      return ld16(r, ok ? (uint32_t)((t * HD + c8) * 2) : kNone);
+    }
   };
   auto hload = [&](int t0) {
 #pragma unroll
     for (int i = 0; i < KPT; i++) {
       const int e = tid + 256 * i;
-      kreg[i] = ld16(rk, e < KC ? (uint32_t)((t0 * HD + e * 8) * 2) : kNone);
+      kreg[i] = piece(rk, rk2, e < KC, t0 + e / (HD / 8), (e % (HD / 8)) * 8);
     }
     const int kg = tid % (kTile / 4), dg = tid / (kTile / 4);
 #pragma unroll
-    for (int i = 0; i < 4; i++)
-      vreg[i] = ld16(rv, tid < VB ? (uint32_t)(((t0 + kg * 4 + i) * HD + dg * 8) * 2) : kNone);
+    for (int i = 0; i < 4; i++) vreg[i] = piece(rv, rv2, tid < VB, t0 + kg * 4 + i, dg * 8);
   };
   auto hstore = [&]() {
 #pragma unroll
@@ -179,11 +205,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
       // fp32 cache: hi and lo planes, 4 values per 16-byte load
       for (int e = tid; e < kTile * (HD / 4); e += 256) {
         const int key = e / (HD / 4), d0 = (e % (HD / 4)) * 4, t = t0 + key;
-        const int64_t idx = head_base + (int64_t)t * HD + d0;
+        const bool in_sfx = BR && t >= a.prefix;
+        const int64_t idx = (in_sfx ? sfx_base + (int64_t)(t - a.prefix) * HD : head_base + (int64_t)t * HD) + d0;
+        // the cache base as address arithmetic, not a select between two fields
+        const uintptr_t kb = reinterpret_cast<uintptr_t>(a.kv.k), vb = reinterpret_cast<uintptr_t>(a.kv.v);
+        const float *kp = reinterpret_cast<const float *>(
+            kb + (in_sfx ? reinterpret_cast<uintptr_t>(a.sfx.k) - kb : uintptr_t(0)));
+        const float *vp = reinterpret_cast<const float *>(
+            vb + (in_sfx ? reinterpret_cast<uintptr_t>(a.sfx.v) - vb : uintptr_t(0)));
         float4 kw = make_float4(0.f, 0.f, 0.f, 0.f), vw = kw;
         if (t <= last_pos) {
-          kw = *reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(a.kv.k) + idx);
-          vw = *reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(a.kv.v) + idx);
+          kw = *reinterpret_cast<const float4 *>(kp + idx);
+          vw = *reinterpret_cast<const float4 *>(vp + idx);
         }
         const float kx[4] = {kw.x, kw.y, kw.z, kw.w}, vx[4] = {vw.x, vw.y, vw.z, vw.w};
 #pragma unroll
@@ -308,14 +341,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
   }
 }
 
-template <int HD>
+template <int HD, bool BR>
 hipError_t flash32_launch(const FlashArgs &a, hipStream_t st) {
   dim3 grid((a.n + kQ32 - 1) / kQ32, a.s.heads);
   if (a.kv.half)
-    hipLaunchKernelGGL((flash32_kernel<HD, true>), grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL((flash32_kernel<HD, true, BR>), grid, dim3(256), 0, st, a);
   else
-    hipLaunchKernelGGL((flash32_kernel<HD, false>), grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL((flash32_kernel<HD, false, BR>), grid, dim3(256), 0, st, a);
   return hipGetLastError();
+}
+
+template <int HD>
+hipError_t flash32_dispatch(const FlashArgs &a, bool br, hipStream_t st) {
+  return br ? flash32_launch<HD, true>(a, st) : flash32_launch<HD, false>(a, st);
 }
 
 }  // namespace
@@ -323,14 +361,17 @@ hipError_t flash32_launch(const FlashArgs &a, hipStream_t st) {
 bool flash_prefill_supported(int hd) { return hd == 64 || hd == 80 || hd == 96 || hd == 128; }
 
 hipError_t launch_flash_prefill(const StableDims &s, const KVDev &kv, const float *q, const int *pos0, int n,
-                                float *out, hipStream_t st, uint16_t *oh, uint16_t *ol) {
-  if (!oh != !ol || (!out && !oh)) return hipErrorInvalidValue;
-  FlashArgs a{s, kv, q, pos0, n, out, oh, ol};
+                                float *out, hipStream_t st, uint16_t *oh, uint16_t *ol, const KVDev *sfx, int prefix,
+                                int sfx_slot0) {
+  if (!oh != !ol || (!out && !oh) || n < 1) return hipErrorInvalidValue;
+  if (sfx && (sfx->half != kv.half || prefix < 0 || prefix > kv.cap || sfx_slot0 < 0)) return hipErrorInvalidValue;
+  FlashArgs a{s, kv, q, pos0, n, out, oh, ol, sfx ? *sfx : KVDev{}, prefix, sfx_slot0};
+  const bool br = sfx != nullptr;
   switch (s.hd) {
-    case 64: return flash32_launch<64>(a, st);
-    case 80: return flash32_launch<80>(a, st);
-    case 96: return flash32_launch<96>(a, st);
-    case 128: return flash32_launch<128>(a, st);
+    case 64: return flash32_dispatch<64>(a, br, st);
+    case 80: return flash32_dispatch<80>(a, br, st);
+    case 96: return flash32_dispatch<96>(a, br, st);
+    case 128: return flash32_dispatch<128>(a, br, st);
   }
   return hipErrorInvalidValue;
 }

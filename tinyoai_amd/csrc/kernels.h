@@ -103,20 +103,25 @@ hipError_t launch_decode_out(const MatDesc &wout, int ka, int km, const float *a
 hipError_t launch_attention(const StableDims &s, const KVDev &kv, const float *q, const int *pos0, int nq,
                             int max_pos, float *partials, unsigned *counters, float *out, hipStream_t st,
                             int steps = 0, int splits = 0);
-// Branch attention (query j = branch j at position *pos0 = max_pos):
-// positions below `prefix` from kv, the rest from slots j * slots + (t -
-// prefix) of sfx. partials holds nq * heads * partial_region(max_splits, hd)
-// floats. Head widths 8, 64 and 80.
-hipError_t launch_branch_attention(const StableDims &s, const KVDev &kv, const KVDev &sfx, int prefix, int slots,
-                                   const float *q, const int *pos0, int nq, int max_pos, float *partials,
+// Branch attention: query j sits at position rows[2j] and its own K/V at
+// slot rows[2j + 1] of the branch cache sfx; positions below `prefix` come
+// from kv (the shared prefix), position t >= prefix from slot rows[2j + 1]
+// - rows[2j] + t of sfx (the branch's suffix, stored contiguously). Every
+// query's position is at most max_pos. partials holds nq * heads *
+// partial_region(max_splits, hd) floats. Head widths 8, 64 and 80.
+hipError_t launch_branch_attention(const StableDims &s, const KVDev &kv, const KVDev &sfx, int prefix,
+                                   const float *q, const int *rows, int nq, int max_pos, float *partials,
                                    unsigned *counters, float *out, int max_splits, hipStream_t st);
 // Causal attention of n prefill queries on the matrix cores (head widths
 // 64, 80, 96, 128): q [n][heads*hd] at positions pos0 + j -> out.
 bool flash_prefill_supported(int hd);
 // out (fp32, may be null) and / or the bf16 operand planes oh, ol of the
-// matrix-core GEMM (null: none).
+// matrix-core GEMM (null: none). With sfx, the queries are one branch's
+// rows: cache positions t >= prefix come from slot sfx_slot0 + (t - prefix)
+// of the branch cache sfx, positions below prefix from kv.
 hipError_t launch_flash_prefill(const StableDims &s, const KVDev &kv, const float *q, const int *pos0, int n,
-                                float *out, hipStream_t st, uint16_t *oh = nullptr, uint16_t *ol = nullptr);
+                                float *out, hipStream_t st, uint16_t *oh = nullptr, uint16_t *ol = nullptr,
+                                const KVDev *sfx = nullptr, int prefix = 0, int sfx_slot0 = 0);
 int attention_steps(int max_pos, int heads);
 // Floats per (query, head) in the partials buffer: max_splits records of
 // hd + 2, rounded to 256 bytes.
@@ -218,11 +223,11 @@ hipError_t launch_split_bf16(const float *x, int ldx, int k, int64_t rows, uint1
 // Epilogue of the fused in-projection for n tokens: y [n][win rows] ->
 // RoPE'd q [n][heads*hd], K/V into the cache at positions pos0 + j, and
 // m [n][inter] = SiLU-gate(gate, up) (m may be null), and / or m as bf16
-// operand planes mh, ml (null: none).
+// operand planes mh, ml (null: none). With rows, token j sits at position
+// rows[2j] and its K/V go to cache slot rows[2j + 1] (branch rows).
 hipError_t launch_in_epilogue(const StableDims &s, const KVDev &kv, const float *y, int ldy, const float *rope,
                               const int *pos0, int n, float *q, float *m, hipStream_t st, uint16_t *mh = nullptr,
-                              uint16_t *ml = nullptr, int slots = 0, int prefix = 0);
-hipError_t launch_silu_gate(float *g, const float *u, int64_t n, hipStream_t st);
+                              uint16_t *ml = nullptr, const int *rows = nullptr);
 // x = (x + p) + d elementwise (stablelm.go:375-377).
 // x = (x + sum_s p[s]) + sum_s d[s] over sp and sd partial products n
 // floats apart (K-split GEMM outputs), summed in order.

@@ -88,6 +88,12 @@ struct StableModel {
   // KV: one [kv_heads][cap][hd] K and V buffer per layer.
   std::vector<KVDev> kv;
   int cap = 0, offset = 0, reserve = 0, kv_half = 0;
+  // Open branch sessions borrowing the resident prefix: while any is open
+  // the model refuses every call that would change its KV (forward, reset,
+  // set_kv_bits, limit_cache) and close, as the reference's session holds
+  // the model gate (branches.go:16-22).
+  int open_branches = 0;
+  int busy_with_branches() const;
 
   // decode workspaces
   float *x = nullptr, *qbuf = nullptr, *mbuf = nullptr, *abuf = nullptr, *logits_dev = nullptr;
@@ -101,6 +107,10 @@ struct StableModel {
   // products Y, RoPE'd queries Q, SiLU-gate M, attention A, o and down
   // products P and D, bf16 planes XH/XL of the current GEMM operand
   int chunk = 0, win_rows = 0;
+  // Device parameter block (ints): [0, 16) scalars, [16, 16 + chunk) token
+  // ids or the decode token's rotary row, then 2 * chunk ints of per-row
+  // (position, KV slot) pairs.
+  int *rows_dev() const { return params + 16 + std::max(chunk, dims.rot); }
   float *X = nullptr, *H = nullptr, *Y = nullptr, *Q = nullptr, *M = nullptr, *A = nullptr, *P = nullptr,
         *D = nullptr;
   uint16_t *XH = nullptr, *XL = nullptr;
@@ -143,37 +153,55 @@ struct StableModel {
   void free_kv();
   int ensure_kv(int needed);
   int upload_params(const int *head_vals, int nh, const int32_t *ids, int n, const float *row = nullptr,
-                    int nrow = 0);
+                    int nrow = 0, const int *rows = nullptr);
   int enqueue_decode(int steps, int splits, bool want_logits);
   void drop_graphs();
   int decode_step(int token, int pos, bool want_logits);
   PersistentDecode persistent_args(bool want_logits) const;
   int check_persistent(int rc);
   // y = x * W^T; with `splits`, the product may come as *splits K-split
-  // partials n * ldy floats apart (y holds kPrefillSplits of them).
-  int project(const MatDesc &w, const float *x, int ldx, int n, float *y, int ldy, int *splits = nullptr);
+  // partials n * ldy floats apart (y holds kPrefillSplits of them). With
+  // rowstream, a product of at most kRowStreamMax rows in a format without
+  // a matrix-core path runs as one row-streaming matvec per row (branch
+  // steps); otherwise every chunk size takes the same arithmetic.
+  int project(const MatDesc &w, const float *x, int ldx, int n, float *y, int ldy, int *splits = nullptr,
+              bool rowstream = false);
   // y = X * W^T with X already in bf16 planes xh, xl (matrix-core formats).
   int project_planes(const MatDesc &w, const uint16_t *xh, const uint16_t *xl, int n, float *y, int ldy,
                      int *splits = nullptr);
   int prefill_chunk(const int32_t *ids, int n, int start, bool want_logits);
   int forward(int prefix, const int32_t *tokens, int n, bool want_logits, float *logits);
-  int branch_step(struct Branches &b, const int32_t *tokens, float *logits);
+  // Rows of open branches: token ids[i] extends branch br[i]; each
+  // branch's rows are consecutive and continue its suffix. Writes each
+  // touched branch's newest-row logits to logits[branch][vocab].
+  int branch_rows(struct Branches &b, const int32_t *ids, const int32_t *br, int n, float *logits);
 };
 
 // Independent suffixes of a resident prefix (nativeBranches,
 // mlx_branches.go:14-20): the prefix KV [0, prefix) of the model is read,
-// never written; each branch owns `slots` positions of suffix KV per layer,
-// laid out [kv_heads][count * slots][hd] so that branch j's step s is slot
-// j * slots + s.
+// never written; branch j owns the suffix positions prefix + [0, len[j]),
+// held in per-layer caches laid out [kv_heads][count * scap][hd], so that
+// branch j's suffix entry s is slot j * scap + s. The caches grow (to a
+// power of two, at most max_len) when a branch needs more positions, as
+// appendBranchKV allocates only the suffix length used
+// (mlx_branches.go:50-69).
 struct Branches {
   StableModel *m = nullptr;
-  int prefix = 0, count = 0, slots = 0, step = 0;
+  int prefix = 0, count = 0, max_len = 0;
+  std::vector<int> len;
+  int scap = 0;
   std::vector<KVDev> kv;
-  float *partials = nullptr;
-  unsigned *counters = nullptr;
-  int max_splits = 0;
-  std::vector<void *> buffers;
+  float *partials = nullptr;     // split-K attention partials
+  size_t partial_floats = 0;
+  unsigned *counters = nullptr;  // their arrival counters (zero between launches)
+  size_t counter_words = 0;
+  float *last = nullptr;         // [count][hidden]: each branch's newest residual row
   ~Branches();
+  void free_kv();
+  // Suffix capacity for `need` positions per branch (existing entries kept).
+  int grow(int need);
+  // Attention scratch for nq queries with up to `splits` splits.
+  int ensure_partials(int nq, int splits);
 };
 
 // The legacy Llama of llama2.c checkpoints (Model.transformer,

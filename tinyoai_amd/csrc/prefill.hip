@@ -88,14 +88,15 @@ __global__ __launch_bounds__(256) void gemm_simt_kernel(MatDesc w, const float *
 // applies it row by row. With mh, the SiLU-gate outputs (the units from
 // mu0 on) also go out as the down projection's bf16 operand planes, and to
 // m only when m is given.
-// With slots > 0 the rows are branches at one position (*pos0): row j's K
-// and V go to slot j * slots + (pos - prefix) of the branch cache kv.
+// With rows, token j sits at position rows[2j] and its K and V go to slot
+// rows[2j + 1] of the cache kv (a branch cache: the slot of the branch's
+// suffix entry).
 __global__ void in_epilogue_kernel(StableDims s, KVDev kv, const float *y, int ldy, const float *rope,
                                    const int *pos0, int units, float *q, float *m, uint16_t *mh, uint16_t *ml,
-                                   int slots, int prefix) {
+                                   const int *rows) {
   const int j = blockIdx.x;
-  const int pos = *pos0 + (slots ? 0 : j);
-  const int slot = slots ? j * slots + (pos - prefix) : pos;
+  const int pos = rows ? rows[2 * j] : *pos0 + j;
+  const int slot = rows ? rows[2 * j + 1] : pos;
   const float *yj = y + (int64_t)j * ldy;
   const float *rope_row = rope + (int64_t)pos * s.rot;
   const int mu0 = (s.win_q + 2 * s.win_kv) / 2;
@@ -110,11 +111,6 @@ __global__ void in_epilogue_kernel(StableDims s, KVDev kv, const float *y, int l
       in_pair_epilogue(s, kv, rope_row, slot, u, v.x, v.y, qj, mj);
     }
   }
-}
-
-__global__ void silu_gate_kernel(float *g, const float *u, int64_t n) {
-  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
-    g[i] = silu_gate(g[i], u[i]);
 }
 
 __global__ void residual_kernel(float *x, const float *p, int sp, const float *d, int sd, int64_t n) {
@@ -150,17 +146,11 @@ hipError_t launch_gemm(const MatDesc &w, const float *x, int n, float *out, hipS
 
 hipError_t launch_in_epilogue(const StableDims &s, const KVDev &kv, const float *y, int ldy, const float *rope,
                               const int *pos0, int n, float *q, float *m, hipStream_t st, uint16_t *mh,
-                              uint16_t *ml, int slots, int prefix) {
-  if (ldy % 2 || !mh != !ml || (!m && !mh) || s.win_q % 2 || slots < 0 || (slots && (int64_t)n * slots > kv.cap))
-    return hipErrorInvalidValue;
+                              uint16_t *ml, const int *rows) {
+  if (ldy % 2 || !mh != !ml || (!m && !mh) || s.win_q % 2 || (!rows && !pos0)) return hipErrorInvalidValue;
   const int units = (s.win_q + 2 * s.win_kv + 2 * s.inter) / 2;
   hipLaunchKernelGGL(in_epilogue_kernel, dim3(n), dim3(256), 0, st, s, kv, y, ldy, rope, pos0, units, q, m, mh,
-                     ml, slots, prefix);
-  return hipGetLastError();
-}
-
-hipError_t launch_silu_gate(float *g, const float *u, int64_t n, hipStream_t st) {
-  hipLaunchKernelGGL(silu_gate_kernel, dim3(elementwise_grid(n)), dim3(256), 0, st, g, u, n);
+                     ml, rows);
   return hipGetLastError();
 }
 

@@ -21,7 +21,7 @@ EXPORTS = [
     "tinyoai_stablelm_read_kv", "tinyoai_stablelm_trace", "tinyoai_stablelm_trace_read",
     "tinyoai_stablelm_trace_read_stages", "tinyoai_stablelm_decode_timeline", "tinyoai_stablelm_set_persistent",
     "tinyoai_stablelm_set_launch", "tinyoai_stablelm_branches_open", "tinyoai_stablelm_branches_forward",
-    "tinyoai_stablelm_branches_close",
+    "tinyoai_stablelm_branches_append", "tinyoai_stablelm_branches_length", "tinyoai_stablelm_branches_close",
     "tinyoai_stablelm_profile", "tinyoai_stablelm_profile_read", "tinyoai_llama_load",
     "tinyoai_llama_forward", "tinyoai_llama_reset", "tinyoai_llama_close", "tinyoai_weight_upload",
     "tinyoai_weight_read_values", "tinyoai_weight_mul", "tinyoai_weight_mul_device", "tinyoai_weight_free",
@@ -79,6 +79,8 @@ def lib():
         L.tinyoai_stablelm_set_launch.argtypes = [P, C.c_int32, C.c_int32, C.c_int32]
         L.tinyoai_stablelm_branches_open.argtypes = [P, C.c_int32, C.c_int32, C.c_int32, C.POINTER(P)]
         L.tinyoai_stablelm_branches_forward.argtypes = [P, ip, C.c_int32, fp]
+        L.tinyoai_stablelm_branches_append.argtypes = [P, ip, ip, C.c_int32, fp]
+        L.tinyoai_stablelm_branches_length.argtypes = [P, C.c_int32]
         L.tinyoai_stablelm_branches_close.argtypes = [P]
         L.tinyoai_stablelm_profile.argtypes = [P, C.c_int32]
         L.tinyoai_stablelm_profile_read.argtypes = [P, C.POINTER(C.c_double), C.POINTER(C.c_int64), C.c_int32]
@@ -155,14 +157,17 @@ LAYER_TENSORS = ("input_layernorm.weight", "input_layernorm.bias", "self_attn.q_
 
 class Branches:
     """nativeBranches (mlx_branches.go:14-182) over the C ABI: forward() takes
-    one token per branch, all at position prefix + step, and returns the
-    logits rows [count][vocab]."""
+    one token per branch (branch j at position prefix + length(j)) and
+    returns the logits rows [count][vocab]; append() gives each branch a
+    private suffix of its own length. The session borrows its forwarder's
+    prefix, so it keeps the forwarder alive; close it before the forwarder."""
 
-    def __init__(self, fwd, prefix: int, count: int, max_steps: int):
+    def __init__(self, fwd, prefix: int, count: int, max_len: int = 0):
         self.h = C.c_void_p()
+        self.fwd = fwd
         self.count = count
         self.vocab = fwd.config["vocab_size"]
-        check(lib().tinyoai_stablelm_branches_open(fwd.h, prefix, count, max_steps, C.byref(self.h)))
+        check(lib().tinyoai_stablelm_branches_open(fwd.h, prefix, count, max_len, C.byref(self.h)))
         self._logits = np.empty((count, self.vocab), np.float32)
 
     def forward(self, tokens) -> np.ndarray:
@@ -170,10 +175,23 @@ class Branches:
         check(lib().tinyoai_stablelm_branches_forward(self.h, _ip(toks), toks.size, _fp(self._logits)))
         return self._logits.copy()
 
+    def append(self, suffixes) -> np.ndarray:
+        """Appends suffixes[j] (a nonempty id sequence) to branch j; returns
+        each branch's last-row logits [count][vocab]."""
+        lengths = np.array([len(x) for x in suffixes], np.int32)
+        toks = np.ascontiguousarray(np.concatenate([np.asarray(x, np.int32) for x in suffixes]), np.int32)
+        check(lib().tinyoai_stablelm_branches_append(self.h, _ip(toks), _ip(lengths), lengths.size,
+                                                     _fp(self._logits)))
+        return self._logits.copy()
+
+    def length(self, branch: int) -> int:
+        return check(lib().tinyoai_stablelm_branches_length(self.h, branch))
+
     def close(self):
         if self.h:
             lib().tinyoai_stablelm_branches_close(self.h)
             self.h = None
+        self.fwd = None
 
     def __del__(self):
         try:
@@ -214,11 +232,11 @@ class StableLMForwarder:
                                              _fp(self._logits)))
         return self._logits.copy() if want_logits else None
 
-    def new_branches(self, prefix: int, count: int, max_steps: int) -> "Branches":
+    def new_branches(self, prefix: int, count: int, max_len: int = 0) -> "Branches":
         """NewBranches (mlx_branches.go:25-33): `count` suffixes borrowing
-        the resident prefix [0, prefix), each with room for `max_steps`
-        tokens. Close them before this forwarder."""
-        return Branches(self, prefix, count, max_steps)
+        the resident prefix [0, prefix), each at most `max_len` tokens long
+        (0: up to the context). Close them before this forwarder."""
+        return Branches(self, prefix, count, max_len)
 
     def set_kv_bits(self, bits: int) -> bool:
         cleared = C.c_int32()

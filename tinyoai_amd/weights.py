@@ -118,10 +118,14 @@ def f32_to_f16_bits(x: np.ndarray) -> np.ndarray:
 
 
 def encode_bf16(x: np.ndarray) -> np.ndarray:
-    """float32 -> bf16 bytes by round-to-nearest-even of the high half."""
-    b = np.asarray(x, np.float32).view(np.uint32).astype(np.uint64)
-    r = ((b + 0x7FFF + ((b >> 16) & 1)) >> 16).astype(np.uint16)
-    return r.view(np.uint8)
+    """float32 -> bf16 bytes by round-to-nearest-even of the high half
+    (finite values: the sum below stays within 32 bits)."""
+    b = np.ascontiguousarray(x, np.float32).view(np.uint32)
+    r = (b >> 16) & np.uint32(1)
+    r += np.uint32(0x7FFF)
+    r += b
+    r >>= 16
+    return r.astype(np.uint16).view(np.uint8)
 
 
 def encode_q8_0(scales: np.ndarray, qs: np.ndarray) -> np.ndarray:
