@@ -184,7 +184,10 @@ int tinyoai_stablelm_set_persistent(tinyoai_model *m, int32_t enable);
  * normalisation moments are grouped by wave). Stage 3 sets the decode
  * attention shape instead: `grid` = positions per block / 64 (1, 2 or 4 on
  * 4-wave blocks, 8 or 16 on 16-wave blocks; 0 = chosen from the position)
- * and `threads` is ignored. Returns 0 or TINYOAI_EINVAL. */
+ * and `threads` is ignored. Stage 4: grid nonzero lets
+ * each layer's decode attention launch also read the next layer's
+ * input-side matrix into the device's last-level cache; zero turns that
+ * off (the default). Returns 0 or TINYOAI_EINVAL. */
 int tinyoai_stablelm_set_launch(tinyoai_model *m, int32_t stage, int32_t grid, int32_t threads);
 /* Timeline of the last profiled single-launch decode step: for each block
  * of the launch, 3 + 6 * layers readings of the GPU's 100 MHz real-time

@@ -486,8 +486,11 @@ int StableModel::init(const tinyoai_stablelm_config &c, const tinyoai_tensor *te
       (rc = alloc((void **)&params, (size_t)(16 + std::max(chunk, dims.rot) + 2 * chunk) * 4)) ||
       (rc = alloc((void **)&trace_dev, (size_t)c.num_hidden_layers * d * 4)) ||
       (rc = alloc((void **)&trace_att, (size_t)c.num_hidden_layers * w_att * 4)) ||
-      (rc = alloc((void **)&trace_gate, (size_t)c.num_hidden_layers * I * 4)))
+      (rc = alloc((void **)&trace_gate, (size_t)c.num_hidden_layers * I * 4)) ||
+      (rc = alloc((void **)&fuse_ctr, fuse_bytes())))
     return rc;
+  e = hipMemsetAsync(fuse_ctr, 0, fuse_bytes(), stream);
+  if (e != hipSuccess) return hip_fail(e, "decode counters");
   max_splits = maxp / 64 + 1;
   const size_t att_queries = flash_prefill_supported(hd) ? 1 : chunk;  // split-K attention queries at once
   if ((rc = alloc((void **)&counters, att_queries * dims.heads * 4))) return rc;
@@ -617,7 +620,27 @@ int StableModel::check_persistent(int rc) {
   hipMemset(psync, 0, psync_words * 4);
   hipMemset(perr, 0, 4);
   epoch = 0;
+  reset_fused();
   return rc ? rc : fail(TINYOAI_EDEVICE, "decode step did not complete: a dependency wait timed out");
+}
+
+// Whether a decode step with this attention shape runs some layer's
+// attention inside its decode_in launch.
+bool StableModel::decode_fused(int steps) const {
+  if (!fuse_attention) return false;
+  for (const LayerDev &w : layers)
+    if (decode_in_att_supported(w, dims, threads_in, steps)) return true;
+  return false;
+}
+
+// The fused launches' counters from zero (after a failed step or a change
+// of the decode_in launch shape, which changes the counters' step); the
+// split-K arrival counters too, which a failed step may have left set.
+void StableModel::reset_fused() {
+  hipStreamSynchronize(stream);
+  hipMemset(fuse_ctr, 0, fuse_bytes());
+  hipMemset(counters, 0, (size_t)dims.heads * 4);
+  fuse_epoch = 0;
 }
 
 // Grows KV to `needed` positions: power-of-two capacity capped at the
@@ -703,23 +726,34 @@ int StableModel::enqueue_decode(int steps, int splits, bool want_logits) {
   for (int l = 0; l < cfg.num_hidden_layers; l++) {
     const LayerDev &w = layers[l];
     const float *rope_row = reinterpret_cast<const float *>(params + 16);
-    STAGE(ST_DECODE_IN,
-          launch_decode_in(w, dims, kv[l], x, l == 0 ? &embed.desc : nullptr, params, rope_row, params + 1, qbuf,
-                           mbuf, grid_in, threads_in, stream),
-          "decode_in");
-    if (w.win2.rows) {  // the gate/up section in a format of its own: every row pair is a SiLU-gate pair
-      LayerDev wm = w;
-      wm.win = w.win2;
-      StableDims dm = dims;
-      dm.win_q = dm.win_kv = 0;
+    const MatDesc *emb = l == 0 ? &embed.desc : nullptr;
+    if (fuse_attention && decode_in_att_supported(w, dims, threads_in, steps)) {
+      // q/k/v rows, then the attention on extra blocks while gate/up stream
       STAGE(ST_DECODE_IN,
-            launch_decode_in(wm, dm, kv[l], x, nullptr, params, rope_row, params + 1, qbuf, mbuf, grid_in, threads_in,
+            launch_decode_in_att(w, dims, kv[l], x, emb, params, rope_row, params + 1, qbuf, mbuf, grid_in, steps,
+                                 splits, partials, counters, abuf, fuse_ctr + (size_t)l * 32 * fuse_lines(),
+                                 params + 2, perr,
+                                 stream),
+            "decode_in + attention");
+    } else {
+      STAGE(ST_DECODE_IN,
+            launch_decode_in(w, dims, kv[l], x, emb, params, rope_row, params + 1, qbuf, mbuf, grid_in, threads_in,
                              stream),
             "decode_in");
+      if (w.win2.rows) {  // the gate/up section in a format of its own: every row pair is a SiLU-gate pair
+        LayerDev wm = w;
+        wm.win = w.win2;
+        StableDims dm = dims;
+        dm.win_q = dm.win_kv = 0;
+        STAGE(ST_DECODE_IN,
+              launch_decode_in(wm, dm, kv[l], x, nullptr, params, rope_row, params + 1, qbuf, mbuf, grid_in,
+                               threads_in, stream),
+              "decode_in");
+      }
+      STAGE(ST_ATTENTION,
+            launch_attention(dims, kv[l], qbuf, params + 1, 1, 0, partials, counters, abuf, stream, steps, splits),
+            "attention");
     }
-    STAGE(ST_ATTENTION,
-          launch_attention(dims, kv[l], qbuf, params + 1, 1, 0, partials, counters, abuf, stream, steps, splits),
-          "attention");
     if (w.wout2.rows) {  // o and down in formats of their own: x = (x + o*a) + down*m in two products
       STAGE(ST_DECODE_OUT, launch_decode_out(w.wout, dims.d, 0, abuf, nullptr, x, grid_out, threads_out, stream),
             "decode_out");
@@ -752,8 +786,8 @@ void StableModel::drop_graphs() {
 // graph of the whole layer stack keyed by the attention launch shape;
 // profiling runs launch the kernels directly so each can be timed.
 int StableModel::decode_step(int token, int pos, bool want_logits) {
-  const int vals[2] = {token, pos};
-  if (int rc = upload_params(vals, 2, nullptr, 0, rope_host.data() + (size_t)pos * dims.rot, dims.rot)) return rc;
+  const int vals[3] = {token, pos, fuse_epoch};
+  if (int rc = upload_params(vals, 3, nullptr, 0, rope_host.data() + (size_t)pos * dims.rot, dims.rot)) return rc;
   if (pgrid > 0 && use_persistent) {
     PersistentDecode args = persistent_args(want_logits);
     if (prof.on) {
@@ -779,6 +813,7 @@ int StableModel::decode_step(int token, int pos, bool want_logits) {
   }
   const int steps = att_steps > 0 ? att_steps : attention_steps(pos, dims.heads);
   const int splits = attention_splits(pos, steps);
+  if (decode_fused(steps)) fuse_epoch++;  // the value the step's launches read is the one uploaded above
   if (prof.on || !use_graphs) return enqueue_decode(steps, splits, want_logits);
   const int64_t key = ((int64_t)steps << 40) | ((int64_t)splits << 8) | (want_logits ? 2 : 0) | (tracing ? 1 : 0);
   auto it = graphs.find(key);
@@ -1420,6 +1455,12 @@ int tinyoai_stablelm_set_persistent(tinyoai_model *m, int32_t enable) {
 int tinyoai_stablelm_set_launch(tinyoai_model *m, int32_t stage, int32_t grid, int32_t threads) {
   if (!m || !m->stable) return fail(TINYOAI_EINVAL, "not a StableLM handle");
   StableModel &s = *m->stable;
+  if (stage == 4) {  // decode attention inside the decode_in launch (1, the default) or after it (0)
+    s.fuse_attention = grid != 0;
+    s.reset_fused();
+    s.drop_graphs();
+    return TINYOAI_OK;
+  }
   if (stage == 3) {  // decode attention: grid = positions per block / 64 (0 = by position)
     if (grid != 0 && grid != 1 && grid != 2 && grid != 4 && grid != 8 && grid != 16)
       return fail(TINYOAI_EINVAL, "attention steps %d", grid);
@@ -1430,7 +1471,7 @@ int tinyoai_stablelm_set_launch(tinyoai_model *m, int32_t stage, int32_t grid, i
   if (grid <= 0 || grid > (1 << 20) || (threads != 256 && threads != 512))
     return fail(TINYOAI_EINVAL, "launch shape %d x %d", grid, threads);
   switch (stage) {
-    case 0: s.grid_in = grid; s.threads_in = threads; break;
+    case 0: s.grid_in = grid; s.threads_in = threads; s.reset_fused(); break;
     case 1: s.grid_out = grid; s.threads_out = threads; break;
     case 2: s.grid_head = grid; s.threads_head = threads; break;
     default: return fail(TINYOAI_EINVAL, "launch stage %d", stage);

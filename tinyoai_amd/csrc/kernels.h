@@ -89,6 +89,21 @@ struct RowMap {
 hipError_t launch_decode_in(const LayerDev &w, const StableDims &s, const KVDev &kv, float *x, const MatDesc *emb,
                             const int *token, const float *rope, const int *pos, float *q_out, float *m_out,
                             int grid, int threads, hipStream_t st);
+// decode_in and the layer's split-K decode attention (launch_attention's
+// arguments: steps, splits, partials, counters, out) in one launch: extra
+// blocks wait until every streaming wave has stored its q/k/v rows, then
+// run the attention while the gate/up rows stream. fuse_ctr holds the
+// layer's 1 + 16 counter lines and then one go-flag line per head (32
+// words each, zero before the first launch), epoch the device int of
+// launches completed on them, err the word a timed-out wait sets. Supported: Q8_0 and BF16 win
+// matrices whose rows fit one column slice, head widths 64, 80 and 128,
+// 256-thread blocks, steps 1 or 2.
+constexpr int kFuseGroups = 16;  // group counters of the fused launch's arrival tree
+bool decode_in_att_supported(const LayerDev &w, const StableDims &s, int threads, int steps);
+hipError_t launch_decode_in_att(const LayerDev &w, const StableDims &s, const KVDev &kv, float *x, const MatDesc *emb,
+                                const int *token, const float *rope, const int *pos, float *q_out, float *m_out,
+                                int grid, int steps, int splits, float *partials, unsigned *counters, float *att_out,
+                                unsigned *fuse_ctr, const int *epoch, unsigned *err, hipStream_t st);
 // x = (x + o * a) + down * m (stablelm.go:365-377), one wout row per wave:
 // a row holds ka values of o then, from the next chunk boundary, km values
 // of down (km = 0: x = x + o * a).

@@ -17,6 +17,7 @@
 
 #include <algorithm>
 
+#include "attention.h"
 #include "epilogue.h"
 #include "rowstream.h"
 
@@ -51,7 +52,26 @@ struct LnMvArgs {
   int xlen;
 };
 
+// The input side and the attention of a decode layer in one launch: the
+// attention's arguments, and how its blocks learn that the q/k/v rows are
+// stored (see decode_in_att_kernel).
+// Arrivals are counted in a tree: the waves of a block in LDS, the blocks
+// of group b % kFuseGroups (kernels.h) on that group's counter, the groups
+// on the top counter; each counter line is 32 words.
+struct FuseArgs {
+  unsigned *ctr;        // the layer's top counter line, then its kFuseGroups group counter lines
+  unsigned *go;         // per head, 32 words apart: the launch number the attention may start on
+  const int *epoch;     // launches completed on ctr (in the parameter block)
+  unsigned waves;       // streaming waves of the launch
+  int blocks;           // streaming blocks; the attention blocks follow them
+  int qkv_units;        // units (row pairs) of win's q, k and v sections
+  unsigned *err;        // set to nonzero when a wait times out
+  unsigned spin_limit;  // polls per wait
+};
+
 template <int F> hipError_t run_decode_in(const InArgs &a, int grid, int threads, hipStream_t st);
+template <int F>
+hipError_t run_decode_in_att(const InArgs &a, const AttArgs &att, const FuseArgs &fz, int steps, hipStream_t st);
 template <int F> hipError_t run_decode_out(OutArgs p, int grid, int threads, hipStream_t st);
 template <int F> hipError_t run_ln_matvec(const LnMvArgs &a, int grid, int threads, hipStream_t st);
 
@@ -67,6 +87,10 @@ TINYOAI_MATVEC_DECLARE(FMT_Q5_1)
 TINYOAI_MATVEC_DECLARE(FMT_Q4_K)
 TINYOAI_MATVEC_DECLARE(FMT_Q5_K)
 TINYOAI_MATVEC_DECLARE(FMT_Q6_K)
+template <>
+hipError_t run_decode_in_att<FMT_Q8_0>(const InArgs &, const AttArgs &, const FuseArgs &, int, hipStream_t);
+template <>
+hipError_t run_decode_in_att<FMT_BF16>(const InArgs &, const AttArgs &, const FuseArgs &, int, hipStream_t);
 
 namespace tinyoai_matvec {
 
@@ -114,10 +138,12 @@ inline size_t slice_lds(int chunks, int split, int n_units, int grid, int R) {
 // up to 4 * kNormRegs * threads; longer ones read the rest directly).
 constexpr int kNormRegs = 3;
 
-template <int F, int T>
-__global__ __launch_bounds__(T) void decode_in_kernel(InArgs a) {
+// decode_in's work for one of `blocks` blocks (COH: outputs stored at
+// agent scope; hook as stream_rows takes it).
+template <int F, int T, bool COH, typename Hook>
+__device__ __forceinline__ void decode_in_body(const InArgs &a, float *lds_raw, Hook hook, int blocks,
+                                               int phase_unit = INT_MAX) {
   // LDS: pending stores | x [d] | 32 doubles | rotary row [rot] | slice partials
-  extern __shared__ __align__(16) float lds_raw[];
   PendingStore *pend = reinterpret_cast<PendingStore *>(lds_raw);
   float *lds = lds_raw + (T / 64) * kPendingPerWave * 4;
   constexpr int VPC = Fmt<F>::VPC;
@@ -168,8 +194,85 @@ __global__ __launch_bounds__(T) void decode_in_kernel(InArgs a) {
   auto done = [&](int u, const float (&r)[2][2], const float (&)[2], const auto &out) {
     in_pair_outputs(s, kv, rope_row, pos, u, r[0][0], r[1][0], a.q_out, a.m_out, out);
   };
-  stream_rows<F, T, cpl_for<F>(), 2, false, true, 1, false>(W, W.rows / 2, W.chunks, part, pend, rows, xload, noaux,
-                                                            pre, prologue, done);
+  stream_rows<F, T, cpl_for<F>(), 2, false, true, 1, false, COH>(W, W.rows / 2, W.chunks, part, pend, rows, xload,
+                                                                  noaux, pre, prologue, done, hook, blocks,
+                                                                  phase_unit);
+}
+
+template <int F, int T>
+__global__ __launch_bounds__(T) void decode_in_kernel(InArgs a) {
+  extern __shared__ __align__(16) float lds_raw[];
+  decode_in_body<F, T, false>(a, lds_raw, [](int) {}, (int)gridDim.x);
+}
+
+__device__ __forceinline__ unsigned poll_counter(unsigned *p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// decode_in and the layer's split-K attention in one launch. Blocks
+// [0, fz.blocks) stream win as decode_in_kernel does, storing the query and
+// the K/V entry at agent scope; every wave runs its q/k/v units first (in
+// groups of their own), waits for its stores, and arrives. The last wave of
+// a block to arrive adds the block to its group's counter, the last block
+// of a group adds the group to the top counter, and the last group raises
+// every head's go flag to the launch number (counters grow by a fixed
+// amount per launch, so nothing is reset between launches). The blocks
+// after the streaming ones run the attention of (split idx % splits, head
+// idx / splits) once their head's flag shows the launch, so the attention
+// overlaps the gate/up rows' stream. A single counter for every wave made
+// each wave stall behind thousands of atomics to one address; the tree
+// keeps one wave per block on a global atomic and a head's few blocks on a
+// flag line. An attention block waits only for blocks before it in
+// dispatch order, which have all started when it runs; the wait is still
+// bounded, and a time-out sets *fz.err (every waiting block then leaves).
+template <int F, int T, int HD, bool HALF, int STEPS>
+__global__ __launch_bounds__(T) void decode_in_att_kernel(InArgs a, AttArgs att, FuseArgs fz) {
+  static_assert(T == 256, "attention blocks are four waves");
+  extern __shared__ __align__(16) float lds_raw[];
+  __shared__ unsigned s_arrived;
+  const unsigned launch = (unsigned)*fz.epoch + 1;
+  if ((int)blockIdx.x >= fz.blocks) {
+    __shared__ int s_ok;
+    const int idx = (int)blockIdx.x - fz.blocks, splits = att.max_splits, h = idx / splits;
+    if (threadIdx.x == 0) {
+      unsigned *flag = fz.go + h * 32;
+      int ok = 1;
+      for (unsigned it = 0; (int)(poll_counter(flag) - launch) < 0; it++) {
+        if (it >= fz.spin_limit || ((it & 15) == 15 && poll_counter(fz.err) != 0)) {
+          ok = 0;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(4);
+      }
+      if (!ok) __hip_atomic_store(fz.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_ok = ok;
+    }
+    __syncthreads();
+    if (s_ok) attention_block<HD, HALF, STEPS, 4, false, true>(att, idx % splits, h, 0);
+    return;
+  }
+  if (threadIdx.x == 0) s_arrived = 0;  // the prologue's barrier orders this before any arrival
+  bool signaled = false;  // wave-uniform
+  auto hook = [&](int next_unit) {
+    if (signaled || next_unit < fz.qkv_units) return;
+    signaled = true;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's q/k/v stores have completed
+    const int lane = threadIdx.x & 63;
+    unsigned last = 0;
+    if (lane == 0 && atomicAdd(&s_arrived, 1u) == T / 64 - 1) {
+      const int g = blockIdx.x % kFuseGroups;
+      const unsigned in_group = (unsigned)(fz.blocks - g + kFuseGroups - 1) / kFuseGroups;
+      const unsigned groups = (unsigned)min(fz.blocks, kFuseGroups);
+      if (__hip_atomic_fetch_add(fz.ctr + 32 * (1 + g), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+              launch * in_group - 1 &&
+          __hip_atomic_fetch_add(fz.ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == launch * groups - 1)
+        last = 1;
+    }
+    if (__builtin_amdgcn_readfirstlane(last))  // every q/k/v row of the launch is stored
+      for (int h = lane; h < a.s.heads; h += 64)
+        __hip_atomic_store(fz.go + h * 32, launch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  };
+  decode_in_body<F, T, true>(a, lds_raw, hook, fz.blocks, fz.qkv_units);
 }
 
 // x = (x + o*a) + down*m: a wout row is [o | down], the down part from
@@ -273,6 +376,42 @@ hipError_t decode_in_launch(const InArgs &a, int grid, int threads, hipStream_t 
   return hipGetLastError();
 }
 
+// The fused launch: 256-thread blocks, rows within one column slice.
+template <int F>
+inline bool decode_in_att_fits(const InArgs &a) {
+  return slice_shape(a.w.win.chunks, a.w.win.chunks, cpl_for<F>()).S == 1;
+}
+
+template <int F, int HD, bool HALF>
+hipError_t decode_in_att_launch_hd(const InArgs &a, const AttArgs &att, const FuseArgs &fz, int steps,
+                                   hipStream_t st) {
+  constexpr int T = 256;
+  const size_t lds = pending_lds(T) + (size_t)round_up(a.s.d, 4) * 4 + 32 * sizeof(double) +
+                     (size_t)round_up(a.s.rot, 4) * 4;
+  if (!decode_in_att_fits<F>(a) || lds > 65536 || fz.blocks < 1) return hipErrorInvalidValue;
+  const dim3 grid(fz.blocks + att.max_splits * a.s.heads);
+  switch (steps) {
+    case 1: TINYOAI_TIMED_LAUNCH((decode_in_att_kernel<F, T, HD, HALF, 1>), grid, dim3(T), lds, st, a, att, fz); break;
+    case 2: TINYOAI_TIMED_LAUNCH((decode_in_att_kernel<F, T, HD, HALF, 2>), grid, dim3(T), lds, st, a, att, fz); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+template <int F>
+hipError_t decode_in_att_launch(const InArgs &a, const AttArgs &att, const FuseArgs &fz, int steps, hipStream_t st) {
+  const bool half = att.kv.half != 0;
+  switch (a.s.hd) {
+    case 64: return half ? decode_in_att_launch_hd<F, 64, true>(a, att, fz, steps, st)
+                         : decode_in_att_launch_hd<F, 64, false>(a, att, fz, steps, st);
+    case 80: return half ? decode_in_att_launch_hd<F, 80, true>(a, att, fz, steps, st)
+                         : decode_in_att_launch_hd<F, 80, false>(a, att, fz, steps, st);
+    case 128: return half ? decode_in_att_launch_hd<F, 128, true>(a, att, fz, steps, st)
+                          : decode_in_att_launch_hd<F, 128, false>(a, att, fz, steps, st);
+  }
+  return hipErrorInvalidValue;
+}
+
 template <int F>
 hipError_t decode_out_launch(OutArgs p, int grid, int threads, hipStream_t st) {
   constexpr int VPC = Fmt<F>::VPC;
@@ -292,6 +431,15 @@ hipError_t decode_out_launch(OutArgs p, int grid, int threads, hipStream_t st) {
 #undef TINYOAI_LAUNCH_T
 
 }  // namespace tinyoai_matvec
+
+// The fused input-side + attention launcher of format F (the formats the
+// decode workloads stream: Q8_0 and BF16).
+#define TINYOAI_MATVEC_DEFINE_FUSED(F)                                                           \
+  template <>                                                                                    \
+  hipError_t run_decode_in_att<F>(const InArgs &a, const AttArgs &att, const FuseArgs &fz, int steps, \
+                                  hipStream_t st) {                                              \
+    return tinyoai_matvec::decode_in_att_launch<F>(a, att, fz, steps, st);                       \
+  }
 
 // The three launchers of format F, for its translation unit.
 #define TINYOAI_MATVEC_DEFINE(F)                                                                  \

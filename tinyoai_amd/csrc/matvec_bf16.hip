@@ -2,3 +2,4 @@
 #include "matvec.h"
 
 TINYOAI_MATVEC_DEFINE(FMT_BF16)
+TINYOAI_MATVEC_DEFINE_FUSED(FMT_BF16)

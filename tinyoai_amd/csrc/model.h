@@ -122,6 +122,14 @@ struct StableModel {
   int grid_in = 0, grid_out = 0, grid_head = 0;
   int threads_in = 256, threads_out = 256, threads_head = 256;
   int att_steps = 0;  // decode attention positions per block / 64; 0 = chosen by position
+  // Decode: each layer's attention runs inside its decode_in launch where
+  // the shapes allow (set_launch stage 4 turns it off); one counter line
+  // per layer, and the launches completed on them (parameter int 2).
+  bool fuse_attention = true;
+  unsigned *fuse_ctr = nullptr;  // per layer: fuse_lines() lines of 32 words (counters, then a go flag per head)
+  int fuse_epoch = 0;
+  int fuse_lines() const { return 1 + kFuseGroups + dims.heads; }
+  size_t fuse_bytes() const { return (size_t)cfg.num_hidden_layers * fuse_lines() * 128; }
 
   // Persistent decode (one cooperative launch per token): device copies of
   // the layer and KV descriptors, per-layer handoff buffers, counters.
@@ -159,6 +167,8 @@ struct StableModel {
   int decode_step(int token, int pos, bool want_logits);
   PersistentDecode persistent_args(bool want_logits) const;
   int check_persistent(int rc);
+  bool decode_fused(int steps) const;
+  void reset_fused();
   // y = x * W^T; with `splits`, the product may come as *splits K-split
   // partials n * ldy floats apart (y holds kPrefillSplits of them). With
   // rowstream, a product of at most kRowStreamMax rows in a format without

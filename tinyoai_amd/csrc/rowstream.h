@@ -26,8 +26,10 @@
 // together (PendingStore).
 #pragma once
 
+#include <climits>
 #include <type_traits>
 
+#include "epilogue.h"  // put<COH>
 #include "formats.h"
 
 // Batches per unrolled group, and how many batches a wave keeps in flight
@@ -236,11 +238,20 @@ __host__ __device__ inline void slice_range(const SliceShape &sh, int nch, int s
 // results to out.f32 / out.f16 (at most two per unit). red: LDS of
 // units_per_block * (S * R * 2 + R) floats when the rows span S > 1
 // slices; pend: LDS of (T / 64) * kPendingPerWave PendingStores.
-template <int F, int T, int CPL, int R, bool XFIRST, bool PREWAIT, int PRE, bool AUX, typename Rows, typename XLoad,
-          typename AuxLoad, typename Pre, typename Prologue, typename Done>
+// With COH the results are stored with agent-scope atomic stores (other
+// blocks of the launch read them); `hook(next)` runs on the wave after
+// each group's results are stored, with the next unit the wave takes
+// (INT_MAX when none), and once more with INT_MAX at the end. `blocks` is
+// the number of blocks sharing the units (blocks 0 .. blocks - 1 of the
+// launch; 0 = the whole grid). A wave's units below `phase_unit` run in
+// groups of their own, before its later units.
+template <int F, int T, int CPL, int R, bool XFIRST, bool PREWAIT, int PRE, bool AUX, bool COH = false,
+          typename Rows, typename XLoad, typename AuxLoad, typename Pre, typename Prologue, typename Done,
+          typename Hook = void (*)(int)>
 __device__ __forceinline__ void stream_rows(const MatDesc &M, int n_units, int split, float *red, PendingStore *pend,
                                             Rows unit_rows, XLoad x_load, AuxLoad aux_load, Pre pre, Prologue prologue,
-                                            Done done) {
+                                            Done done, Hook hook = [](int) {}, int blocks = 0,
+                                            int phase_unit = INT_MAX) {
   constexpr int VPC = Fmt<F>::VPC, K = kRowGroup;
   // The wave index in a scalar register: everything per wave below (slice,
   // row group, units, whether a batch is real) is then scalar, and so is
@@ -255,11 +266,11 @@ __device__ __forceinline__ void stream_rows(const MatDesc &M, int n_units, int s
   const int part = s >= sh.S0;            // which part of the row this wave's slice sums
   int c0, width;
   slice_range(sh, M.chunks, split, s, c0, width);
-  // The block's units, by local index j < nj: unit_of(j) = blockIdx.x + j * gridDim.x.
+  // The block's units, by local index j < nj: unit_of(j) = blockIdx.x + j * G.
   // Interleaving the blocks' units keeps the whole grid reading one advancing
   // window of the matrix (contiguous ranges per block had every block open
   // its own DRAM rows).
-  const int G = gridDim.x, b0 = blockIdx.x;
+  const int G = blocks > 0 ? blocks : (int)gridDim.x, b0 = blockIdx.x;
   const int nj = n_units > b0 ? (n_units - b0 + G - 1) / G : 0;
   auto unit_of = [&](int j) { return b0 + j * G; };
   const int slot = S * R * 2 + R;  // LDS floats per unit (S > 1)
@@ -268,8 +279,8 @@ __device__ __forceinline__ void stream_rows(const MatDesc &M, int n_units, int s
   auto flush = [&]() {
     if (lane < np) {
       const PendingStore e = pw[lane];
-      if (e.half) *reinterpret_cast<uint16_t *>(e.addr) = (uint16_t)e.bits;
-      else *reinterpret_cast<uint32_t *>(e.addr) = e.bits;
+      if (e.half) put<COH>(reinterpret_cast<uint16_t *>(e.addr), (uint16_t)e.bits);
+      else put<COH>(reinterpret_cast<uint32_t *>(e.addr), e.bits);
     }
     np = 0;
   };
@@ -361,6 +372,7 @@ __device__ __forceinline__ void stream_rows(const MatDesc &M, int n_units, int s
     // the next group's loads are not hoisted into the result code
     __builtin_amdgcn_sched_barrier(0);
     first_j += N * RG;
+    hook(first_j < nj ? unit_of(first_j) : INT_MAX);
   };
   using P0 = std::integral_constant<int, 0>;
   // The first group issues its first min(N, PRE) batches before the
@@ -374,19 +386,28 @@ __device__ __forceinline__ void stream_rows(const MatDesc &M, int n_units, int s
     if constexpr (!XFIRST) load_x();
     group(n_tag, std::integral_constant<int, PI>{});
   };
-  int left = nb;
+  // Units below phase_unit: the local indices below nj1, so this wave's
+  // first nb1 units.
+  const int nj1 = phase_unit == INT_MAX ? nj : min(nj, max(0, (phase_unit - b0 + G - 1) / G));
+  const int nb1 = rg < RG && nj1 > rg ? min(nb, (nj1 - rg + RG - 1) / RG) : 0;
+  int left = nb, left1 = nb1;
+  auto take = [&]() {
+    const int n = left1 > 0 ? min(left1, K) : min(left, K);
+    left -= n;
+    left1 = max(left1 - n, 0);
+    return n;
+  };
   if (left > 0) {
-    group_of_size<K>(min(left, K), first);
+    group_of_size<K>(take(), first);
   } else {
     prologue();
     if constexpr (!XFIRST) load_x();
   }
-  left -= min(left, K);
-  while (left > 0) {
-    group_of_size<K>(min(left, K), [&](auto n_tag) { group(n_tag, P0{}); });
-    left -= min(left, K);
+  while (left > 0) group_of_size<K>(take(), [&](auto n_tag) { group(n_tag, P0{}); });
+  if (S == 1) {
+    hook(INT_MAX);
+    return;
   }
-  if (S == 1) return;
   __syncthreads();  // every slice's partial sums are in LDS
   for (int j = wave; j < nj; j += W) {
     float r[R][2], a[R];
@@ -403,4 +424,5 @@ __device__ __forceinline__ void stream_rows(const MatDesc &M, int n_units, int s
     done(unit_of(j), r, a, sink);
   }
   flush();
+  hook(INT_MAX);
 }

@@ -289,7 +289,7 @@ class StableLMForwarder:
         (the default); returns whether the single-launch path is available."""
         return bool(check(lib().tinyoai_stablelm_set_persistent(self.h, int(enable))))
 
-    LAUNCH_STAGES = {"decode_in": 0, "decode_out": 1, "lm_head": 2, "attention": 3}
+    LAUNCH_STAGES = {"decode_in": 0, "decode_out": 1, "lm_head": 2, "attention": 3, "prefetch": 4}
 
     def set_launch(self, stage: str, grid: int, threads: int) -> None:
         """Launch shape (blocks, threads per block) of a decode matrix
