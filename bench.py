@@ -42,14 +42,17 @@ def q8_bytes(rows, cols):
     return int(rows * cols * WEIGHT_BYTES[FORMAT["q8_0"]])
 
 
-def decode_in_bytes(c):
+def decode_in_bytes(c, kv_positions=0, kv_bytes=4):
     """Algorithmic HBM bytes of one decode_in launch: the layer's q, k, v,
-    gate and up rows once, plus its activations (x, LayerNorm w/b, q, k, v, m)."""
+    gate and up rows once, plus its activations (x, LayerNorm w/b, q, k, v,
+    m); with the attention run in the same launch, also the K and V of
+    kv_positions positions and the attention output."""
     d, I = c["hidden_size"], c["intermediate_size"]
     kv = d // c["num_attention_heads"] * c["num_key_value_heads"]
     weights = q8_bytes(d, d) + 2 * q8_bytes(kv, d) + 2 * q8_bytes(I, d)
     acts = 4 * (d + 2 * d + d + 2 * kv + I)
-    return weights + acts
+    attention = 2 * kv * kv_bytes * kv_positions + 4 * d if kv_positions else 0
+    return weights + acts + attention
 
 
 def token_bytes(c, pos, kv_bytes=4):
@@ -416,7 +419,12 @@ def main():
 
     ms, count = prof["decode_in"]
     avg_s = ms / 1e3 / max(count, 1)
-    nbytes = decode_in_bytes(config)
+    # With the attention inside the decode_in launch (no attention stage
+    # launches), its KV read counts too: positions 0..p at the profiled
+    # step's mean position.
+    fused = prof["attention"][1] == 0
+    mean_kv_positions = args.prompt + (args.generate - 2) / 2 + 1
+    nbytes = int(decode_in_bytes(config, mean_kv_positions if fused else 0, args.kv // 8))
     achieved = nbytes / avg_s / 1e9
     mean_pos = args.prompt + (args.generate - 2) / 2
     roof_tok_s = 1.0 / (token_bytes(config, mean_pos, args.kv // 8) / (HBM_PEAK_GBS * 1e9))
@@ -447,7 +455,9 @@ def main():
         "decode_roofline_tok_s": round(roof_tok_s, 1),
         "decode_frac_of_hbm_roofline": round(decode_tok_s / roof_tok_s, 4),
         "greedy_stream_stable": all(s == streams[0] for s in streams),
-        "roofline": {"kernel": "decode_in (LayerNorm + Q8_0 q/k/v/gate/up matvec + RoPE + KV append + SiLU-gate)",
+        "roofline": {"kernel": ("decode_in + attention (LayerNorm, Q8_0 q/k/v/gate/up matvec, RoPE, KV append, "
+                               "SiLU-gate; split-K attention on extra blocks of the same launch)") if fused else
+                              "decode_in (LayerNorm + Q8_0 q/k/v/gate/up matvec + RoPE + KV append + SiLU-gate)",
                      "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                      "algorithmic_bytes_per_launch": nbytes, "avg_launch_us": round(avg_s * 1e6, 2),

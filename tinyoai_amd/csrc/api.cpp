@@ -308,6 +308,7 @@ StableModel::~StableModel() {
   free_kv();
   for (void *p : buffers) hipFree(p);
   if (h_pinned) hipHostFree(h_pinned);
+  if (h_io) hipHostFree(h_io);
   if (params_copied) hipEventDestroy(params_copied);
   if (stream) hipStreamDestroy(stream);
 }
@@ -527,6 +528,9 @@ int StableModel::init(const tinyoai_stablelm_config &c, const tinyoai_tensor *te
                     (size_t)c.vocab_size * 4 + 4096 + (size_t)(std::max(chunk, dims.rot) + 2 * chunk) * 4 + 64,
                     hipHostMallocDefault);
   if (e != hipSuccess) return fail(TINYOAI_ENOMEM, "hipHostMalloc: %s", hipGetErrorString(e));
+  e = hipHostMalloc(&h_io, (size_t)(io_words_logits() + 16 + dims.rot) * 4 + 256, hipHostMallocMapped);
+  if (e == hipSuccess) e = hipHostGetDevicePointer(&d_io, h_io, 0);
+  if (e != hipSuccess) return fail(TINYOAI_ENOMEM, "mapped host memory: %s", hipGetErrorString(e));
   e = hipStreamSynchronize(stream);
   if (e != hipSuccess) return hip_fail(e, "model upload");
   const int cus = device_cu_count();
@@ -723,6 +727,8 @@ int StableModel::upload_params(const int *head_vals, int nh, const int32_t *ids,
 // The attention launch shape (steps, splits) is fixed by the caller so the
 // sequence can be captured once per shape.
 int StableModel::enqueue_decode(int steps, int splits, bool want_logits) {
+  const int io_params = io_words_logits();
+  TRY_HIP(launch_copy_words((const uint32_t *)d_io + io_params, params, 16 + dims.rot, stream), "parameters");
   for (int l = 0; l < cfg.num_hidden_layers; l++) {
     const LayerDev &w = layers[l];
     const float *rope_row = reinterpret_cast<const float *>(params + 16);
@@ -771,9 +777,12 @@ int StableModel::enqueue_decode(int steps, int splits, bool want_logits) {
       TRY_HIP(launch_copy_row(mbuf, trace_gate + (size_t)l * dims.inter, dims.inter, stream), "trace");
     }
   }
-  if (want_logits)
+  if (want_logits) {
     STAGE(ST_LM_HEAD, launch_ln_matvec(head.desc, norm_w, norm_b, dims.eps, 0, x, logits_dev, grid_head, threads_head, stream),
           "lm_head");
+    // the logits and the error word after them
+    TRY_HIP(launch_copy_words(logits_dev, d_io, cfg.vocab_size + 1, stream), "logits");
+  }
   return TINYOAI_OK;
 }
 
@@ -787,8 +796,9 @@ void StableModel::drop_graphs() {
 // profiling runs launch the kernels directly so each can be timed.
 int StableModel::decode_step(int token, int pos, bool want_logits) {
   const int vals[3] = {token, pos, fuse_epoch};
-  if (int rc = upload_params(vals, 3, nullptr, 0, rope_host.data() + (size_t)pos * dims.rot, dims.rot)) return rc;
+  logits_mapped = false;
   if (pgrid > 0 && use_persistent) {
+    if (int rc = upload_params(vals, 3, nullptr, 0, rope_host.data() + (size_t)pos * dims.rot, dims.rot)) return rc;
     PersistentDecode args = persistent_args(want_logits);
     if (prof.on) {
       if (!pstamps && alloc((void **)&pstamps, (size_t)pgrid * persistent_stamps(cfg.num_hidden_layers) * 8))
@@ -811,9 +821,16 @@ int StableModel::decode_step(int token, int pos, bool want_logits) {
     }
     return TINYOAI_OK;
   }
+  // The parameter block goes to host-mapped memory, which the step's first
+  // kernel reads (the previous step has completed: every forward ends
+  // with a synchronisation).
+  int *hp = (int *)h_io + io_words_logits();
+  for (int i = 0; i < 3; i++) hp[i] = vals[i];
+  memcpy(hp + 16, rope_host.data() + (size_t)pos * dims.rot, (size_t)dims.rot * 4);
+  logits_mapped = want_logits;
   const int steps = att_steps > 0 ? att_steps : attention_steps(pos, dims.heads);
   const int splits = attention_splits(pos, steps);
-  if (decode_fused(steps)) fuse_epoch++;  // the value the step's launches read is the one uploaded above
+  if (decode_fused(steps)) fuse_epoch++;  // the value the step's launches read is the one written above
   if (prof.on || !use_graphs) return enqueue_decode(steps, splits, want_logits);
   const int64_t key = ((int64_t)steps << 40) | ((int64_t)splits << 8) | (want_logits ? 2 : 0) | (tracing ? 1 : 0);
   auto it = graphs.find(key);
@@ -1181,15 +1198,20 @@ int StableModel::forward(int prefix, const int32_t *tokens, int n, bool want_log
       rc = prefill_chunk(tokens + done, m, prefix + done, last && want_logits);
     done += m;
   }
-  // The word after the logits is the persistent decode's error word: it
-  // comes back with the logits.
-  unsigned *err_host = (unsigned *)h_pinned + cfg.vocab_size;
+  // The word after the logits is the error word of the decode kernels'
+  // bounded waits: it comes back with the logits, which a decode step's
+  // graph has already copied to h_io (otherwise they come through h_pinned).
+  const bool mapped = logits_mapped && n == 1;
+  float *src = (float *)(mapped ? h_io : h_pinned);
+  unsigned *err_host = (unsigned *)src + cfg.vocab_size;
   if (!rc && want_logits) {
-    hipError_t e = hipMemcpyAsync(h_pinned, logits_dev, (size_t)cfg.vocab_size * 4 + 4, hipMemcpyDeviceToHost, stream);
+    hipError_t e = mapped ? hipSuccess
+                          : hipMemcpyAsync(h_pinned, logits_dev, (size_t)cfg.vocab_size * 4 + 4,
+                                           hipMemcpyDeviceToHost, stream);
     if (e == hipSuccess) e = hipStreamSynchronize(stream);
     if (e != hipSuccess) rc = hip_fail(e, "logits");
     else if (*err_host) rc = check_persistent(rc);
-    else memcpy(logits, h_pinned, (size_t)cfg.vocab_size * 4);
+    else memcpy(logits, src, (size_t)cfg.vocab_size * 4);
   } else if (!rc) {
     hipError_t e = hipStreamSynchronize(stream);
     if (e != hipSuccess) rc = hip_fail(e, "forward");

@@ -248,6 +248,9 @@ hipError_t launch_in_epilogue(const StableDims &s, const KVDev &kv, const float 
 // floats apart (K-split GEMM outputs), summed in order.
 hipError_t launch_residual(float *x, const float *p, int sp, const float *d, int sd, int64_t n, hipStream_t st);
 hipError_t launch_copy_row(const float *src, float *dst, int n, hipStream_t st);
+// n 32-bit words from src to dst (both 16-byte aligned; either may be
+// host-mapped memory), with 16-byte accesses.
+hipError_t launch_copy_words(const void *src, void *dst, int n, hipStream_t st);
 
 // ---- weights ----
 // Places raw GGUF-encoded bytes (already in device memory) of a

@@ -139,7 +139,8 @@ inline size_t slice_lds(int chunks, int split, int n_units, int grid, int R) {
 constexpr int kNormRegs = 3;
 
 // decode_in's work for one of `blocks` blocks (COH: outputs stored at
-// agent scope; hook as stream_rows takes it).
+// agent scope, the units below phase_unit run first; hook as stream_rows
+// takes it).
 template <int F, int T, bool COH, typename Hook>
 __device__ __forceinline__ void decode_in_body(const InArgs &a, float *lds_raw, Hook hook, int blocks,
                                                int phase_unit = INT_MAX) {
@@ -194,7 +195,7 @@ __device__ __forceinline__ void decode_in_body(const InArgs &a, float *lds_raw, 
   auto done = [&](int u, const float (&r)[2][2], const float (&)[2], const auto &out) {
     in_pair_outputs(s, kv, rope_row, pos, u, r[0][0], r[1][0], a.q_out, a.m_out, out);
   };
-  stream_rows<F, T, cpl_for<F>(), 2, false, true, 1, false, COH>(W, W.rows / 2, W.chunks, part, pend, rows, xload,
+  stream_rows<F, T, cpl_for<F>(), 2, false, true, 1, false, COH, COH>(W, W.rows / 2, W.chunks, part, pend, rows, xload,
                                                                   noaux, pre, prologue, done, hook, blocks,
                                                                   phase_unit);
 }

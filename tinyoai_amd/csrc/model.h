@@ -117,6 +117,13 @@ struct StableModel {
   uint16_t *MH = nullptr, *ML = nullptr;  // the SiLU-gate outputs as bf16 planes (down projection operand)
   void *h_pinned = nullptr;
   hipEvent_t params_copied = nullptr;  // last H2D copy out of h_pinned's parameter slot
+  // Host-mapped pinned memory of the decode graph: logits and the error
+  // word (io_words_logits() words), then the step's parameter block (16 +
+  // rot words). The graph's first kernel copies the parameters in and its
+  // last the logits out, so a decode step needs no copy-engine transfer.
+  void *h_io = nullptr, *d_io = nullptr;
+  bool logits_mapped = false;  // the last decode step left its logits in h_io
+  int io_words_logits() const { return (cfg.vocab_size + 1 + 63) / 64 * 64; }
   bool tracing = false;
   float *trace_dev = nullptr, *trace_att = nullptr, *trace_gate = nullptr;  // [L][d], [L][heads*hd], [L][inter]
   int grid_in = 0, grid_out = 0, grid_head = 0;

@@ -126,6 +126,16 @@ __global__ void copy_kernel(const float *src, float *dst, int n) {
   for (int i = threadIdx.x; i < n; i += blockDim.x) dst[i] = src[i];
 }
 
+// n 32-bit words, 16 bytes per store where both ends allow it: a wide copy
+// (a host-mapped destination then takes full PCIe writes).
+__global__ void copy_words_kernel(const uint32_t *src, uint32_t *dst, int n) {
+  const int i4 = (blockIdx.x * blockDim.x + threadIdx.x);
+  const int n4 = n / 4;
+  if (i4 < n4) reinterpret_cast<uint4 *>(dst)[i4] = reinterpret_cast<const uint4 *>(src)[i4];
+  const int t = n4 * 4 + i4;
+  if (i4 < n - n4 * 4) dst[t] = src[t];
+}
+
 int elementwise_grid(int64_t n) { return (int)std::min<int64_t>((n + 255) / 256, 4096); }
 
 }  // namespace
@@ -157,6 +167,14 @@ hipError_t launch_in_epilogue(const StableDims &s, const KVDev &kv, const float 
 hipError_t launch_residual(float *x, const float *p, int sp, const float *d, int sd, int64_t n, hipStream_t st) {
   if (sp < 1 || sd < 1) return hipErrorInvalidValue;
   hipLaunchKernelGGL(residual_kernel, dim3(elementwise_grid(n)), dim3(256), 0, st, x, p, sp, d, sd, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_copy_words(const void *src, void *dst, int n, hipStream_t st) {
+  if ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 15) return hipErrorInvalidValue;
+  const int threads = 256, blocks = std::max(1, (n / 4 + threads - 1) / threads);
+  hipLaunchKernelGGL(copy_words_kernel, dim3(blocks), dim3(threads), 0, st, reinterpret_cast<const uint32_t *>(src),
+                     reinterpret_cast<uint32_t *>(dst), n);
   return hipGetLastError();
 }
 

@@ -57,6 +57,14 @@ struct PendingSink {
   __device__ void f16(uint16_t *p, uint16_t v) const { rec(p, (uint32_t)v, 1u); }
 };
 constexpr int kAhead = 2;
+// Batches of the next group issued before a group's result code: one for
+// the 16-byte-value formats; none for the 5/6-bit formats, whose batches
+// (with block headers and high bits) would then exceed the registers of
+// two waves per SIMD, as would a second batch for any format.
+template <int F>
+constexpr int carry_for() {
+  return F == FMT_Q5_1 || F == FMT_Q4_K || F == FMT_Q5_K || F == FMT_Q6_K ? 0 : 1;
+}
 static_assert(kAhead >= 1 && kAhead + 1 <= kRowGroup, "the first group issues kAhead + 1 batches");
 constexpr uint32_t kOffNone = 0x80000000u;  // a buffer offset past every plane (planes_fit)
 
@@ -243,10 +251,10 @@ __host__ __device__ inline void slice_range(const SliceShape &sh, int nch, int s
 // each group's results are stored, with the next unit the wave takes
 // (INT_MAX when none), and once more with INT_MAX at the end. `blocks` is
 // the number of blocks sharing the units (blocks 0 .. blocks - 1 of the
-// launch; 0 = the whole grid). A wave's units below `phase_unit` run in
-// groups of their own, before its later units.
+// launch; 0 = the whole grid). With PHASED, a wave's units below
+// `phase_unit` run in groups of their own, before its later units.
 template <int F, int T, int CPL, int R, bool XFIRST, bool PREWAIT, int PRE, bool AUX, bool COH = false,
-          typename Rows, typename XLoad, typename AuxLoad, typename Pre, typename Prologue, typename Done,
+          bool PHASED = false, typename Rows, typename XLoad, typename AuxLoad, typename Pre, typename Prologue, typename Done,
           typename Hook = void (*)(int)>
 __device__ __forceinline__ void stream_rows(const MatDesc &M, int n_units, int split, float *red, PendingStore *pend,
                                             Rows unit_rows, XLoad x_load, AuxLoad aux_load, Pre pre, Prologue prologue,
@@ -313,23 +321,29 @@ __device__ __forceinline__ void stream_rows(const MatDesc &M, int n_units, int s
   RowBatch<CPL, R> b[K];
   float aux[K][R];
   int first_j = rg;  // local index of the group's first unit
-  auto issue = [&](int k) {
+  // Batch k of the group starting at local index j0.
+  auto issue_at = [&](int j0, int k) {
     int row[R];
-    unit_rows(unit_of(first_j + k * RG), row);
+    unit_rows(unit_of(j0 + k * RG), row);
     if constexpr (AUX) {
 #pragma unroll
       for (int i = 0; i < R; i++) aux[k][i] = aux_load(row[i]);
     }
     rows_issue<F, CPL, R>(b[k], L, P, M, row);
   };
+  auto issue = [&](int k) { issue_at(first_j, k); };
   if constexpr (XFIRST) load_x();
   pre();
   if constexpr (PREWAIT) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   // One group of N batches, P0 of them already issued; step k issues the
   // batches up to k + kAhead, then consumes batch k; the units' results
   // follow the last consume (result code between the consumes reuses
-  // registers and makes the wave wait for the batches in flight).
-  auto group = [&](auto n_tag, auto p0_tag) {
+  // registers and makes the wave wait for the batches in flight). After
+  // the last consume the first min(kCarry, n_next) batches of the next
+  // group (n_next units) are issued into the consumed batches' registers,
+  // so the wave's loads stay in flight through the result code.
+  constexpr int kCarry = carry_for<F>();
+  auto group = [&](auto n_tag, auto p0_tag, int n_next) {
     constexpr int N = decltype(n_tag)::value, P0 = decltype(p0_tag)::value;
     int r[N][R];  // float bits, wave-uniform (scalar registers)
 #pragma unroll
@@ -345,6 +359,19 @@ __device__ __forceinline__ void stream_rows(const MatDesc &M, int n_units, int s
 #pragma unroll
       for (int i = 0; i < R; i++) r[k][i] = __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, wave_total(acc[i])));
     }
+    float ax[N][R];  // this group's per-row operands (their slots take the next group's)
+#pragma unroll
+    for (int k = 0; k < N; k++)
+#pragma unroll
+      for (int i = 0; i < R; i++) ax[k][i] = AUX ? aux[k][i] : 0.f;
+    if constexpr (kCarry > 0) {
+      group_of_size<kCarry>(min(n_next, kCarry), [&](auto pn_tag) {
+        constexpr int PN = decltype(pn_tag)::value;
+#pragma unroll
+        for (int t = 0; t < PN; t++) issue_at(first_j + N * RG, t);
+      });
+    }
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int k = 0; k < N; k++) {
       float rk[R][2];
@@ -356,7 +383,7 @@ __device__ __forceinline__ void stream_rows(const MatDesc &M, int n_units, int s
       }
       const int j = first_j + k * RG;
       if (S == 1) {
-        done(unit_of(j), rk, aux[k], sink);
+        done(unit_of(j), rk, ax[k], sink);
         __builtin_amdgcn_sched_barrier(0);  // one unit's result code at a time
       } else if (lane == 0) {
         float *dst = red + j * slot;
@@ -364,7 +391,7 @@ __device__ __forceinline__ void stream_rows(const MatDesc &M, int n_units, int s
         for (int i = 0; i < R; i++) {
           dst[s * R * 2 + 2 * i] = rk[i][0];
           dst[s * R * 2 + 2 * i + 1] = rk[i][1];
-          if (s == 0) dst[S * R * 2 + i] = aux[k][i];
+          if (s == 0) dst[S * R * 2 + i] = ax[k][i];
         }
       }
     }
@@ -374,36 +401,48 @@ __device__ __forceinline__ void stream_rows(const MatDesc &M, int n_units, int s
     first_j += N * RG;
     hook(first_j < nj ? unit_of(first_j) : INT_MAX);
   };
-  using P0 = std::integral_constant<int, 0>;
   // The first group issues its first min(N, PRE) batches before the
   // prologue (older than every later load, so later wait counts stay
   // exact); a wave with no units still runs the prologue (its barriers).
-  auto first = [&](auto n_tag) {
+  auto first = [&](auto n_tag, int n_next) {
     constexpr int N = decltype(n_tag)::value, PI = N < PRE ? N : PRE;
 #pragma unroll
     for (int t = 0; t < PI; t++) issue(t);
     prologue();
     if constexpr (!XFIRST) load_x();
-    group(n_tag, std::integral_constant<int, PI>{});
+    group(n_tag, std::integral_constant<int, PI>{}, n_next);
   };
   // Units below phase_unit: the local indices below nj1, so this wave's
   // first nb1 units.
-  const int nj1 = phase_unit == INT_MAX ? nj : min(nj, max(0, (phase_unit - b0 + G - 1) / G));
-  const int nb1 = rg < RG && nj1 > rg ? min(nb, (nj1 - rg + RG - 1) / RG) : 0;
-  int left = nb, left1 = nb1;
+  int left = nb, left1 = 0;
+  if constexpr (PHASED) {
+    const int nj1 = min(nj, max(0, (phase_unit - b0 + G - 1) / G));
+    left1 = rg < RG && nj1 > rg ? min(nb, (nj1 - rg + RG - 1) / RG) : 0;
+  }
+  auto peek = [&]() { return PHASED && left1 > 0 ? min(left1, K) : min(left, K); };
   auto take = [&]() {
-    const int n = left1 > 0 ? min(left1, K) : min(left, K);
+    const int n = peek();
     left -= n;
-    left1 = max(left1 - n, 0);
+    if constexpr (PHASED) left1 = max(left1 - n, 0);
     return n;
   };
+  // Groups after the first find min(kCarry, N) of their batches issued by
+  // the group before.
+  auto rest = [&](auto n_tag, int n_next) {
+    constexpr int N = decltype(n_tag)::value;
+    group(n_tag, std::integral_constant<int, (N < kCarry ? N : kCarry)>{}, n_next);
+  };
   if (left > 0) {
-    group_of_size<K>(take(), first);
+    const int n = take(), nn = peek();
+    group_of_size<K>(n, [&](auto n_tag) { first(n_tag, nn); });
   } else {
     prologue();
     if constexpr (!XFIRST) load_x();
   }
-  while (left > 0) group_of_size<K>(take(), [&](auto n_tag) { group(n_tag, P0{}); });
+  while (left > 0) {
+    const int n = take(), nn = peek();
+    group_of_size<K>(n, [&](auto n_tag) { rest(n_tag, nn); });
+  }
   if (S == 1) {
     hook(INT_MAX);
     return;

@@ -228,9 +228,9 @@ class StableLMForwarder:
 
     def forward(self, prefix: int, tokens, want_logits: bool = True) -> np.ndarray | None:
         toks = np.ascontiguousarray(tokens, np.int32)
-        check(lib().tinyoai_stablelm_forward(self.h, prefix, _ip(toks), toks.size, int(want_logits),
-                                             _fp(self._logits)))
-        return self._logits.copy() if want_logits else None
+        out = np.empty(self.vocab, np.float32) if want_logits else self._logits  # the caller's own copy
+        check(lib().tinyoai_stablelm_forward(self.h, prefix, _ip(toks), toks.size, int(want_logits), _fp(out)))
+        return out if want_logits else None
 
     def new_branches(self, prefix: int, count: int, max_len: int = 0) -> "Branches":
         """NewBranches (mlx_branches.go:25-33): `count` suffixes borrowing
