@@ -93,6 +93,25 @@ int tinyoai_stablelm_load(const tinyoai_stablelm_config *config, const tinyoai_t
 int tinyoai_stablelm_forward(tinyoai_model *m, int32_t prefix, const int32_t *tokens, int32_t n,
                              int32_t want_logits, float *logits);
 
+/* ForwardWithLogprobs (mlx.go:53-57; mlx_native.go:300-311): the forward
+ * of `tokens` after `prefix` (semantics and failure behaviour of
+ * tinyoai_stablelm_forward, always with logits) that also scores position i
+ * against targets[i]: chosen[i] = log p(targets[i]) and the `count` most
+ * likely ids top_ids[i][count] with their log probabilities
+ * top_logprobs[i][count], descending, ties to the lower id, normalised over
+ * the whole vocabulary in float64 (summarizeLogits, logprobs.go:60-95).
+ * `logits` receives the last position's row. 1 <= count <= min(vocab,
+ * 1024); every target in [0, vocab). */
+int tinyoai_stablelm_forward_logprobs(tinyoai_model *m, int32_t prefix, const int32_t *tokens,
+                                      const int32_t *targets, int32_t n, int32_t count, float *logits,
+                                      double *chosen, int32_t *top_ids, double *top_logprobs);
+
+/* summarizeLogits (logprobs.go:60-95) on the device for `rows` caller rows
+ * of logits [rows][vocab]: chosen[r] = log p(targets[r]) and the `count`
+ * best ids and log probabilities per row, as forward_logprobs scores them. */
+int tinyoai_summarize_logits(const float *logits, int32_t rows, int32_t vocab, const int32_t *targets, int32_t count,
+                             double *chosen, int32_t *top_ids, double *top_logprobs);
+
 /* SetKVBits (mlx_kv.go:78-91): 16 = fp16 KV rounded with floatHalf
  * (kv_cache.go:27-65), 32 = fp32 KV (the CPU engine's StableLMOptions{KVCache:
  * "f32"}). The MLX forwarder's 8 (affine 8-bit KV in groups of 64,

@@ -309,6 +309,7 @@ StableModel::~StableModel() {
   for (void *p : buffers) hipFree(p);
   if (h_pinned) hipHostFree(h_pinned);
   if (h_io) hipHostFree(h_io);
+  if (score_mem) hipFree(score_mem);
   if (params_copied) hipEventDestroy(params_copied);
   if (stream) hipStreamDestroy(stream);
 }
@@ -969,6 +970,8 @@ int StableModel::prefill_chunk(const int32_t *ids, int n, int start, bool want_l
       TRY_HIP(launch_copy_row(M + (size_t)(n - 1) * I, trace_gate + (size_t)l * I, I, stream), "trace");
     }
   }
+  if (scoring.targets)
+    if (int rc = score_rows(n)) return rc;
   if (want_logits) {
     TRY_HIP(launch_copy_row(X + (size_t)(n - 1) * d, x, d, stream), "last row");
     STAGE(ST_LM_HEAD, launch_ln_matvec(head.desc, norm_w, norm_b, dims.eps, 0, x, logits_dev, grid_head, threads_head, stream),
@@ -990,6 +993,25 @@ void Branches::free_kv() {
   }
   kv.clear();
   scap = 0;
+}
+
+// Every row of the chunk through the final LayerNorm and the classifier,
+// in batches that fit the product buffer Y, then its log probabilities.
+int StableModel::score_rows(int n) {
+  const int d = dims.d, V = cfg.vocab_size;
+  TRY_HIP(launch_layer_norm_rows(X, norm_w, norm_b, dims.eps, n, d, H, stream), "final norm");
+  const int per = (int)std::max<int64_t>(1, (int64_t)chunk * win_rows / V);
+  for (int r0 = 0; r0 < n; r0 += per) {
+    const int nr = std::min(per, n - r0);
+    if (int rc = project(head.desc, H + (size_t)r0 * d, d, nr, Y, V)) return rc;
+    const int row = scoring.row + r0;
+    const size_t c = (size_t)scoring.count;
+    TRY_HIP(launch_logprobs(Y, V, nr, V, scoring.targets + row, scoring.count, scoring.chosen + row,
+                            scoring.top_ids + row * c, scoring.top_lp + row * c, stream),
+            "log probabilities");
+  }
+  scoring.row += n;
+  return TINYOAI_OK;
 }
 
 Branches::~Branches() {
@@ -1178,6 +1200,73 @@ int StableModel::branch_rows(Branches &b, const int32_t *ids, const int32_t *br,
   return TINYOAI_OK;
 }
 
+// ForwardWithLogprobs (mlx.go:53-57; mlx_native.go:300-311): the forward
+// of `tokens` through the prefill path (every row's logits are needed),
+// scoring row i against targets[i]; results copied to the caller's arrays.
+int StableModel::forward_logprobs(int prefix, const int32_t *tokens, const int32_t *targets, int n, int count,
+                                  float *logits, double *chosen, int32_t *top_ids, double *top_lp) {
+  if (int rc = busy_with_branches()) return rc;
+  const int V = cfg.vocab_size;
+  if (!tokens || !targets || !logits || !chosen || !top_ids || !top_lp || n <= 0 || count < 1 ||
+      count > std::min(V, logprob_max_count()))
+    return fail(TINYOAI_EINVAL, "invalid probability request");
+  for (int i = 0; i < n; i++)
+    if (targets[i] < 0 || targets[i] >= V) return fail(TINYOAI_EINVAL, "invalid probability target %d", targets[i]);
+  if (prefix < 0 || prefix > offset || prefix + n > cfg.max_position_embeddings)
+    return fail(TINYOAI_EINVAL, "invalid cached prefix or context length (prefix %d, offset %d, n %d)", prefix,
+                offset, n);
+  for (int i = 0; i < n; i++)
+    if (tokens[i] < 0 || tokens[i] >= V) return fail(TINYOAI_EINVAL, "invalid token %d", tokens[i]);
+  // device scratch: targets, chosen, top ids, top log probabilities
+  auto r256 = [](size_t b) { return (b + 255) / 256 * 256; };
+  const size_t bt = r256((size_t)n * 4), bc = r256((size_t)n * 8), bi = r256((size_t)n * count * 4),
+               bl = r256((size_t)n * count * 8);
+  if (bt + bc + bi + bl > score_bytes) {
+    hipStreamSynchronize(stream);
+    if (score_mem) hipFree(score_mem);
+    score_mem = nullptr;
+    score_bytes = 0;
+    hipError_t e = hipMalloc(&score_mem, bt + bc + bi + bl);
+    if (e != hipSuccess) return fail(TINYOAI_ENOMEM, "probability scratch: %s", hipGetErrorString(e));
+    score_bytes = bt + bc + bi + bl;
+  }
+  char *base = (char *)score_mem;
+  int *d_targets = (int *)base;
+  TRY_HIP(hipMemcpyAsync(d_targets, targets, (size_t)n * 4, hipMemcpyHostToDevice, stream), "targets");
+  scoring = Scoring{d_targets, count, 0, (double *)(base + bt), (double *)(base + bt + bc + bi),
+                    (int *)(base + bt + bc)};
+  offset = prefix;
+  int rc = ensure_kv(prefix + n);
+  for (int done = 0; done < n && !rc;) {
+    const int m = std::min(chunk, n - done);
+    rc = prefill_chunk(tokens + done, m, prefix + done, done + m == n);
+    done += m;
+  }
+  const Scoring sc = scoring;
+  scoring = Scoring{};
+  if (!rc) {
+    hipError_t e = hipMemcpyAsync(h_pinned, logits_dev, (size_t)V * 4, hipMemcpyDeviceToHost, stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(chosen, sc.chosen, (size_t)n * 8, hipMemcpyDeviceToHost, stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(top_ids, sc.top_ids, (size_t)n * count * 4, hipMemcpyDeviceToHost, stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(top_lp, sc.top_lp, (size_t)n * count * 8, hipMemcpyDeviceToHost, stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(stream);
+    if (e != hipSuccess) rc = hip_fail(e, "log probabilities");
+    else memcpy(logits, h_pinned, (size_t)V * 4);
+  }
+  if (rc) {
+    std::string msg = g_error;
+    hipStreamSynchronize(stream);
+    prof.marks.clear();
+    prof.used = 0;
+    free_kv();
+    g_error = msg;
+    return rc;
+  }
+  prof.resolve();
+  offset = prefix + n;
+  return TINYOAI_OK;
+}
+
 int StableModel::forward(int prefix, const int32_t *tokens, int n, bool want_logits, float *logits) {
   if (int rc = busy_with_branches()) return rc;
   if (prefix < 0 || prefix > offset || n <= 0 || !tokens || prefix + n > cfg.max_position_embeddings)
@@ -1268,6 +1357,41 @@ int tinyoai_stablelm_forward(tinyoai_model *m, int32_t prefix, const int32_t *to
                              float *logits) {
   if (!m || !m->stable) return fail(TINYOAI_EINVAL, "not a StableLM handle");
   return m->stable->forward(prefix, tokens, n, want_logits != 0, logits);
+}
+
+int tinyoai_stablelm_forward_logprobs(tinyoai_model *m, int32_t prefix, const int32_t *tokens,
+                                      const int32_t *targets, int32_t n, int32_t count, float *logits,
+                                      double *chosen, int32_t *top_ids, double *top_logprobs) {
+  if (!m || !m->stable) return fail(TINYOAI_EINVAL, "not a StableLM handle");
+  return m->stable->forward_logprobs(prefix, tokens, targets, n, count, logits, chosen, top_ids, top_logprobs);
+}
+
+int tinyoai_summarize_logits(const float *logits, int32_t rows, int32_t vocab, const int32_t *targets, int32_t count,
+                             double *chosen, int32_t *top_ids, double *top_logprobs) {
+  if (!logits || !targets || !chosen || !top_ids || !top_logprobs || rows < 1 || vocab < 1 || count < 1 ||
+      count > std::min<int>(vocab, logprob_max_count()))
+    return fail(TINYOAI_EINVAL, "invalid probability request");
+  for (int i = 0; i < rows; i++)
+    if (targets[i] < 0 || targets[i] >= vocab) return fail(TINYOAI_EINVAL, "invalid probability target %d", targets[i]);
+  const size_t nl = (size_t)rows * vocab * 4, nt = (size_t)rows * 4, nc = (size_t)rows * 8;
+  const size_t ni = (size_t)rows * count * 4, np = (size_t)rows * count * 8;
+  auto r256 = [](size_t b) { return (b + 255) / 256 * 256; };
+  char *mem = nullptr;
+  hipError_t e = hipMalloc(&mem, r256(nl) + r256(nt) + r256(nc) + r256(ni) + r256(np));
+  if (e != hipSuccess) return fail(TINYOAI_ENOMEM, "hipMalloc: %s", hipGetErrorString(e));
+  float *dl = (float *)mem;
+  int *dt = (int *)(mem + r256(nl));
+  double *dc = (double *)((char *)dt + r256(nt));
+  int *di = (int *)((char *)dc + r256(nc));
+  double *dp = (double *)((char *)di + r256(ni));
+  e = hipMemcpy(dl, logits, nl, hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemcpy(dt, targets, nt, hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = launch_logprobs(dl, vocab, rows, vocab, dt, count, dc, di, dp, nullptr);
+  if (e == hipSuccess) e = hipMemcpy(chosen, dc, nc, hipMemcpyDeviceToHost);
+  if (e == hipSuccess) e = hipMemcpy(top_ids, di, ni, hipMemcpyDeviceToHost);
+  if (e == hipSuccess) e = hipMemcpy(top_logprobs, dp, np, hipMemcpyDeviceToHost);
+  hipFree(mem);
+  return e == hipSuccess ? TINYOAI_OK : hip_fail(e, "log probabilities");
 }
 
 int tinyoai_stablelm_set_kv_bits(tinyoai_model *m, int32_t bits, int32_t *cleared) {

@@ -252,6 +252,15 @@ hipError_t launch_copy_row(const float *src, float *dst, int n, hipStream_t st);
 // host-mapped memory), with 16-byte accesses.
 hipError_t launch_copy_words(const void *src, void *dst, int n, hipStream_t st);
 
+// Log probabilities of `rows` rows of logits (row stride ld floats, vocab
+// entries each), normalised over the whole row in float64: chosen[r] for
+// targets[r], and the count largest entries of each row as top_ids[r][k] /
+// top_lp[r][k], descending with ties to the lower id (summarizeLogits,
+// logprobs.go:60-95). 1 <= count <= min(vocab, logprob_max_count()).
+int logprob_max_count();
+hipError_t launch_logprobs(const float *logits, int64_t ld, int rows, int vocab, const int *targets, int count,
+                           double *chosen, int *top_ids, double *top_lp, hipStream_t st);
+
 // ---- weights ----
 // Places raw GGUF-encoded bytes (already in device memory) of a
 // [rows][cols] tensor into `dst` under `map`, starting at column col0.

@@ -187,6 +187,20 @@ struct StableModel {
   int project_planes(const MatDesc &w, const uint16_t *xh, const uint16_t *xl, int n, float *y, int ldy,
                      int *splits = nullptr);
   int prefill_chunk(const int32_t *ids, int n, int start, bool want_logits);
+  // Scoring of a forward_logprobs call: while set, prefill_chunk also
+  // computes every row's logits and their log probabilities (device
+  // buffers, rows from score_row on).
+  struct Scoring {
+    const int *targets = nullptr;
+    int count = 0, row = 0;
+    double *chosen = nullptr, *top_lp = nullptr;
+    int *top_ids = nullptr;
+  } scoring;
+  void *score_mem = nullptr;
+  size_t score_bytes = 0;
+  int score_rows(int n);
+  int forward_logprobs(int prefix, const int32_t *tokens, const int32_t *targets, int n, int count, float *logits,
+                       double *chosen, int32_t *top_ids, double *top_lp);
   int forward(int prefix, const int32_t *tokens, int n, bool want_logits, float *logits);
   // Rows of open branches: token ids[i] extends branch br[i]; each
   // branch's rows are consecutive and continue its suffix. Writes each

@@ -16,7 +16,8 @@ from . import weights as W
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libtinyoai_hip.so")
 
 EXPORTS = [
-    "tinyoai_last_error", "tinyoai_stablelm_load", "tinyoai_stablelm_forward", "tinyoai_stablelm_set_kv_bits",
+    "tinyoai_last_error", "tinyoai_stablelm_load", "tinyoai_stablelm_forward", "tinyoai_stablelm_forward_logprobs",
+    "tinyoai_stablelm_set_kv_bits", "tinyoai_summarize_logits",
     "tinyoai_stablelm_limit_cache", "tinyoai_stablelm_reset", "tinyoai_stablelm_offset", "tinyoai_stablelm_close",
     "tinyoai_stablelm_read_kv", "tinyoai_stablelm_trace", "tinyoai_stablelm_trace_read",
     "tinyoai_stablelm_trace_read_stages", "tinyoai_stablelm_decode_timeline", "tinyoai_stablelm_set_persistent",
@@ -64,7 +65,10 @@ def lib():
         L.tinyoai_last_error.restype = C.c_char_p
         L.tinyoai_stablelm_load.argtypes = [C.POINTER(StableLMConfig), C.POINTER(Tensor), C.c_int32, C.POINTER(P)]
         L.tinyoai_stablelm_forward.argtypes = [P, C.c_int32, ip, C.c_int32, C.c_int32, fp]
+        dp = C.POINTER(C.c_double)
+        L.tinyoai_stablelm_forward_logprobs.argtypes = [P, C.c_int32, ip, ip, C.c_int32, C.c_int32, fp, dp, ip, dp]
         L.tinyoai_stablelm_set_kv_bits.argtypes = [P, C.c_int32, ip]
+        L.tinyoai_summarize_logits.argtypes = [fp, C.c_int32, C.c_int32, ip, C.c_int32, dp, ip, dp]
         L.tinyoai_stablelm_limit_cache.argtypes = [P, C.c_int32, ip]
         L.tinyoai_stablelm_reset.argtypes = [P]
         L.tinyoai_stablelm_offset.argtypes = [P]
@@ -111,6 +115,22 @@ def _fp(a: np.ndarray):
 def _ip(a: np.ndarray):
     assert a.dtype == np.int32 and a.flags.c_contiguous
     return a.ctypes.data_as(C.POINTER(C.c_int32))
+
+
+def summarize_logits(logits: np.ndarray, targets, count: int):
+    """summarizeLogits (logprobs.go:60-95) on the device for rows of logits
+    [rows][vocab]: (chosen [rows], top ids [rows][count], top log
+    probabilities [rows][count])."""
+    x = np.ascontiguousarray(np.atleast_2d(logits), np.float32)
+    tg = np.ascontiguousarray(targets, np.int32)
+    rows, vocab = x.shape
+    chosen = np.empty(rows, np.float64)
+    ids = np.empty((rows, count), np.int32)
+    lp = np.empty((rows, count), np.float64)
+    dp = C.POINTER(C.c_double)
+    check(lib().tinyoai_summarize_logits(_fp(x), rows, vocab, _ip(tg), count, chosen.ctypes.data_as(dp), _ip(ids),
+                                         lp.ctypes.data_as(dp)))
+    return chosen, ids, lp
 
 
 class Weight:
@@ -231,6 +251,23 @@ class StableLMForwarder:
         out = np.empty(self.vocab, np.float32) if want_logits else self._logits  # the caller's own copy
         check(lib().tinyoai_stablelm_forward(self.h, prefix, _ip(toks), toks.size, int(want_logits), _fp(out)))
         return out if want_logits else None
+
+    def forward_with_logprobs(self, prefix: int, tokens, targets, count: int):
+        """ForwardWithLogprobs (mlx.go:53-57): the forward of `tokens` after
+        `prefix`, scoring position i against targets[i]. Returns (last
+        logits [vocab], chosen [n] float64, top ids [n][count], top log
+        probabilities [n][count] float64)."""
+        toks = np.ascontiguousarray(tokens, np.int32)
+        tg = np.ascontiguousarray(targets, np.int32)
+        n = toks.size
+        logits = np.empty(self.vocab, np.float32)
+        chosen = np.empty(n, np.float64)
+        ids = np.empty((n, count), np.int32)
+        lp = np.empty((n, count), np.float64)
+        dp = C.POINTER(C.c_double)
+        check(lib().tinyoai_stablelm_forward_logprobs(self.h, prefix, _ip(toks), _ip(tg), n, count, _fp(logits),
+                                                      chosen.ctypes.data_as(dp), _ip(ids), lp.ctypes.data_as(dp)))
+        return logits, chosen, ids, lp
 
     def new_branches(self, prefix: int, count: int, max_len: int = 0) -> "Branches":
         """NewBranches (mlx_branches.go:25-33): `count` suffixes borrowing
