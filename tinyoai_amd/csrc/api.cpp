@@ -14,6 +14,7 @@
 #include <cstring>
 #include <map>
 #include <memory>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -1328,6 +1329,7 @@ using namespace tinyoai;
 
 struct tinyoai_weight {
   DevMatrix m;
+  int device = 0;  // the device the weight lives on
   hipStream_t stream = nullptr;
   uint16_t *planes = nullptr;  // bf16 hi/lo planes of the last batched product's input
   size_t planes_bytes = 0;
@@ -1655,7 +1657,9 @@ int tinyoai_weight_upload(int32_t dtype, int64_t rows, int64_t cols, const void 
   if (!out || !data) return fail(TINYOAI_EINVAL, "invalid weight upload arguments");
   *out = nullptr;
   auto w = std::make_unique<tinyoai_weight>();
-  hipError_t e = hipStreamCreateWithFlags(&w->stream, hipStreamNonBlocking);
+  hipError_t e = hipGetDevice(&w->device);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  e = hipStreamCreateWithFlags(&w->stream, hipStreamNonBlocking);
   if (e != hipSuccess) return hip_fail(e, "hipStreamCreate");
   int rc = w->m.upload(dtype, rows, cols, data, nbytes, w->stream);
   if (rc) return rc;
@@ -1702,6 +1706,68 @@ int tinyoai_weight_mul_device(tinyoai_weight *w, const float *x_dev, int32_t n, 
       w->planes_bytes = need;
     }
     uint16_t *hi = w->planes, *lo = gemm_planes(m) == 2 ? w->planes + plane / 2 : nullptr;
+    e = launch_split_bf16(x_dev, m.cols, m.cols, n, hi, lo, st);
+    if (e == hipSuccess) e = launch_gemm_mfma(m, hi, lo, n, out_dev, m.rows, st);
+  } else {
+    e = launch_gemm(m, x_dev, n, out_dev, st);
+  }
+  return e == hipSuccess ? TINYOAI_OK : hip_fail(e, "product launch");
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------- no-allocation product
+// The operand planes of tinyoai_weight_mul_device_noalloc: a file-scope
+// device array, one copy on each GPU the library runs on, held until the
+// process ends. In host code `scratch` names a host-side stand-in; the
+// device address of each GPU's copy comes from hipGetSymbolAddress (once
+// per device, with that device current) and only that address is used.
+constexpr size_t kScratchValues = (size_t)4 << 20;  // activation values per call (n * cols)
+static __device__ __align__(256) uint16_t scratch[2 * kScratchValues];  // bf16 hi and lo planes: 16 MiB
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_dev[kMaxDevices];
+
+// The current device's copy of `scratch`, looked up on the first call on
+// that device.
+int scratch_address(void **out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices) return fail(TINYOAI_EINVAL, "device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    void *p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+    g_scratch_dev[dev] = p;
+  }
+  *out = g_scratch_dev[dev];
+  return TINYOAI_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int tinyoai_weight_mul_device_noalloc(tinyoai_weight *w, const float *x_dev, int32_t n, float *out_dev, void *stream) {
+  if (!w || !x_dev || !out_dev || n <= 0) return fail(TINYOAI_EINVAL, "invalid product arguments");
+  const MatDesc &m = w->m.desc;
+  if ((size_t)n * m.cols > kScratchValues)
+    return fail(TINYOAI_EINVAL, "product of %d x %d activation values exceeds the no-allocation limit of %zu", n, m.cols,
+                kScratchValues);
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  if (dev != w->device) return fail(TINYOAI_EINVAL, "the weight lives on device %d, not the current %d", w->device, dev);
+  hipStream_t st = stream ? (hipStream_t)stream : w->stream;
+  if (n == 1) {
+    e = launch_ln_matvec(m, nullptr, nullptr, 0.0, 0, x_dev, out_dev, device_cu_count() * 4, 256, st);
+  } else if (gemm_mfma_supported(m)) {
+    void *planes = nullptr;
+    if (int rc = scratch_address(&planes)) return rc;
+    uint16_t *hi = (uint16_t *)planes, *lo = gemm_planes(m) == 2 ? hi + (size_t)n * m.cols : nullptr;
     e = launch_split_bf16(x_dev, m.cols, m.cols, n, hi, lo, st);
     if (e == hipSuccess) e = launch_gemm_mfma(m, hi, lo, n, out_dev, m.rows, st);
   } else {

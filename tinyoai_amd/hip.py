@@ -25,7 +25,8 @@ EXPORTS = [
     "tinyoai_stablelm_branches_append", "tinyoai_stablelm_branches_length", "tinyoai_stablelm_branches_close",
     "tinyoai_stablelm_profile", "tinyoai_stablelm_profile_read", "tinyoai_llama_load",
     "tinyoai_llama_forward", "tinyoai_llama_reset", "tinyoai_llama_close", "tinyoai_weight_upload",
-    "tinyoai_weight_read_values", "tinyoai_weight_mul", "tinyoai_weight_mul_device", "tinyoai_weight_free",
+    "tinyoai_weight_read_values", "tinyoai_weight_mul", "tinyoai_weight_mul_device",
+    "tinyoai_weight_mul_device_noalloc", "tinyoai_weight_free",
 ]
 
 
@@ -96,6 +97,7 @@ def lib():
         L.tinyoai_weight_read_values.argtypes = [P, C.c_int64, C.c_int64, fp]
         L.tinyoai_weight_mul.argtypes = [P, fp, C.c_int32, fp]
         L.tinyoai_weight_mul_device.argtypes = [P, P, C.c_int32, P, P]
+        L.tinyoai_weight_mul_device_noalloc.argtypes = [P, P, C.c_int32, P, P]
         L.tinyoai_weight_free.argtypes = [P]
         _lib = L
     return _lib
@@ -156,6 +158,11 @@ class Weight:
 
     def mul_device(self, x_ptr: int, n: int, out_ptr: int, stream: int = 0) -> None:
         check(lib().tinyoai_weight_mul_device(self.h, x_ptr, n, out_ptr, stream or None))
+
+    def mul_device_noalloc(self, x_ptr: int, n: int, out_ptr: int, stream: int = 0) -> None:
+        """mul_device without any allocation (operand planes in the
+        library's per-GPU array; n * cols <= 4,194,304)."""
+        check(lib().tinyoai_weight_mul_device_noalloc(self.h, x_ptr, n, out_ptr, stream or None))
 
     def close(self):
         if self.h:
