@@ -166,6 +166,19 @@ int tinyoai_stablelm_branches_length(const tinyoai_branches *b, int32_t branch);
  * shared prefix stays. NULL is accepted. */
 int tinyoai_stablelm_branches_close(tinyoai_branches *b);
 
+/* KV snapshots (SaveCache / LoadCache, cache_file.go:49-186): the host keeps
+ * the TNYKV001 container (magic, JSON header with the model identity and
+ * tokens, SHA-256 trailer); these move its payload, cachePayload's byte
+ * order (cache_file.go:188-216): for each layer, each kv head, K then V,
+ * positions [0, n) of head_dim values, little-endian fp32 or fp16 bits as
+ * the model's KV format (`half` must match it; "KV cache precision does
+ * not match model options" otherwise). nbytes = layers * kv_heads * 2 * n *
+ * head_dim * (half ? 2 : 4). save reads positions [0, n) of the resident
+ * prefix (n <= offset); load replaces the resident cache with the payload
+ * and sets the offset to n (on a copy failure the KV is reset). */
+int tinyoai_stablelm_kv_save(tinyoai_model *m, int32_t n, int32_t half, void *payload, uint64_t nbytes);
+int tinyoai_stablelm_kv_load(tinyoai_model *m, int32_t n, int32_t half, const void *payload, uint64_t nbytes);
+
 /* Debug hooks for parity checks: copy KV head `kv_head` of `layer` for
  * positions [0, n) as fp32 [n][head_dim] (stableState keys/values,
  * kv_cache.go:91-96); record the residual stream after every layer for the

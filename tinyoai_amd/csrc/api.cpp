@@ -1568,6 +1568,54 @@ int tinyoai_stablelm_read_kv(tinyoai_model *m, int32_t layer, int32_t kv_head, i
   return TINYOAI_OK;
 }
 
+// cachePayload (cache_file.go:188-216): per layer, per kv head, K then V,
+// positions [0, n) of head_dim values in the KV format (capacity padding
+// left out). The device cache is [kv_heads][cap][hd] per layer, so each of
+// K and V of a layer is one strided copy.
+static int kv_payload(StableModel &s, int32_t n, int32_t half, void *payload, uint64_t nbytes, bool save) {
+  if (n < 0 || n > s.cfg.max_position_embeddings || (half != 0) != (s.kv_half != 0) || (n > 0 && !payload))
+    return fail(TINYOAI_EINVAL, "invalid KV payload request (n %d, float16 %d, model float16 %d)", n, half, s.kv_half);
+  const size_t esz = s.kv_half ? 2 : 4, row = (size_t)n * s.dims.hd * esz;
+  const uint64_t want = (uint64_t)s.cfg.num_hidden_layers * s.dims.kv_heads * 2 * row;
+  if (nbytes != want) return fail(TINYOAI_EINVAL, "KV payload of %d positions is %llu bytes, got %llu", n,
+                                  (unsigned long long)want, (unsigned long long)nbytes);
+  if (save && n > s.offset) return fail(TINYOAI_EINVAL, "only %d positions are resident", s.offset);
+  if (!save) {
+    if (int rc = s.busy_with_branches()) return rc;
+    if (n == 0) {
+      s.offset = 0;
+      return TINYOAI_OK;
+    }
+    if (int rc = s.ensure_kv(n)) return rc;
+  }
+  if (n == 0) return TINYOAI_OK;
+  hipStreamSynchronize(s.stream);
+  for (int l = 0; l < s.cfg.num_hidden_layers; l++)
+    for (int kind = 0; kind < 2; kind++) {
+      const size_t pitch = (size_t)s.kv[l].cap * s.dims.hd * esz;  // one head's positions on the device
+      char *dev = (char *)(kind ? s.kv[l].v : s.kv[l].k);
+      char *host = (char *)payload + ((size_t)l * s.dims.kv_heads * 2 + kind) * row;
+      hipError_t e = save ? hipMemcpy2D(host, 2 * row, dev, pitch, row, s.dims.kv_heads, hipMemcpyDeviceToHost)
+                          : hipMemcpy2D(dev, pitch, host, 2 * row, row, s.dims.kv_heads, hipMemcpyHostToDevice);
+      if (e != hipSuccess) {
+        if (!save) s.free_kv();
+        return hip_fail(e, save ? "KV save" : "KV load");
+      }
+    }
+  if (!save) s.offset = n;
+  return TINYOAI_OK;
+}
+
+int tinyoai_stablelm_kv_save(tinyoai_model *m, int32_t n, int32_t half, void *payload, uint64_t nbytes) {
+  if (!m || !m->stable) return fail(TINYOAI_EINVAL, "not a StableLM handle");
+  return kv_payload(*m->stable, n, half, payload, nbytes, true);
+}
+
+int tinyoai_stablelm_kv_load(tinyoai_model *m, int32_t n, int32_t half, const void *payload, uint64_t nbytes) {
+  if (!m || !m->stable) return fail(TINYOAI_EINVAL, "not a StableLM handle");
+  return kv_payload(*m->stable, n, half, const_cast<void *>(payload), nbytes, false);
+}
+
 int tinyoai_stablelm_trace(tinyoai_model *m, int32_t enable) {
   if (!m || !m->stable) return fail(TINYOAI_EINVAL, "not a StableLM handle");
   m->stable->tracing = enable != 0;

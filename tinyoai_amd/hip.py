@@ -19,7 +19,8 @@ EXPORTS = [
     "tinyoai_last_error", "tinyoai_stablelm_load", "tinyoai_stablelm_forward", "tinyoai_stablelm_forward_logprobs",
     "tinyoai_stablelm_set_kv_bits", "tinyoai_summarize_logits",
     "tinyoai_stablelm_limit_cache", "tinyoai_stablelm_reset", "tinyoai_stablelm_offset", "tinyoai_stablelm_close",
-    "tinyoai_stablelm_read_kv", "tinyoai_stablelm_trace", "tinyoai_stablelm_trace_read",
+    "tinyoai_stablelm_read_kv", "tinyoai_stablelm_kv_save", "tinyoai_stablelm_kv_load",
+    "tinyoai_stablelm_trace", "tinyoai_stablelm_trace_read",
     "tinyoai_stablelm_trace_read_stages", "tinyoai_stablelm_decode_timeline", "tinyoai_stablelm_set_persistent",
     "tinyoai_stablelm_set_launch", "tinyoai_stablelm_branches_open", "tinyoai_stablelm_branches_forward",
     "tinyoai_stablelm_branches_append", "tinyoai_stablelm_branches_length", "tinyoai_stablelm_branches_close",
@@ -75,6 +76,8 @@ def lib():
         L.tinyoai_stablelm_offset.argtypes = [P]
         L.tinyoai_stablelm_close.argtypes = [P]
         L.tinyoai_stablelm_read_kv.argtypes = [P, C.c_int32, C.c_int32, C.c_int32, fp, fp]
+        L.tinyoai_stablelm_kv_save.argtypes = [P, C.c_int32, C.c_int32, P, C.c_uint64]
+        L.tinyoai_stablelm_kv_load.argtypes = [P, C.c_int32, C.c_int32, P, C.c_uint64]
         L.tinyoai_stablelm_trace.argtypes = [P, C.c_int32]
         L.tinyoai_stablelm_trace_read.argtypes = [P, fp]
         L.tinyoai_stablelm_trace_read_stages.argtypes = [P, fp, fp]
@@ -251,6 +254,7 @@ class StableLMForwarder:
         h = C.c_void_p()
         check(lib().tinyoai_stablelm_load(C.byref(cfg), arr, len(names), C.byref(h)))
         self.h = h
+        self.kv_half = False
         self._logits = np.empty(self.vocab, np.float32)
 
     def forward(self, prefix: int, tokens, want_logits: bool = True) -> np.ndarray | None:
@@ -285,6 +289,7 @@ class StableLMForwarder:
     def set_kv_bits(self, bits: int) -> bool:
         cleared = C.c_int32()
         check(lib().tinyoai_stablelm_set_kv_bits(self.h, bits, C.byref(cleared)))
+        self.kv_half = bits == 16
         return bool(cleared.value)
 
     def limit_cache(self, limit: int) -> bool:
@@ -305,6 +310,22 @@ class StableLMForwarder:
         v = np.empty(n * hd, np.float32)
         check(lib().tinyoai_stablelm_read_kv(self.h, layer, kv_head, n, _fp(k), _fp(v)))
         return k.reshape(n, hd), v.reshape(n, hd)
+
+    def kv_payload_bytes(self, n: int, half: bool) -> int:
+        c = self.config
+        hd = c["hidden_size"] // c["num_attention_heads"]
+        return c["num_hidden_layers"] * c["num_key_value_heads"] * 2 * n * hd * (2 if half else 4)
+
+    def kv_save(self, n: int, half: bool) -> bytes:
+        """The cachePayload bytes of resident positions [0, n)."""
+        buf = np.empty(self.kv_payload_bytes(n, half), np.uint8)
+        check(lib().tinyoai_stablelm_kv_save(self.h, n, int(half), buf.ctypes.data, buf.size))
+        return buf.tobytes()
+
+    def kv_load(self, n: int, half: bool, payload: bytes) -> None:
+        """Replaces the resident cache with a cachePayload of n positions."""
+        buf = np.frombuffer(payload, np.uint8)
+        check(lib().tinyoai_stablelm_kv_load(self.h, n, int(half), buf.ctypes.data, buf.size))
 
     def trace(self, enable: bool = True) -> None:
         check(lib().tinyoai_stablelm_trace(self.h, int(enable)))
