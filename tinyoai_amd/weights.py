@@ -8,6 +8,7 @@ exactly these bytes and repacks them for HBM itself.
 from __future__ import annotations
 
 import json
+import math
 import os
 import struct
 from dataclasses import dataclass
@@ -248,7 +249,8 @@ def validate_stablelm_config(c: dict) -> dict:
     c.setdefault("rope_theta", 10000.0)
     c.setdefault("partial_rotary_factor", 0.25)
     rot = c["hidden_size"] // c["num_attention_heads"] * c["partial_rotary_factor"]
-    if (not c["layer_norm_eps"] > 0 or not c["rope_theta"] > 0 or not 0 < c["partial_rotary_factor"] <= 1
+    if (not c["layer_norm_eps"] > 0 or math.isinf(c["layer_norm_eps"]) or not c["rope_theta"] > 0
+            or math.isinf(c["rope_theta"]) or not 0 < c["partial_rotary_factor"] <= 1
             or rot != int(rot) or int(rot) % 2 or rot < 2):
         raise ValueError("invalid LayerNorm or partial RoPE settings")
     for k in ("bos_token_id", "eos_token_id"):
