@@ -153,13 +153,15 @@ def test_q5_1_tail_row(hip, oracle):
 
 
 @pytest.mark.parametrize("dtype", [W.Q5_1, W.Q4_K, W.Q5_K, W.Q6_K])
-@pytest.mark.parametrize("n", [1, 7, 128])
-def test_kquant_products(hip, oracle, dtype, n):
+@pytest.mark.parametrize("n,rows,cols", [(1, 37, 2560), (7, 37, 2560), (128, 37, 2560), (2, 300, 6912),
+                                         (16, 129, 2560), (17, 300, 1024), (32, 300, 6912)])
+def test_kquant_products(hip, oracle, dtype, n, rows, cols):
     """mulScratch (n = 1) and mulBatch (n > 1) of 5/6-bit matrices against
     float64 of the decoded values: 2e-5 * sum |x w| for the single row,
-    2e-4 * max(1, |y|) batched (the reference's tolerances)."""
+    2e-4 * max(1, |y|) batched (the reference's tolerances). 2 to 32 rows
+    take the few-row matrix-core product (row counts past its 128-row
+    blocks, K ranges of several staging windows)."""
     rng = np.random.default_rng(100 + n)
-    rows, cols = 37, 2560
     if dtype == W.Q5_1:
         raw, _ = _kq_golden("Q5_1")
         reps = -(-rows * cols // 32 * 24 // raw.size)

@@ -862,16 +862,22 @@ int StableModel::decode_step(int token, int pos, bool want_logits) {
 // row, whatever the chunk size (a prefix reused from the cache gives the
 // same results).
 int StableModel::project(const MatDesc &w, const float *x, int ldx, int n, float *y, int ldy, int *splits,
-                         bool rowstream) {
+                         bool rowstream, int max_splits) {
   if (splits) *splits = 1;
   if (gemm_mfma_supported(w)) {
     const bool two = gemm_planes(w) == 2;
     // K-split partial products (summed by the caller) where the output
     // tiles alone would leave most of the device idle.
-    const int ks = splits ? gemm_splits(w, n, kPrefillSplits) : 1;
+    const int ks = splits ? gemm_splits(w, n, std::max(1, std::min(max_splits, (int)kPrefillSplits))) : 1;
     if (splits) *splits = ks;
     STAGE(ST_PREFILL_GEMM, launch_split_bf16(x, ldx, w.cols, n, XH, two ? XL : nullptr, stream), "bf16 split");
     STAGE(ST_PREFILL_GEMM, launch_gemm_mfma(w, XH, two ? XL : nullptr, n, y, ldy, stream, ks), "projection");
+  } else if (rowstream && kq_rows_supported(w, n) && (reinterpret_cast<uintptr_t>(x) & 15) == 0 && ldx % 4 == 0) {
+    // A few branch rows with a 5/6-bit matrix: every quant read once for
+    // all rows, on the matrix cores; K-split partials where the caller sums.
+    const int ks = splits ? kq_rows_splits(w, max_splits) : 1;
+    if (splits) *splits = ks;
+    STAGE(ST_PREFILL_GEMM, launch_kq_rows(w, x, ldx, n, y, ldy, ks, stream), "projection");
   } else if (rowstream && n <= kRowStreamMax) {
     // A few branch rows: one row-streaming matvec per row. The vector-unit
     // GEMM costs about as much for 16 rows as for 64 (677 us for a 16-row
@@ -1150,27 +1156,39 @@ int StableModel::branch_rows(Branches &b, const int32_t *ids, const int32_t *br,
       const MatDesc wd = split_out ? w.wout2 : column_view(w.wout, down0, I);
       int rc;
       TRY_HIP(launch_layer_norm_rows(X, w.ln_w, w.ln_b, dims.eps, nc, d, H, stream), "layer_norm");
+      // Y holds chunk * win_rows floats: with few rows, K-split partials of
+      // the in-products fit within it (half each when the two groups are
+      // separate matrices); P and D hold kPrefillSplits * chunk * d.
+      const size_t ycap = (size_t)chunk * win_rows;
+      const bool few = nc <= 32;
+      const int pd_splits = (int)std::min<int64_t>(256, (int64_t)kPrefillSplits * chunk / nc);
       if (split_in) {
         StableDims da = dims, dm = dims;
         da.inter = 0;
         dm.win_q = dm.win_kv = 0;
         const int ra = w.win.rows, rm = w.win2.rows;
-        float *Ya = Y, *Ym = Y + (size_t)nc * ra;
-        if ((rc = project(w.win, H, d, nc, Ya, ra, nullptr, true)) ||
-            (rc = project(w.win2, H, d, nc, Ym, rm, nullptr, true)))
+        float *Ya = Y, *Ym = few ? Y + ycap / 2 / 4 * 4 : Y + (size_t)nc * ra;
+        int sa = 1, sm = 1;
+        if ((rc = project(w.win, H, d, nc, Ya, ra, few ? &sa : nullptr, true, (int)(ycap / 2 / ((size_t)nc * ra)))) ||
+            (rc = project(w.win2, H, d, nc, Ym, rm, few ? &sm : nullptr, true, (int)(ycap / 2 / ((size_t)nc * rm)))))
           return rc;
-        TRY_HIP(launch_in_epilogue(da, b.kv[l], Ya, ra, rope, nullptr, nc, Q, M, stream, nullptr, nullptr, d_rows),
+        TRY_HIP(launch_in_epilogue(da, b.kv[l], Ya, ra, rope, nullptr, nc, Q, M, stream, nullptr, nullptr, d_rows,
+                                   sa),
                 "in_epilogue");
-        TRY_HIP(launch_in_epilogue(dm, b.kv[l], Ym, rm, rope, nullptr, nc, Q, M, stream, nullptr, nullptr, d_rows),
+        TRY_HIP(launch_in_epilogue(dm, b.kv[l], Ym, rm, rope, nullptr, nc, Q, M, stream, nullptr, nullptr, d_rows,
+                                   sm),
                 "in_epilogue");
       } else {
-        if ((rc = project(w.win, H, d, nc, Y, win_rows, nullptr, true))) return rc;
+        int sy = 1;
+        if ((rc = project(w.win, H, d, nc, Y, win_rows, few ? &sy : nullptr, true,
+                          (int)(ycap / ((size_t)nc * win_rows)))))
+          return rc;
         TRY_HIP(launch_in_epilogue(dims, b.kv[l], Y, win_rows, rope, nullptr, nc, Q, M, stream, nullptr, nullptr,
-                                   d_rows),
+                                   d_rows, sy),
                 "in_epilogue");
       }
       int sp = 1, sd = 1;
-      if ((rc = project(wd, M, I, nc, D, d, &sd, true))) return rc;
+      if ((rc = project(wd, M, I, nc, D, d, &sd, true, pd_splits))) return rc;
       if (use_flash) {
         for (size_t k = 0; k + 1 < seg.size(); k++) {
           const int a0 = seg[k], cnt = seg[k + 1] - seg[k], j = br[r0 + a0];
@@ -1183,7 +1201,7 @@ int StableModel::branch_rows(Branches &b, const int32_t *ids, const int32_t *br,
                                         A, max_splits, stream),
                 "branch attention");
       }
-      if ((rc = project(wo, A, d, nc, P, d, &sp, true))) return rc;
+      if ((rc = project(wo, A, d, nc, P, d, &sp, true, pd_splits))) return rc;
       TRY_HIP(launch_residual(X, P, sp, D, sd, (int64_t)nc * d, stream), "residual");
     }
     // each branch's newest row of this chunk
@@ -1731,14 +1749,28 @@ int tinyoai_weight_read_values(tinyoai_weight *w, int64_t offset, int64_t n, flo
   return e == hipSuccess ? TINYOAI_OK : hip_fail(e, "readValues");
 }
 
+}  // extern "C"
+
+// The products that need no operand planes: one row (the row-streaming
+// matvec), a few rows of a 5/6-bit matrix (the few-row matrix-core
+// product) and the rest of the non-matrix-core formats (the vector-unit
+// GEMM).
+static hipError_t product_without_planes(const MatDesc &m, const float *x_dev, int n, float *out_dev,
+                                         hipStream_t st) {
+  if (n == 1) return launch_ln_matvec(m, nullptr, nullptr, 0.0, 0, x_dev, out_dev, device_cu_count() * 4, 256, st);
+  if (kq_rows_supported(m, n) && (reinterpret_cast<uintptr_t>(x_dev) & 15) == 0 && m.cols % 4 == 0)
+    return launch_kq_rows(m, x_dev, m.cols, n, out_dev, m.rows, 1, st);
+  return launch_gemm(m, x_dev, n, out_dev, st);
+}
+
+extern "C" {
+
 int tinyoai_weight_mul_device(tinyoai_weight *w, const float *x_dev, int32_t n, float *out_dev, void *stream) {
   if (!w || !x_dev || !out_dev || n <= 0) return fail(TINYOAI_EINVAL, "invalid product arguments");
   hipStream_t st = stream ? (hipStream_t)stream : w->stream;
   const MatDesc &m = w->m.desc;
   hipError_t e;
-  if (n == 1) {
-    e = launch_ln_matvec(m, nullptr, nullptr, 0.0, 0, x_dev, out_dev, device_cu_count() * 4, 256, st);
-  } else if (gemm_mfma_supported(m)) {
+  if (n > 1 && gemm_mfma_supported(m)) {
     // Batched products on the matrix cores; the plane buffer grows on demand
     // (the stream is drained before an old buffer is released).
     const size_t plane = (size_t)n * m.cols * 2, need = plane * gemm_planes(m);
@@ -1757,7 +1789,7 @@ int tinyoai_weight_mul_device(tinyoai_weight *w, const float *x_dev, int32_t n, 
     e = launch_split_bf16(x_dev, m.cols, m.cols, n, hi, lo, st);
     if (e == hipSuccess) e = launch_gemm_mfma(m, hi, lo, n, out_dev, m.rows, st);
   } else {
-    e = launch_gemm(m, x_dev, n, out_dev, st);
+    e = product_without_planes(m, x_dev, n, out_dev, st);
   }
   return e == hipSuccess ? TINYOAI_OK : hip_fail(e, "product launch");
 }
@@ -1810,16 +1842,14 @@ int tinyoai_weight_mul_device_noalloc(tinyoai_weight *w, const float *x_dev, int
   if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
   if (dev != w->device) return fail(TINYOAI_EINVAL, "the weight lives on device %d, not the current %d", w->device, dev);
   hipStream_t st = stream ? (hipStream_t)stream : w->stream;
-  if (n == 1) {
-    e = launch_ln_matvec(m, nullptr, nullptr, 0.0, 0, x_dev, out_dev, device_cu_count() * 4, 256, st);
-  } else if (gemm_mfma_supported(m)) {
+  if (n > 1 && gemm_mfma_supported(m)) {
     void *planes = nullptr;
     if (int rc = scratch_address(&planes)) return rc;
     uint16_t *hi = (uint16_t *)planes, *lo = gemm_planes(m) == 2 ? hi + (size_t)n * m.cols : nullptr;
     e = launch_split_bf16(x_dev, m.cols, m.cols, n, hi, lo, st);
     if (e == hipSuccess) e = launch_gemm_mfma(m, hi, lo, n, out_dev, m.rows, st);
   } else {
-    e = launch_gemm(m, x_dev, n, out_dev, st);
+    e = product_without_planes(m, x_dev, n, out_dev, st);
   }
   return e == hipSuccess ? TINYOAI_OK : hip_fail(e, "product launch");
 }

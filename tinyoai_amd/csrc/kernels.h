@@ -216,6 +216,16 @@ int gemm_planes(const MatDesc &w);
 int gemm_splits(const MatDesc &w, int M, int max_splits);
 hipError_t launch_gemm_mfma(const MatDesc &w, const uint16_t *xh, const uint16_t *xl, int M, float *y, int ldy,
                             hipStream_t st, int ksplit = 1);
+// Products of at most 32 rows with a 5/6-bit matrix (Q4_K, Q5_K, Q6_K,
+// Q5_1) on the matrix cores: y[M][N] (row stride ldy) = X * W^T, X fp32
+// [M][ldx] (16-byte aligned, ldx % 4 == 0). With ks > 1 the K range is cut
+// in ks parts whose products go to y + s * M * ldy, for the caller to sum;
+// kq_rows_splits: the split count that fills the device for this matrix
+// (at most max_splits).
+bool kq_rows_supported(const MatDesc &w, int M);
+int kq_rows_splits(const MatDesc &w, int max_splits);
+hipError_t launch_kq_rows(const MatDesc &w, const float *x, int ldx, int M, float *y, int ldy, int ks,
+                          hipStream_t st);
 // The fused in-projection epilogue of a matrix-core win product for M
 // tokens at positions *pos0 + j: RoPE'd q [M][heads*hd], K/V into the
 // cache, and the SiLU-gate outputs as bf16 planes mh, ml [M][inter] (and
@@ -239,10 +249,11 @@ hipError_t launch_split_bf16(const float *x, int ldx, int k, int64_t rows, uint1
 // RoPE'd q [n][heads*hd], K/V into the cache at positions pos0 + j, and
 // m [n][inter] = SiLU-gate(gate, up) (m may be null), and / or m as bf16
 // operand planes mh, ml (null: none). With rows, token j sits at position
-// rows[2j] and its K/V go to cache slot rows[2j + 1] (branch rows).
+// rows[2j] and its K/V go to cache slot rows[2j + 1] (branch rows). y may
+// hold ys partial products n * ldy floats apart, summed in order.
 hipError_t launch_in_epilogue(const StableDims &s, const KVDev &kv, const float *y, int ldy, const float *rope,
                               const int *pos0, int n, float *q, float *m, hipStream_t st, uint16_t *mh = nullptr,
-                              uint16_t *ml = nullptr, const int *rows = nullptr);
+                              uint16_t *ml = nullptr, const int *rows = nullptr, int ys = 1);
 // x = (x + p) + d elementwise (stablelm.go:375-377).
 // x = (x + sum_s p[s]) + sum_s d[s] over sp and sd partial products n
 // floats apart (K-split GEMM outputs), summed in order.

@@ -177,12 +177,14 @@ struct StableModel {
   bool decode_fused(int steps) const;
   void reset_fused();
   // y = x * W^T; with `splits`, the product may come as *splits K-split
-  // partials n * ldy floats apart (y holds kPrefillSplits of them). With
-  // rowstream, a product of at most kRowStreamMax rows in a format without
-  // a matrix-core path runs as one row-streaming matvec per row (branch
-  // steps); otherwise every chunk size takes the same arithmetic.
+  // partials n * ldy floats apart (y holds max_splits of them). With
+  // rowstream (branch steps), a product of at most 32 rows with a 5/6-bit
+  // matrix runs on the matrix cores as one few-row product, and of at most
+  // kRowStreamMax rows in another format without a matrix-core path as one
+  // row-streaming matvec per row; otherwise every chunk size takes the
+  // same arithmetic.
   int project(const MatDesc &w, const float *x, int ldx, int n, float *y, int ldy, int *splits = nullptr,
-              bool rowstream = false);
+              bool rowstream = false, int max_splits = kPrefillSplits);
   // y = X * W^T with X already in bf16 planes xh, xl (matrix-core formats).
   int project_planes(const MatDesc &w, const uint16_t *xh, const uint16_t *xl, int n, float *y, int ldy,
                      int *splits = nullptr);

@@ -93,7 +93,7 @@ __global__ __launch_bounds__(256) void gemm_simt_kernel(MatDesc w, const float *
 // suffix entry).
 __global__ void in_epilogue_kernel(StableDims s, KVDev kv, const float *y, int ldy, const float *rope,
                                    const int *pos0, int units, float *q, float *m, uint16_t *mh, uint16_t *ml,
-                                   const int *rows) {
+                                   const int *rows, int ys) {
   const int j = blockIdx.x;
   const int pos = rows ? rows[2 * j] : *pos0 + j;
   const int slot = rows ? rows[2 * j + 1] : pos;
@@ -101,8 +101,14 @@ __global__ void in_epilogue_kernel(StableDims s, KVDev kv, const float *y, int l
   const float *rope_row = rope + (int64_t)pos * s.rot;
   const int mu0 = (s.win_q + 2 * s.win_kv) / 2;
   float *qj = q + (int64_t)j * s.heads * s.hd, *mj = m ? m + (int64_t)j * s.inter : nullptr;
+  const int64_t split = (int64_t)gridDim.x * ldy;
   for (int u = threadIdx.x; u < units; u += blockDim.x) {
-    const float2 v = *reinterpret_cast<const float2 *>(yj + 2 * u);
+    float2 v = *reinterpret_cast<const float2 *>(yj + 2 * u);
+    for (int s2 = 1; s2 < ys; s2++) {
+      const float2 t = *reinterpret_cast<const float2 *>(yj + s2 * split + 2 * u);
+      v.x = __fadd_rn(v.x, t.x);
+      v.y = __fadd_rn(v.y, t.y);
+    }
     if (mh && u >= mu0) {
       const float g = s.silu ? silu_gate_llama(v.x, v.y) : silu_gate(v.x, v.y);
       if (mj) mj[u - mu0] = g;
@@ -156,11 +162,12 @@ hipError_t launch_gemm(const MatDesc &w, const float *x, int n, float *out, hipS
 
 hipError_t launch_in_epilogue(const StableDims &s, const KVDev &kv, const float *y, int ldy, const float *rope,
                               const int *pos0, int n, float *q, float *m, hipStream_t st, uint16_t *mh,
-                              uint16_t *ml, const int *rows) {
-  if (ldy % 2 || !mh != !ml || (!m && !mh) || s.win_q % 2 || (!rows && !pos0)) return hipErrorInvalidValue;
+                              uint16_t *ml, const int *rows, int ys) {
+  if (ldy % 2 || !mh != !ml || (!m && !mh) || s.win_q % 2 || (!rows && !pos0) || ys < 1)
+    return hipErrorInvalidValue;
   const int units = (s.win_q + 2 * s.win_kv + 2 * s.inter) / 2;
   hipLaunchKernelGGL(in_epilogue_kernel, dim3(n), dim3(256), 0, st, s, kv, y, ldy, rope, pos0, units, q, m, mh,
-                     ml, rows);
+                     ml, rows, ys);
   return hipGetLastError();
 }
 
