@@ -1144,7 +1144,7 @@ int StableModel::branch_rows(Branches &b, const int32_t *ids, const int32_t *br,
     const bool use_flash = flash && run > 1;
     int max_splits = 0;
     if (!use_flash) {
-      max_splits = attention_splits(max_pos, std::min(attention_steps(max_pos, dims.heads), 4));
+      max_splits = branch_attention_records(dims, pfx, max_pos, nc);
       if (int rc = b.ensure_partials(nc, max_splits)) return rc;
     }
     TRY_HIP(launch_embed(embed.desc, d_ids, nc, X, stream), "embed");

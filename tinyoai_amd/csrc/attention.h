@@ -22,6 +22,11 @@ struct AttArgs {
   KVDev sfx;
   int prefix;
   const int *rows;
+  // Branches after a shared-prefix pass (BR): positions below t_begin were
+  // attended by that pass, whose pre_splits partial records lead each
+  // (query, head) region; this launch's splits cover [t_begin, position]
+  // and write their records after them, and the last of them combines all.
+  int t_begin = 0, pre_splits = 0;
 };
 
 // Agent-scope relaxed atomic store of a partial result, and the matching
@@ -97,7 +102,8 @@ __device__ __forceinline__ void attention_block(const AttArgs &a, const int spli
   // t >= prefix at sfx_base + t * HD (t clamped to the query's position).
   const int qpos = BR ? a.rows[2 * j] : 0;
   const int64_t sfx_base = BR ? ((int64_t)kvh * a.sfx.cap + a.rows[2 * j + 1] - qpos) * HD : 0;
-  const int t0 = split * SPLIT + wave * STEPS * 16 + pl;
+  const int tb = BR ? a.t_begin : 0, pre = BR ? a.pre_splits : 0;
+  const int t0 = tb + split * SPLIT + wave * STEPS * 16 + pl;
   // Element offset of position t (clamped into its region) and whether it
   // lies in the branch cache. The base is chosen by address arithmetic on
   // the two caches (as in_pair_outputs does), not by a pointer select.
@@ -142,7 +148,7 @@ __device__ __forceinline__ void attention_block(const AttArgs &a, const int spli
   }
   const int pos = BR ? qpos : *a.pos0 + j;
   const int npos = pos + 1;
-  const int nsplit = (npos + SPLIT - 1) / SPLIT;
+  const int nsplit = (npos - tb + SPLIT - 1) / SPLIT;  // this launch's splits
   if (split >= nsplit) return;
   float score[STEPS];
   float mx = -INFINITY;
@@ -212,7 +218,7 @@ __device__ __forceinline__ void attention_block(const AttArgs &a, const int spli
   }
   const int64_t qh = (int64_t)j * s.heads + h;
   float *outp = a.out + (int64_t)j * s.heads * HD + h * HD;
-  if (nsplit == 1) {
+  if (nsplit == 1 && pre == 0) {
     for (int d = tid; d < HD; d += kThreads) {
       float acc = 0.f;
 #pragma unroll
@@ -230,7 +236,7 @@ __device__ __forceinline__ void attention_block(const AttArgs &a, const int spli
   // completed; they are agent-scope atomic loads, which read the coherence
   // point rather than a line an XCD's L2 may hold from earlier.
   float *region = a.partials + qh * partial_region(a.max_splits, HD);
-  float *part = region + split * (HD + 2);
+  float *part = region + (pre + split) * (HD + 2);
   if (tid == 0) {
     publish(part, M);
     publish(part + 1, L);
@@ -248,10 +254,12 @@ __device__ __forceinline__ void attention_block(const AttArgs &a, const int spli
              (unsigned)(nsplit - 1);
   __syncthreads();
   if (!s_last) return;
-  // Last block of this (query, head): every other split has published.
+  // Last block of this (query, head): every other split has published
+  // (and the shared-prefix records were written by an earlier launch).
   const float *base = region;
+  const int total = pre + nsplit;
   float m = -INFINITY;
-  for (int sp = tid; sp < nsplit; sp += kThreads) m = fmaxf(m, collect(base + sp * (HD + 2)));
+  for (int sp = tid; sp < total; sp += kThreads) m = fmaxf(m, collect(base + sp * (HD + 2)));
   m = wave_max(m);
   if (lane == 0) s_m[wave] = m;
   __syncthreads();
@@ -259,7 +267,7 @@ __device__ __forceinline__ void attention_block(const AttArgs &a, const int spli
 #pragma unroll
   for (int w = 1; w < kWaves; w++) m = fmaxf(m, s_m[w]);
   float lsum = 0.f;
-  for (int sp = tid; sp < nsplit; sp += kThreads) {
+  for (int sp = tid; sp < total; sp += kThreads) {
     const float e = expf(collect(base + sp * (HD + 2)) - m);
     s_e[sp] = e;
     lsum = fmaf(collect(base + sp * (HD + 2) + 1), e, lsum);
@@ -278,7 +286,7 @@ __device__ __forceinline__ void attention_block(const AttArgs &a, const int spli
   for (int d = tid; d < HD; d += kThreads) {
     float acc = 0.f;
 #pragma unroll 8
-    for (int sp = 0; sp < nsplit; sp++) acc = fmaf(collect(base + sp * (HD + 2) + 2 + d), s_e[sp], acc);
+    for (int sp = 0; sp < total; sp++) acc = fmaf(collect(base + sp * (HD + 2) + 2 + d), s_e[sp], acc);
     outp[d] = acc / Ltot;
   }
   if (tid == 0) __hip_atomic_store(&a.counters[qh], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

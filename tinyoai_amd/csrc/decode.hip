@@ -176,14 +176,49 @@ hipError_t launch_attention(const StableDims &s, const KVDev &kv, const float *q
   return hipErrorInvalidValue;
 }
 
+namespace {
+// The shared-prefix pass applies: a prefix, a head width the matrix-core
+// attention takes, and at most one query tile of it.
+bool branch_shared(const StableDims &s, int prefix, int nq) {
+  return prefix > 0 && nq <= 128 && flash_prefill_supported(s.hd);
+}
+// Suffix blocks' positions / 64 and their count after a shared pass.
+void suffix_splits(const StableDims &s, int prefix, int max_pos, int &steps, int &splits) {
+  const int span = max_pos - prefix + 1;
+  steps = std::min(attention_steps(span - 1, s.heads), 4);
+  splits = attention_splits(span - 1, steps);
+}
+}  // namespace
+
+int branch_attention_records(const StableDims &s, int prefix, int max_pos, int nq) {
+  if (branch_shared(s, prefix, nq)) {
+    int steps, splits;
+    suffix_splits(s, prefix, max_pos, steps, splits);
+    return shared_prefix_splits(prefix) + splits;
+  }
+  return attention_splits(max_pos, std::min(attention_steps(max_pos, s.heads), 4));
+}
+
 hipError_t launch_branch_attention(const StableDims &s, const KVDev &kv, const KVDev &sfx, int prefix,
                                    const float *q, const int *rows, int nq, int max_pos, float *partials,
                                    unsigned *counters, float *out, int max_splits, hipStream_t st) {
-  const int steps = std::min(attention_steps(max_pos, s.heads), 4), splits = attention_splits(max_pos, steps);
-  if (splits > 512 || splits > max_splits || prefix < 0 || prefix > kv.cap || nq < 1 || !rows ||
-      kv.half != sfx.half)
+  if (prefix < 0 || prefix > kv.cap || nq < 1 || !rows || kv.half != sfx.half || max_pos < prefix)
     return hipErrorInvalidValue;
+  int steps = std::min(attention_steps(max_pos, s.heads), 4), splits = attention_splits(max_pos, steps);
   AttArgs a{s, kv, q, nullptr, max_splits, partials, counters, out, sfx, prefix, rows};
+  if (branch_shared(s, prefix, nq)) {
+    // One matrix-core pass reads the prefix once for every query and leaves
+    // its records first in each region; the suffix splits follow.
+    suffix_splits(s, prefix, max_pos, steps, splits);
+    a.t_begin = prefix;
+    a.pre_splits = shared_prefix_splits(prefix);
+    if (a.pre_splits + splits > 512 || a.pre_splits + splits > max_splits) return hipErrorInvalidValue;
+    const hipError_t e =
+        launch_shared_prefix_attention(s, kv, prefix, q, nq, partials, partial_region(max_splits, s.hd), st);
+    if (e != hipSuccess) return e;
+  } else if (splits > 512 || splits > max_splits) {
+    return hipErrorInvalidValue;
+  }
   switch (s.hd) {
     case 64: return kv.half ? launch_branch_attention_hd<64, true>(a, nq, splits, steps, st)
                             : launch_branch_attention_hd<64, false>(a, nq, splits, steps, st);

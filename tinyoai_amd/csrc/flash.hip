@@ -29,6 +29,15 @@ struct FlashArgs {
   // sfx_slot0 + (t - prefix) of the branch cache sfx.
   KVDev sfx;
   int prefix, sfx_slot0;
+  // Shared prefix (SH instances): block x attends cache positions
+  // [x * split_keys, min(prefix, (x + 1) * split_keys)) for all n queries
+  // (branch rows, each past the prefix, so no causal mask) and writes the
+  // unnormalised record {m, l, o[hd]} (m in natural-log units, o and l
+  // weighted by exp(score - m)) at partials + (j * heads + h) * region +
+  // x * (hd + 2), the split-K decode attention's partial layout.
+  float *partials;
+  int64_t region;
+  int split_keys;
 };
 
 // x = hi + lo to about 2^-22. The empty asm pins x as one fp32 value: when x
@@ -54,10 +63,11 @@ __device__ __forceinline__ void split_half(float x, _Float16 &hi, _Float16 &lo) 
 //   read with the same key order. O rows are queries ((v / 4) * 8 + g * 4 +
 //   v % 4), so each lane fetches the softmax factors of its 16 rows.
 constexpr int kQ32 = 128;  // queries per block
+constexpr int kSharedKeys = 256;  // cache positions per block of the shared-prefix pass
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-template <int HD, bool HALF, bool BR>
+template <int HD, bool HALF, bool BR, bool SH = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void flash32_kernel(FlashArgs a) {
   static_assert(HD % 16 == 0, "head width in 16-dim k-steps");
   constexpr int KS = HD / 16;         // k-steps over head dims
@@ -77,17 +87,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h = blockIdx.y, kvh = h / (s.heads / s.kv_heads);
-  const int p0 = *a.pos0;
+  const int p0 = SH ? 0 : *a.pos0;
   // Query tiles run in reverse order for the second half of the heads:
   // workgroups k and k + grid / 2 share a CU when the grid fills two per
   // CU, and the reversal pairs a long causal range with a short one there.
-  const int qt = blockIdx.y >= (gridDim.y + 1) / 2 ? gridDim.x - 1 - blockIdx.x : blockIdx.x;
+  // SH: one query tile; blockIdx.x is the key range.
+  const int qt = SH ? 0 : blockIdx.y >= (gridDim.y + 1) / 2 ? gridDim.x - 1 - blockIdx.x : blockIdx.x;
   const int qb = qt * kQ32;                          // first query of the block
   const int qw = qb + wave * 32;                     // first query of the wave
   const int col = lane & 31, g = lane >> 5;          // S^T column (query) / B row, lane group
   const int myq = qw + col;                          // this lane's query as an S^T column
-  const int myq_pos = p0 + min(myq, a.n - 1);
-  const int last_pos = p0 + min(qb + kQ32, a.n) - 1;  // causal bound of the block
+  const int k_lo = SH ? blockIdx.x * a.split_keys : 0;
+  const int k_hi = SH ? min(a.prefix, k_lo + a.split_keys) : 0;
+  // the last key a query sees (SH: every key of the range)
+  const int myq_pos = SH ? k_hi - 1 : p0 + min(myq, a.n - 1);
+  const int last_pos = SH ? k_hi - 1 : p0 + min(qb + kQ32, a.n) - 1;  // causal bound of the block
   const float qscale = kLog2e / s.att_scale;          // Q pre-scaled: scores come out in base 2
 
   // Q^T as B operands: column = query, k = dims 16 * step + 8 * g .. + 8.
@@ -124,7 +138,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
   const int64_t head_base = (int64_t)kvh * a.kv.cap * HD;
   // BR: the branch's suffix, position t >= prefix at element sfx_base + (t - prefix) * HD.
   const int64_t sfx_base = BR ? ((int64_t)kvh * a.sfx.cap + a.sfx_slot0) * HD : 0;
-  const int ntiles = last_pos / kTile + 1;
+  const int ntiles = last_pos / kTile + 1, tile0 = k_lo / kTile;
   // fp16 cache: a tile is loaded into registers while the previous one is
   // computed. Buffer loads read zeros past the block's last position.
   constexpr int KC = kTile * (HD / 8), KPT = (KC + 255) / 256;  // 16-byte K pieces
@@ -194,8 +208,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
       }
     }
   };
-  if constexpr (HALF) hload(0);
-  for (int tile = 0; tile < ntiles; tile++) {
+  if constexpr (HALF) hload(tile0 * kTile);
+  for (int tile = tile0; tile < ntiles; tile++) {
     const int t0 = tile * kTile;
     __syncthreads();
     if constexpr (HALF) {
@@ -232,7 +246,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
       }
     }
     __syncthreads();
-    if (qw >= a.n || t0 > p0 + qw + 31) continue;  // nothing for this wave in this tile
+    if (qw >= a.n || (!SH && t0 > p0 + qw + 31)) continue;  // nothing for this wave in this tile
 
     // ---- S^T - ref (two 32-key halves; the Q hi/lo parts chain into one accumulator)
     f32x16 sc[2];
@@ -253,7 +267,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
           sc[kh] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kl, qh[k], sc[kh], 0, 0, 0);
         }
       }
-    if (t0 + kTile - 1 > p0 + qw) {  // tile reaches past the wave's first query: causal mask
+    if (SH ? t0 + kTile > k_hi : t0 + kTile - 1 > p0 + qw) {  // tile reaches past a visible key: mask
 #pragma unroll
       for (int kh = 0; kh < 2; kh++)
 #pragma unroll
@@ -265,15 +279,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
     for (int kh = 0; kh < 2; kh++)
 #pragma unroll
       for (int v = 0; v < 16; v++) tmax = fmaxf(tmax, sc[kh][v]);
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));  // finite: key 0 of tile 0 is visible to every query
-    if (tile == 0 || __ballot(tmax > kRescale)) {
-      const float d = tile == 0 ? tmax : fmaxf(tmax, 0.f);  // reference shift of this lane's query
+    // finite: the first key of the first tile is visible to every query
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    if (tile == tile0 || __ballot(tmax > kRescale)) {
+      const float d = tile == tile0 ? tmax : fmaxf(tmax, 0.f);  // reference shift of this lane's query
       ref += d;
 #pragma unroll
       for (int kh = 0; kh < 2; kh++)
 #pragma unroll
         for (int v = 0; v < 16; v++) sc[kh][v] -= d;
-      if (tile > 0) {
+      if (tile > tile0) {
         const float corr = __builtin_amdgcn_exp2f(-d);
         if constexpr (!ONES) l_run *= corr;
 #pragma unroll
@@ -322,6 +337,28 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
       }
   }
   // ---- normalise and store: lane holds queries (v / 4) * 8 + g * 4 + v % 4, dim t * 32 + col
+  if constexpr (SH) {
+    constexpr float kLn2 = 0.6931471805599453f;
+#pragma unroll
+    for (int v = 0; v < 16; v++) {
+      const int src = (v >> 2) * 8 + g * 4 + (v & 3);
+      const float lq = ONES ? __shfl(o[DT - 1][v], g * 32 + HD % 32, 64) : __shfl(l_run, src, 64);
+      const float mq = __shfl(ref, src, 64) * kLn2;
+      const int qi = qw + src;
+      if (qi >= a.n) continue;
+      float *part = a.partials + ((int64_t)qi * s.heads + h) * a.region + (int64_t)blockIdx.x * (HD + 2);
+      if (col == 0) {
+        part[0] = mq;
+        part[1] = lq;
+      }
+#pragma unroll
+      for (int t = 0; t < DT; t++) {
+        const int dd = t * 32 + col;
+        if (dd < HD) part[2 + dd] = o[t][v];
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int v = 0; v < 16; v++) {
     const float lq = ONES ? __shfl(o[DT - 1][v], g * 32 + HD % 32, 64)
@@ -356,16 +393,44 @@ hipError_t flash32_dispatch(const FlashArgs &a, bool br, hipStream_t st) {
   return br ? flash32_launch<HD, true>(a, st) : flash32_launch<HD, false>(a, st);
 }
 
+template <int HD>
+hipError_t flash32_shared(const FlashArgs &a, int splits, hipStream_t st) {
+  dim3 grid(splits, a.s.heads);
+  if (a.kv.half)
+    hipLaunchKernelGGL((flash32_kernel<HD, true, false, true>), grid, dim3(256), 0, st, a);
+  else
+    hipLaunchKernelGGL((flash32_kernel<HD, false, false, true>), grid, dim3(256), 0, st, a);
+  return hipGetLastError();
+}
+
 }  // namespace
 
 bool flash_prefill_supported(int hd) { return hd == 64 || hd == 80 || hd == 96 || hd == 128; }
+
+int shared_prefix_splits(int prefix) { return (prefix + kSharedKeys - 1) / kSharedKeys; }
+
+hipError_t launch_shared_prefix_attention(const StableDims &s, const KVDev &kv, int prefix, const float *q, int nq,
+                                          float *partials, int64_t region, hipStream_t st) {
+  if (nq < 1 || nq > kQ32 || prefix < 1 || prefix > kv.cap || !flash_prefill_supported(s.hd) ||
+      region < (int64_t)shared_prefix_splits(prefix) * (s.hd + 2))
+    return hipErrorInvalidValue;
+  FlashArgs a{s, kv, q, nullptr, nq, nullptr, nullptr, nullptr, KVDev{}, prefix, 0, partials, region, kSharedKeys};
+  const int splits = shared_prefix_splits(prefix);
+  switch (s.hd) {
+    case 64: return flash32_shared<64>(a, splits, st);
+    case 80: return flash32_shared<80>(a, splits, st);
+    case 96: return flash32_shared<96>(a, splits, st);
+    case 128: return flash32_shared<128>(a, splits, st);
+  }
+  return hipErrorInvalidValue;
+}
 
 hipError_t launch_flash_prefill(const StableDims &s, const KVDev &kv, const float *q, const int *pos0, int n,
                                 float *out, hipStream_t st, uint16_t *oh, uint16_t *ol, const KVDev *sfx, int prefix,
                                 int sfx_slot0) {
   if (!oh != !ol || (!out && !oh) || n < 1) return hipErrorInvalidValue;
   if (sfx && (sfx->half != kv.half || prefix < 0 || prefix > kv.cap || sfx_slot0 < 0)) return hipErrorInvalidValue;
-  FlashArgs a{s, kv, q, pos0, n, out, oh, ol, sfx ? *sfx : KVDev{}, prefix, sfx_slot0};
+  FlashArgs a{s, kv, q, pos0, n, out, oh, ol, sfx ? *sfx : KVDev{}, prefix, sfx_slot0, nullptr, 0, 0};
   const bool br = sfx != nullptr;
   switch (s.hd) {
     case 64: return flash32_dispatch<64>(a, br, st);

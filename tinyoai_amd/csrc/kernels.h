@@ -124,9 +124,22 @@ hipError_t launch_attention(const StableDims &s, const KVDev &kv, const float *q
 // - rows[2j] + t of sfx (the branch's suffix, stored contiguously). Every
 // query's position is at most max_pos. partials holds nq * heads *
 // partial_region(max_splits, hd) floats. Head widths 8, 64 and 80.
+// With a prefix, at most 128 queries and a matrix-core head width, the
+// prefix is attended once for all queries (launch_shared_prefix_attention)
+// and the suffix splits continue from its records. max_splits must be at
+// least branch_attention_records(s, prefix, max_pos, nq).
 hipError_t launch_branch_attention(const StableDims &s, const KVDev &kv, const KVDev &sfx, int prefix,
                                    const float *q, const int *rows, int nq, int max_pos, float *partials,
                                    unsigned *counters, float *out, int max_splits, hipStream_t st);
+int branch_attention_records(const StableDims &s, int prefix, int max_pos, int nq);
+// The shared-prefix pass on the matrix cores: nq <= 128 queries q
+// [nq][heads*hd], every one past `prefix`, against cache positions
+// [0, prefix) of kv, in blocks of 256 positions; block x writes the record
+// {m, l, o[hd]} (natural-log max, unnormalised sums) of (query j, head h)
+// at partials + (j * heads + h) * region + x * (hd + 2).
+int shared_prefix_splits(int prefix);
+hipError_t launch_shared_prefix_attention(const StableDims &s, const KVDev &kv, int prefix, const float *q, int nq,
+                                          float *partials, int64_t region, hipStream_t st);
 // Causal attention of n prefill queries on the matrix cores (head widths
 // 64, 80, 96, 128): q [n][heads*hd] at positions pos0 + j -> out.
 bool flash_prefill_supported(int hd);

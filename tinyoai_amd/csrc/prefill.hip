@@ -102,7 +102,8 @@ __global__ void in_epilogue_kernel(StableDims s, KVDev kv, const float *y, int l
   const int mu0 = (s.win_q + 2 * s.win_kv) / 2;
   float *qj = q + (int64_t)j * s.heads * s.hd, *mj = m ? m + (int64_t)j * s.inter : nullptr;
   const int64_t split = (int64_t)gridDim.x * ldy;
-  for (int u = threadIdx.x; u < units; u += blockDim.x) {
+  // blockIdx.y takes every gridDim.y-th group of blockDim.x units
+  for (int u = blockIdx.y * blockDim.x + threadIdx.x; u < units; u += gridDim.y * blockDim.x) {
     float2 v = *reinterpret_cast<const float2 *>(yj + 2 * u);
     for (int s2 = 1; s2 < ys; s2++) {
       const float2 t = *reinterpret_cast<const float2 *>(yj + s2 * split + 2 * u);
@@ -166,8 +167,10 @@ hipError_t launch_in_epilogue(const StableDims &s, const KVDev &kv, const float 
   if (ldy % 2 || !mh != !ml || (!m && !mh) || s.win_q % 2 || (!rows && !pos0) || ys < 1)
     return hipErrorInvalidValue;
   const int units = (s.win_q + 2 * s.win_kv + 2 * s.inter) / 2;
-  hipLaunchKernelGGL(in_epilogue_kernel, dim3(n), dim3(256), 0, st, s, kv, y, ldy, rope, pos0, units, q, m, mh,
-                     ml, rows, ys);
+  // a few tokens: spread each token's units over several blocks
+  const int per_token = std::max(1, std::min((units + 255) / 256, 2048 / std::max(1, n)));
+  hipLaunchKernelGGL(in_epilogue_kernel, dim3(n, per_token), dim3(256), 0, st, s, kv, y, ldy, rope, pos0, units, q,
+                     m, mh, ml, rows, ys);
   return hipGetLastError();
 }
 
