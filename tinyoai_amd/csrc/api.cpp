@@ -872,12 +872,14 @@ int StableModel::project(const MatDesc &w, const float *x, int ldx, int n, float
     if (splits) *splits = ks;
     STAGE(ST_PREFILL_GEMM, launch_split_bf16(x, ldx, w.cols, n, XH, two ? XL : nullptr, stream), "bf16 split");
     STAGE(ST_PREFILL_GEMM, launch_gemm_mfma(w, XH, two ? XL : nullptr, n, y, ldy, stream, ks), "projection");
-  } else if (rowstream && kq_rows_supported(w, n) && (reinterpret_cast<uintptr_t>(x) & 15) == 0 && ldx % 4 == 0) {
+  } else if (rowstream && kq_rows_supported(w, n) && (reinterpret_cast<uintptr_t>(x) & 15) == 0 && ldx % 4 == 0 &&
+             kq_rows_stage_bytes(w.cols, n) <= (size_t)chunk * std::max(dims.d, dims.inter) * 2) {
     // A few branch rows with a 5/6-bit matrix: every quant read once for
-    // all rows, on the matrix cores; K-split partials where the caller sums.
+    // all rows, on the matrix cores (X staged in the XH workspace); K-split
+    // partials where the caller sums.
     const int ks = splits ? kq_rows_splits(w, max_splits) : 1;
     if (splits) *splits = ks;
-    STAGE(ST_PREFILL_GEMM, launch_kq_rows(w, x, ldx, n, y, ldy, ks, stream), "projection");
+    STAGE(ST_PREFILL_GEMM, launch_kq_rows(w, x, ldx, n, y, ldy, ks, XH, stream), "projection");
   } else if (rowstream && n <= kRowStreamMax) {
     // A few branch rows: one row-streaming matvec per row. The vector-unit
     // GEMM costs about as much for 16 rows as for 64 (677 us for a 16-row
@@ -1751,15 +1753,27 @@ int tinyoai_weight_read_values(tinyoai_weight *w, int64_t offset, int64_t n, flo
 
 }  // extern "C"
 
-// The products that need no operand planes: one row (the row-streaming
-// matvec), a few rows of a 5/6-bit matrix (the few-row matrix-core
-// product) and the rest of the non-matrix-core formats (the vector-unit
-// GEMM).
-static hipError_t product_without_planes(const MatDesc &m, const float *x_dev, int n, float *out_dev,
-                                         hipStream_t st) {
-  if (n == 1) return launch_ln_matvec(m, nullptr, nullptr, 0.0, 0, x_dev, out_dev, device_cu_count() * 4, 256, st);
+// Bytes of operand scratch a product of n rows needs: bf16 planes of the
+// matrix-core GEMM, the staged X of the few-row 5/6-bit product, or none
+// (one row: the row-streaming matvec; other formats: the vector-unit GEMM).
+static size_t product_scratch(const MatDesc &m, const float *x_dev, int n) {
+  if (n == 1) return 0;
+  if (gemm_mfma_supported(m)) return (size_t)n * m.cols * 2 * gemm_planes(m);
   if (kq_rows_supported(m, n) && (reinterpret_cast<uintptr_t>(x_dev) & 15) == 0 && m.cols % 4 == 0)
-    return launch_kq_rows(m, x_dev, m.cols, n, out_dev, m.rows, 1, st);
+    return kq_rows_stage_bytes(m.cols, n);
+  return 0;
+}
+
+// out = x * W^T with `scratch` of product_scratch bytes.
+static hipError_t product_launch(const MatDesc &m, const float *x_dev, int n, float *out_dev, void *scratch,
+                                 hipStream_t st) {
+  if (n == 1) return launch_ln_matvec(m, nullptr, nullptr, 0.0, 0, x_dev, out_dev, device_cu_count() * 4, 256, st);
+  if (gemm_mfma_supported(m)) {
+    uint16_t *hi = (uint16_t *)scratch, *lo = gemm_planes(m) == 2 ? hi + (size_t)n * m.cols : nullptr;
+    hipError_t e = launch_split_bf16(x_dev, m.cols, m.cols, n, hi, lo, st);
+    return e == hipSuccess ? launch_gemm_mfma(m, hi, lo, n, out_dev, m.rows, st) : e;
+  }
+  if (product_scratch(m, x_dev, n)) return launch_kq_rows(m, x_dev, m.cols, n, out_dev, m.rows, 1, scratch, st);
   return launch_gemm(m, x_dev, n, out_dev, st);
 }
 
@@ -1769,28 +1783,21 @@ int tinyoai_weight_mul_device(tinyoai_weight *w, const float *x_dev, int32_t n, 
   if (!w || !x_dev || !out_dev || n <= 0) return fail(TINYOAI_EINVAL, "invalid product arguments");
   hipStream_t st = stream ? (hipStream_t)stream : w->stream;
   const MatDesc &m = w->m.desc;
-  hipError_t e;
-  if (n > 1 && gemm_mfma_supported(m)) {
-    // Batched products on the matrix cores; the plane buffer grows on demand
-    // (the stream is drained before an old buffer is released).
-    const size_t plane = (size_t)n * m.cols * 2, need = plane * gemm_planes(m);
-    if (need > w->planes_bytes) {
-      if (w->planes) {
-        hipStreamSynchronize(st);
-        hipFree(w->planes);
-        w->planes = nullptr;
-        w->planes_bytes = 0;
-      }
-      e = hipMalloc(&w->planes, need);
-      if (e != hipSuccess) return fail(TINYOAI_ENOMEM, "hipMalloc(%zu): %s", need, hipGetErrorString(e));
-      w->planes_bytes = need;
+  // The operand scratch grows on demand (the stream is drained before an
+  // old buffer is released).
+  const size_t need = product_scratch(m, x_dev, n);
+  if (need > w->planes_bytes) {
+    if (w->planes) {
+      hipStreamSynchronize(st);
+      hipFree(w->planes);
+      w->planes = nullptr;
+      w->planes_bytes = 0;
     }
-    uint16_t *hi = w->planes, *lo = gemm_planes(m) == 2 ? w->planes + plane / 2 : nullptr;
-    e = launch_split_bf16(x_dev, m.cols, m.cols, n, hi, lo, st);
-    if (e == hipSuccess) e = launch_gemm_mfma(m, hi, lo, n, out_dev, m.rows, st);
-  } else {
-    e = product_without_planes(m, x_dev, n, out_dev, st);
+    hipError_t e = hipMalloc(&w->planes, need);
+    if (e != hipSuccess) return fail(TINYOAI_ENOMEM, "hipMalloc(%zu): %s", need, hipGetErrorString(e));
+    w->planes_bytes = need;
   }
+  const hipError_t e = product_launch(m, x_dev, n, out_dev, w->planes, st);
   return e == hipSuccess ? TINYOAI_OK : hip_fail(e, "product launch");
 }
 
@@ -1842,15 +1849,14 @@ int tinyoai_weight_mul_device_noalloc(tinyoai_weight *w, const float *x_dev, int
   if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
   if (dev != w->device) return fail(TINYOAI_EINVAL, "the weight lives on device %d, not the current %d", w->device, dev);
   hipStream_t st = stream ? (hipStream_t)stream : w->stream;
-  if (n > 1 && gemm_mfma_supported(m)) {
-    void *planes = nullptr;
+  void *planes = nullptr;
+  if (product_scratch(m, x_dev, n)) {
+    if (product_scratch(m, x_dev, n) > sizeof(scratch))
+      return fail(TINYOAI_EINVAL, "product of %d x %d needs more than the no-allocation limit of %zu bytes", n, m.cols,
+                  sizeof(scratch));
     if (int rc = scratch_address(&planes)) return rc;
-    uint16_t *hi = (uint16_t *)planes, *lo = gemm_planes(m) == 2 ? hi + (size_t)n * m.cols : nullptr;
-    e = launch_split_bf16(x_dev, m.cols, m.cols, n, hi, lo, st);
-    if (e == hipSuccess) e = launch_gemm_mfma(m, hi, lo, n, out_dev, m.rows, st);
-  } else {
-    e = product_without_planes(m, x_dev, n, out_dev, st);
   }
+  e = product_launch(m, x_dev, n, out_dev, planes, st);
   return e == hipSuccess ? TINYOAI_OK : hip_fail(e, "product launch");
 }
 

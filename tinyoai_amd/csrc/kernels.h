@@ -231,13 +231,15 @@ hipError_t launch_gemm_mfma(const MatDesc &w, const uint16_t *xh, const uint16_t
                             hipStream_t st, int ksplit = 1);
 // Products of at most 32 rows with a 5/6-bit matrix (Q4_K, Q5_K, Q6_K,
 // Q5_1) on the matrix cores: y[M][N] (row stride ldy) = X * W^T, X fp32
-// [M][ldx] (16-byte aligned, ldx % 4 == 0). With ks > 1 the K range is cut
-// in ks parts whose products go to y + s * M * ldy, for the caller to sum;
-// kq_rows_splits: the split count that fills the device for this matrix
-// (at most max_splits).
+// [M][ldx] (16-byte aligned, ldx % 4 == 0), converted first into `stage`
+// (16-byte aligned device memory of kq_rows_stage_bytes(K, M) bytes). With
+// ks > 1 the K range is cut in ks parts whose products go to
+// y + s * M * ldy, for the caller to sum; kq_rows_splits: the split count
+// that fills the device for this matrix (at most max_splits).
 bool kq_rows_supported(const MatDesc &w, int M);
+size_t kq_rows_stage_bytes(int K, int M);
 int kq_rows_splits(const MatDesc &w, int max_splits);
-hipError_t launch_kq_rows(const MatDesc &w, const float *x, int ldx, int M, float *y, int ldy, int ks,
+hipError_t launch_kq_rows(const MatDesc &w, const float *x, int ldx, int M, float *y, int ldy, int ks, void *stage,
                           hipStream_t st);
 // The fused in-projection epilogue of a matrix-core win product for M
 // tokens at positions *pos0 + j: RoPE'd q [M][heads*hd], K/V into the

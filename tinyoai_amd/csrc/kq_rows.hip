@@ -6,21 +6,25 @@
 // or (q - 32) * a (Q6_K), with a small integer q and constants a, b shared
 // by a sub-block of 32 values (16 for Q6_K) (decodeKBlock,
 // quant_k.go:31-86). q is exact in bf16, so each sub-block's products run
-// on the matrix cores unscaled,
+// on the matrix cores unscaled (Q6_K: over q, with -32 * xsum added),
 //   t[m][n] = sum over the sub-block of x[m][k] * q[n][k],
 // with x as three bf16 planes (hi + mid + lo: 24 significant bits, as
 // fp32 holds), and are added to fp32 accumulators as
 // acc += a * t - b * xsum, xsum[m] being the sub-block's sum of x (of
 // hi + mid + lo, the values the products saw).
 //
-// A block of 4 waves takes 128 matrix rows (32 a wave, two 16-row tiles)
-// over one range of K, in windows of up to 16 chunks (8 with 32 rows):
-// the window's X is staged in LDS as bf16 planes (with the sub-block
-// sums), then each wave streams its rows' quants straight from HBM and
+// X is converted once per product (kq_stage_kernel) into staged chunks:
+// three bf16 planes of each row's 32 values and three sums per row (whole
+// chunk, first and second 16 values). A block of 4 waves takes 128 matrix
+// rows (32 a wave, two 16-row tiles) over one range of K, a batch of 8
+// chunks (a K-quant super-block) at a time: the batch's staged chunks are
+// copied into LDS, each wave reads its rows' quants straight from HBM and
 // forms v_mfma_f32_16x16x32_bf16 products per 32-value chunk (two
-// v_mfma_f32_16x16x16_bf16, one per 16-value sub-block, for Q6_K). K
-// ranges (splits) write separate partial outputs, split s at
-// y + s * M * ldy, which the consumer sums.
+// v_mfma_f32_16x16x16_bf16, one per 16-value sub-block, for Q6_K). The
+// batches run as a software pipeline: the next batch's quants and staged
+// chunks are in flight while one is computed. K ranges (splits) write
+// separate partial outputs, split s at y + s * M * ldy, which the
+// consumer sums.
 //
 // Staged value order: a 16x16x32 product gives lane group g = lane / 16
 // the 8 positions 8g..8g+7 of each chunk. The quants of a chunk sit as
@@ -43,93 +47,146 @@ namespace {
 constexpr int kThreads = 256, kWaveRows = 32, kBlockRows = 128;
 constexpr uint32_t kNone = 0x80000000u;  // past every plane (each < 2 GiB)
 constexpr int kPlanes = 3;
+constexpr int kWindow = 8;  // chunks per batch (a K-quant super-block)
 
-// Chunks (32 values) of one K range a block can stage: 16 * MT rows,
-// three bf16 planes and a float sum per chunk, within 50 KB of LDS.
+// A staged chunk of R = 16 * MT rows: planes [3][R][32] bf16 (in the
+// permuted value order), then sums [3][R] floats.
 template <int MT>
-constexpr int max_chunks() { return MT == 1 ? 16 : 8; }
+constexpr int chunk_bytes() { return 16 * MT * (kPlanes * 64 + 3 * 4); }
+// Two window buffers in LDS: one is computed while the next is filled.
 template <int MT>
-constexpr size_t lds_bytes() { return (size_t)max_chunks<MT>() * 16 * MT * (kPlanes * 64 + 4); }
+constexpr size_t lds_bytes() { return (size_t)2 * kWindow * chunk_bytes<MT>(); }
 
 struct KqArgs {
   MatDesc w;
-  const float *x;
-  int ldx, M;
+  const uint8_t *stage;  // staged chunks of X, chunk c at c * chunk_bytes
+  int M;
   float *y;
   int ldy, ks;
 };
+
+// x [M][K] -> staged chunks. Item i: group of 4 values i % 8 of row
+// (i / 8) % R and chunk i / (8 R); a chunk's 8 groups are 8 consecutive
+// lanes, which form the sums by fixed-order shuffles.
+template <int MT>
+__global__ __launch_bounds__(256) void kq_stage_kernel(const float *x, int ldx, int M, int K, uint8_t *stage) {
+  constexpr int R = 16 * MT;
+  const int nch = K / 32;
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= R * nch * 8) return;  // whole groups of 8: R * nch * 8 and the block are multiples of 8
+  const int gq = i & 7, row = (i >> 3) % R, c = (i >> 3) / R;
+  float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (row < M) v = *reinterpret_cast<const float4 *>(x + (int64_t)row * ldx + c * 32 + 4 * gq);
+  const float vv[4] = {v.x, v.y, v.z, v.w};
+  uint32_t pl[kPlanes][2];
+  float s = 0.f;
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    float r = vv[e], part = 0.f;
+#pragma unroll
+    for (int p = 0; p < kPlanes; p++) {
+      const __bf16 h = (__bf16)r;
+      const uint32_t bits = __builtin_bit_cast(uint16_t, h);
+      pl[p][e / 2] = e % 2 ? pl[p][e / 2] | bits << 16 : bits;
+      part += (float)h;
+      r -= (float)h;
+    }
+    s += part;
+  }
+  s += __shfl_xor(s, 1, 64);
+  s += __shfl_xor(s, 2, 64);
+  const float s32 = s + __shfl_xor(s, 4, 64);
+  uint8_t *cb = stage + (size_t)c * chunk_bytes<MT>();
+  const int pos = gq < 4 ? 8 * gq : 8 * (gq - 4) + 4;
+#pragma unroll
+  for (int p = 0; p < kPlanes; p++)
+    *reinterpret_cast<uint2 *>(cb + ((p * R + row) * 32 + pos) * 2) = make_uint2(pl[p][0], pl[p][1]);
+  float *sums = reinterpret_cast<float *>(cb + kPlanes * R * 64);
+  if (gq == 0) {
+    sums[row] = s32;
+    sums[R + row] = s;
+  } else if (gq == 4) {
+    sums[2 * R + row] = s;
+  }
+}
 
 // bf16 bits of an integer-valued float with |v| <= 256 (exact).
 __device__ __forceinline__ uint32_t pack_exact(float a, float b) {
   return (__float_as_uint(a) >> 16) | (__float_as_uint(b) & 0xFFFF0000u);
 }
+// The four bytes of v as exact bf16 (byte conversions, then the upper
+// halves). A biased form (bits 0x4300 | q = 128 + q) would save the
+// conversions but put 128 * xsum into every product, whose fp32 rounding
+// then exceeds the reference's tolerance where a sum nearly cancels.
+__device__ __forceinline__ uint2 exact_bf16(uint32_t v) {
+  // opaque to the compiler, which would otherwise fold the callers' masks
+  // into a bit-field extract per value instead of v_cvt_f32_ubyteN
+  asm volatile("" : "+v"(v));
+  return make_uint2(pack_exact((float)(v & 255u), (float)((v >> 8) & 255u)),
+                    pack_exact((float)((v >> 16) & 255u), (float)(v >> 24)));
+}
+// Bit e of a 4-bit x to bit 0 of byte e.
+__device__ __forceinline__ uint32_t spread1(uint32_t x) {
+  uint32_t t = x | (x << 7);
+  t |= t << 14;
+  return t & 0x01010101u;
+}
+// Bits 2e..2e+1 of an 8-bit x to bits 0-1 of byte e.
+__device__ __forceinline__ uint32_t spread2(uint32_t x) {
+  uint32_t t = x | (x << 6);
+  t |= t << 12;
+  return t & 0x03030303u;
+}
+
+// One batch (8 chunks) of a wave's two 16-row tiles, as loaded.
+struct Quants {
+  uint32_t qv[2][8], hv[2][8][2], m1[2][8];
+  uint4 mt[2];
+  uint32_t d6[2];
+};
 
 template <int F, int MT>
 __global__ __launch_bounds__(kThreads) void kq_rows_kernel(KqArgs g) {
   extern __shared__ __align__(16) uint8_t lds[];
-  constexpr int R = 16 * MT;  // staged rows
+  constexpr int R = 16 * MT;
+  constexpr int CB = chunk_bytes<MT>();
+  constexpr int kCopy = (kWindow * CB / 16 + kThreads - 1) / kThreads;  // 16-byte pieces per thread
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const MatDesc w = g.w;
   const int N = w.rows, K = w.cols, nch = (K + 31) / 32;
   const int NB = (N + kBlockRows - 1) / kBlockRows;
   const int nb = blockIdx.x % NB, split = blockIdx.x / NB;
-  // K range of the split, in whole batches of 8 chunks (a super-block)
+  // K range of the split, in whole batches of 8 chunks
   const int batches = (nch + 7) / 8;
   const int b_lo = (int)((int64_t)batches * split / g.ks), b_hi = (int)((int64_t)batches * (split + 1) / g.ks);
   const int c_lo = b_lo * 8, c_hi = min(nch, b_hi * 8);
   float *y = g.y + (int64_t)split * g.M * g.ldy;
-  constexpr int kWindow = max_chunks<MT>();
 
-  uint16_t *xs = reinterpret_cast<uint16_t *>(lds);
-  // ---- stage X rows [0, M) x chunks [w0, w0 + cn): planes [3][cn][R][32] bf16, sums [cn][R]
-  auto stage = [&](int w0, int cn, float *xsum) {
-    const int items = R * cn * 8;  // float4 groups: (row, chunk, group of 4 values)
-    for (int i = tid; i < items; i += kThreads) {
-      const int row = i / (cn * 8), q = i % (cn * 8), cl = q >> 3, gq = q & 7;
-      const int k = (w0 + cl) * 32 + 4 * gq;
-      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (row < g.M) {
-        const float *p = g.x + (int64_t)row * g.ldx + k;
-        if (k + 3 < K) {
-          v = *reinterpret_cast<const float4 *>(p);
-        } else {
-          v.x = k < K ? p[0] : 0.f;
-          v.y = k + 1 < K ? p[1] : 0.f;
-          v.z = k + 2 < K ? p[2] : 0.f;
-          v.w = k + 3 < K ? p[3] : 0.f;
-        }
-      }
-      const float vv[4] = {v.x, v.y, v.z, v.w};
-      uint32_t pl[kPlanes][2];
-      float s = 0.f;
+  // ---- staged chunks [c0, min(c0 + 8, c_hi)) -> window buffer buf.
+  // Buffer loads: pieces past the staged chunks read zeros (stored into
+  // window slots no product reads), so no lane branches.
+  const __amdgpu_buffer_rsrc_t rs = plane_rsrc(g.stage, (int64_t)nch * CB);
+  auto load_x = [&](uint4 (&xr)[kCopy], int c0) {
+    const uint32_t end = (uint32_t)min(c0 + kWindow, c_hi) * CB;
 #pragma unroll
-      for (int e = 0; e < 4; e++) {
-        float r = vv[e], part = 0.f;
+    for (int j = 0; j < kCopy; j++) {
+      const uint32_t off = (uint32_t)c0 * CB + (uint32_t)(tid + j * kThreads) * 16;
+      const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)(off < end ? off : kNone), 0, 0);
+      xr[j] = make_uint4(v.x, v.y, v.z, v.w);
+    }
+  };
+  auto store_x = [&](const uint4 (&xr)[kCopy], int buf) {
+    uint4 *dst = reinterpret_cast<uint4 *>(lds + (size_t)buf * kWindow * CB);
 #pragma unroll
-        for (int p = 0; p < kPlanes; p++) {
-          const __bf16 h = (__bf16)r;
-          const uint32_t bits = __builtin_bit_cast(uint16_t, h);
-          pl[p][e / 2] = e % 2 ? pl[p][e / 2] | bits << 16 : bits;
-          part += (float)h;
-          r -= (float)h;
-        }
-        s += part;
-      }
-      // the chunk's 8 groups are 8 consecutive lanes (items and the block
-      // are multiples of 8): a fixed-order sum
-      s += __shfl_xor(s, 1, 64);
-      s += __shfl_xor(s, 2, 64);
-      s += __shfl_xor(s, 4, 64);
-      const int pos = gq < 4 ? 8 * gq : 8 * (gq - 4) + 4;
-      const size_t at = ((size_t)cl * R + row) * 32 + pos;
-#pragma unroll
-      for (int p = 0; p < kPlanes; p++)
-        *reinterpret_cast<uint2 *>(xs + (size_t)p * cn * R * 32 + at) = make_uint2(pl[p][0], pl[p][1]);
-      if (gq == 0) xsum[cl * R + row] = s;
+    for (int j = 0; j < kCopy; j++) {
+      const int i = tid + j * kThreads;
+      if (kWindow * CB % (16 * kThreads) == 0 || i < kWindow * CB / 16) dst[i] = xr[j];
     }
   };
 
-  // ---- stream the wave's 32 rows over the range
+  // ---- the wave's 32 matrix rows: lane = 16 * g4 + r16 holds row r16 of
+  // each 16-row tile and (after the transpose below) bytes 4 * g4 .. + 3 of
+  // every chunk
   const int g4 = lane >> 4, r16 = lane & 15;
   const int row0 = nb * kBlockRows + wave * kWaveRows + r16;
   const __amdgpu_buffer_rsrc_t rv = plane_rsrc(w.vals, (int64_t)N * w.vstride);
@@ -140,7 +197,7 @@ __global__ __launch_bounds__(kThreads) void kq_rows_kernel(KqArgs g) {
   for (int t = 0; t < 2; t++) {
     const int row = row0 + 16 * t;
     const bool in = row < N;
-    voff[t] = in ? (uint32_t)(row * w.vstride + 4 * g4) : kNone;
+    voff[t] = in ? (uint32_t)(row * w.vstride + 16 * g4) : kNone;
     moff[t] = in ? (uint32_t)(row * w.mstride) : kNone;
     hoff[t] = in ? (uint32_t)(row * w.hstride) : kNone;
   }
@@ -150,124 +207,216 @@ __global__ __launch_bounds__(kThreads) void kq_rows_kernel(KqArgs g) {
 #pragma unroll
     for (int t = 0; t < 2; t++) acc[m][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  for (int w0 = c_lo; w0 < c_hi; w0 += kWindow) {
-    const int cn = min(kWindow, c_hi - w0), w1 = w0 + cn;
-    float *xsum = reinterpret_cast<float *>(lds + (size_t)kPlanes * cn * R * 64);
-    if (w0 > c_lo) __syncthreads();  // the previous window's reads are done
-    stage(w0, cn, xsum);
-    __syncthreads();
-    for (int c0 = w0; c0 < w1; c0 += 8) {
-      // the batch's loads: 8 chunks x 2 tiles of quant bytes, high bits and
-      // block constants
-      uint32_t qv[2][8], hv[2][8][2];
-      uint4 mt[2];
-      uint32_t d6[2];
+  // Quant bytes: the four lanes of a row read 64 contiguous bytes per load
+  // (lane group g: chunks c0 + g and c0 + 4 + g), then a 4 x 4 transpose
+  // of dwords across the groups (v_permlane32_swap, v_permlane16_swap)
+  // gives group g dword g of every chunk. High bits and block constants
+  // are read whole by the four lanes of a row (one cache line).
+  auto load_q = [&](Quants &q, int c0) {
 #pragma unroll
-      for (int t = 0; t < 2; t++) {
+    for (int t = 0; t < 2; t++) {
+#pragma unroll
+      for (int i = 0; i < 2; i++) {
+        const bool ok = voff[t] != kNone && c0 + 4 * i + g4 < c_hi;
+        const u32x4 q4 = __builtin_amdgcn_raw_buffer_load_b128(
+            rv, (int)(ok ? voff[t] + (uint32_t)(c0 + 4 * i) * 16 : kNone), 0, 0);
+        uint32_t d[4] = {q4.x, q4.y, q4.z, q4.w};
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+          const u32x2 r = __builtin_amdgcn_permlane32_swap(d[j], d[j + 2], false, false);
+          d[j] = r.x;
+          d[j + 2] = r.y;
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j += 2) {
+          const u32x2 r = __builtin_amdgcn_permlane16_swap(d[j], d[j + 1], false, false);
+          d[j] = r.x;
+          d[j + 1] = r.y;
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++) q.qv[t][4 * i + j] = d[j];
+      }
+      const bool rok = voff[t] != kNone;
+      if constexpr (F == FMT_Q5_K || F == FMT_Q5_1) {
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+          const u32x4 h4 = __builtin_amdgcn_raw_buffer_load_b128(
+              rh, (int)(rok ? hoff[t] + (uint32_t)(c0 + 4 * i) * 4 : kNone), 0, 0);
+          q.hv[t][4 * i][0] = h4.x;
+          q.hv[t][4 * i + 1][0] = h4.y;
+          q.hv[t][4 * i + 2][0] = h4.z;
+          q.hv[t][4 * i + 3][0] = h4.w;
+        }
+      }
+      if constexpr (F == FMT_Q6_K) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const u32x4 h4 = __builtin_amdgcn_raw_buffer_load_b128(
+              rh, (int)(rok ? hoff[t] + (uint32_t)(c0 + 2 * i) * 8 : kNone), 0, 0);
+          q.hv[t][2 * i][0] = h4.x;
+          q.hv[t][2 * i][1] = h4.y;
+          q.hv[t][2 * i + 1][0] = h4.z;
+          q.hv[t][2 * i + 1][1] = h4.w;
+        }
+      }
+      if constexpr (F == FMT_Q5_1) {
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+          const u32x4 m4 = __builtin_amdgcn_raw_buffer_load_b128(
+              rm, (int)(rok ? moff[t] + (uint32_t)(c0 + 4 * i) * 4 : kNone), 0, 0);
+          q.m1[t][4 * i] = m4.x;
+          q.m1[t][4 * i + 1] = m4.y;
+          q.m1[t][4 * i + 2] = m4.z;
+          q.m1[t][4 * i + 3] = m4.w;
+        }
+      }
+      if constexpr (F == FMT_Q4_K || F == FMT_Q5_K) {
+        const u32x4 m4 = __builtin_amdgcn_raw_buffer_load_b128(
+            rm, (int)(rok ? moff[t] + (uint32_t)(c0 / 8) * 16 : kNone), 0, 0);
+        q.mt[t] = make_uint4(m4.x, m4.y, m4.z, m4.w);
+      } else if constexpr (F == FMT_Q6_K) {
+        const uint32_t mo = rok ? moff[t] + (uint32_t)(c0 / 8) * 32 : kNone;
+        const u32x4 m4 = __builtin_amdgcn_raw_buffer_load_b128(rm, (int)mo, 0, 0);
+        q.mt[t] = make_uint4(m4.x, m4.y, m4.z, m4.w);
+        q.d6[t] = __builtin_amdgcn_raw_buffer_load_b32(rm, (int)(mo == kNone ? kNone : mo + 16), 0, 0);
+      }
+    }
+  };
+
+  auto compute = [&](const Quants &q, int c0, int buf) {
+    const uint8_t *wb = lds + (size_t)buf * kWindow * CB;
+    // Sub-block constants of the batch: acc += a * t - c * xsum per 32
+    // values (c = b for q a - b, -b for q a + b), or a * (t - 32 xsum) per
+    // 16 values (Q6_K, t over q). Values and roundings as decodeKBlock's
+    // (a = d * scale, b = dmin * min); the 6-bit scales and mins of
+    // Q4_K / Q5_K are unpacked four at a time (quant_k.go:69-77).
+    float ka[2][16], kc[2][8];
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+      if constexpr (F == FMT_Q6_K) {
+        const float d = half_to_float((uint16_t)q.d6[t]);
+        const uint32_t sw[4] = {q.mt[t].x, q.mt[t].y, q.mt[t].z, q.mt[t].w};
+#pragma unroll
+        for (int i = 0; i < 16; i++) ka[t][i] = __fmul_rn(d, (float)(int8_t)(sw[i / 4] >> (8 * (i % 4))));
+      } else if constexpr (F == FMT_Q5_1) {
 #pragma unroll
         for (int u = 0; u < 8; u++) {
-          const uint32_t off = voff[t] == kNone || c0 + u >= c_hi ? kNone : voff[t] + (uint32_t)(c0 + u) * 16;
-          qv[t][u] = __builtin_amdgcn_raw_buffer_load_b32(rv, (int)off, 0, 0);
-          if constexpr (F == FMT_Q5_K || F == FMT_Q5_1) {
-            const uint32_t ho = hoff[t] == kNone || c0 + u >= c_hi ? kNone : hoff[t] + (uint32_t)(c0 + u) * 4;
-            hv[t][u][0] = __builtin_amdgcn_raw_buffer_load_b32(rh, (int)ho, 0, 0);
-          } else if constexpr (F == FMT_Q6_K) {
-            const uint32_t ho = hoff[t] == kNone || c0 + u >= c_hi ? kNone : hoff[t] + (uint32_t)(c0 + u) * 8;
-            const u32x2 h2 = __builtin_amdgcn_raw_buffer_load_b64(rh, (int)ho, 0, 0);
-            hv[t][u][0] = h2.x;
-            hv[t][u][1] = h2.y;
-          }
+          ka[t][u] = half_to_float((uint16_t)q.m1[t][u]);
+          kc[t][u] = -half_to_float((uint16_t)(q.m1[t][u] >> 16));
         }
-        if constexpr (F == FMT_Q4_K || F == FMT_Q5_K) {
-          const u32x4 m4 = __builtin_amdgcn_raw_buffer_load_b128(rm, (int)(moff[t] == kNone ? kNone : moff[t] + (uint32_t)(c0 / 8) * 16), 0, 0);
-          mt[t] = make_uint4(m4.x, m4.y, m4.z, m4.w);
-        } else if constexpr (F == FMT_Q6_K) {
-          const uint32_t mo = moff[t] == kNone ? kNone : moff[t] + (uint32_t)(c0 / 8) * 32;
-          const u32x4 m4 = __builtin_amdgcn_raw_buffer_load_b128(rm, (int)mo, 0, 0);
-          mt[t] = make_uint4(m4.x, m4.y, m4.z, m4.w);
-          d6[t] = __builtin_amdgcn_raw_buffer_load_b32(rm, (int)(mo == kNone ? kNone : mo + 16), 0, 0);
+      } else {
+        const float d = half_to_float((uint16_t)q.mt[t].x), dmin = half_to_float((uint16_t)(q.mt[t].x >> 16));
+        const uint32_t y0 = q.mt[t].y, z0 = q.mt[t].z, w0 = q.mt[t].w;
+        const uint32_t sc[2] = {y0 & 0x3F3F3F3Fu, (w0 & 0x0F0F0F0Fu) | ((y0 >> 2) & 0x30303030u)};
+        const uint32_t mn[2] = {z0 & 0x3F3F3F3Fu, ((w0 >> 4) & 0x0F0F0F0Fu) | ((z0 >> 2) & 0x30303030u)};
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+          ka[t][u] = __fmul_rn(d, (float)((sc[u / 4] >> (8 * (u % 4))) & 255u));
+          kc[t][u] = __fmul_rn(dmin, (float)((mn[u / 4] >> (8 * (u % 4))) & 255u));
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      if (c0 + u >= c_hi) break;
+      const uint8_t *cb = wb + u * CB;
+      // A operands: the staged rows of this chunk, every plane
+      bf16x8 a[kPlanes][MT];
+#pragma unroll
+      for (int p = 0; p < kPlanes; p++)
+#pragma unroll
+        for (int m = 0; m < MT; m++)
+          a[p][m] = *reinterpret_cast<const bf16x8 *>(cb + ((p * R + 16 * m + r16) * 32 + 8 * g4) * 2);
+      const float *sums = reinterpret_cast<const float *>(cb + kPlanes * R * 64);
+      f32x4 xsm[MT][2];
+#pragma unroll
+      for (int m = 0; m < MT; m++) {
+        if constexpr (F == FMT_Q6_K) {
+          xsm[m][0] = *reinterpret_cast<const f32x4 *>(sums + R + 16 * m + 4 * g4);
+          xsm[m][1] = *reinterpret_cast<const f32x4 *>(sums + 2 * R + 16 * m + 4 * g4);
+        } else {
+          xsm[m][0] = *reinterpret_cast<const f32x4 *>(sums + 16 * m + 4 * g4);
         }
       }
 #pragma unroll
-      for (int u = 0; u < 8; u++) {
-        const int c = c0 + u;
-        if (c >= c_hi) break;
-        const int cl = c - w0;
-        // A operands: the staged rows of this chunk, every plane
-        bf16x8 a[kPlanes][MT];
-#pragma unroll
-        for (int p = 0; p < kPlanes; p++)
-#pragma unroll
-          for (int m = 0; m < MT; m++)
-            a[p][m] = *reinterpret_cast<const bf16x8 *>(xs + (size_t)p * cn * R * 32 +
-                                                       ((size_t)cl * R + 16 * m + r16) * 32 + 8 * g4);
-        f32x4 xsm[MT];
-        if constexpr (F != FMT_Q6_K) {
-#pragma unroll
-          for (int m = 0; m < MT; m++) xsm[m] = *reinterpret_cast<const f32x4 *>(xsum + cl * R + 16 * m + 4 * g4);
+      for (int t = 0; t < 2; t++) {
+        // the lane's 8 quants: values 4g..4g+3 (lo bytes) and 16+4g.. (hi)
+        const uint32_t b = q.qv[t][u];
+        uint32_t lo = b & 0x0F0F0F0Fu, hi = (b >> 4) & 0x0F0F0F0Fu;
+        if constexpr (F == FMT_Q5_K || F == FMT_Q5_1) {
+          lo |= spread1((q.hv[t][u][0] >> (4 * g4)) & 15u) << 4;
+          hi |= spread1((q.hv[t][u][0] >> (16 + 4 * g4)) & 15u) << 4;
+        } else if constexpr (F == FMT_Q6_K) {
+          lo |= spread2((q.hv[t][u][0] >> (8 * g4)) & 255u) << 4;
+          hi |= spread2((q.hv[t][u][1] >> (8 * g4)) & 255u) << 4;
         }
+        const uint2 bl = exact_bf16(lo), bh = exact_bf16(hi);
+        const uint4 bw = make_uint4(bl.x, bl.y, bh.x, bh.y);
+        if constexpr (F == FMT_Q6_K) {
+          const bf16x4 b0 = __builtin_bit_cast(bf16x4, make_uint2(bw.x, bw.y));
+          const bf16x4 b1 = __builtin_bit_cast(bf16x4, make_uint2(bw.z, bw.w));
 #pragma unroll
-        for (int t = 0; t < 2; t++) {
-          // the lane's 8 quants: values 4g..4g+3 (low nibbles), 16+4g.. (high)
-          const uint32_t b = qv[t][u];
-          float qf[8];
+          for (int m = 0; m < MT; m++) {
+            f32x4 t0 = {0.f, 0.f, 0.f, 0.f}, t1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int e = 0; e < 4; e++) {
-            int ql = (b >> (8 * e)) & 15, qh = (b >> (8 * e + 4)) & 15;
-            if constexpr (F == FMT_Q5_K || F == FMT_Q5_1) {
-              ql |= ((hv[t][u][0] >> (4 * g4 + e)) & 1) << 4;
-              qh |= ((hv[t][u][0] >> (16 + 4 * g4 + e)) & 1) << 4;
-            } else if constexpr (F == FMT_Q6_K) {
-              ql |= ((hv[t][u][0] >> (8 * g4 + 2 * e)) & 3) << 4;
-              qh |= ((hv[t][u][1] >> (8 * g4 + 2 * e)) & 3) << 4;
-              ql -= 32;
-              qh -= 32;
+            for (int p = 0; p < kPlanes; p++) {
+              const uint4 av = __builtin_bit_cast(uint4, a[p][m]);
+              t0 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(bf16x4, make_uint2(av.x, av.y)), b0,
+                                                             t0, 0, 0, 0);
+              t1 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(bf16x4, make_uint2(av.z, av.w)), b1,
+                                                             t1, 0, 0, 0);
             }
-            qf[e] = (float)ql;
-            qf[4 + e] = (float)qh;
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+              acc[m][t][v] = fmaf(ka[t][2 * u], fmaf(-32.f, xsm[m][0][v], t0[v]), acc[m][t][v]);
+              acc[m][t][v] = fmaf(ka[t][2 * u + 1], fmaf(-32.f, xsm[m][1][v], t1[v]), acc[m][t][v]);
+            }
           }
-          const uint4 bw = make_uint4(pack_exact(qf[0], qf[1]), pack_exact(qf[2], qf[3]), pack_exact(qf[4], qf[5]),
-                                      pack_exact(qf[6], qf[7]));
-          KConst k;
-          if constexpr (F == FMT_Q5_1) {
-            const uint32_t mo = moff[t] == kNone ? kNone : moff[t] + (uint32_t)c * 4;
-            const uint32_t m1 = __builtin_amdgcn_raw_buffer_load_b32(rm, (int)mo, 0, 0);
-            k = kquant_const<F>(make_uint4(m1, 0, 0, 0), 0, c);
-          } else {
-            k = kquant_const<F>(mt[t], (uint16_t)d6[t], c);
-          }
-          if constexpr (F == FMT_Q6_K) {
-            const bf16x4 b0 = __builtin_bit_cast(bf16x4, make_uint2(bw.x, bw.y));
-            const bf16x4 b1 = __builtin_bit_cast(bf16x4, make_uint2(bw.z, bw.w));
+        } else {
+          const bf16x8 bb = __builtin_bit_cast(bf16x8, bw);
 #pragma unroll
-            for (int m = 0; m < MT; m++) {
-              f32x4 t0 = {0.f, 0.f, 0.f, 0.f}, t1 = {0.f, 0.f, 0.f, 0.f};
+          for (int m = 0; m < MT; m++) {
+            f32x4 tt = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-              for (int p = 0; p < kPlanes; p++) {
-                const uint4 av = __builtin_bit_cast(uint4, a[p][m]);
-                t0 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(bf16x4, make_uint2(av.x, av.y)), b0,
-                                                               t0, 0, 0, 0);
-                t1 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(bf16x4, make_uint2(av.z, av.w)), b1,
-                                                               t1, 0, 0, 0);
-              }
+            for (int p = 0; p < kPlanes; p++) tt = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[p][m], bb, tt, 0, 0, 0);
 #pragma unroll
-              for (int v = 0; v < 4; v++) acc[m][t][v] = fmaf(k.a2, t1[v], fmaf(k.a, t0[v], acc[m][t][v]));
-            }
-          } else {
-            const bf16x8 bb = __builtin_bit_cast(bf16x8, bw);
-#pragma unroll
-            for (int m = 0; m < MT; m++) {
-              f32x4 tt = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-              for (int p = 0; p < kPlanes; p++) tt = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[p][m], bb, tt, 0, 0, 0);
-              const float bs = F == FMT_Q5_1 ? k.b : -k.b;
-#pragma unroll
-              for (int v = 0; v < 4; v++) acc[m][t][v] = fmaf(k.a, tt[v], fmaf(bs, xsm[m][v], acc[m][t][v]));
-            }
+            for (int v = 0; v < 4; v++)
+              acc[m][t][v] = fmaf(ka[t][u], tt[v], fmaf(-kc[t][u], xsm[m][0][v], acc[m][t][v]));
           }
         }
       }
     }
+  };
+
+  // Software pipeline over the batches: the next batch's quants and
+  // staged chunks are loaded while this one is computed, then the chunks
+  // go to the other window buffer before the barrier that ends the step.
+  Quants qa, qb;
+  uint4 xr[kCopy];
+  if (c_lo < c_hi) {
+    load_q(qa, c_lo);
+    load_x(xr, c_lo);
+    store_x(xr, 0);
+  }
+  __syncthreads();
+  for (int c0 = c_lo; c0 < c_hi; c0 += 16) {
+    const bool more = c0 + 8 < c_hi;
+    if (more) {
+      load_q(qb, c0 + 8);
+      load_x(xr, c0 + 8);
+    }
+    compute(qa, c0, 0);
+    if (more) store_x(xr, 1);
+    __syncthreads();
+    if (!more) break;
+    const bool more2 = c0 + 16 < c_hi;
+    if (more2) {
+      load_q(qa, c0 + 16);
+      load_x(xr, c0 + 16);
+    }
+    compute(qb, c0 + 8, 1);
+    if (more2) store_x(xr, 0);
+    __syncthreads();
   }
   // lane holds rows 4 * g4 + v of X tile m against matrix row row0 + 16 t
 #pragma unroll
@@ -278,8 +427,8 @@ __global__ __launch_bounds__(kThreads) void kq_rows_kernel(KqArgs g) {
     for (int m = 0; m < MT; m++)
 #pragma unroll
       for (int v = 0; v < 4; v++) {
-        const int xr = 16 * m + 4 * g4 + v;
-        if (xr < g.M) y[(int64_t)xr * g.ldy + n] = acc[m][t][v];
+        const int xrow = 16 * m + 4 * g4 + v;
+        if (xrow < g.M) y[(int64_t)xrow * g.ldy + n] = acc[m][t][v];
       }
   }
 }
@@ -306,6 +455,13 @@ hipError_t kq_dispatch(const KqArgs &g, hipStream_t st) {
   }
 }
 
+template <int MT>
+hipError_t kq_stage(const float *x, int ldx, int M, int K, uint8_t *stage, hipStream_t st) {
+  const int items = 16 * MT * (K / 32) * 8;
+  hipLaunchKernelGGL((kq_stage_kernel<MT>), dim3((items + 255) / 256), dim3(256), 0, st, x, ldx, M, K, stage);
+  return hipGetLastError();
+}
+
 }  // namespace
 
 bool kq_rows_supported(const MatDesc &w, int M) {
@@ -313,17 +469,27 @@ bool kq_rows_supported(const MatDesc &w, int M) {
          (w.fmt == FMT_Q5_1 || w.cols % 256 == 0);
 }
 
+size_t kq_rows_stage_bytes(int K, int M) {
+  return (size_t)(K / 32) * (M <= 16 ? chunk_bytes<1>() : chunk_bytes<2>());
+}
+
 int kq_rows_splits(const MatDesc &w, int max_splits) {
   const int NB = (w.rows + kBlockRows - 1) / kBlockRows, batches = (w.cols / 32 + 7) / 8;
-  // about two blocks per CU, at least one super-block per split
+  // about two blocks per CU, at least one batch per split
   return std::max(1, std::min({(512 + NB - 1) / NB, batches, max_splits}));
 }
 
-hipError_t launch_kq_rows(const MatDesc &w, const float *x, int ldx, int M, float *y, int ldy, int ks,
+hipError_t launch_kq_rows(const MatDesc &w, const float *x, int ldx, int M, float *y, int ldy, int ks, void *stage,
                           hipStream_t st) {
-  if (!kq_rows_supported(w, M) || ks < 1 || ks > (w.cols / 32 + 7) / 8 || ldx < w.cols ||
-      ldy < w.rows || (reinterpret_cast<uintptr_t>(x) & 15) || (ldx & 3))
+  if (!kq_rows_supported(w, M) || ks < 1 || ks > (w.cols / 32 + 7) / 8 || ldx < w.cols || ldy < w.rows ||
+      (reinterpret_cast<uintptr_t>(x) & 15) || (ldx & 3) || !stage || (reinterpret_cast<uintptr_t>(stage) & 15))
     return hipErrorInvalidValue;
-  KqArgs g{w, x, ldx, M, y, ldy, ks};
-  return M <= 16 ? kq_dispatch<1>(g, st) : kq_dispatch<2>(g, st);
+  KqArgs g{w, static_cast<const uint8_t *>(stage), M, y, ldy, ks};
+  uint8_t *sb = static_cast<uint8_t *>(stage);
+  if (M <= 16) {
+    const hipError_t e = kq_stage<1>(x, ldx, M, w.cols, sb, st);
+    return e != hipSuccess ? e : kq_dispatch<1>(g, st);
+  }
+  const hipError_t e = kq_stage<2>(x, ldx, M, w.cols, sb, st);
+  return e != hipSuccess ? e : kq_dispatch<2>(g, st);
 }
