@@ -862,8 +862,10 @@ int StableModel::decode_step(int token, int pos, bool want_logits) {
 // row, whatever the chunk size (a prefix reused from the cache gives the
 // same results).
 int StableModel::project(const MatDesc &w, const float *x, int ldx, int n, float *y, int ldy, int *splits,
-                         bool rowstream, int max_splits) {
+                         bool rowstream, int max_splits, bool *staged) {
   if (splits) *splits = 1;
+  const bool reuse = staged && *staged;
+  if (staged) *staged = false;
   if (gemm_mfma_supported(w)) {
     const bool two = gemm_planes(w) == 2;
     // K-split partial products (summed by the caller) where the output
@@ -879,7 +881,8 @@ int StableModel::project(const MatDesc &w, const float *x, int ldx, int n, float
     // partials where the caller sums.
     const int ks = splits ? kq_rows_splits(w, max_splits) : 1;
     if (splits) *splits = ks;
-    STAGE(ST_PREFILL_GEMM, launch_kq_rows(w, x, ldx, n, y, ldy, ks, XH, stream), "projection");
+    STAGE(ST_PREFILL_GEMM, launch_kq_rows(w, x, ldx, n, y, ldy, ks, XH, stream, reuse), "projection");
+    if (staged) *staged = true;
   } else if (rowstream && n <= kRowStreamMax) {
     // A few branch rows: one row-streaming matvec per row. The vector-unit
     // GEMM costs about as much for 16 rows as for 64 (677 us for a 16-row
@@ -1171,8 +1174,11 @@ int StableModel::branch_rows(Branches &b, const int32_t *ids, const int32_t *br,
         const int ra = w.win.rows, rm = w.win2.rows;
         float *Ya = Y, *Ym = few ? Y + ycap / 2 / 4 * 4 : Y + (size_t)nc * ra;
         int sa = 1, sm = 1;
-        if ((rc = project(w.win, H, d, nc, Ya, ra, few ? &sa : nullptr, true, (int)(ycap / 2 / ((size_t)nc * ra)))) ||
-            (rc = project(w.win2, H, d, nc, Ym, rm, few ? &sm : nullptr, true, (int)(ycap / 2 / ((size_t)nc * rm)))))
+        bool staged = false;  // H staged by the first product serves the second
+        if ((rc = project(w.win, H, d, nc, Ya, ra, few ? &sa : nullptr, true, (int)(ycap / 2 / ((size_t)nc * ra)),
+                          &staged)) ||
+            (rc = project(w.win2, H, d, nc, Ym, rm, few ? &sm : nullptr, true, (int)(ycap / 2 / ((size_t)nc * rm)),
+                          &staged)))
           return rc;
         TRY_HIP(launch_in_epilogue(da, b.kv[l], Ya, ra, rope, nullptr, nc, Q, M, stream, nullptr, nullptr, d_rows,
                                    sa),

@@ -475,21 +475,22 @@ size_t kq_rows_stage_bytes(int K, int M) {
 
 int kq_rows_splits(const MatDesc &w, int max_splits) {
   const int NB = (w.rows + kBlockRows - 1) / kBlockRows, batches = (w.cols / 32 + 7) / 8;
-  // about two blocks per CU, at least one batch per split
-  return std::max(1, std::min({(512 + NB - 1) / NB, batches, max_splits}));
+  // about 320 blocks (measured best at M = 16 for 2560-13824 rows: more
+  // splits only add partial sums), at least one batch per split
+  return std::max(1, std::min({(320 + NB - 1) / NB, batches, max_splits}));
 }
 
 hipError_t launch_kq_rows(const MatDesc &w, const float *x, int ldx, int M, float *y, int ldy, int ks, void *stage,
-                          hipStream_t st) {
+                          hipStream_t st, bool staged) {
   if (!kq_rows_supported(w, M) || ks < 1 || ks > (w.cols / 32 + 7) / 8 || ldx < w.cols || ldy < w.rows ||
       (reinterpret_cast<uintptr_t>(x) & 15) || (ldx & 3) || !stage || (reinterpret_cast<uintptr_t>(stage) & 15))
     return hipErrorInvalidValue;
   KqArgs g{w, static_cast<const uint8_t *>(stage), M, y, ldy, ks};
   uint8_t *sb = static_cast<uint8_t *>(stage);
   if (M <= 16) {
-    const hipError_t e = kq_stage<1>(x, ldx, M, w.cols, sb, st);
+    const hipError_t e = staged ? hipSuccess : kq_stage<1>(x, ldx, M, w.cols, sb, st);
     return e != hipSuccess ? e : kq_dispatch<1>(g, st);
   }
-  const hipError_t e = kq_stage<2>(x, ldx, M, w.cols, sb, st);
+  const hipError_t e = staged ? hipSuccess : kq_stage<2>(x, ldx, M, w.cols, sb, st);
   return e != hipSuccess ? e : kq_dispatch<2>(g, st);
 }

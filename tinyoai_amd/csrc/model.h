@@ -183,8 +183,10 @@ struct StableModel {
   // kRowStreamMax rows in another format without a matrix-core path as one
   // row-streaming matvec per row; otherwise every chunk size takes the
   // same arithmetic.
+  // staged (few-row 5/6-bit products): in, the workspace already holds
+  // this x from the previous product of the same shape; out, it does now.
   int project(const MatDesc &w, const float *x, int ldx, int n, float *y, int ldy, int *splits = nullptr,
-              bool rowstream = false, int max_splits = kPrefillSplits);
+              bool rowstream = false, int max_splits = kPrefillSplits, bool *staged = nullptr);
   // y = X * W^T with X already in bf16 planes xh, xl (matrix-core formats).
   int project_planes(const MatDesc &w, const uint16_t *xh, const uint16_t *xl, int n, float *y, int ldy,
                      int *splits = nullptr);
