@@ -211,6 +211,14 @@ def long_context_workload(args):
         if i + 1 < T:
             logits = fwd.forward(n + i, [toks[-1]])
     decode_s = time.perf_counter() - t0
+    # the same prefill on the bf16 path (BF16 products with bf16
+    # activations; an option, off by default)
+    fwd.set_launch("bf16_activations", 1, 0)
+    t0 = time.perf_counter()
+    fwd.forward(0, prompt, want_logits=False)
+    fwd.forward(0, prompt, want_logits=False)
+    torch.cuda.synchronize()
+    bf16_prefill_s = (time.perf_counter() - t0) / 2
     fwd.close()
     d, I, L = config["hidden_size"], config["intermediate_size"], config["num_hidden_layers"]
     hd, H = d // config["num_attention_heads"], config["num_attention_heads"]
@@ -226,6 +234,8 @@ def long_context_workload(args):
             "layers": L, "prefill_s": round(prefill_s, 4), "prefill_tok_s": round(n / prefill_s, 1),
             "prefill_useful_tflops": round(tflops, 1), "prefill_flops": flops,
             "prefill_mfma_frac_bf16": round(tflops / 2500.0, 4),
+            "prefill_s_bf16_activations": round(bf16_prefill_s, 4),
+            "prefill_mfma_frac_bf16_activations": round(flops / bf16_prefill_s / 1e12 / 2500.0, 4),
             "decode_tok_s": round(dec_tok_s, 2), "decode_roofline_tok_s": round(roof_tok_s, 1),
             "decode_frac_of_hbm_roofline": round(dec_tok_s / roof_tok_s, 4), "first_tokens": toks[:8]}
 

@@ -216,10 +216,14 @@ int tinyoai_stablelm_set_persistent(tinyoai_model *m, int32_t enable);
  * normalisation moments are grouped by wave). Stage 3 sets the decode
  * attention shape instead: `grid` = positions per block / 64 (1, 2 or 4 on
  * 4-wave blocks, 8 or 16 on 16-wave blocks; 0 = chosen from the position)
- * and `threads` is ignored. Stage 4: grid nonzero lets
- * each layer's decode attention launch also read the next layer's
- * input-side matrix into the device's last-level cache; zero turns that
- * off (the default). Returns 0 or TINYOAI_EINVAL. */
+ * and `threads` is ignored. Stage 4: grid nonzero (the default) runs each
+ * layer's decode attention on extra blocks of the decode_in launch, zero
+ * as a launch of its own (same arithmetic). Stage 5: grid nonzero makes
+ * the prefill products of BF16 matrices take bf16 activations (the bf16
+ * path: within 2e-2 of the logit range, faster on the matrix cores; greedy
+ * ids may then differ from the fp32 engine's where logits nearly tie),
+ * zero (the default) keeps two bf16 planes per activation (16 significant
+ * bits). Returns 0 or TINYOAI_EINVAL. */
 int tinyoai_stablelm_set_launch(tinyoai_model *m, int32_t stage, int32_t grid, int32_t threads);
 /* Timeline of the last profiled single-launch decode step: for each block
  * of the launch, 3 + 6 * layers readings of the GPU's 100 MHz real-time

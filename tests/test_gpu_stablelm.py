@@ -307,9 +307,10 @@ def test_mixed_format_layers_against_oracle(hip, oracle, mlp, attn):
     (Q6_K attention with Q4_K MLP is the mix of the K-quant workload): each
     keeps its sections as matrices of their own. StableLM-3B layer shapes,
     two layers, fp16 KV, a 300-token prompt (prefill in one chunk) and 8
-    decode tokens: logits within 1e-3 of their range of the oracle's,
-    identical greedy ids; the single-launch decode reports itself
-    unavailable."""
+    decode tokens: logits within 1e-3 of their range of the oracle's (2e-2
+    where BF16 matrices make it a bf16 path: their prefill products take
+    bf16 activations), identical greedy ids; the single-launch decode
+    reports itself unavailable."""
     config = W.validate_stablelm_config(dict(W.STABLELM_3B, num_hidden_layers=2, max_position_embeddings=512))
     tensors = W.synthetic_stablelm(config, mlp, seed=23, attn_dtype=attn, head_dtype=attn)
     prompt = np.random.default_rng(29).integers(0, 65536, 300).astype(np.int32)
@@ -319,15 +320,16 @@ def test_mixed_format_layers_against_oracle(hip, oracle, mlp, attn):
     f.set_kv_bits(16)
     assert not f.set_persistent(True)
     f.set_persistent(False)
+    tol = 2e-2 if W.BF16 in (mlp, attn) else 1e-3
     want = ref.prefill(prompt, 0)
     got = f.forward(0, prompt)
-    assert np.max(np.abs(got - want)) <= 1e-3 * float(np.ptp(want))
+    assert np.max(np.abs(got - want)) <= tol * float(np.ptp(want))
     for step in range(8):
         tr, tg = int(np.argmax(want)), int(np.argmax(got))
         assert tr == tg, step
         want = ref.forward(tr, 300 + step)
         got = f.forward(300 + step, [tg])
-        assert np.max(np.abs(got - want)) <= 1e-3 * float(np.ptp(want)), step
+        assert np.max(np.abs(got - want)) <= tol * float(np.ptp(want)), step
     f.close()
 
 

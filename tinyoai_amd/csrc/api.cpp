@@ -867,7 +867,7 @@ int StableModel::project(const MatDesc &w, const float *x, int ldx, int n, float
   const bool reuse = staged && *staged;
   if (staged) *staged = false;
   if (gemm_mfma_supported(w)) {
-    const bool two = gemm_planes(w) == 2;
+    const bool two = gemm_planes(w, bf16_acts) == 2;
     // K-split partial products (summed by the caller) where the output
     // tiles alone would leave most of the device idle.
     const int ks = splits ? gemm_splits(w, n, std::max(1, std::min(max_splits, (int)kPrefillSplits))) : 1;
@@ -899,6 +899,7 @@ int StableModel::project(const MatDesc &w, const float *x, int ldx, int n, float
   }
   return TINYOAI_OK;
 }
+
 
 int StableModel::project_planes(const MatDesc &w, const uint16_t *xh, const uint16_t *xl, int n, float *y, int ldy,
                                 int *splits) {
@@ -955,9 +956,11 @@ int StableModel::prefill_chunk(const int32_t *ids, int n, int start, bool want_l
             "in_epilogue");
     } else if (pin && pd) {
       const InEpilogue e{dims, kv[l], rope, d_pos0, Q, m32, MH, ML};
-      STAGE(ST_PREFILL_GEMM, launch_gemm_in_epilogue(w.win, XH, XL, n, e, stream), "projection + epilogue");
+      STAGE(ST_PREFILL_GEMM, launch_gemm_in_epilogue(w.win, XH, lo_plane(w.win), n, e, stream),
+            "projection + epilogue");
     } else {
-      if ((rc = pin ? project_planes(w.win, XH, XL, n, Y, win_rows) : project(w.win, H, d, n, Y, win_rows)))
+      if ((rc = pin ? project_planes(w.win, XH, lo_plane(w.win), n, Y, win_rows)
+                    : project(w.win, H, d, n, Y, win_rows)))
         return rc;
       STAGE(ST_PREFILL_EPILOGUE,
             launch_in_epilogue(dims, kv[l], Y, win_rows, rope, d_pos0, n, Q, m32, stream, pd ? MH : nullptr,
@@ -965,7 +968,8 @@ int StableModel::prefill_chunk(const int32_t *ids, int n, int start, bool want_l
             "in_epilogue");
     }
     int sp = 1, sd = 1;
-    if ((rc = pd ? project_planes(wd, MH, ML, n, D, d, &sd) : project(wd, M, I, n, D, d, &sd))) return rc;
+    if ((rc = pd ? project_planes(wd, MH, gemm_planes(wd, bf16_acts) == 2 ? ML : nullptr, n, D, d, &sd) : project(wd, M, I, n, D, d, &sd)))
+      return rc;
     if (flash)
       STAGE(ST_PREFILL_ATTENTION,
             launch_flash_prefill(dims, kv[l], Q, d_pos0, n, po && !tracing ? nullptr : A, stream, po ? XH : nullptr,
@@ -974,7 +978,8 @@ int StableModel::prefill_chunk(const int32_t *ids, int n, int start, bool want_l
     else
       STAGE(ST_PREFILL_ATTENTION,
             launch_attention(dims, kv[l], Q, d_pos0, n, start + n - 1, partials, counters, A, stream), "attention");
-    if ((rc = po ? project_planes(wo, XH, XL, n, P, d, &sp) : project(wo, A, d, n, P, d, &sp))) return rc;
+    if ((rc = po ? project_planes(wo, XH, lo_plane(wo), n, P, d, &sp) : project(wo, A, d, n, P, d, &sp)))
+      return rc;
     STAGE(ST_PREFILL_ELEMENTWISE, launch_residual(X, P, sp, D, sd, (int64_t)n * d, stream), "residual");
     if (tracing) {
       TRY_HIP(launch_copy_row(X + (size_t)(n - 1) * d, trace_dev + (size_t)l * d, d, stream), "trace");
@@ -1677,6 +1682,10 @@ int tinyoai_stablelm_set_persistent(tinyoai_model *m, int32_t enable) {
 int tinyoai_stablelm_set_launch(tinyoai_model *m, int32_t stage, int32_t grid, int32_t threads) {
   if (!m || !m->stable) return fail(TINYOAI_EINVAL, "not a StableLM handle");
   StableModel &s = *m->stable;
+  if (stage == 5) {  // BF16-weight prefill products with bf16 activations (1) or two planes (0, the default)
+    s.bf16_acts = grid != 0;
+    return TINYOAI_OK;
+  }
   if (stage == 4) {  // decode attention inside the decode_in launch (1, the default) or after it (0)
     s.fuse_attention = grid != 0;
     s.reset_fused();

@@ -225,7 +225,7 @@ hipError_t launch_gemm(const MatDesc &w, const float *x, int n, float *out, hipS
 // gemm_splits: the split count that fills the device for this shape (at
 // most max_splits).
 bool gemm_mfma_supported(const MatDesc &w);
-int gemm_planes(const MatDesc &w);
+int gemm_planes(const MatDesc &w, bool bf16_path = false);
 int gemm_splits(const MatDesc &w, int M, int max_splits);
 hipError_t launch_gemm_mfma(const MatDesc &w, const uint16_t *xh, const uint16_t *xl, int M, float *y, int ldy,
                             hipStream_t st, int ksplit = 1);

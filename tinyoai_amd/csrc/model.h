@@ -188,6 +188,12 @@ struct StableModel {
   int project(const MatDesc &w, const float *x, int ldx, int n, float *y, int ldy, int *splits = nullptr,
               bool rowstream = false, int max_splits = kPrefillSplits, bool *staged = nullptr);
   // y = X * W^T with X already in bf16 planes xh, xl (matrix-core formats).
+  // BF16-weight prefill products take bf16 activations (one plane) when
+  // set: the bf16 path's accuracy (2e-2 of the logit range), about 1.3x
+  // the matrix-core rate; off by default, which keeps greedy streams equal
+  // to the fp32 engine's where logits nearly tie.
+  bool bf16_acts = false;
+  const uint16_t *lo_plane(const MatDesc &w) const { return gemm_planes(w, bf16_acts) == 2 ? XL : nullptr; }
   int project_planes(const MatDesc &w, const uint16_t *xh, const uint16_t *xl, int n, float *y, int ldy,
                      int *splits = nullptr);
   int prefill_chunk(const int32_t *ids, int n, int start, bool want_logits);

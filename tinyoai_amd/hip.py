@@ -354,11 +354,13 @@ class StableLMForwarder:
         (the default); returns whether the single-launch path is available."""
         return bool(check(lib().tinyoai_stablelm_set_persistent(self.h, int(enable))))
 
-    LAUNCH_STAGES = {"decode_in": 0, "decode_out": 1, "lm_head": 2, "attention": 3, "prefetch": 4}
+    LAUNCH_STAGES = {"decode_in": 0, "decode_out": 1, "lm_head": 2, "attention": 3, "fused_attention": 4,
+                     "bf16_activations": 5}
 
     def set_launch(self, stage: str, grid: int, threads: int) -> None:
         """Launch shape (blocks, threads per block) of a decode matrix
-        kernel; results do not depend on it."""
+        kernel (results do not depend on it), or a switch (stages
+        "fused_attention" and "bf16_activations": grid nonzero = on)."""
         check(lib().tinyoai_stablelm_set_launch(self.h, self.LAUNCH_STAGES[stage], int(grid), int(threads)))
 
     def decode_timeline(self) -> np.ndarray:
