@@ -203,11 +203,6 @@ int tinyoai_stablelm_trace_read_stages(tinyoai_model *m, float *attention, float
  * profile_read fills ms[] and counts[] (n_stages >= 10) and returns the
  * number of stages. */
 int tinyoai_stablelm_profile(tinyoai_model *m, int32_t enable);
-/* Decode path for one-token forwards: nonzero runs each token as one
- * cooperative launch when the shapes and device allow it; zero (the
- * default) runs three kernels per layer from a replayed HIP graph. Returns 1
- * when the single-launch path is available, else 0. */
-int tinyoai_stablelm_set_persistent(tinyoai_model *m, int32_t enable);
 /* Launch shape of a decode matrix kernel: stage 0 decode_in, 1 decode_out,
  * 2 lm_head; `grid` blocks (> 0) of `threads` threads (256 or 512). Takes
  * effect from the next forward (cached graphs are dropped); a shape the
@@ -225,13 +220,6 @@ int tinyoai_stablelm_set_persistent(tinyoai_model *m, int32_t enable);
  * zero (the default) keeps two bf16 planes per activation (16 significant
  * bits). Returns 0 or TINYOAI_EINVAL. */
 int tinyoai_stablelm_set_launch(tinyoai_model *m, int32_t stage, int32_t grid, int32_t threads);
-/* Timeline of the last profiled single-launch decode step: for each block
- * of the launch, 3 + 6 * layers readings of the GPU's 100 MHz real-time
- * counter (start; per layer: input-side wait over, input rows done,
- * attention wait over, attention done, output-side wait over, output rows
- * done; head wait over, head done), [block][reading]. Copies at most
- * `capacity` values and returns the number available (0: none recorded). */
-int64_t tinyoai_stablelm_decode_timeline(tinyoai_model *m, uint64_t *stamps, int64_t capacity);
 int tinyoai_stablelm_profile_read(tinyoai_model *m, double *ms, int64_t *counts, int32_t n_stages);
 
 /* ---------------- legacy Llama forwarder (llamaMLXForwarder, mlx_llama.go:27-35) ---------------- */

@@ -508,22 +508,11 @@ int StableModel::init(const tinyoai_stablelm_config &c, const tinyoai_tensor *te
       (rc = alloc((void **)&XH, B * wide * 2)) || (rc = alloc((void **)&XL, B * wide * 2)) ||
       (rc = alloc((void **)&MH, B * I * 2)) || (rc = alloc((void **)&ML, B * I * 2)))
     return rc;
-  // Persistent decode state.
-  const int L = c.num_hidden_layers;
-  psync_words = persistent_sync_words(L, dims.heads);
-  if ((rc = alloc((void **)&layers_dev, sizeof(LayerDev) * L)) || (rc = alloc((void **)&kv_dev, sizeof(KVDev) * L)) ||
-      (rc = alloc((void **)&xs, (size_t)(L + 1) * persistent_stride(d) * 4)) ||
-      (rc = alloc((void **)&qs, (size_t)L * persistent_stride(w_att) * 4)) ||
-      (rc = alloc((void **)&as, (size_t)L * persistent_stride(w_att) * 4)) ||
-      (rc = alloc((void **)&ms, (size_t)L * persistent_stride(I) * 4)) ||
-      (rc = alloc((void **)&psync, psync_words * 4)) ||
-      (rc = alloc((void **)&ppart, (size_t)L * dims.heads * partial_region((maxp + 15) / 16, hd) * 4)))
-    return rc;
+  // The error word after the logits: set by a decode step whose bounded
+  // in-kernel wait timed out.
   perr = (unsigned *)(logits_dev + c.vocab_size);
-  e = hipMemcpyAsync(layers_dev, layers.data(), sizeof(LayerDev) * L, hipMemcpyHostToDevice, stream);
-  if (e == hipSuccess) e = hipMemsetAsync(psync, 0, psync_words * 4, stream);
-  if (e == hipSuccess) e = hipMemsetAsync(perr, 0, 4, stream);
-  if (e != hipSuccess) return hip_fail(e, "persistent decode state");
+  e = hipMemsetAsync(perr, 0, 4, stream);
+  if (e != hipSuccess) return hip_fail(e, "decode error word");
   e = hipEventCreateWithFlags(&params_copied, hipEventDisableTiming);
   if (e != hipSuccess) return hip_fail(e, "hipEventCreate");
   e = hipHostMalloc(&h_pinned,
@@ -545,87 +534,16 @@ int StableModel::init(const tinyoai_stablelm_config &c, const tinyoai_tensor *te
   threads_out = 256;
   grid_head = cus * 2;
   threads_head = 512;
-  // The single-launch decode streams fused layer matrices only.
-  pgrid = mixed_layers ? 0 : persistent_decode_grid(persistent_args(true), layers[0]);
   return TINYOAI_OK;
 }
 
-PersistentDecode StableModel::persistent_args(bool want_logits) const {
-  PersistentDecode a{};
-  a.layers = layers_dev;
-  a.kv = kv_dev;
-  a.L = cfg.num_hidden_layers;
-  a.s = dims;
-  a.emb = embed.desc;
-  a.head = head.desc;
-  a.norm_w = norm_w;
-  a.norm_b = norm_b;
-  a.rope = rope;
-  a.params = params;
-  a.xs = xs;
-  a.qs = qs;
-  a.as = as;
-  a.ms = ms;
-  a.partials = ppart;
-  a.max_splits = (cfg.max_position_embeddings + 15) / 16;
-  a.cap_max = cfg.max_position_embeddings;
-  a.half_kv = kv_half;
-  a.sync = psync;
-  a.err = perr;
-  a.logits = logits_dev;
-  a.epoch = epoch;
-  a.want_logits = want_logits;
-  a.spin_limit = 1u << 20;
-  a.stamps = nullptr;
-  return a;
-}
-
-// Per-layer stage times from the timeline of the last profiled persistent
-// launch, on the critical path: decode_in runs from the last block leaving
-// the previous layer to the last block finishing win rows; attention until
-// the last block sees every head combined; decode_out until the last block
-// has written its rows; lm_head until the last block is done. The counter
-// runs at 100 MHz.
-void StableModel::resolve_timeline() {
-  if (!stamps_pending) return;
-  stamps_pending = false;
-  const int L = cfg.num_hidden_layers, P = persistent_stamps(L);
-  timeline.assign((size_t)pgrid * P, 0);
-  if (hipMemcpy(timeline.data(), pstamps, timeline.size() * 8, hipMemcpyDeviceToHost) != hipSuccess) return;
-  auto latest = [&](int k) {
-    uint64_t v = 0;
-    for (int b = 0; b < pgrid; b++) v = std::max(v, timeline[(size_t)b * P + k]);
-    return v;
-  };
-  auto earliest = [&](int k) {
-    uint64_t v = UINT64_MAX;
-    for (int b = 0; b < pgrid; b++) v = std::min(v, timeline[(size_t)b * P + k]);
-    return v;
-  };
-  auto add = [&](int stage, uint64_t from, uint64_t to) {
-    prof.ms[stage] += to > from ? (double)(to - from) * 1e-5 : 0.0;
-    prof.count[stage]++;
-  };
-  uint64_t t = earliest(0);
-  for (int l = 0; l < L; l++) {
-    const uint64_t in_done = latest(2 + 6 * l), att_done = latest(5 + 6 * l), out_done = latest(6 + 6 * l);
-    add(ST_DECODE_IN, t, in_done);
-    add(ST_ATTENTION, in_done, att_done);
-    add(ST_DECODE_OUT, att_done, out_done);
-    t = out_done;
-  }
-  if (latest(2 + 6 * L)) add(ST_LM_HEAD, t, latest(2 + 6 * L));
-}
-
-// After a forward that used the persistent kernel has synchronized: a set
-// error word means a dependency wait timed out, so the counters are
-// rebuilt from zero.
-int StableModel::check_persistent(int rc) {
+// After a decode forward has synchronized: a set error word means an
+// in-kernel dependency wait timed out, so the arrival counters are rebuilt
+// from zero.
+int StableModel::check_wait_error(int rc) {
   unsigned word = 0;
   if (hipMemcpy(&word, perr, 4, hipMemcpyDeviceToHost) != hipSuccess || word == 0) return rc;
-  hipMemset(psync, 0, psync_words * 4);
   hipMemset(perr, 0, 4);
-  epoch = 0;
   reset_fused();
   return rc ? rc : fail(TINYOAI_EDEVICE, "decode step did not complete: a dependency wait timed out");
 }
@@ -685,7 +603,6 @@ int StableModel::ensure_kv(int needed) {
   kv = grown;
   cap = want;
   offset = keep;
-  if (e == hipSuccess) e = hipMemcpy(kv_dev, kv.data(), sizeof(KVDev) * kv.size(), hipMemcpyHostToDevice);
   return e == hipSuccess ? TINYOAI_OK : hip_fail(e, "KV growth");
 }
 
@@ -799,30 +716,6 @@ void StableModel::drop_graphs() {
 int StableModel::decode_step(int token, int pos, bool want_logits) {
   const int vals[3] = {token, pos, fuse_epoch};
   logits_mapped = false;
-  if (pgrid > 0 && use_persistent) {
-    if (int rc = upload_params(vals, 3, nullptr, 0, rope_host.data() + (size_t)pos * dims.rot, dims.rot)) return rc;
-    PersistentDecode args = persistent_args(want_logits);
-    if (prof.on) {
-      if (!pstamps && alloc((void **)&pstamps, (size_t)pgrid * persistent_stamps(cfg.num_hidden_layers) * 8))
-        return TINYOAI_ENOMEM;
-      TRY_HIP(hipMemsetAsync(pstamps, 0, (size_t)pgrid * persistent_stamps(cfg.num_hidden_layers) * 8, stream),
-              "timeline");
-      args.stamps = pstamps;
-      stamps_pending = true;
-    }
-    TRY_HIP(launch_persistent_decode(args, layers[0], pgrid, stream), "persistent decode");
-    epoch++;
-    if (tracing) {
-      const int hq = dims.heads * dims.hd;
-      const int64_t sd = persistent_stride(dims.d), sq = persistent_stride(hq), si = persistent_stride(dims.inter);
-      for (int l = 0; l < cfg.num_hidden_layers; l++) {
-        TRY_HIP(launch_copy_row(xs + (l + 1) * sd, trace_dev + (size_t)l * dims.d, dims.d, stream), "trace");
-        TRY_HIP(launch_copy_row(as + l * sq, trace_att + (size_t)l * hq, hq, stream), "trace");
-        TRY_HIP(launch_copy_row(ms + l * si, trace_gate + (size_t)l * dims.inter, dims.inter, stream), "trace");
-      }
-    }
-    return TINYOAI_OK;
-  }
   // The parameter block goes to host-mapped memory, which the step's first
   // kernel reads (the previous step has completed: every forward ends
   // with a synchronisation).
@@ -1331,25 +1224,23 @@ int StableModel::forward(int prefix, const int32_t *tokens, int n, bool want_log
                                            hipMemcpyDeviceToHost, stream);
     if (e == hipSuccess) e = hipStreamSynchronize(stream);
     if (e != hipSuccess) rc = hip_fail(e, "logits");
-    else if (*err_host) rc = check_persistent(rc);
+    else if (*err_host) rc = check_wait_error(rc);
     else memcpy(logits, src, (size_t)cfg.vocab_size * 4);
   } else if (!rc) {
     hipError_t e = hipStreamSynchronize(stream);
     if (e != hipSuccess) rc = hip_fail(e, "forward");
-    else if (n == 1) rc = check_persistent(rc);
+    else if (n == 1) rc = check_wait_error(rc);
   }
   if (rc) {
     std::string msg = g_error;
     hipStreamSynchronize(stream);
     prof.marks.clear();
     prof.used = 0;
-    stamps_pending = false;
     free_kv();
     g_error = msg;
     return rc;
   }
   prof.resolve();
-  resolve_timeline();
   offset = prefix + n;
   return TINYOAI_OK;
 }
@@ -1673,11 +1564,6 @@ int tinyoai_stablelm_trace_read_stages(tinyoai_model *m, float *attention, float
   return e == hipSuccess ? TINYOAI_OK : hip_fail(e, "trace read");
 }
 
-int tinyoai_stablelm_set_persistent(tinyoai_model *m, int32_t enable) {
-  if (!m || !m->stable) return fail(TINYOAI_EINVAL, "not a StableLM handle");
-  m->stable->use_persistent = enable != 0;
-  return m->stable->pgrid > 0 ? 1 : 0;
-}
 
 int tinyoai_stablelm_set_launch(tinyoai_model *m, int32_t stage, int32_t grid, int32_t threads) {
   if (!m || !m->stable) return fail(TINYOAI_EINVAL, "not a StableLM handle");
@@ -1718,13 +1604,6 @@ int tinyoai_stablelm_profile(tinyoai_model *m, int32_t enable) {
   return TINYOAI_OK;
 }
 
-int64_t tinyoai_stablelm_decode_timeline(tinyoai_model *m, uint64_t *stamps, int64_t capacity) {
-  if (!m || !m->stable || (capacity > 0 && !stamps)) return fail(TINYOAI_EINVAL, "invalid timeline read");
-  const std::vector<uint64_t> &t = m->stable->timeline;
-  const int64_t n = std::min<int64_t>(capacity, (int64_t)t.size());
-  if (n > 0) memcpy(stamps, t.data(), (size_t)n * 8);
-  return (int64_t)t.size();
-}
 
 int tinyoai_stablelm_profile_read(tinyoai_model *m, double *ms, int64_t *counts, int32_t n_stages) {
   if (!m || !m->stable || !ms || !counts || n_stages < ST_COUNT) return fail(TINYOAI_EINVAL, "invalid profile read");

@@ -174,43 +174,6 @@ hipError_t launch_ln_matvec(const MatDesc &w, const float *ln_w, const float *ln
 // x[n][cols] = rows ids[j] of an embedding matrix, bit-exact dequantized.
 hipError_t launch_embed(const MatDesc &emb, const int *ids, int n, float *x, hipStream_t st);
 
-// ---- persistent decode (one cooperative launch per token) ----
-struct PersistentDecode {
-  const LayerDev *layers;  // device array [L]
-  const KVDev *kv;         // device array [L]
-  int L;
-  StableDims s;
-  MatDesc emb, head;
-  const float *norm_w, *norm_b, *rope;
-  const int *params;       // [0] token, [1] position
-  // Per-layer handoff buffers, rows persistent_stride(n) floats apart:
-  float *xs;               // [L + 1][d]: the residual entering each layer, then the final one
-  float *qs, *as;          // [L][heads * hd]: RoPE'd queries, attention outputs
-  float *ms;               // [L][inter]: SiLU-gate outputs
-  float *partials;         // [L][heads][partial_region(max_splits, hd)]
-  int max_splits;
-  int cap_max;             // largest KV capacity the launch may see (positions)
-  int half_kv;
-  unsigned *sync;          // persistent_sync_words(L, heads) words, zero before the first launch
-  unsigned *err;           // set to nonzero when a dependency wait timed out
-  float *logits;
-  unsigned epoch;          // number of earlier completed launches on `sync`
-  int want_logits;
-  unsigned spin_limit;     // polls per wait before giving up
-  // Optional phase timeline: thread 0 of every block records the 100 MHz
-  // real-time counter at persistent_stamps(L) points, [block][point].
-  uint64_t *stamps;
-};
-// Timeline points per block: start, then per layer {in wait done, in
-// arrived, attention wait done, attention done, out wait done, out arrived},
-// then head wait done and head done.
-__host__ __device__ inline int persistent_stamps(int layers) { return 3 + 6 * layers; }
-size_t persistent_sync_words(int layers, int heads);
-__host__ __device__ inline int64_t persistent_stride(int64_t n) { return (n + 63) / 64 * 64; }
-// Grid size (one block per CU) when the shapes have an instantiation and the
-// device can keep every block resident, else 0.
-int persistent_decode_grid(const PersistentDecode &a, const LayerDev &layer0);
-hipError_t launch_persistent_decode(const PersistentDecode &a, const LayerDev &layer0, int grid, hipStream_t st);
 
 // ---- prefill (n tokens) ----
 // out (fp32, may be null) and / or bf16 operand planes oh, ol (null: none).

@@ -138,23 +138,7 @@ struct StableModel {
   int fuse_lines() const { return 1 + kFuseGroups + dims.heads; }
   size_t fuse_bytes() const { return (size_t)cfg.num_hidden_layers * fuse_lines() * 128; }
 
-  // Persistent decode (one cooperative launch per token): device copies of
-  // the layer and KV descriptors, per-layer handoff buffers, counters.
-  LayerDev *layers_dev = nullptr;
-  KVDev *kv_dev = nullptr;
-  float *xs = nullptr, *qs = nullptr, *as = nullptr, *ms = nullptr;
-  float *ppart = nullptr;  // attention partials [L][heads][max_pos / 16][hd + 2]
-  unsigned *psync = nullptr, *perr = nullptr;  // perr: the word after the logits
-  size_t psync_words = 0;
-  int pgrid = 0;
-  unsigned epoch = 0;
-  bool use_persistent = false;
-  // Phase timeline of profiled persistent launches ([block][point] of the
-  // real-time counter), resolved into the profile stages after a forward.
-  uint64_t *pstamps = nullptr;
-  bool stamps_pending = false;
-  std::vector<uint64_t> timeline;
-  void resolve_timeline();
+  unsigned *perr = nullptr;  // the word after the logits: an in-kernel wait timed out
 
   std::vector<void *> buffers;
   Profiler prof;
@@ -172,8 +156,7 @@ struct StableModel {
   int enqueue_decode(int steps, int splits, bool want_logits);
   void drop_graphs();
   int decode_step(int token, int pos, bool want_logits);
-  PersistentDecode persistent_args(bool want_logits) const;
-  int check_persistent(int rc);
+  int check_wait_error(int rc);
   bool decode_fused(int steps) const;
   void reset_fused();
   // y = x * W^T; with `splits`, the product may come as *splits K-split

@@ -21,7 +21,7 @@ EXPORTS = [
     "tinyoai_stablelm_limit_cache", "tinyoai_stablelm_reset", "tinyoai_stablelm_offset", "tinyoai_stablelm_close",
     "tinyoai_stablelm_read_kv", "tinyoai_stablelm_kv_save", "tinyoai_stablelm_kv_load",
     "tinyoai_stablelm_trace", "tinyoai_stablelm_trace_read",
-    "tinyoai_stablelm_trace_read_stages", "tinyoai_stablelm_decode_timeline", "tinyoai_stablelm_set_persistent",
+    "tinyoai_stablelm_trace_read_stages",
     "tinyoai_stablelm_set_launch", "tinyoai_stablelm_branches_open", "tinyoai_stablelm_branches_forward",
     "tinyoai_stablelm_branches_append", "tinyoai_stablelm_branches_length", "tinyoai_stablelm_branches_close",
     "tinyoai_stablelm_profile", "tinyoai_stablelm_profile_read", "tinyoai_llama_load",
@@ -81,9 +81,6 @@ def lib():
         L.tinyoai_stablelm_trace.argtypes = [P, C.c_int32]
         L.tinyoai_stablelm_trace_read.argtypes = [P, fp]
         L.tinyoai_stablelm_trace_read_stages.argtypes = [P, fp, fp]
-        L.tinyoai_stablelm_decode_timeline.argtypes = [P, C.POINTER(C.c_uint64), C.c_int64]
-        L.tinyoai_stablelm_decode_timeline.restype = C.c_int64
-        L.tinyoai_stablelm_set_persistent.argtypes = [P, C.c_int32]
         L.tinyoai_stablelm_set_launch.argtypes = [P, C.c_int32, C.c_int32, C.c_int32]
         L.tinyoai_stablelm_branches_open.argtypes = [P, C.c_int32, C.c_int32, C.c_int32, C.POINTER(P)]
         L.tinyoai_stablelm_branches_forward.argtypes = [P, ip, C.c_int32, fp]
@@ -349,11 +346,6 @@ class StableLMForwarder:
     STAGES = ("embedding", "decode_in", "attention", "decode_out", "lm_head", "prefill_layer_norm",
               "prefill_projections", "prefill_epilogue", "prefill_attention", "prefill_elementwise")
 
-    def set_persistent(self, enable: bool) -> bool:
-        """Selects the single-launch decode path or three kernels per layer
-        (the default); returns whether the single-launch path is available."""
-        return bool(check(lib().tinyoai_stablelm_set_persistent(self.h, int(enable))))
-
     LAUNCH_STAGES = {"decode_in": 0, "decode_out": 1, "lm_head": 2, "attention": 3, "fused_attention": 4,
                      "bf16_activations": 5}
 
@@ -362,18 +354,6 @@ class StableLMForwarder:
         kernel (results do not depend on it), or a switch (stages
         "fused_attention" and "bf16_activations": grid nonzero = on)."""
         check(lib().tinyoai_stablelm_set_launch(self.h, self.LAUNCH_STAGES[stage], int(grid), int(threads)))
-
-    def decode_timeline(self) -> np.ndarray:
-        """Phase timeline of the last profiled single-launch decode step:
-        [blocks][3 + 6 * layers] readings of the 100 MHz GPU clock (empty
-        when none was recorded)."""
-        n = lib().tinyoai_stablelm_decode_timeline(self.h, None, 0)
-        check(n if n < 0 else 0)
-        out = np.zeros(n, np.uint64)
-        if n:
-            lib().tinyoai_stablelm_decode_timeline(self.h, out.ctypes.data_as(C.POINTER(C.c_uint64)), n)
-        points = 3 + 6 * self.config["num_hidden_layers"]
-        return out.reshape(-1, points)
 
     def profile(self, enable: bool = True) -> None:
         check(lib().tinyoai_stablelm_profile(self.h, int(enable)))
