@@ -17,8 +17,12 @@
  *   RoPE                  closed form + rope.json (stablelm_test.go:168-205)
  *   StableLM forward      expected.json logits + greedy ids (stablelm_test.go:50-82)
  *   batched prefill       sequential forward within 3e-5 (prefill_test.go:217-277)
- *   Llama transformer     parity unpinned: the reference holds no Llama logits
- *                         or tokens; checked only by closed-form sub-steps.
+ *   Llama transformer     the reference holds no Llama logits or tokens: pinned by
+ *                         a float64 statement of the same model on stories260K at
+ *                         positions 0-8 (rotations other than the identity, 8
+ *                         query heads on 4 kv heads, up to 9 softmax terms),
+ *                         which detects planted mistakes (swapped cos/sin, a
+ *                         wrong kv head, a dropped key), and closed-form steps.
  *
  * Build: -O2 -ffp-contract=off -fopenmp (see oracle/Makefile). With contraction
  * off, every float32 operation rounds separately, like Go on amd64.

@@ -325,10 +325,11 @@ def test_llama_checkpoint_layout(oracle):
 
 
 def test_llama_rmsnorm_rope_closed_form(oracle):
-    """The Llama engine has no golden outputs in the reference (parity
-    unpinned); this pins its first layer on a one-layer model whose attention
-    at position 0 reduces to V (softmax of one score is 1) against a float64
-    restatement, within float32 rounding."""
+    """The Llama engine has no golden outputs in the reference; this pins
+    its first layer on a one-layer model whose attention at position 0
+    reduces to V (softmax of one score is 1) against a float64 restatement,
+    within float32 rounding (the later positions are pinned by
+    test_llama_float64_brute_force)."""
     c = dict(dim=16, hidden_dim=24, n_layers=1, n_heads=4, n_kv_heads=2, vocab_size=10, seq_len=8)
     w = W.synthetic_llama(c, 1)
     m = oracle.Llama(c, w)
