@@ -254,40 +254,40 @@ __device__ __forceinline__ void attention_block(const AttArgs &a, const int spli
              (unsigned)(nsplit - 1);
   __syncthreads();
   if (!s_last) return;
-  // Last block of this (query, head): every other split has published
-  // (and the shared-prefix records were written by an earlier launch).
-  const float *base = region;
+  // Last block of this (query, head): every other split has published (and
+  // the shared-prefix records were written by an earlier launch). The
+  // records are staged in LDS kRec at a time by independent loads (one
+  // memory round trip per kRec records) and combined from there: with
+  // M = max m_r, e_r = exp(m_r - M), out[d] = sum o_r[d] e_r / sum l_r e_r,
+  // rescaled from one staged chunk to the next. Every thread forms the same
+  // M and L from the same LDS values.
+  // (4 KiB of LDS: the input-side launch that runs these blocks holds two
+  // blocks per CU.)
+  constexpr int RS = HD + 2, kRec = 1024 / RS;
+  static_assert(HD <= kThreads && kRec <= 512, "one output dimension per thread; weights in s_e");
+  __shared__ float s_rec[kRec * RS];
   const int total = pre + nsplit;
-  float m = -INFINITY;
-  for (int sp = tid; sp < total; sp += kThreads) m = fmaxf(m, collect(base + sp * (HD + 2)));
-  m = wave_max(m);
-  if (lane == 0) s_m[wave] = m;
-  __syncthreads();
-  m = s_m[0];
-#pragma unroll
-  for (int w = 1; w < kWaves; w++) m = fmaxf(m, s_m[w]);
-  float lsum = 0.f;
-  for (int sp = tid; sp < total; sp += kThreads) {
-    const float e = expf(collect(base + sp * (HD + 2)) - m);
-    s_e[sp] = e;
-    lsum = fmaf(collect(base + sp * (HD + 2) + 1), e, lsum);
+  float m_run = -INFINITY, l_run = 0.f, acc = 0.f;
+  for (int c0 = 0; c0 < total; c0 += kRec) {
+    const int nr = min(kRec, total - c0);
+    for (int i = tid; i < nr * RS; i += kThreads) s_rec[i] = collect(region + (int64_t)c0 * RS + i);
+    __syncthreads();
+    float mc = m_run;
+    for (int r = 0; r < nr; r++) mc = fmaxf(mc, s_rec[r * RS]);
+    for (int r = tid; r < nr; r += kThreads) s_e[r] = expf(s_rec[r * RS] - mc);
+    __syncthreads();
+    const float scale = expf(m_run - mc);  // 0 for the first chunk
+    float lc = 0.f;
+    for (int r = 0; r < nr; r++) lc = fmaf(s_rec[r * RS + 1], s_e[r], lc);
+    l_run = fmaf(l_run, scale, lc);
+    if (tid < HD) {
+      float ac = 0.f;
+      for (int r = 0; r < nr; r++) ac = fmaf(s_rec[r * RS + 2 + tid], s_e[r], ac);
+      acc = fmaf(acc, scale, ac);
+    }
+    m_run = mc;
+    __syncthreads();  // the next chunk reuses s_rec and s_e
   }
-  lsum = wave_sum(lsum);
-  __syncthreads();
-  if (lane == 0) s_l[wave] = lsum;
-  __syncthreads();
-  float Ltot = 0.f;
-  if constexpr (kWaves == 4) {
-    Ltot = (s_l[0] + s_l[1]) + (s_l[2] + s_l[3]);
-  } else {
-#pragma unroll
-    for (int w = 0; w < kWaves; w++) Ltot += s_l[w];
-  }
-  for (int d = tid; d < HD; d += kThreads) {
-    float acc = 0.f;
-#pragma unroll 8
-    for (int sp = 0; sp < total; sp++) acc = fmaf(collect(base + sp * (HD + 2) + 2 + d), s_e[sp], acc);
-    outp[d] = acc / Ltot;
-  }
+  if (tid < HD) outp[tid] = acc / l_run;
   if (tid == 0) __hip_atomic_store(&a.counters[qh], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
