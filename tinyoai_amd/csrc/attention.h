@@ -70,6 +70,11 @@ __device__ __forceinline__ void load_kv_lanes_coherent(const void *base, int64_t
   }
 }
 
+// The wait of a block whose inputs are ready at launch.
+struct NoWait {
+  __device__ bool operator()() const { return true; }
+};
+
 // One block of WAVES waves per (split, head, query); a split covers
 // WAVES * STEPS * 16 positions. Lane = 4 * position-in-step + dim group:
 // four lanes share a position, each holding hd/4 dimensions. Online-softmax
@@ -79,11 +84,15 @@ __device__ __forceinline__ void load_kv_lanes_coherent(const void *base, int64_t
 // block per head and no cross-block combine at all.
 //
 // FUSED: the block runs inside the launch that writes this token's query
-// and K/V entry (after waiting for them); it reads the query and the entry
-// at the token's own position with agent-scope atomic loads, which see the
-// other blocks' stores, and the older positions with plain loads.
-template <int HD, bool HALF, int STEPS, int WAVES, bool BR, bool FUSED>
-__device__ __forceinline__ void attention_block(const AttArgs &a, const int split, const int h, const int j) {
+// and K/V entry. It issues the loads of the older positions' K/V, then
+// calls wait() (block-uniform: true once the query and the entry are
+// stored, false to give up), then reads the query and the entry at the
+// token's own position with agent-scope atomic loads, which see the other
+// blocks' stores.
+template <int HD, bool HALF, int STEPS, int WAVES, bool BR, bool FUSED, typename Wait = NoWait>
+__device__ __forceinline__ void attention_block(const AttArgs &a, const int split, const int h, const int j,
+                                                Wait wait = Wait{}) {
+  static_assert(!(FUSED && BR), "the fused launch runs single-sequence decode");
   constexpr int kWaves = WAVES, kThreads = WAVES * 64;
   constexpr int DPL = HD / 4;
   constexpr int SPLIT = kWaves * STEPS * 16;
@@ -95,8 +104,10 @@ __device__ __forceinline__ void attention_block(const AttArgs &a, const int spli
   const int kvh = h / (s.heads / s.kv_heads);
   const float *q = a.q + (int64_t)j * s.heads * HD + h * HD;
   float qr[DPL];
+  if constexpr (!FUSED) {
 #pragma unroll
-  for (int i = 0; i < DPL; i++) qr[i] = FUSED ? collect(q + att_dim<DPL>(g, i)) : q[att_dim<DPL>(g, i)];
+    for (int i = 0; i < DPL; i++) qr[i] = q[att_dim<DPL>(g, i)];
+  }
   const int64_t head_base = (int64_t)kvh * a.kv.cap * HD;
   // BR: the query's position, and its suffix as element offsets: position
   // t >= prefix at sfx_base + t * HD (t clamped to the query's position).
@@ -138,10 +149,7 @@ __device__ __forceinline__ void attention_block(const AttArgs &a, const int spli
     const bool b = where(t0 + st * 16, e);
     const void *kp = reinterpret_cast<const void *>(kbase + (b ? kdelta : 0));
     const void *vp = reinterpret_cast<const void *>(vbase + (b ? vdelta : 0));
-    if (FUSED && t0 + st * 16 == fpos) {
-      load_kv_lanes_coherent<DPL, HALF>(kp, e, g, kr[st]);
-      if constexpr (kEarlyV) load_kv_lanes_coherent<DPL, HALF>(vp, e, g, vr[st]);
-    } else {
+    if (!FUSED || t0 + st * 16 != fpos) {
       load_kv_lanes<DPL, HALF>(kp, e, g, kr[st]);
       if constexpr (kEarlyV) load_kv_lanes<DPL, HALF>(vp, e, g, vr[st]);
     }
@@ -150,6 +158,19 @@ __device__ __forceinline__ void attention_block(const AttArgs &a, const int spli
   const int npos = pos + 1;
   const int nsplit = (npos - tb + SPLIT - 1) / SPLIT;  // this launch's splits
   if (split >= nsplit) return;
+  if constexpr (FUSED) {
+    if (!wait()) return;
+#pragma unroll
+    for (int i = 0; i < DPL; i++) qr[i] = collect(q + att_dim<DPL>(g, i));
+#pragma unroll
+    for (int st = 0; st < STEPS; st++)
+      if (t0 + st * 16 == fpos) {
+        int64_t e;
+        where(t0 + st * 16, e);
+        load_kv_lanes_coherent<DPL, HALF>(a.kv.k, e, g, kr[st]);
+        if constexpr (kEarlyV) load_kv_lanes_coherent<DPL, HALF>(a.kv.v, e, g, vr[st]);
+      }
+  }
   float score[STEPS];
   float mx = -INFINITY;
 #pragma unroll

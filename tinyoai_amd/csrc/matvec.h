@@ -139,11 +139,9 @@ inline size_t slice_lds(int chunks, int split, int n_units, int grid, int R) {
 constexpr int kNormRegs = 3;
 
 // decode_in's work for one of `blocks` blocks (COH: outputs stored at
-// agent scope, the units below phase_unit run first; hook as stream_rows
-// takes it).
+// agent scope; hook as stream_rows takes it).
 template <int F, int T, bool COH, typename Hook>
-__device__ __forceinline__ void decode_in_body(const InArgs &a, float *lds_raw, Hook hook, int blocks,
-                                               int phase_unit = INT_MAX) {
+__device__ __forceinline__ void decode_in_body(const InArgs &a, float *lds_raw, Hook hook, int blocks) {
   // LDS: pending stores | x [d] | 32 doubles | rotary row [rot] | slice partials
   PendingStore *pend = reinterpret_cast<PendingStore *>(lds_raw);
   float *lds = lds_raw + (T / 64) * kPendingPerWave * 4;
@@ -195,9 +193,8 @@ __device__ __forceinline__ void decode_in_body(const InArgs &a, float *lds_raw, 
   auto done = [&](int u, const float (&r)[2][2], const float (&)[2], const auto &out) {
     in_pair_outputs(s, kv, rope_row, pos, u, r[0][0], r[1][0], a.q_out, a.m_out, out);
   };
-  stream_rows<F, T, cpl_for<F>(), 2, false, true, 1, false, COH, COH>(W, W.rows / 2, W.chunks, part, pend, rows, xload,
-                                                                  noaux, pre, prologue, done, hook, blocks,
-                                                                  phase_unit);
+  stream_rows<F, T, cpl_for<F>(), 2, false, true, 1, false, COH>(W, W.rows / 2, W.chunks, part, pend, rows, xload,
+                                                             noaux, pre, prologue, done, hook, blocks);
 }
 
 template <int F, int T>
@@ -212,22 +209,39 @@ __device__ __forceinline__ unsigned poll_counter(unsigned *p) {
 
 // decode_in and the layer's split-K attention in one launch. Blocks
 // [0, fz.blocks) stream win as decode_in_kernel does, storing the query and
-// the K/V entry at agent scope; every wave runs its q/k/v units first (in
-// groups of their own), waits for its stores, and arrives. The last wave of
-// a block to arrive adds the block to its group's counter, the last block
-// of a group adds the group to the top counter, and the last group raises
-// every head's go flag to the launch number (counters grow by a fixed
-// amount per launch, so nothing is reset between launches). The blocks
-// after the streaming ones run the attention of (split idx % splits, head
-// idx / splits) once their head's flag shows the launch, so the attention
-// overlaps the gate/up rows' stream. A single counter for every wave made
-// each wave stall behind thousands of atomics to one address; the tree
-// keeps one wave per block on a global atomic and a head's few blocks on a
-// flag line. An attention block waits only for blocks before it in
-// dispatch order, which have all started when it runs; the wait is still
-// bounded, and a time-out sets *fz.err (every waiting block then leaves).
+// the K/V entry at agent scope; a wave's units come in increasing order, so
+// once the next unit it would take lies past the q/k/v sections, its q/k/v
+// results are stored: it waits for its stores and arrives (with 512 blocks
+// of four waves and groups of two units, right after its first group).
+// The last wave of a block to arrive adds the block to its group's
+// counter, the last block of a group adds the group to the top counter,
+// and the last group raises every head's go flag to the launch number
+// (counters grow by a fixed amount per launch, so nothing is reset between
+// launches). The blocks after the streaming ones run the attention of
+// (split idx % splits, head idx / splits). Where the kernel fits 168 VGPRs
+// (fused_waves), three blocks share a CU, so with up to 256 attention
+// blocks beside 512 streaming ones every block is resident from the start
+// (elsewhere attention blocks start as streaming blocks retire); an
+// attention block issues
+// its older positions' K/V loads at once, waits for its head's flag, then
+// reads the query and the token's own entry, so the attention overlaps
+// the gate/up rows' stream. A single counter for every wave made each wave
+// stall behind thousands of atomics to one address; the tree keeps one
+// wave per block on a global atomic and a head's few blocks on a flag
+// line. An attention block waits only for blocks before it in dispatch
+// order, which have all started when it runs; the wait is still bounded,
+// and a time-out sets *fz.err (every waiting block then leaves).
+// Waves per SIMD the fused kernel is compiled for: three where its
+// registers fit 168 VGPRs without spilling (Q8_0 rows with at most 160
+// attention values per lane step), else two.
+template <int F, int HD, int STEPS>
+constexpr int fused_waves() {
+  return F == FMT_Q8_0 && HD * STEPS <= 160 ? 3 : 2;
+}
+
 template <int F, int T, int HD, bool HALF, int STEPS>
-__global__ __launch_bounds__(T) void decode_in_att_kernel(InArgs a, AttArgs att, FuseArgs fz) {
+__global__ __launch_bounds__(T, (fused_waves<F, HD, STEPS>())) void decode_in_att_kernel(InArgs a, AttArgs att,
+                                                                                       FuseArgs fz) {
   static_assert(T == 256, "attention blocks are four waves");
   extern __shared__ __align__(16) float lds_raw[];
   __shared__ unsigned s_arrived;
@@ -235,21 +249,24 @@ __global__ __launch_bounds__(T) void decode_in_att_kernel(InArgs a, AttArgs att,
   if ((int)blockIdx.x >= fz.blocks) {
     __shared__ int s_ok;
     const int idx = (int)blockIdx.x - fz.blocks, splits = att.max_splits, h = idx / splits;
-    if (threadIdx.x == 0) {
-      unsigned *flag = fz.go + h * 32;
-      int ok = 1;
-      for (unsigned it = 0; (int)(poll_counter(flag) - launch) < 0; it++) {
-        if (it >= fz.spin_limit || ((it & 15) == 15 && poll_counter(fz.err) != 0)) {
-          ok = 0;
-          break;
+    auto wait = [&]() {
+      if (threadIdx.x == 0) {
+        unsigned *flag = fz.go + h * 32;
+        int ok = 1;
+        for (unsigned it = 0; (int)(poll_counter(flag) - launch) < 0; it++) {
+          if (it >= fz.spin_limit || ((it & 15) == 15 && poll_counter(fz.err) != 0)) {
+            ok = 0;
+            break;
+          }
+          __builtin_amdgcn_s_sleep(4);
         }
-        __builtin_amdgcn_s_sleep(4);
+        if (!ok) __hip_atomic_store(fz.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_ok = ok;
       }
-      if (!ok) __hip_atomic_store(fz.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      s_ok = ok;
-    }
-    __syncthreads();
-    if (s_ok) attention_block<HD, HALF, STEPS, 4, false, true>(att, idx % splits, h, 0);
+      __syncthreads();
+      return s_ok != 0;
+    };
+    attention_block<HD, HALF, STEPS, 4, false, true>(att, idx % splits, h, 0, wait);
     return;
   }
   if (threadIdx.x == 0) s_arrived = 0;  // the prologue's barrier orders this before any arrival
@@ -273,7 +290,7 @@ __global__ __launch_bounds__(T) void decode_in_att_kernel(InArgs a, AttArgs att,
       for (int h = lane; h < a.s.heads; h += 64)
         __hip_atomic_store(fz.go + h * 32, launch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   };
-  decode_in_body<F, T, true>(a, lds_raw, hook, fz.blocks, fz.qkv_units);
+  decode_in_body<F, T, true>(a, lds_raw, hook, fz.blocks);
 }
 
 // x = (x + o*a) + down*m: a wout row is [o | down], the down part from

@@ -33,10 +33,12 @@
 #include "formats.h"
 
 // Batches per unrolled group, and how many batches a wave keeps in flight
-// ahead of the one it consumes: with 12 waves on a CU, two 6 KiB batches
-// each put ~144 KiB per CU in flight, what the HBM latency under load asks
-// for at full bandwidth (one batch ahead measured ~3 TB/s).
-constexpr int kRowGroup = 4;
+// ahead of the one it consumes. Groups of two with one batch ahead keep a
+// row-streaming wave within 168 VGPRs, so three waves fit a SIMD (twelve
+// per CU hold ~130 KiB of 5.5 KiB batches in flight); measured on the 3B
+// decode matrices, groups of four with two batches ahead (two waves per
+// SIMD) were slower in every kernel.
+constexpr int kRowGroup = 2;
 // Result stores a wave holds back per group (two per unit).
 constexpr int kPendingPerWave = 2 * kRowGroup;
 
@@ -56,11 +58,10 @@ struct PendingSink {
   __device__ void f32(float *p, float v) const { rec(p, __float_as_uint(v), 0u); }
   __device__ void f16(uint16_t *p, uint16_t v) const { rec(p, (uint32_t)v, 1u); }
 };
-constexpr int kAhead = 2;
+constexpr int kAhead = 1;
 // Batches of the next group issued before a group's result code: one for
 // the 16-byte-value formats; none for the 5/6-bit formats, whose batches
-// (with block headers and high bits) would then exceed the registers of
-// two waves per SIMD, as would a second batch for any format.
+// carry block headers and high bits as well.
 template <int F>
 constexpr int carry_for() {
   return F == FMT_Q5_1 || F == FMT_Q4_K || F == FMT_Q5_K || F == FMT_Q6_K ? 0 : 1;
@@ -251,15 +252,13 @@ __host__ __device__ inline void slice_range(const SliceShape &sh, int nch, int s
 // each group's results are stored, with the next unit the wave takes
 // (INT_MAX when none), and once more with INT_MAX at the end. `blocks` is
 // the number of blocks sharing the units (blocks 0 .. blocks - 1 of the
-// launch; 0 = the whole grid). With PHASED, a wave's units below
-// `phase_unit` run in groups of their own, before its later units.
+// launch; 0 = the whole grid).
 template <int F, int T, int CPL, int R, bool XFIRST, bool PREWAIT, int PRE, bool AUX, bool COH = false,
-          bool PHASED = false, typename Rows, typename XLoad, typename AuxLoad, typename Pre, typename Prologue, typename Done,
+          typename Rows, typename XLoad, typename AuxLoad, typename Pre, typename Prologue, typename Done,
           typename Hook = void (*)(int)>
 __device__ __forceinline__ void stream_rows(const MatDesc &M, int n_units, int split, float *red, PendingStore *pend,
                                             Rows unit_rows, XLoad x_load, AuxLoad aux_load, Pre pre, Prologue prologue,
-                                            Done done, Hook hook = [](int) {}, int blocks = 0,
-                                            int phase_unit = INT_MAX) {
+                                            Done done, Hook hook = [](int) {}, int blocks = 0) {
   constexpr int VPC = Fmt<F>::VPC, K = kRowGroup;
   // The wave index in a scalar register: everything per wave below (slice,
   // row group, units, whether a batch is real) is then scalar, and so is
@@ -412,18 +411,11 @@ __device__ __forceinline__ void stream_rows(const MatDesc &M, int n_units, int s
     if constexpr (!XFIRST) load_x();
     group(n_tag, std::integral_constant<int, PI>{}, n_next);
   };
-  // Units below phase_unit: the local indices below nj1, so this wave's
-  // first nb1 units.
-  int left = nb, left1 = 0;
-  if constexpr (PHASED) {
-    const int nj1 = min(nj, max(0, (phase_unit - b0 + G - 1) / G));
-    left1 = rg < RG && nj1 > rg ? min(nb, (nj1 - rg + RG - 1) / RG) : 0;
-  }
-  auto peek = [&]() { return PHASED && left1 > 0 ? min(left1, K) : min(left, K); };
+  int left = nb;
+  auto peek = [&]() { return min(left, K); };
   auto take = [&]() {
     const int n = peek();
     left -= n;
-    if constexpr (PHASED) left1 = max(left1 - n, 0);
     return n;
   };
   // Groups after the first find min(kCarry, N) of their batches issued by
