@@ -193,8 +193,8 @@ __device__ __forceinline__ void decode_in_body(const InArgs &a, float *lds_raw, 
   auto done = [&](int u, const float (&r)[2][2], const float (&)[2], const auto &out) {
     in_pair_outputs(s, kv, rope_row, pos, u, r[0][0], r[1][0], a.q_out, a.m_out, out);
   };
-  stream_rows<F, T, cpl_for<F>(), 2, false, true, 1, false, COH>(W, W.rows / 2, W.chunks, part, pend, rows, xload,
-                                                             noaux, pre, prologue, done, hook, blocks);
+  stream_rows<F, T, cpl_for<F>(), 2, false, true, 1, false, COH, COH>(W, W.rows / 2, W.chunks, part, pend, rows,
+                                                                  xload, noaux, pre, prologue, done, hook, blocks);
 }
 
 template <int F, int T>

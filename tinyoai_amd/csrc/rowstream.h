@@ -252,9 +252,11 @@ __host__ __device__ inline void slice_range(const SliceShape &sh, int nch, int s
 // each group's results are stored, with the next unit the wave takes
 // (INT_MAX when none), and once more with INT_MAX at the end. `blocks` is
 // the number of blocks sharing the units (blocks 0 .. blocks - 1 of the
-// launch; 0 = the whole grid).
+// launch; 0 = the whole grid). With DRAIN_FIRST the first group issues
+// none of the next group's batches, so a hook that waits for the wave's
+// stores after it waits for nothing else.
 template <int F, int T, int CPL, int R, bool XFIRST, bool PREWAIT, int PRE, bool AUX, bool COH = false,
-          typename Rows, typename XLoad, typename AuxLoad, typename Pre, typename Prologue, typename Done,
+          bool DRAIN_FIRST = false, typename Rows, typename XLoad, typename AuxLoad, typename Pre, typename Prologue, typename Done,
           typename Hook = void (*)(int)>
 __device__ __forceinline__ void stream_rows(const MatDesc &M, int n_units, int split, float *red, PendingStore *pend,
                                             Rows unit_rows, XLoad x_load, AuxLoad aux_load, Pre pre, Prologue prologue,
@@ -409,7 +411,7 @@ __device__ __forceinline__ void stream_rows(const MatDesc &M, int n_units, int s
     for (int t = 0; t < PI; t++) issue(t);
     prologue();
     if constexpr (!XFIRST) load_x();
-    group(n_tag, std::integral_constant<int, PI>{}, n_next);
+    group(n_tag, std::integral_constant<int, PI>{}, DRAIN_FIRST ? 0 : n_next);
   };
   int left = nb;
   auto peek = [&]() { return min(left, K); };
@@ -427,6 +429,12 @@ __device__ __forceinline__ void stream_rows(const MatDesc &M, int n_units, int s
   if (left > 0) {
     const int n = take(), nn = peek();
     group_of_size<K>(n, [&](auto n_tag) { first(n_tag, nn); });
+    if constexpr (DRAIN_FIRST) {  // the second group issues all of its batches
+      if (left > 0) {
+        const int n2 = take(), nn2 = peek();
+        group_of_size<K>(n2, [&](auto n_tag) { group(n_tag, std::integral_constant<int, 0>{}, nn2); });
+      }
+    }
   } else {
     prologue();
     if constexpr (!XFIRST) load_x();
