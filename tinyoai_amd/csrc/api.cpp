@@ -526,13 +526,13 @@ int StableModel::init(const tinyoai_stablelm_config &c, const tinyoai_tensor *te
   if (e != hipSuccess) return hip_fail(e, "model upload");
   const int cus = device_cu_count();
   // Row-streaming matvecs (measured on MI355X at the 3B shapes): two
-  // 256-thread blocks per CU for the layer products, 512 threads for the
-  // classifier.
+  // 256-thread blocks per CU for the layer products, one 512-thread block
+  // per CU for the classifier.
   grid_in = cus * 2;
   threads_in = 256;
   grid_out = cus * 2;
   threads_out = 256;
-  grid_head = cus * 2;
+  grid_head = cus;
   threads_head = 512;
   return TINYOAI_OK;
 }

@@ -254,9 +254,10 @@ __host__ __device__ inline void slice_range(const SliceShape &sh, int nch, int s
 // the number of blocks sharing the units (blocks 0 .. blocks - 1 of the
 // launch; 0 = the whole grid). With DRAIN_FIRST the first group issues
 // none of the next group's batches, so a hook that waits for the wave's
-// stores after it waits for nothing else.
+// stores after it waits for nothing else; with NOCARRY no group does (a
+// kernel held to fewer registers).
 template <int F, int T, int CPL, int R, bool XFIRST, bool PREWAIT, int PRE, bool AUX, bool COH = false,
-          bool DRAIN_FIRST = false, typename Rows, typename XLoad, typename AuxLoad, typename Pre, typename Prologue, typename Done,
+          bool DRAIN_FIRST = false, bool NOCARRY = false, typename Rows, typename XLoad, typename AuxLoad, typename Pre, typename Prologue, typename Done,
           typename Hook = void (*)(int)>
 __device__ __forceinline__ void stream_rows(const MatDesc &M, int n_units, int split, float *red, PendingStore *pend,
                                             Rows unit_rows, XLoad x_load, AuxLoad aux_load, Pre pre, Prologue prologue,
@@ -343,7 +344,7 @@ __device__ __forceinline__ void stream_rows(const MatDesc &M, int n_units, int s
   // the last consume the first min(kCarry, n_next) batches of the next
   // group (n_next units) are issued into the consumed batches' registers,
   // so the wave's loads stay in flight through the result code.
-  constexpr int kCarry = carry_for<F>();
+  constexpr int kCarry = NOCARRY ? 0 : carry_for<F>();
   auto group = [&](auto n_tag, auto p0_tag, int n_next) {
     constexpr int N = decltype(n_tag)::value, P0 = decltype(p0_tag)::value;
     int r[N][R];  // float bits, wave-uniform (scalar registers)
