@@ -218,7 +218,10 @@ int tinyoai_stablelm_profile(tinyoai_model *m, int32_t enable);
  * path: within 2e-2 of the logit range, faster on the matrix cores; greedy
  * ids may then differ from the fp32 engine's where logits nearly tie),
  * zero (the default) keeps two bf16 planes per activation (16 significant
- * bits). Returns 0 or TINYOAI_EINVAL. */
+ * bits). Stage 7: grid nonzero (the default) runs the BF16-weight prefill
+ * products on hipBLASLt (fp32 accumulation; the sums' order differs from
+ * the hand-written matrix-core kernel's, which zero selects). Returns 0 or
+ * TINYOAI_EINVAL. */
 int tinyoai_stablelm_set_launch(tinyoai_model *m, int32_t stage, int32_t grid, int32_t threads);
 int tinyoai_stablelm_profile_read(tinyoai_model *m, double *ms, int64_t *counts, int32_t n_stages);
 

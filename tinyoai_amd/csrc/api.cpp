@@ -307,6 +307,7 @@ void Profiler::clear() {
 // ---------------------------------------------------------------- StableLM
 StableModel::~StableModel() {
   free_kv();
+  blaslt_destroy(blas);
   for (void *p : buffers) hipFree(p);
   if (h_pinned) hipHostFree(h_pinned);
   if (h_io) hipHostFree(h_io);
@@ -794,8 +795,27 @@ int StableModel::project(const MatDesc &w, const float *x, int ldx, int n, float
 }
 
 
+bool StableModel::blas_product(const MatDesc &w, const uint16_t *xh, const uint16_t *xl, int n, float *y,
+                               int ldy) {
+  if (!use_blaslt || w.fmt != FMT_BF16) return false;
+  if (!blas_tried) {
+    blas_tried = true;
+    blas = blaslt_create();
+  }
+  if (!blas) return false;
+  prof.begin(ST_PREFILL_GEMM, stream);
+  hipError_t e = blaslt_bf16_product(blas, w, xh, n, y, ldy, false, stream);
+  if (e == hipSuccess && xl) e = blaslt_bf16_product(blas, w, xl, n, y, ldy, true, stream);
+  prof.end(stream);
+  return e == hipSuccess;
+}
+
 int StableModel::project_planes(const MatDesc &w, const uint16_t *xh, const uint16_t *xl, int n, float *y, int ldy,
                                 int *splits) {
+  if (blas_product(w, xh, xl, n, y, ldy)) {
+    if (splits) *splits = 1;
+    return TINYOAI_OK;
+  }
   const int ks = splits ? gemm_splits(w, n, kPrefillSplits) : 1;
   if (splits) *splits = ks;
   STAGE(ST_PREFILL_GEMM, launch_gemm_mfma(w, xh, xl, n, y, ldy, stream, ks), "projection");
@@ -847,10 +867,13 @@ int StableModel::prefill_chunk(const int32_t *ids, int n, int start, bool want_l
             launch_in_epilogue(dm, kv[l], Ym, rm, rope, d_pos0, n, Q, m32, stream, pd ? MH : nullptr,
                                pd ? ML : nullptr),
             "in_epilogue");
-    } else if (pin && pd) {
+    } else if (pin && pd && !blas_product(w.win, XH, lo_plane(w.win), n, Y, win_rows)) {
       const InEpilogue e{dims, kv[l], rope, d_pos0, Q, m32, MH, ML};
       STAGE(ST_PREFILL_GEMM, launch_gemm_in_epilogue(w.win, XH, lo_plane(w.win), n, e, stream),
             "projection + epilogue");
+    } else if (pin && pd) {  // the product is in Y (hipBLASLt)
+      STAGE(ST_PREFILL_EPILOGUE,
+            launch_in_epilogue(dims, kv[l], Y, win_rows, rope, d_pos0, n, Q, m32, stream, MH, ML), "in_epilogue");
     } else {
       if ((rc = pin ? project_planes(w.win, XH, lo_plane(w.win), n, Y, win_rows)
                     : project(w.win, H, d, n, Y, win_rows)))
@@ -1568,6 +1591,10 @@ int tinyoai_stablelm_trace_read_stages(tinyoai_model *m, float *attention, float
 int tinyoai_stablelm_set_launch(tinyoai_model *m, int32_t stage, int32_t grid, int32_t threads) {
   if (!m || !m->stable) return fail(TINYOAI_EINVAL, "not a StableLM handle");
   StableModel &s = *m->stable;
+  if (stage == 7) {  // BF16-weight prefill products on hipBLASLt (1, the default) or the matrix-core kernel (0)
+    s.use_blaslt = grid != 0;
+    return TINYOAI_OK;
+  }
   if (stage == 5) {  // BF16-weight prefill products with bf16 activations (1) or two planes (0, the default)
     s.bf16_acts = grid != 0;
     return TINYOAI_OK;

@@ -189,6 +189,15 @@ hipError_t launch_gemm(const MatDesc &w, const float *x, int n, float *out, hipS
 // most max_splits).
 bool gemm_mfma_supported(const MatDesc &w);
 int gemm_planes(const MatDesc &w, bool bf16_path = false);
+// The same product for BF16 weights on hipBLASLt (one bf16 plane X per
+// call; accumulate: y += X W^T, else y = X W^T). hipErrorNotSupported when
+// the library has no algorithm for the shape (the caller's own kernel then
+// runs it).
+struct BlasLt;
+BlasLt *blaslt_create();
+void blaslt_destroy(BlasLt *b);
+hipError_t blaslt_bf16_product(BlasLt *b, const MatDesc &w, const uint16_t *x, int m, float *y, int ldy,
+                               bool accumulate, hipStream_t st);
 int gemm_splits(const MatDesc &w, int M, int max_splits);
 hipError_t launch_gemm_mfma(const MatDesc &w, const uint16_t *xh, const uint16_t *xl, int M, float *y, int ldy,
                             hipStream_t st, int ksplit = 1);

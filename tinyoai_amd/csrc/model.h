@@ -179,6 +179,13 @@ struct StableModel {
   const uint16_t *lo_plane(const MatDesc &w) const { return gemm_planes(w, bf16_acts) == 2 ? XL : nullptr; }
   int project_planes(const MatDesc &w, const uint16_t *xh, const uint16_t *xl, int n, float *y, int ldy,
                      int *splits = nullptr);
+  // BF16-weight prefill products on hipBLASLt (set_launch stage 7, on by
+  // default; the handle is made on first use): y = xh W^T (+ xl W^T).
+  // False where it does not apply or the library has no algorithm (the
+  // matrix-core kernel then runs the product).
+  bool use_blaslt = true, blas_tried = false;
+  BlasLt *blas = nullptr;
+  bool blas_product(const MatDesc &w, const uint16_t *xh, const uint16_t *xl, int n, float *y, int ldy);
   int prefill_chunk(const int32_t *ids, int n, int start, bool want_logits);
   // Scoring of a forward_logprobs call: while set, prefill_chunk also
   // computes every row's logits and their log probabilities (device

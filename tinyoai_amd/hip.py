@@ -268,6 +268,8 @@ class StableLMForwarder:
         toks = np.ascontiguousarray(tokens, np.int32)
         tg = np.ascontiguousarray(targets, np.int32)
         n = toks.size
+        if tg.size != n:  # the C entry point takes one count for both (mlx_native.go:303-305)
+            raise TinyoaiError("invalid probability request: targets do not align with tokens")
         logits = np.empty(self.vocab, np.float32)
         chosen = np.empty(n, np.float64)
         ids = np.empty((n, count), np.int32)
@@ -347,12 +349,12 @@ class StableLMForwarder:
               "prefill_projections", "prefill_epilogue", "prefill_attention", "prefill_elementwise")
 
     LAUNCH_STAGES = {"decode_in": 0, "decode_out": 1, "lm_head": 2, "attention": 3, "fused_attention": 4,
-                     "bf16_activations": 5}
+                     "bf16_activations": 5, "blaslt": 7}
 
     def set_launch(self, stage: str, grid: int, threads: int) -> None:
         """Launch shape (blocks, threads per block) of a decode matrix
         kernel (results do not depend on it), or a switch (stages
-        "fused_attention" and "bf16_activations": grid nonzero = on)."""
+        "fused_attention", "bf16_activations" and "blaslt": grid nonzero = on)."""
         check(lib().tinyoai_stablelm_set_launch(self.h, self.LAUNCH_STAGES[stage], int(grid), int(threads)))
 
     def profile(self, enable: bool = True) -> None:
