@@ -102,20 +102,36 @@ __global__ void in_epilogue_kernel(StableDims s, KVDev kv, const float *y, int l
   const int mu0 = (s.win_q + 2 * s.win_kv) / 2;
   float *qj = q + (int64_t)j * s.heads * s.hd, *mj = m ? m + (int64_t)j * s.inter : nullptr;
   const int64_t split = (int64_t)gridDim.x * ldy;
-  // blockIdx.y takes every gridDim.y-th group of blockDim.x units
-  for (int u = blockIdx.y * blockDim.x + threadIdx.x; u < units; u += gridDim.y * blockDim.x) {
-    float2 v = *reinterpret_cast<const float2 *>(yj + 2 * u);
-    for (int s2 = 1; s2 < ys; s2++) {
-      const float2 t = *reinterpret_cast<const float2 *>(yj + s2 * split + 2 * u);
-      v.x = __fadd_rn(v.x, t.x);
-      v.y = __fadd_rn(v.y, t.y);
+  // blockIdx.y takes every gridDim.y-th group of blockDim.x units; a thread
+  // loads kBatch of its units before it stores any (the stores could alias
+  // y as far as the compiler knows, so loads placed after them would each
+  // wait a memory round trip).
+  constexpr int kBatch = 4;
+  const int stride = gridDim.y * blockDim.x;
+  for (int u0 = blockIdx.y * blockDim.x + threadIdx.x; u0 < units; u0 += kBatch * stride) {
+    float2 v[kBatch];
+#pragma unroll
+    for (int b = 0; b < kBatch; b++) {
+      const int u = u0 + b * stride;
+      v[b] = u < units ? *reinterpret_cast<const float2 *>(yj + 2 * u) : make_float2(0.f, 0.f);
+      for (int s2 = 1; s2 < ys; s2++) {
+        if (u >= units) break;
+        const float2 t = *reinterpret_cast<const float2 *>(yj + s2 * split + 2 * u);
+        v[b].x = __fadd_rn(v[b].x, t.x);
+        v[b].y = __fadd_rn(v[b].y, t.y);
+      }
     }
-    if (mh && u >= mu0) {
-      const float g = s.silu ? silu_gate_llama(v.x, v.y) : silu_gate(v.x, v.y);
-      if (mj) mj[u - mu0] = g;
-      store_bf16_split(mh, ml, (int64_t)j * s.inter + (u - mu0), g);
-    } else {
-      in_pair_epilogue(s, kv, rope_row, slot, u, v.x, v.y, qj, mj);
+#pragma unroll
+    for (int b = 0; b < kBatch; b++) {
+      const int u = u0 + b * stride;
+      if (u >= units) break;
+      if (mh && u >= mu0) {
+        const float g = s.silu ? silu_gate_llama(v[b].x, v[b].y) : silu_gate(v[b].x, v[b].y);
+        if (mj) mj[u - mu0] = g;
+        store_bf16_split(mh, ml, (int64_t)j * s.inter + (u - mu0), g);
+      } else {
+        in_pair_epilogue(s, kv, rope_row, slot, u, v[b].x, v[b].y, qj, mj);
+      }
     }
   }
 }
