@@ -282,9 +282,10 @@ __device__ __forceinline__ void attention_block(const AttArgs &a, const int spli
   // M = max m_r, e_r = exp(m_r - M), out[d] = sum o_r[d] e_r / sum l_r e_r,
   // rescaled from one staged chunk to the next. Every thread forms the same
   // M and L from the same LDS values.
-  // (4 KiB of LDS: the input-side launch that runs these blocks holds two
-  // blocks per CU.)
-  constexpr int RS = HD + 2, kRec = 1024 / RS;
+  // (FUSED: 4 KiB of LDS, so the input-side launch that runs these blocks
+  // keeps three blocks per CU; else 16 KiB, which holds a branch query's
+  // shared-prefix records and suffix splits in one round.)
+  constexpr int RS = HD + 2, kRec = (FUSED ? 1024 : 4096) / RS;
   static_assert(HD <= kThreads && kRec <= 512, "one output dimension per thread; weights in s_e");
   __shared__ float s_rec[kRec * RS];
   const int total = pre + nsplit;
