@@ -206,14 +206,16 @@ hipError_t launch_gemm_mfma(const MatDesc &w, const uint16_t *xh, const uint16_t
 // [M][ldx] (16-byte aligned, ldx % 4 == 0), converted first into `stage`
 // (16-byte aligned device memory of kq_rows_stage_bytes(K, M) bytes). With
 // ks > 1 the K range is cut in ks parts whose products go to
-// y + s * M * ldy, for the caller to sum; kq_rows_splits: the split count
-// that fills the device for this matrix (at most max_splits). With staged,
-// `stage` already holds this X (a previous call's, same M and K).
+// y + s * split_stride (0: M * ldy; a larger stride lets row slices of one
+// product share the caller's split layout), for the caller to sum;
+// kq_rows_splits: the split count that fills the device for this matrix
+// (at most max_splits). With staged, `stage` already holds this X (a
+// previous call's, same M and K).
 bool kq_rows_supported(const MatDesc &w, int M);
 size_t kq_rows_stage_bytes(int K, int M);
 int kq_rows_splits(const MatDesc &w, int max_splits);
 hipError_t launch_kq_rows(const MatDesc &w, const float *x, int ldx, int M, float *y, int ldy, int ks, void *stage,
-                          hipStream_t st, bool staged = false);
+                          hipStream_t st, bool staged = false, int64_t split_stride = 0);
 // The fused in-projection epilogue of a matrix-core win product for M
 // tokens at positions *pos0 + j: RoPE'd q [M][heads*hd], K/V into the
 // cache, and the SiLU-gate outputs as bf16 planes mh, ml [M][inter] (and

@@ -23,8 +23,8 @@
 // v_mfma_f32_16x16x16_bf16, one per 16-value sub-block, for Q6_K). The
 // batches run as a software pipeline: the next batch's quants and staged
 // chunks are in flight while one is computed. K ranges (splits) write
-// separate partial outputs, split s at y + s * M * ldy, which the
-// consumer sums.
+// separate partial outputs, split s at y + s * split_stride (by default
+// M * ldy), which the consumer sums.
 //
 // Staged value order: a 16x16x32 product gives lane group g = lane / 16
 // the 8 positions 8g..8g+7 of each chunk. The quants of a chunk sit as
@@ -63,6 +63,7 @@ struct KqArgs {
   int M;
   float *y;
   int ldy, ks;
+  int64_t split_stride;  // floats between the K splits' outputs
 };
 
 // x [M][K] -> staged chunks. Item i: group of 4 values i % 8 of row
@@ -160,7 +161,7 @@ __global__ __launch_bounds__(kThreads) void kq_rows_kernel(KqArgs g) {
   const int batches = (nch + 7) / 8;
   const int b_lo = (int)((int64_t)batches * split / g.ks), b_hi = (int)((int64_t)batches * (split + 1) / g.ks);
   const int c_lo = b_lo * 8, c_hi = min(nch, b_hi * 8);
-  float *y = g.y + (int64_t)split * g.M * g.ldy;
+  float *y = g.y + (int64_t)split * g.split_stride;
 
   // ---- staged chunks [c0, min(c0 + 8, c_hi)) -> window buffer buf.
   // Buffer loads: pieces past the staged chunks read zeros (stored into
@@ -481,11 +482,13 @@ int kq_rows_splits(const MatDesc &w, int max_splits) {
 }
 
 hipError_t launch_kq_rows(const MatDesc &w, const float *x, int ldx, int M, float *y, int ldy, int ks, void *stage,
-                          hipStream_t st, bool staged) {
+                          hipStream_t st, bool staged, int64_t split_stride) {
   if (!kq_rows_supported(w, M) || ks < 1 || ks > (w.cols / 32 + 7) / 8 || ldx < w.cols || ldy < w.rows ||
       (reinterpret_cast<uintptr_t>(x) & 15) || (ldx & 3) || !stage || (reinterpret_cast<uintptr_t>(stage) & 15))
     return hipErrorInvalidValue;
-  KqArgs g{w, static_cast<const uint8_t *>(stage), M, y, ldy, ks};
+  if (split_stride == 0) split_stride = (int64_t)M * ldy;
+  if (ks > 1 && split_stride < (int64_t)M * ldy) return hipErrorInvalidValue;
+  KqArgs g{w, static_cast<const uint8_t *>(stage), M, y, ldy, ks, split_stride};
   uint8_t *sb = static_cast<uint8_t *>(stage);
   if (M <= 16) {
     const hipError_t e = staged ? hipSuccess : kq_stage<1>(x, ldx, M, w.cols, sb, st);
