@@ -506,9 +506,12 @@ int StableModel::init(const tinyoai_stablelm_config &c, const tinyoai_tensor *te
       (rc = alloc((void **)&Y, B * win_rows * 4)) || (rc = alloc((void **)&Q, B * w_att * 4)) ||
       (rc = alloc((void **)&M, B * I * 4)) || (rc = alloc((void **)&A, B * w_att * 4)) ||
       (rc = alloc((void **)&P, kPrefillSplits * B * d * 4)) || (rc = alloc((void **)&D, kPrefillSplits * B * d * 4)) ||
-      (rc = alloc((void **)&XH, B * wide * 2)) || (rc = alloc((void **)&XL, B * wide * 2)) ||
-      (rc = alloc((void **)&MH, B * I * 2)) || (rc = alloc((void **)&ML, B * I * 2)))
+      (rc = alloc((void **)&XH, 2 * B * wide * 2)) || (rc = alloc((void **)&MH, 2 * B * I * 2)))
     return rc;
+  // One allocation per operand: the hi plane, then the lo plane; joined
+  // products use the whole of it as rows [hi | lo].
+  XL = XH + B * wide;
+  ML = MH + B * I;
   // The error word after the logits: set by a decode step whose bounded
   // in-kernel wait timed out.
   perr = (unsigned *)(logits_dev + c.vocab_size);
@@ -809,14 +812,17 @@ int StableModel::project(const MatDesc &w, const float *x, int ldx, int n, float
 }
 
 
-bool StableModel::blas_product(const MatDesc &w, const uint16_t *xh, const uint16_t *xl, int n, float *y,
-                               int ldy) {
-  if (!use_blaslt || w.fmt != FMT_BF16) return false;
+bool StableModel::blas_ready() {
   if (!blas_tried) {
     blas_tried = true;
     blas = blaslt_create();
   }
-  if (!blas) return false;
+  return blas != nullptr;
+}
+
+bool StableModel::blas_product(const MatDesc &w, const uint16_t *xh, const uint16_t *xl, int n, float *y,
+                               int ldy) {
+  if (!use_blaslt || w.fmt != FMT_BF16 || !blas_ready()) return false;
   prof.begin(ST_PREFILL_GEMM, stream);
   hipError_t e = blaslt_bf16_product(blas, w, xh, n, y, ldy, false, stream);
   if (e == hipSuccess && xl) e = blaslt_bf16_product(blas, w, xl, n, y, ldy, true, stream);
@@ -834,6 +840,70 @@ int StableModel::project_planes(const MatDesc &w, const uint16_t *xh, const uint
   if (splits) *splits = ks;
   STAGE(ST_PREFILL_GEMM, launch_gemm_mfma(w, xh, xl, n, y, ldy, stream, ks), "projection");
   return TINYOAI_OK;
+}
+
+// The prefill copies of the joined-plane products for every layer whose
+// win and wout are BF16 and fused (rows of each weight row twice).
+int StableModel::ensure_joined() {
+  if (joined_tried) return TINYOAI_OK;
+  joined_tried = true;
+  const int L = cfg.num_hidden_layers;
+  joined_in.assign(L, MatDesc{});
+  joined_out.assign(L, MatDesc{});
+  const int64_t d = dims.d, I = dims.inter;
+  for (int l = 0; l < L; l++) {
+    const LayerDev &w = layers[l];
+    if (w.win.fmt != FMT_BF16 || w.wout.fmt != FMT_BF16 || w.win2.rows || w.wout2.rows) continue;
+    const int64_t down0 = (d + 7) / 8 * 8;
+    if (w.wout.cols < down0 + I) continue;
+    MatDesc a{}, b{};
+    a.fmt = b.fmt = FMT_BF16;
+    a.rows = w.win.rows;
+    a.cols = 2 * w.win.cols;
+    a.vstride = ((int64_t)a.cols * 2 + 15) / 16 * 16;
+    a.chunks = (int32_t)(a.vstride / 16);
+    b.rows = w.wout.rows;
+    b.cols = (int32_t)(2 * d + 2 * I);
+    b.vstride = ((int64_t)b.cols * 2 + 15) / 16 * 16;
+    b.chunks = (int32_t)(b.vstride / 16);
+    void *pa = nullptr, *pb = nullptr;
+    if (int rc = alloc(&pa, (size_t)a.rows * a.vstride)) return rc;
+    if (int rc = alloc(&pb, (size_t)b.rows * b.vstride)) return rc;
+    a.vals = (const uint8_t *)pa;
+    b.vals = (const uint8_t *)pb;
+    const size_t wi = (size_t)w.win.cols * 2;
+    for (int c = 0; c < 2; c++)
+      TRY_HIP(hipMemcpy2DAsync((char *)pa + c * wi, a.vstride, w.win.vals, w.win.vstride, wi, a.rows,
+                               hipMemcpyDeviceToDevice, stream),
+              "joined copy");
+    const size_t wo = (size_t)d * 2, wd = (size_t)I * 2;
+    for (int c = 0; c < 2; c++) {
+      TRY_HIP(hipMemcpy2DAsync((char *)pb + c * wo, b.vstride, w.wout.vals, w.wout.vstride, wo, b.rows,
+                               hipMemcpyDeviceToDevice, stream),
+              "joined copy");
+      TRY_HIP(hipMemcpy2DAsync((char *)pb + 2 * wo + c * wd, b.vstride, w.wout.vals + down0 * 2, w.wout.vstride, wd,
+                               b.rows, hipMemcpyDeviceToDevice, stream),
+              "joined copy");
+    }
+    joined_in[l] = a;
+    joined_out[l] = b;
+  }
+  return TINYOAI_OK;
+}
+
+// Whether layer l's products of an n-row chunk run joined (the copies made
+// and the library holding a plan for each of the three shapes).
+bool StableModel::joined_layer(int l, int n) {
+  if (!use_joined || !use_blaslt || bf16_acts || !blas_ready()) return false;
+  const LayerDev &w = layers[l];
+  if (w.win.fmt != FMT_BF16 || w.wout.fmt != FMT_BF16 || w.win2.rows || w.wout2.rows ||
+      !flash_prefill_supported(dims.hd) || dims.heads * dims.hd != dims.d)
+    return false;
+  if (ensure_joined() || joined_in[l].rows == 0) return false;
+  const int64_t d = dims.d, I = dims.inter;
+  return blaslt_bf16_ready(blas, joined_in[l], n, win_rows) &&
+         blaslt_bf16_ready(blas, column_view(joined_out[l], 0, 2 * d), n, (int)d) &&
+         blaslt_bf16_ready(blas, column_view(joined_out[l], 2 * d, 2 * I), n, (int)d);
 }
 
 // n tokens at positions start.. (StableLM.prefill, prefill.go:33-115): per
@@ -860,57 +930,79 @@ int StableModel::prefill_chunk(const int32_t *ids, int n, int start, bool want_l
     // the matrix cores) -> MH, ML -> down; attention -> XH, XL -> o.
     const bool pin = !split_in && gemm_mfma_supported(w.win), pd = gemm_mfma_supported(wd);
     const bool flash = flash_prefill_supported(dims.hd), po = flash && gemm_mfma_supported(wo);
-    STAGE(ST_PREFILL_NORM,
-          launch_layer_norm_rows(X, w.ln_w, w.ln_b, dims.eps, n, d, pin ? nullptr : H, stream, pin ? XH : nullptr,
-                                 pin ? XL : nullptr),
-          "layer_norm");
-    float *m32 = pd && !tracing ? nullptr : M;
-    if (split_in) {
-      // [q | k | v] and the gate/up pairs in formats of their own: two
-      // products from the fp32 LayerNorm output, then the epilogue of each
-      // section (q/k/v rows only, then gate/up pairs only).
-      StableDims da = dims, dm = dims;
-      da.inter = 0;
-      dm.win_q = dm.win_kv = 0;
-      const int ra = w.win.rows, rm = w.win2.rows;
-      float *Ya = Y, *Ym = Y + (size_t)n * ra;
-      if ((rc = project(w.win, H, d, n, Ya, ra)) || (rc = project(w.win2, H, d, n, Ym, rm))) return rc;
+    if (pin && pd && po && joined_layer(l, n)) {
+      // One product per matrix over operand rows [hi | lo] (K doubled)
+      // against the layer's prefill copies.
+      const MatDesc wj = joined_in[l], woj = column_view(joined_out[l], 0, 2 * d),
+                    wdj = column_view(joined_out[l], 2 * d, 2 * I);
+      STAGE(ST_PREFILL_NORM,
+            launch_layer_norm_rows(X, w.ln_w, w.ln_b, dims.eps, n, d, nullptr, stream, XH, XH + d, 2 * d),
+            "layer_norm");
+      STAGE(ST_PREFILL_GEMM, blaslt_bf16_product(blas, wj, XH, n, Y, win_rows, false, stream), "projection");
       STAGE(ST_PREFILL_EPILOGUE,
-            launch_in_epilogue(da, kv[l], Ya, ra, rope, d_pos0, n, Q, M, stream, nullptr, nullptr), "in_epilogue");
-      STAGE(ST_PREFILL_EPILOGUE,
-            launch_in_epilogue(dm, kv[l], Ym, rm, rope, d_pos0, n, Q, m32, stream, pd ? MH : nullptr,
-                               pd ? ML : nullptr),
+            launch_in_epilogue(dims, kv[l], Y, win_rows, rope, d_pos0, n, Q, tracing ? M : nullptr, stream, MH,
+                               MH + I, nullptr, 1, 2 * I),
             "in_epilogue");
-    } else if (pin && pd && !blas_product(w.win, XH, lo_plane(w.win), n, Y, win_rows)) {
-      const InEpilogue e{dims, kv[l], rope, d_pos0, Q, m32, MH, ML};
-      STAGE(ST_PREFILL_GEMM, launch_gemm_in_epilogue(w.win, XH, lo_plane(w.win), n, e, stream),
-            "projection + epilogue");
-    } else if (pin && pd) {  // the product is in Y (hipBLASLt)
-      STAGE(ST_PREFILL_EPILOGUE,
-            launch_in_epilogue(dims, kv[l], Y, win_rows, rope, d_pos0, n, Q, m32, stream, MH, ML), "in_epilogue");
-    } else {
-      if ((rc = pin ? project_planes(w.win, XH, lo_plane(w.win), n, Y, win_rows)
-                    : project(w.win, H, d, n, Y, win_rows)))
-        return rc;
-      STAGE(ST_PREFILL_EPILOGUE,
-            launch_in_epilogue(dims, kv[l], Y, win_rows, rope, d_pos0, n, Q, m32, stream, pd ? MH : nullptr,
-                               pd ? ML : nullptr),
-            "in_epilogue");
-    }
-    int sp = 1, sd = 1;
-    if ((rc = pd ? project_planes(wd, MH, gemm_planes(wd, bf16_acts) == 2 ? ML : nullptr, n, D, d, &sd) : project(wd, M, I, n, D, d, &sd)))
-      return rc;
-    if (flash)
+      STAGE(ST_PREFILL_GEMM, blaslt_bf16_product(blas, wdj, MH, n, D, d, false, stream), "projection");
       STAGE(ST_PREFILL_ATTENTION,
-            launch_flash_prefill(dims, kv[l], Q, d_pos0, n, po && !tracing ? nullptr : A, stream, po ? XH : nullptr,
-                                 po ? XL : nullptr),
+            launch_flash_prefill(dims, kv[l], Q, d_pos0, n, tracing ? A : nullptr, stream, XH, XH + d, nullptr, 0,
+                                 0, 2 * d),
             "attention");
-    else
-      STAGE(ST_PREFILL_ATTENTION,
-            launch_attention(dims, kv[l], Q, d_pos0, n, start + n - 1, partials, counters, A, stream), "attention");
-    if ((rc = po ? project_planes(wo, XH, lo_plane(wo), n, P, d, &sp) : project(wo, A, d, n, P, d, &sp)))
-      return rc;
-    STAGE(ST_PREFILL_ELEMENTWISE, launch_residual(X, P, sp, D, sd, (int64_t)n * d, stream), "residual");
+      STAGE(ST_PREFILL_GEMM, blaslt_bf16_product(blas, woj, XH, n, P, d, false, stream), "projection");
+      STAGE(ST_PREFILL_ELEMENTWISE, launch_residual(X, P, 1, D, 1, (int64_t)n * d, stream), "residual");
+    } else {
+      STAGE(ST_PREFILL_NORM,
+            launch_layer_norm_rows(X, w.ln_w, w.ln_b, dims.eps, n, d, pin ? nullptr : H, stream, pin ? XH : nullptr,
+                                   pin ? XL : nullptr),
+            "layer_norm");
+      float *m32 = pd && !tracing ? nullptr : M;
+      if (split_in) {
+        // [q | k | v] and the gate/up pairs in formats of their own: two
+        // products from the fp32 LayerNorm output, then the epilogue of each
+        // section (q/k/v rows only, then gate/up pairs only).
+        StableDims da = dims, dm = dims;
+        da.inter = 0;
+        dm.win_q = dm.win_kv = 0;
+        const int ra = w.win.rows, rm = w.win2.rows;
+        float *Ya = Y, *Ym = Y + (size_t)n * ra;
+        if ((rc = project(w.win, H, d, n, Ya, ra)) || (rc = project(w.win2, H, d, n, Ym, rm))) return rc;
+        STAGE(ST_PREFILL_EPILOGUE,
+              launch_in_epilogue(da, kv[l], Ya, ra, rope, d_pos0, n, Q, M, stream, nullptr, nullptr), "in_epilogue");
+        STAGE(ST_PREFILL_EPILOGUE,
+              launch_in_epilogue(dm, kv[l], Ym, rm, rope, d_pos0, n, Q, m32, stream, pd ? MH : nullptr,
+                                 pd ? ML : nullptr),
+              "in_epilogue");
+      } else if (pin && pd && !blas_product(w.win, XH, lo_plane(w.win), n, Y, win_rows)) {
+        const InEpilogue e{dims, kv[l], rope, d_pos0, Q, m32, MH, ML};
+        STAGE(ST_PREFILL_GEMM, launch_gemm_in_epilogue(w.win, XH, lo_plane(w.win), n, e, stream),
+              "projection + epilogue");
+      } else if (pin && pd) {  // the product is in Y (hipBLASLt)
+        STAGE(ST_PREFILL_EPILOGUE,
+              launch_in_epilogue(dims, kv[l], Y, win_rows, rope, d_pos0, n, Q, m32, stream, MH, ML), "in_epilogue");
+      } else {
+        if ((rc = pin ? project_planes(w.win, XH, lo_plane(w.win), n, Y, win_rows)
+                      : project(w.win, H, d, n, Y, win_rows)))
+          return rc;
+        STAGE(ST_PREFILL_EPILOGUE,
+              launch_in_epilogue(dims, kv[l], Y, win_rows, rope, d_pos0, n, Q, m32, stream, pd ? MH : nullptr,
+                                 pd ? ML : nullptr),
+              "in_epilogue");
+      }
+      int sp = 1, sd = 1;
+      if ((rc = pd ? project_planes(wd, MH, gemm_planes(wd, bf16_acts) == 2 ? ML : nullptr, n, D, d, &sd) : project(wd, M, I, n, D, d, &sd)))
+        return rc;
+      if (flash)
+        STAGE(ST_PREFILL_ATTENTION,
+              launch_flash_prefill(dims, kv[l], Q, d_pos0, n, po && !tracing ? nullptr : A, stream, po ? XH : nullptr,
+                                   po ? XL : nullptr),
+              "attention");
+      else
+        STAGE(ST_PREFILL_ATTENTION,
+              launch_attention(dims, kv[l], Q, d_pos0, n, start + n - 1, partials, counters, A, stream), "attention");
+      if ((rc = po ? project_planes(wo, XH, lo_plane(wo), n, P, d, &sp) : project(wo, A, d, n, P, d, &sp)))
+        return rc;
+      STAGE(ST_PREFILL_ELEMENTWISE, launch_residual(X, P, sp, D, sd, (int64_t)n * d, stream), "residual");
+    }
     if (tracing) {
       TRY_HIP(launch_copy_row(X + (size_t)(n - 1) * d, trace_dev + (size_t)l * d, d, stream), "trace");
       TRY_HIP(launch_copy_row(A + (size_t)(n - 1) * d, trace_att + (size_t)l * d, d, stream), "trace");
@@ -1605,6 +1697,10 @@ int tinyoai_stablelm_trace_read_stages(tinyoai_model *m, float *attention, float
 int tinyoai_stablelm_set_launch(tinyoai_model *m, int32_t stage, int32_t grid, int32_t threads) {
   if (!m || !m->stable) return fail(TINYOAI_EINVAL, "not a StableLM handle");
   StableModel &s = *m->stable;
+  if (stage == 9) {  // joined-plane BF16 prefill products (1, the default) or two calls per product (0)
+    s.use_joined = grid != 0;
+    return TINYOAI_OK;
+  }
   if (stage == 7) {  // BF16-weight prefill products on hipBLASLt (1, the default) or the matrix-core kernel (0)
     s.use_blaslt = grid != 0;
     return TINYOAI_OK;

@@ -90,21 +90,30 @@ void blaslt_destroy(BlasLt *b) {
   delete b;
 }
 
+namespace {
+
+// The cached plan of a shape (made on first use; null where the library
+// has none).
+Plan *find_plan(BlasLt *b, const MatDesc &w, int m, int ldy, bool accumulate) {
+  if (!b || w.fmt != FMT_BF16 || m < 1 || w.vstride % 2 || ldy < w.rows) return nullptr;
+  const int64_t n = w.rows, k = w.cols, lda = w.vstride / 2;
+  for (Plan &q : b->plans)
+    if (q.m == m && q.n == n && q.k == k && q.lda == lda && q.ldy == ldy && q.acc == accumulate) return q.ok ? &q : nullptr;
+  Plan q;
+  q.m = m, q.n = n, q.k = k, q.lda = lda, q.ldy = ldy, q.acc = accumulate;
+  q.ok = make_plan(*b, q);
+  b->plans.push_back(q);
+  return q.ok ? &b->plans.back() : nullptr;
+}
+
+}  // namespace
+
+bool blaslt_bf16_ready(BlasLt *b, const MatDesc &w, int m, int ldy) { return find_plan(b, w, m, ldy, false) != nullptr; }
+
 hipError_t blaslt_bf16_product(BlasLt *b, const MatDesc &w, const uint16_t *x, int m, float *y, int ldy,
                                bool accumulate, hipStream_t st) {
-  if (!b || w.fmt != FMT_BF16 || m < 1 || w.vstride % 2 || ldy < w.rows) return hipErrorNotSupported;
-  const int64_t n = w.rows, k = w.cols, lda = w.vstride / 2;
-  Plan *p = nullptr;
-  for (Plan &q : b->plans)
-    if (q.m == m && q.n == n && q.k == k && q.lda == lda && q.ldy == ldy && q.acc == accumulate) p = &q;
-  if (!p) {
-    Plan q;
-    q.m = m, q.n = n, q.k = k, q.lda = lda, q.ldy = ldy, q.acc = accumulate;
-    q.ok = make_plan(*b, q);
-    b->plans.push_back(q);
-    p = &b->plans.back();
-  }
-  if (!p->ok) return hipErrorNotSupported;
+  Plan *p = find_plan(b, w, m, ldy, accumulate);
+  if (!p) return hipErrorNotSupported;
   const float alpha = 1.f, beta = accumulate ? 1.f : 0.f;
   const hipblasStatus_t s = hipblasLtMatmul(b->h, p->desc, &alpha, w.vals, p->la, x, p->lb, &beta, y, p->lc, y,
                                             p->lc, &p->algo, b->ws, p->ws, st);

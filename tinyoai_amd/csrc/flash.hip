@@ -38,6 +38,7 @@ struct FlashArgs {
   float *partials;
   int64_t region;
   int split_keys;
+  int64_t ld_o;  // values between the query rows of oh, ol (0: heads * hd)
 };
 
 // x = hi + lo to about 2^-22. The empty asm pins x as one fp32 value: when x
@@ -366,13 +367,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
     const int qi = qw + (v >> 2) * 8 + g * 4 + (v & 3);
     if (qi >= a.n) continue;
     const int64_t ob = ((int64_t)qi * s.heads + h) * HD;
+    const int64_t obp = a.ld_o ? (int64_t)qi * a.ld_o + h * HD : ob;
 #pragma unroll
     for (int t = 0; t < DT; t++) {
       const int dd = t * 32 + col;
       if (dd < HD) {
         const float r = o[t][v] / lq;
         if (a.out) a.out[ob + dd] = r;
-        if (a.oh) store_bf16_split(a.oh, a.ol, ob + dd, r);
+        if (a.oh) store_bf16_split(a.oh, a.ol, obp + dd, r);
       }
     }
   }
@@ -427,10 +429,10 @@ hipError_t launch_shared_prefix_attention(const StableDims &s, const KVDev &kv, 
 
 hipError_t launch_flash_prefill(const StableDims &s, const KVDev &kv, const float *q, const int *pos0, int n,
                                 float *out, hipStream_t st, uint16_t *oh, uint16_t *ol, const KVDev *sfx, int prefix,
-                                int sfx_slot0) {
-  if (!oh != !ol || (!out && !oh) || n < 1) return hipErrorInvalidValue;
+                                int sfx_slot0, int64_t ld_o) {
+  if (!oh != !ol || (!out && !oh) || n < 1 || (ld_o && ld_o < (int64_t)s.heads * s.hd)) return hipErrorInvalidValue;
   if (sfx && (sfx->half != kv.half || prefix < 0 || prefix > kv.cap || sfx_slot0 < 0)) return hipErrorInvalidValue;
-  FlashArgs a{s, kv, q, pos0, n, out, oh, ol, sfx ? *sfx : KVDev{}, prefix, sfx_slot0, nullptr, 0, 0};
+  FlashArgs a{s, kv, q, pos0, n, out, oh, ol, sfx ? *sfx : KVDev{}, prefix, sfx_slot0, nullptr, 0, 0, ld_o};
   const bool br = sfx != nullptr;
   switch (s.hd) {
     case 64: return flash32_dispatch<64>(a, br, st);

@@ -146,10 +146,11 @@ bool flash_prefill_supported(int hd);
 // out (fp32, may be null) and / or the bf16 operand planes oh, ol of the
 // matrix-core GEMM (null: none). With sfx, the queries are one branch's
 // rows: cache positions t >= prefix come from slot sfx_slot0 + (t - prefix)
-// of the branch cache sfx, positions below prefix from kv.
+// of the branch cache sfx, positions below prefix from kv. The planes' query
+// rows lie ld_o values apart (0: heads * hd).
 hipError_t launch_flash_prefill(const StableDims &s, const KVDev &kv, const float *q, const int *pos0, int n,
                                 float *out, hipStream_t st, uint16_t *oh = nullptr, uint16_t *ol = nullptr,
-                                const KVDev *sfx = nullptr, int prefix = 0, int sfx_slot0 = 0);
+                                const KVDev *sfx = nullptr, int prefix = 0, int sfx_slot0 = 0, int64_t ld_o = 0);
 int attention_steps(int max_pos, int heads);
 // Floats per (query, head) in the partials buffer: max_splits records of
 // hd + 2, rounded to 256 bytes.
@@ -176,9 +177,11 @@ hipError_t launch_embed(const MatDesc &emb, const int *ids, int n, float *x, hip
 
 
 // ---- prefill (n tokens) ----
-// out (fp32, may be null) and / or bf16 operand planes oh, ol (null: none).
+// out (fp32, may be null) and / or bf16 operand planes oh, ol (null: none)
+// with rows ldo values apart (0: d).
 hipError_t launch_layer_norm_rows(const float *x, const float *w, const float *b, double eps, int n, int d,
-                                  float *out, hipStream_t st, uint16_t *oh = nullptr, uint16_t *ol = nullptr);
+                                  float *out, hipStream_t st, uint16_t *oh = nullptr, uint16_t *ol = nullptr,
+                                  int ldo = 0);
 // out[n][rows] = x[n][cols] * W^T on the vector units (any format/shape).
 hipError_t launch_gemm(const MatDesc &w, const float *x, int n, float *out, hipStream_t st);
 // The matrix-core product: y[M][N] (row stride ldy) = X * W^T with X given
@@ -198,6 +201,9 @@ BlasLt *blaslt_create();
 void blaslt_destroy(BlasLt *b);
 hipError_t blaslt_bf16_product(BlasLt *b, const MatDesc &w, const uint16_t *x, int m, float *y, int ldy,
                                bool accumulate, hipStream_t st);
+// Whether the library has an algorithm for y = X W^T at this shape (the
+// plan is made and kept).
+bool blaslt_bf16_ready(BlasLt *b, const MatDesc &w, int m, int ldy);
 int gemm_splits(const MatDesc &w, int M, int max_splits);
 hipError_t launch_gemm_mfma(const MatDesc &w, const uint16_t *xh, const uint16_t *xl, int M, float *y, int ldy,
                             hipStream_t st, int ksplit = 1);
@@ -238,12 +244,13 @@ hipError_t launch_split_bf16(const float *x, int ldx, int k, int64_t rows, uint1
 // Epilogue of the fused in-projection for n tokens: y [n][win rows] ->
 // RoPE'd q [n][heads*hd], K/V into the cache at positions pos0 + j, and
 // m [n][inter] = SiLU-gate(gate, up) (m may be null), and / or m as bf16
-// operand planes mh, ml (null: none). With rows, token j sits at position
-// rows[2j] and its K/V go to cache slot rows[2j + 1] (branch rows). y may
-// hold ys partial products n * ldy floats apart, summed in order.
+// operand planes mh, ml (null: none; rows ldm values apart, 0: inter).
+// With rows, token j sits at position rows[2j] and its K/V go to cache
+// slot rows[2j + 1] (branch rows). y may hold ys partial products n * ldy
+// floats apart, summed in order.
 hipError_t launch_in_epilogue(const StableDims &s, const KVDev &kv, const float *y, int ldy, const float *rope,
                               const int *pos0, int n, float *q, float *m, hipStream_t st, uint16_t *mh = nullptr,
-                              uint16_t *ml = nullptr, const int *rows = nullptr, int ys = 1);
+                              uint16_t *ml = nullptr, const int *rows = nullptr, int ys = 1, int ldm = 0);
 // x = (x + p) + d elementwise (stablelm.go:375-377).
 // x = (x + sum_s p[s]) + sum_s d[s] over sp and sd partial products n
 // floats apart (K-split GEMM outputs), summed in order.

@@ -185,6 +185,18 @@ struct StableModel {
   // matrix-core kernel then runs the product).
   bool use_blaslt = true, blas_tried = false;
   BlasLt *blas = nullptr;
+  bool blas_ready();
+  // Joined-plane products (set_launch stage 9, on by default): with two
+  // activation planes a BF16 product is one hipBLASLt call over rows
+  // [hi | lo] (K doubled) against a prefill copy of the matrix whose rows
+  // hold each weight row twice (win: [w | w]; wout: [o | o | down | down]),
+  // instead of two calls of which the second reads and rewrites y. The
+  // copies (twice the layer matrices' bytes) are made at the first such
+  // prefill; a layer whose sections differ in format has none.
+  bool use_joined = true, joined_tried = false;
+  std::vector<MatDesc> joined_in, joined_out;  // per layer; rows == 0: none
+  int ensure_joined();
+  bool joined_layer(int l, int n);
   bool blas_product(const MatDesc &w, const uint16_t *xh, const uint16_t *xl, int n, float *y, int ldy);
   int prefill_chunk(const int32_t *ids, int n, int start, bool want_logits);
   // Scoring of a forward_logprobs call: while set, prefill_chunk also

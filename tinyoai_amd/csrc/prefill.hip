@@ -10,7 +10,7 @@ namespace {
 
 __global__ __launch_bounds__(256) void layer_norm_rows_kernel(const float *x, const float *w, const float *b,
                                                                double eps, int d, float *out, uint16_t *oh,
-                                                               uint16_t *ol) {
+                                                               uint16_t *ol, int ldo) {
   extern __shared__ __align__(16) float lds[];
   double *red = reinterpret_cast<double *>(lds + ((d + 3) & ~3));
   const int64_t row = blockIdx.x;
@@ -19,7 +19,7 @@ __global__ __launch_bounds__(256) void layer_norm_rows_kernel(const float *x, co
   layer_norm_lds(lds, d, w, b, eps, red);
   for (int i = threadIdx.x; i < d; i += blockDim.x) {
     if (out) out[row * d + i] = lds[i];
-    if (oh) store_bf16_split(oh, ol, row * d + i, lds[i]);
+    if (oh) store_bf16_split(oh, ol, row * ldo + i, lds[i]);
   }
 }
 
@@ -93,7 +93,7 @@ __global__ __launch_bounds__(256) void gemm_simt_kernel(MatDesc w, const float *
 // suffix entry).
 __global__ void in_epilogue_kernel(StableDims s, KVDev kv, const float *y, int ldy, const float *rope,
                                    const int *pos0, int units, float *q, float *m, uint16_t *mh, uint16_t *ml,
-                                   const int *rows, int ys) {
+                                   const int *rows, int ys, int ldm) {
   const int j = blockIdx.x;
   const int pos = rows ? rows[2 * j] : *pos0 + j;
   const int slot = rows ? rows[2 * j + 1] : pos;
@@ -128,7 +128,7 @@ __global__ void in_epilogue_kernel(StableDims s, KVDev kv, const float *y, int l
       if (mh && u >= mu0) {
         const float g = s.silu ? silu_gate_llama(v[b].x, v[b].y) : silu_gate(v[b].x, v[b].y);
         if (mj) mj[u - mu0] = g;
-        store_bf16_split(mh, ml, (int64_t)j * s.inter + (u - mu0), g);
+        store_bf16_split(mh, ml, (int64_t)j * ldm + (u - mu0), g);
       } else {
         in_pair_epilogue(s, kv, rope_row, slot, u, v[b].x, v[b].y, qj, mj);
       }
@@ -164,10 +164,11 @@ int elementwise_grid(int64_t n) { return (int)std::min<int64_t>((n + 255) / 256,
 }  // namespace
 
 hipError_t launch_layer_norm_rows(const float *x, const float *w, const float *b, double eps, int n, int d,
-                                  float *out, hipStream_t st, uint16_t *oh, uint16_t *ol) {
-  if (!oh != !ol) return hipErrorInvalidValue;
+                                  float *out, hipStream_t st, uint16_t *oh, uint16_t *ol, int ldo) {
+  if (!oh != !ol || (ldo && ldo < d)) return hipErrorInvalidValue;
   const size_t lds = (size_t)((d + 3) & ~3) * 4 + 8 * sizeof(double);
-  hipLaunchKernelGGL(layer_norm_rows_kernel, dim3(n), dim3(256), lds, st, x, w, b, eps, d, out, oh, ol);
+  hipLaunchKernelGGL(layer_norm_rows_kernel, dim3(n), dim3(256), lds, st, x, w, b, eps, d, out, oh, ol,
+                     ldo ? ldo : d);
   return hipGetLastError();
 }
 
@@ -179,14 +180,14 @@ hipError_t launch_gemm(const MatDesc &w, const float *x, int n, float *out, hipS
 
 hipError_t launch_in_epilogue(const StableDims &s, const KVDev &kv, const float *y, int ldy, const float *rope,
                               const int *pos0, int n, float *q, float *m, hipStream_t st, uint16_t *mh,
-                              uint16_t *ml, const int *rows, int ys) {
-  if (ldy % 2 || !mh != !ml || (!m && !mh) || s.win_q % 2 || (!rows && !pos0) || ys < 1)
+                              uint16_t *ml, const int *rows, int ys, int ldm) {
+  if (ldy % 2 || !mh != !ml || (!m && !mh) || s.win_q % 2 || (!rows && !pos0) || ys < 1 || (ldm && ldm < s.inter))
     return hipErrorInvalidValue;
   const int units = (s.win_q + 2 * s.win_kv + 2 * s.inter) / 2;
   // a few tokens: spread each token's units over several blocks
   const int per_token = std::max(1, std::min((units + 255) / 256, 2048 / std::max(1, n)));
   hipLaunchKernelGGL(in_epilogue_kernel, dim3(n, per_token), dim3(256), 0, st, s, kv, y, ldy, rope, pos0, units, q,
-                     m, mh, ml, rows, ys);
+                     m, mh, ml, rows, ys, ldm ? ldm : s.inter);
   return hipGetLastError();
 }
 
