@@ -103,13 +103,13 @@ __global__ void in_epilogue_kernel(StableDims s, KVDev kv, const float *y, int l
   float *qj = q + (int64_t)j * s.heads * s.hd, *mj = m ? m + (int64_t)j * s.inter : nullptr;
   const int64_t split = (int64_t)gridDim.x * ldy;
   // blockIdx.y takes every gridDim.y-th group of blockDim.x units; a thread
-  // loads kBatch of its units before it stores any (the stores could alias
-  // y as far as the compiler knows, so loads placed after them would each
-  // wait a memory round trip).
+  // loads kBatch of its units before it stores any, and the next kBatch
+  // before it stores those (the stores could alias y as far as the
+  // compiler knows, so loads placed after them would each wait a memory
+  // round trip).
   constexpr int kBatch = 4;
   const int stride = gridDim.y * blockDim.x;
-  for (int u0 = blockIdx.y * blockDim.x + threadIdx.x; u0 < units; u0 += kBatch * stride) {
-    float2 v[kBatch];
+  auto load = [&](int u0, float2 (&v)[kBatch]) {
 #pragma unroll
     for (int b = 0; b < kBatch; b++) {
       const int u = u0 + b * stride;
@@ -121,6 +121,13 @@ __global__ void in_epilogue_kernel(StableDims s, KVDev kv, const float *y, int l
         v[b].y = __fadd_rn(v[b].y, t.y);
       }
     }
+  };
+  float2 v[kBatch], nv[kBatch];
+  int u0 = blockIdx.y * blockDim.x + threadIdx.x;
+  if (u0 < units) load(u0, v);
+  for (; u0 < units; u0 += kBatch * stride) {
+    const int un = u0 + kBatch * stride;
+    if (un < units) load(un, nv);
 #pragma unroll
     for (int b = 0; b < kBatch; b++) {
       const int u = u0 + b * stride;
@@ -133,6 +140,8 @@ __global__ void in_epilogue_kernel(StableDims s, KVDev kv, const float *y, int l
         in_pair_epilogue(s, kv, rope_row, slot, u, v[b].x, v[b].y, qj, mj);
       }
     }
+#pragma unroll
+    for (int b = 0; b < kBatch; b++) v[b] = nv[b];
   }
 }
 
@@ -184,8 +193,8 @@ hipError_t launch_in_epilogue(const StableDims &s, const KVDev &kv, const float 
   if (ldy % 2 || !mh != !ml || (!m && !mh) || s.win_q % 2 || (!rows && !pos0) || ys < 1 || (ldm && ldm < s.inter))
     return hipErrorInvalidValue;
   const int units = (s.win_q + 2 * s.win_kv + 2 * s.inter) / 2;
-  // a few tokens: spread each token's units over several blocks
-  const int per_token = std::max(1, std::min((units + 255) / 256, 2048 / std::max(1, n)));
+  // each token's units over several blocks (about 8192 blocks for a chunk)
+  const int per_token = std::max(1, std::min((units + 255) / 256, 8192 / std::max(1, n)));
   hipLaunchKernelGGL(in_epilogue_kernel, dim3(n, per_token), dim3(256), 0, st, s, kv, y, ldy, rope, pos0, units, q,
                      m, mh, ml, rows, ys, ldm ? ldm : s.inter);
   return hipGetLastError();
