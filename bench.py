@@ -109,7 +109,8 @@ def q8_0_kernel(seed=2, reps=192, copies=16):
     [-127, 127], fp16 d = RNE(|N(0, 0.02)| / 127), x ~ N(0, 1)): the decode
     matvec (M = 1) and the batched product (M = 128: bf16 operand planes of
     x, then the matrix-core GEMM) through tinyoai_weight_mul_device, timed
-    back to back with events on the stream the kernels run on. The launches
+    back to back with events on the stream the kernels run on (a torch
+    stream of its own, passed to every call). The launches
     cycle through `copies` device copies of the weight (16 x 18.8 MB, more
     than the 256 MB last-level cache), so each reads its weight from HBM as
     a decode step does, not from the cache that holds a repeated one. Algorithmic
@@ -126,8 +127,10 @@ def q8_0_kernel(seed=2, reps=192, copies=16):
     d = raw[:, :2].copy().view(np.float16).ravel().astype(np.float64)
     wref = (raw[:, 2:].view(np.int8).astype(np.float64) * d[:, None]).reshape(rows, cols)
     ws = [hip.Weight(t) for _ in range(copies)]
-    w = ws[0]
-    st = torch.cuda.current_stream()
+    # A stream of its own (default priority): the library launches on the
+    # stream it is given, and a null handle would send the kernels to the
+    # weight's own stream, which events on torch's default stream do not see.
+    st = torch.cuda.Stream()
     out = {}
     for m in (1, 128):
         x = torch.randn(m, cols, generator=torch.Generator().manual_seed(seed + m)).cuda()

@@ -259,8 +259,9 @@ int tinyoai_weight_mul_device(tinyoai_weight *w, const float *x_dev, int32_t n, 
 /* tinyoai_weight_mul_device without any allocation, for callers that
  * cannot allocate (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc); it has no counterpart in the reference.
- * The activations' operand planes live in a library array of 16 MiB on
- * each GPU the library runs on (held until the process ends), so n * cols
+ * The activations' operand planes (16 MiB) and the product's K-split
+ * partials (32 MiB) live in a library array of 48 MiB on each GPU the
+ * library runs on (held until the process ends), so n * cols
  * may be at most 4,194,304 (TINYOAI_EINVAL beyond), the current device
  * must be the weight's, and calls that overlap on one GPU race for that
  * array; each call overwrites what the previous one left there. */

@@ -1797,9 +1797,27 @@ int tinyoai_weight_read_values(tinyoai_weight *w, int64_t offset, int64_t n, flo
 // Bytes of operand scratch a product of n rows needs: bf16 planes of the
 // matrix-core GEMM, the staged X of the few-row 5/6-bit product, or none
 // (one row: the row-streaming matvec; other formats: the vector-unit GEMM).
+// K splits of a matrix-core product (the output tiles alone leave most of
+// the CUs idle below a few hundred rows: 27 tiles for 128 x 6912), their
+// partials within kProductPartialBytes. A rule of the shape alone, so the
+// allocating and the no-allocation entry points sum alike.
+constexpr size_t kProductPartialBytes = (size_t)32 << 20;
+static int product_splits(const MatDesc &m, int n) {
+  if (n == 1 || !gemm_mfma_supported(m)) return 1;
+  int ks = gemm_splits(m, n, StableModel::kPrefillSplits);
+  while (ks > 1 && (size_t)ks * n * m.rows * 4 > kProductPartialBytes) ks--;
+  return ks;
+}
+static size_t product_planes_bytes(const MatDesc &m, int n) {
+  return ((size_t)n * m.cols * 2 * gemm_planes(m) + 255) / 256 * 256;
+}
+
 static size_t product_scratch(const MatDesc &m, const float *x_dev, int n) {
   if (n == 1) return 0;
-  if (gemm_mfma_supported(m)) return (size_t)n * m.cols * 2 * gemm_planes(m);
+  if (gemm_mfma_supported(m)) {
+    const int ks = product_splits(m, n);
+    return product_planes_bytes(m, n) + (ks > 1 ? (size_t)ks * n * m.rows * 4 : 0);
+  }
   if (kq_rows_supported(m, n) && (reinterpret_cast<uintptr_t>(x_dev) & 15) == 0 && m.cols % 4 == 0)
     return kq_rows_stage_bytes(m.cols, n);
   return 0;
@@ -1808,11 +1826,17 @@ static size_t product_scratch(const MatDesc &m, const float *x_dev, int n) {
 // out = x * W^T with `scratch` of product_scratch bytes.
 static hipError_t product_launch(const MatDesc &m, const float *x_dev, int n, float *out_dev, void *scratch,
                                  hipStream_t st) {
-  if (n == 1) return launch_ln_matvec(m, nullptr, nullptr, 0.0, 0, x_dev, out_dev, device_cu_count() * 4, 256, st);
+  // One row: the row-streaming matvec, two blocks per CU (6912 x 2560 Q8_0:
+  // 7.2 us against 9.4 with four and 8.1 with one).
+  if (n == 1) return launch_ln_matvec(m, nullptr, nullptr, 0.0, 0, x_dev, out_dev, device_cu_count() * 2, 256, st);
   if (gemm_mfma_supported(m)) {
     uint16_t *hi = (uint16_t *)scratch, *lo = gemm_planes(m) == 2 ? hi + (size_t)n * m.cols : nullptr;
+    const int ks = product_splits(m, n);
+    float *part = reinterpret_cast<float *>((char *)scratch + product_planes_bytes(m, n));
     hipError_t e = launch_split_bf16(x_dev, m.cols, m.cols, n, hi, lo, st);
-    return e == hipSuccess ? launch_gemm_mfma(m, hi, lo, n, out_dev, m.rows, st) : e;
+    if (e == hipSuccess) e = launch_gemm_mfma(m, hi, lo, n, ks > 1 ? part : out_dev, m.rows, st, ks);
+    if (e == hipSuccess && ks > 1) e = launch_sum_splits(out_dev, part, ks, (int64_t)n * m.rows, st);
+    return e;
   }
   if (product_scratch(m, x_dev, n)) return launch_kq_rows(m, x_dev, m.cols, n, out_dev, m.rows, 1, scratch, st);
   return launch_gemm(m, x_dev, n, out_dev, st);
@@ -1851,7 +1875,8 @@ int tinyoai_weight_mul_device(tinyoai_weight *w, const float *x_dev, int32_t n, 
 // device address of each GPU's copy comes from hipGetSymbolAddress (once
 // per device, with that device current) and only that address is used.
 constexpr size_t kScratchValues = (size_t)4 << 20;  // activation values per call (n * cols)
-static __device__ __align__(256) uint16_t scratch[2 * kScratchValues];  // bf16 hi and lo planes: 16 MiB
+// bf16 hi and lo planes (16 MiB), then the K-split partials (32 MiB)
+static __device__ __align__(256) uint16_t scratch[2 * kScratchValues + kProductPartialBytes / 2];
 
 namespace {
 constexpr int kMaxDevices = 64;

@@ -255,6 +255,8 @@ hipError_t launch_in_epilogue(const StableDims &s, const KVDev &kv, const float 
 // x = (x + sum_s p[s]) + sum_s d[s] over sp and sd partial products n
 // floats apart (K-split GEMM outputs), summed in order.
 hipError_t launch_residual(float *x, const float *p, int sp, const float *d, int sd, int64_t n, hipStream_t st);
+// out[i] = sum over s < sp of p[s * n + i], in order of s.
+hipError_t launch_sum_splits(float *out, const float *p, int sp, int64_t n, hipStream_t st);
 hipError_t launch_copy_row(const float *src, float *dst, int n, hipStream_t st);
 // n 32-bit words from src to dst (both 16-byte aligned; either may be
 // host-mapped memory), with 16-byte accesses.

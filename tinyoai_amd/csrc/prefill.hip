@@ -154,6 +154,15 @@ __global__ void residual_kernel(float *x, const float *p, int sp, const float *d
   }
 }
 
+// out[i] = ((p[0][i] + p[1][i]) + p[2][i]) + ... over sp partials n apart.
+__global__ void sum_splits_kernel(float *out, const float *p, int sp, int64_t n) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    float v = p[i];
+    for (int s = 1; s < sp; s++) v = __fadd_rn(v, p[s * n + i]);
+    out[i] = v;
+  }
+}
+
 __global__ void copy_kernel(const float *src, float *dst, int n) {
   for (int i = threadIdx.x; i < n; i += blockDim.x) dst[i] = src[i];
 }
@@ -203,6 +212,12 @@ hipError_t launch_in_epilogue(const StableDims &s, const KVDev &kv, const float 
 hipError_t launch_residual(float *x, const float *p, int sp, const float *d, int sd, int64_t n, hipStream_t st) {
   if (sp < 1 || sd < 1) return hipErrorInvalidValue;
   hipLaunchKernelGGL(residual_kernel, dim3(elementwise_grid(n)), dim3(256), 0, st, x, p, sp, d, sd, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_sum_splits(float *out, const float *p, int sp, int64_t n, hipStream_t st) {
+  if (sp < 1 || n < 1) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(sum_splits_kernel, dim3(elementwise_grid(n)), dim3(256), 0, st, out, p, sp, n);
   return hipGetLastError();
 }
 
