@@ -727,7 +727,7 @@ int StableModel::decode_step(int token, int pos, bool want_logits) {
   for (int i = 0; i < 3; i++) hp[i] = vals[i];
   memcpy(hp + 16, rope_host.data() + (size_t)pos * dims.rot, (size_t)dims.rot * 4);
   logits_mapped = want_logits;
-  const int steps = att_steps > 0 ? att_steps : attention_steps(pos, dims.heads);
+  const int steps = att_steps > 0 ? att_steps : decode_attention_steps(pos, dims.heads, dims.hd);
   const int splits = attention_splits(pos, steps);
   if (decode_fused(steps)) fuse_epoch++;  // the value the step's launches read is the one written above
   if (prof.on || !use_graphs) return enqueue_decode(steps, splits, want_logits);

@@ -155,6 +155,19 @@ int attention_steps(int max_pos, int heads) {
   return steps;
 }
 
+int decode_attention_steps(int pos, int heads, int hd) {
+  // Measured at the 3B shapes (Q8_0 with fp32 KV, BF16 with fp16 KV), tok/s
+  // of the whole decode step: two steps inside the decode_in launch lead up
+  // to ~1500 positions (869 against 798 at 640, Q8_0); four steps as a
+  // launch of its own lead from ~2000 (BF16 at 4096: 550 against 476);
+  // 1024 positions per 16-wave block beyond ~5000 (BF16 at 8000: 512
+  // against 475 with four steps and 360 fused).
+  const int npos = pos + 1;
+  if (npos <= 1800) return attention_steps(pos, heads);
+  if (npos <= 5000 || hd > 80) return 4;
+  return 16;
+}
+
 int attention_splits(int max_pos, int steps) { return (max_pos + 64 * steps) / (64 * steps); }
 
 hipError_t launch_attention(const StableDims &s, const KVDev &kv, const float *q, const int *pos0, int nq,

@@ -152,6 +152,11 @@ hipError_t launch_flash_prefill(const StableDims &s, const KVDev &kv, const floa
                                 float *out, hipStream_t st, uint16_t *oh = nullptr, uint16_t *ol = nullptr,
                                 const KVDev *sfx = nullptr, int prefix = 0, int sfx_slot0 = 0, int64_t ld_o = 0);
 int attention_steps(int max_pos, int heads);
+// The decode step's attention shape at position pos: attention_steps up to
+// about 1800 positions (fused into the decode_in launch), then wider
+// separate blocks (4 steps; 16 beyond about 5000 positions for head widths
+// up to 80).
+int decode_attention_steps(int pos, int heads, int hd);
 // Floats per (query, head) in the partials buffer: max_splits records of
 // hd + 2, rounded to 256 bytes.
 __host__ __device__ inline int64_t partial_region(int max_splits, int hd) {
