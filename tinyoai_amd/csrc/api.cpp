@@ -790,13 +790,14 @@ int StableModel::project(const MatDesc &w, const float *x, int ldx, int n, float
             launch_ln_matvec(w, nullptr, nullptr, 0.0, 0, x + (size_t)j * ldx, y + (size_t)j * ldy, grid_out,
                              threads_out, stream),
             "projection");
-  } else if (!rowstream && kq_rows_supported(w, 32) && (reinterpret_cast<uintptr_t>(x) & 15) == 0 && ldx % 4 == 0 &&
+  } else if (kq_rows_supported(w, 32) && (reinterpret_cast<uintptr_t>(x) & 15) == 0 && ldx % 4 == 0 &&
              kq_rows_stage_bytes(w.cols, 32) <= (size_t)chunk * std::max(dims.d, dims.inter) * 2) {
-    // Prefill rows with a 5/6-bit matrix: the few-row matrix-core product
-    // over slices of 32 rows (each slice re-reads the matrix, mostly from
-    // the last-level cache), its K splits in the caller's layout: the
-    // 4096-token prefix of the 3B K-quant branch workload prefills in
-    // 0.63 s against 0.84 s on the vector-unit GEMM.
+    // Prefill rows (and branch appends of more than 32 rows) with a 5/6-bit
+    // matrix: the few-row matrix-core product over slices of 32 rows (each
+    // slice re-reads the matrix, mostly from the last-level cache), its K
+    // splits in the caller's layout: the 4096-token prefix of the 3B
+    // K-quant branch workload prefills in 0.63 s against 0.84 s on the
+    // vector-unit GEMM.
     const int ks = splits ? kq_rows_splits(w, max_splits) : 1;
     if (splits) *splits = ks;
     for (int j0 = 0; j0 < n; j0 += 32)
