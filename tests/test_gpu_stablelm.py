@@ -209,6 +209,35 @@ def test_decode_attention_shapes_agree(hip, kv_bits):
         f.close()
 
 
+@pytest.mark.parametrize("start", [1790, 4990])
+def test_decode_attention_shape_by_position(hip, start):
+    """The decode step's attention shape chosen by position (fused two
+    steps up to 1800 positions, four steps as a launch of its own up to
+    5000, 1024 positions per 16-wave block beyond) against the fused shape
+    forced at every position (launch stage 3 = 2), fp32 KV: 20 decode
+    tokens across each switch give logits and per-layer residuals within
+    2e-5 of their range (only the order of the softmax sums differs) and the
+    same greedy ids."""
+    config = W.validate_stablelm_config(dict(W.STABLELM_3B, num_hidden_layers=2, max_position_embeddings=8192))
+    tensors = W.synthetic_stablelm(config, W.Q8_0, seed=17)
+    prompt = np.random.default_rng(19).integers(0, 65536, start).astype(np.int32)
+    auto, ref = hip.StableLMForwarder(config, tensors), hip.StableLMForwarder(config, tensors)
+    del tensors
+    ref.set_launch("attention", 2, 0)
+    for f in (auto, ref):
+        f.trace(True)
+    la, lr = auto.forward(0, prompt), ref.forward(0, prompt)
+    for step in range(20):
+        tok = int(np.argmax(lr))
+        assert int(np.argmax(la)) == tok, step
+        la, lr = auto.forward(start + step, [tok]), ref.forward(start + step, [tok])
+        assert np.max(np.abs(la - lr)) <= 2e-5 * float(np.ptp(lr)), step
+        tr = ref.trace_read()
+        assert np.max(np.abs(auto.trace_read() - tr)) <= 2e-5 * float(np.ptp(tr)), step
+    auto.close()
+    ref.close()
+
+
 @pytest.mark.parametrize("dtype,kv_bits", [(W.Q8_0, 32), (W.Q8_0, 16), (W.BF16, 32)])
 def test_fused_decode_attention_matches_separate_launch(hip, dtype, kv_bits):
     """The decode attention on extra blocks of the decode_in launch (the
