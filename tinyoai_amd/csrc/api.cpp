@@ -798,11 +798,15 @@ int StableModel::project(const MatDesc &w, const float *x, int ldx, int n, float
     // splits in the caller's layout: the 4096-token prefix of the 3B
     // K-quant branch workload prefills in 0.63 s against 0.84 s on the
     // vector-unit GEMM.
+    // As many slices per launch as the staging workspace holds (each slice
+    // staged once; the launch's blocks cover every slice at once).
     const int ks = splits ? kq_rows_splits(w, max_splits) : 1;
     if (splits) *splits = ks;
-    for (int j0 = 0; j0 < n; j0 += 32)
+    const size_t cap = (size_t)chunk * std::max(dims.d, dims.inter) * 2;
+    const int per = std::max<int>(1, (int)(cap / kq_rows_stage_bytes(w.cols, 32))) * 32;
+    for (int j0 = 0; j0 < n; j0 += per)
       STAGE(ST_PREFILL_GEMM,
-            launch_kq_rows(w, x + (size_t)j0 * ldx, ldx, std::min(32, n - j0), y + (size_t)j0 * ldy, ldy, ks, XH,
+            launch_kq_rows(w, x + (size_t)j0 * ldx, ldx, std::min(per, n - j0), y + (size_t)j0 * ldy, ldy, ks, XH,
                            stream, false, (int64_t)n * ldy),
             "projection");
   } else {

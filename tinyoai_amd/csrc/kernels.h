@@ -212,10 +212,11 @@ bool blaslt_bf16_ready(BlasLt *b, const MatDesc &w, int m, int ldy);
 int gemm_splits(const MatDesc &w, int M, int max_splits);
 hipError_t launch_gemm_mfma(const MatDesc &w, const uint16_t *xh, const uint16_t *xl, int M, float *y, int ldy,
                             hipStream_t st, int ksplit = 1);
-// Products of at most 32 rows with a 5/6-bit matrix (Q4_K, Q5_K, Q6_K,
-// Q5_1) on the matrix cores: y[M][N] (row stride ldy) = X * W^T, X fp32
-// [M][ldx] (16-byte aligned, ldx % 4 == 0), converted first into `stage`
-// (16-byte aligned device memory of kq_rows_stage_bytes(K, M) bytes). With
+// Few-row products with a 5/6-bit matrix (Q4_K, Q5_K, Q6_K, Q5_1) on the
+// matrix cores: y[M][N] (row stride ldy) = X * W^T, X fp32 [M][ldx]
+// (16-byte aligned, ldx % 4 == 0), converted first into `stage` (16-byte
+// aligned device memory of kq_rows_stage_bytes(K, M) bytes); more than 32
+// rows run as slices of 32 on the grid's second dimension. With
 // ks > 1 the K range is cut in ks parts whose products go to
 // y + s * split_stride (0: M * ldy; a larger stride lets row slices of one
 // product share the caller's split layout), for the caller to sum;

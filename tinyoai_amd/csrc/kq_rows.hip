@@ -59,8 +59,8 @@ constexpr size_t lds_bytes() { return (size_t)2 * kWindow * chunk_bytes<MT>(); }
 
 struct KqArgs {
   MatDesc w;
-  const uint8_t *stage;  // staged chunks of X, chunk c at c * chunk_bytes
-  int M;
+  const uint8_t *stage;  // staged chunks of X, chunk c at c * chunk_bytes (per slice of R rows)
+  int M;                 // rows; slices of R rows on the grid's y dimension
   float *y;
   int ldy, ks;
   int64_t split_stride;  // floats between the K splits' outputs
@@ -68,11 +68,15 @@ struct KqArgs {
 
 // x [M][K] -> staged chunks. Item i: group of 4 values i % 8 of row
 // (i / 8) % R and chunk i / (8 R); a chunk's 8 groups are 8 consecutive
-// lanes, which form the sums by fixed-order shuffles.
+// lanes, which form the sums by fixed-order shuffles. Slice blockIdx.y
+// stages rows [R y, R y + R) at y * nch * chunk_bytes.
 template <int MT>
 __global__ __launch_bounds__(256) void kq_stage_kernel(const float *x, int ldx, int M, int K, uint8_t *stage) {
   constexpr int R = 16 * MT;
   const int nch = K / 32;
+  x += (int64_t)blockIdx.y * R * ldx;
+  M -= blockIdx.y * R;
+  stage += (size_t)blockIdx.y * nch * chunk_bytes<MT>();
   const int i = blockIdx.x * 256 + threadIdx.x;
   if (i >= R * nch * 8) return;  // whole groups of 8: R * nch * 8 and the block are multiples of 8
   const int gq = i & 7, row = (i >> 3) % R, c = (i >> 3) / R;
@@ -161,12 +165,15 @@ __global__ __launch_bounds__(kThreads) void kq_rows_kernel(KqArgs g) {
   const int batches = (nch + 7) / 8;
   const int b_lo = (int)((int64_t)batches * split / g.ks), b_hi = (int)((int64_t)batches * (split + 1) / g.ks);
   const int c_lo = b_lo * 8, c_hi = min(nch, b_hi * 8);
-  float *y = g.y + (int64_t)split * g.split_stride;
+  // slice blockIdx.y: rows [R y, R y + R) of x, staged at y * nch * CB
+  const int Ms = min(R, g.M - (int)blockIdx.y * R);
+  const uint8_t *stage = g.stage + (int64_t)blockIdx.y * nch * CB;
+  float *y = g.y + (int64_t)split * g.split_stride + (int64_t)blockIdx.y * R * g.ldy;
 
   // ---- staged chunks [c0, min(c0 + 8, c_hi)) -> window buffer buf.
   // Buffer loads: pieces past the staged chunks read zeros (stored into
   // window slots no product reads), so no lane branches.
-  const __amdgpu_buffer_rsrc_t rs = plane_rsrc(g.stage, (int64_t)nch * CB);
+  const __amdgpu_buffer_rsrc_t rs = plane_rsrc(stage, (int64_t)nch * CB);
   auto load_x = [&](uint4 (&xr)[kCopy], int c0) {
     const uint32_t end = (uint32_t)min(c0 + kWindow, c_hi) * CB;
 #pragma unroll
@@ -429,7 +436,7 @@ __global__ __launch_bounds__(kThreads) void kq_rows_kernel(KqArgs g) {
 #pragma unroll
       for (int v = 0; v < 4; v++) {
         const int xrow = 16 * m + 4 * g4 + v;
-        if (xrow < g.M) y[(int64_t)xrow * g.ldy + n] = acc[m][t][v];
+        if (xrow < Ms) y[(int64_t)xrow * g.ldy + n] = acc[m][t][v];
       }
   }
 }
@@ -441,7 +448,8 @@ hipError_t kq_launch(const KqArgs &g, hipStream_t st) {
                                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (attr != hipSuccess) return attr;
   const int NB = (g.w.rows + kBlockRows - 1) / kBlockRows;
-  hipLaunchKernelGGL((kq_rows_kernel<F, MT>), dim3(NB * g.ks), dim3(kThreads), lds, st, g);
+  hipLaunchKernelGGL((kq_rows_kernel<F, MT>), dim3(NB * g.ks, (g.M + 16 * MT - 1) / (16 * MT)), dim3(kThreads), lds,
+                     st, g);
   return hipGetLastError();
 }
 
@@ -459,7 +467,8 @@ hipError_t kq_dispatch(const KqArgs &g, hipStream_t st) {
 template <int MT>
 hipError_t kq_stage(const float *x, int ldx, int M, int K, uint8_t *stage, hipStream_t st) {
   const int items = 16 * MT * (K / 32) * 8;
-  hipLaunchKernelGGL((kq_stage_kernel<MT>), dim3((items + 255) / 256), dim3(256), 0, st, x, ldx, M, K, stage);
+  hipLaunchKernelGGL((kq_stage_kernel<MT>), dim3((items + 255) / 256, (M + 16 * MT - 1) / (16 * MT)), dim3(256), 0,
+                     st, x, ldx, M, K, stage);
   return hipGetLastError();
 }
 
@@ -471,7 +480,7 @@ bool kq_rows_supported(const MatDesc &w, int M) {
 }
 
 size_t kq_rows_stage_bytes(int K, int M) {
-  return (size_t)(K / 32) * (M <= 16 ? chunk_bytes<1>() : chunk_bytes<2>());
+  return (size_t)(K / 32) * (M <= 16 ? chunk_bytes<1>() : chunk_bytes<2>() * (size_t)((M + 31) / 32));
 }
 
 int kq_rows_splits(const MatDesc &w, int max_splits) {
@@ -483,7 +492,8 @@ int kq_rows_splits(const MatDesc &w, int max_splits) {
 
 hipError_t launch_kq_rows(const MatDesc &w, const float *x, int ldx, int M, float *y, int ldy, int ks, void *stage,
                           hipStream_t st, bool staged, int64_t split_stride) {
-  if (!kq_rows_supported(w, M) || ks < 1 || ks > (w.cols / 32 + 7) / 8 || ldx < w.cols || ldy < w.rows ||
+  if (!kq_rows_supported(w, std::min(M, 32)) || M > 32 * 1024 || ks < 1 || ks > (w.cols / 32 + 7) / 8 ||
+      ldx < w.cols || ldy < w.rows ||
       (reinterpret_cast<uintptr_t>(x) & 15) || (ldx & 3) || !stage || (reinterpret_cast<uintptr_t>(stage) & 15))
     return hipErrorInvalidValue;
   if (split_stride == 0) split_stride = (int64_t)M * ldy;
