@@ -1074,6 +1074,7 @@ Branches::~Branches() {
   if (partials) hipFree(partials);
   if (counters) hipFree(counters);
   if (last) hipFree(last);
+  if (segs) hipFree(segs);
   if (m) m->open_branches--;
 }
 
@@ -1189,6 +1190,27 @@ int StableModel::branch_rows(Branches &b, const int32_t *ids, const int32_t *br,
     int max_pos = 0;
     for (int i = 0; i < nc; i++) max_pos = std::max(max_pos, crow[2 * i]);
     const bool use_flash = flash && run > 1;
+    // The chunk's runs for the flash attention: one launch covers them all.
+    int longest = 0;
+    if (use_flash) {
+      if (!b.segs) {  // at most one run per row of a chunk
+        hipError_t e = hipMalloc(&b.segs, (size_t)chunk * 3 * sizeof(int));
+        if (e != hipSuccess) return fail(TINYOAI_ENOMEM, "branch run table: %s", hipGetErrorString(e));
+      }
+      // the previous chunk's table may still be in flight from the host copy
+      if (!b.segs_host.empty()) TRY_HIP(hipStreamSynchronize(stream), "branch run table");
+      b.segs_host.assign((seg.size() - 1) * 3, 0);
+      for (size_t k = 0; k + 1 < seg.size(); k++) {
+        const int a0 = seg[k], cnt = seg[k + 1] - seg[k];
+        b.segs_host[3 * k] = a0;
+        b.segs_host[3 * k + 1] = cnt;
+        b.segs_host[3 * k + 2] = br[r0 + a0] * b.scap;
+        longest = std::max(longest, cnt);
+      }
+      TRY_HIP(hipMemcpyAsync(b.segs, b.segs_host.data(), b.segs_host.size() * sizeof(int), hipMemcpyHostToDevice,
+                             stream),
+              "branch run table");
+    }
     int max_splits = 0;
     if (!use_flash) {
       max_splits = branch_attention_records(dims, pfx, max_pos, nc);
@@ -1240,12 +1262,9 @@ int StableModel::branch_rows(Branches &b, const int32_t *ids, const int32_t *br,
       int sp = 1, sd = 1;
       if ((rc = project(wd, M, I, nc, D, d, &sd, true, pd_splits))) return rc;
       if (use_flash) {
-        for (size_t k = 0; k + 1 < seg.size(); k++) {
-          const int a0 = seg[k], cnt = seg[k + 1] - seg[k], j = br[r0 + a0];
-          TRY_HIP(launch_flash_prefill(dims, kv[l], Q + (size_t)a0 * hq, d_rows + 2 * a0, cnt, A + (size_t)a0 * hq,
-                                       stream, nullptr, nullptr, &b.kv[l], pfx, j * b.scap),
-                  "branch attention");
-        }
+        TRY_HIP(launch_flash_prefill(dims, kv[l], Q, d_rows, longest, A, stream, nullptr, nullptr, &b.kv[l], pfx, 0, 0,
+                                     b.segs, (int)seg.size() - 1),
+                "branch attention");
       } else {
         TRY_HIP(launch_branch_attention(dims, kv[l], b.kv[l], pfx, Q, d_rows, nc, max_pos, b.partials, b.counters,
                                         A, max_splits, stream),

@@ -39,6 +39,11 @@ struct FlashArgs {
   int64_t region;
   int split_keys;
   int64_t ld_o;  // values between the query rows of oh, ol (0: heads * hd)
+  // Branch runs in one launch (BR instances): segment blockIdx.z is
+  // segs[3z..3z+2] = (first row a0, rows, slot of its first position): its
+  // queries are rows a0.. of q / out and its positions and slots rows a0..
+  // of pos0 (pairs); n is the longest run.
+  const int *segs;
 };
 
 // x = hi + lo to about 2^-22. The empty asm pins x as one fp32 value: when x
@@ -88,12 +93,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h = blockIdx.y, kvh = h / (s.heads / s.kv_heads);
+  if (BR && a.segs) {
+    const int *sg = a.segs + 3 * blockIdx.z;
+    const int a0 = sg[0];
+    a.n = sg[1];
+    a.sfx_slot0 = sg[2];
+    a.q += (int64_t)a0 * s.heads * HD;
+    a.pos0 += 2 * a0;
+    if (a.out) a.out += (int64_t)a0 * s.heads * HD;
+  }
   const int p0 = SH ? 0 : *a.pos0;
   // Query tiles run in reverse order for the second half of the heads:
   // workgroups k and k + grid / 2 share a CU when the grid fills two per
   // CU, and the reversal pairs a long causal range with a short one there.
   // SH: one query tile; blockIdx.x is the key range.
   const int qt = SH ? 0 : blockIdx.y >= (gridDim.y + 1) / 2 ? gridDim.x - 1 - blockIdx.x : blockIdx.x;
+  if (BR && a.segs && qt * kQ32 >= a.n) return;      // past this run's queries (the whole block)
   const int qb = qt * kQ32;                          // first query of the block
   const int qw = qb + wave * 32;                     // first query of the wave
   const int col = lane & 31, g = lane >> 5;          // S^T column (query) / B row, lane group
@@ -381,8 +396,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
 }
 
 template <int HD, bool BR>
-hipError_t flash32_launch(const FlashArgs &a, hipStream_t st) {
-  dim3 grid((a.n + kQ32 - 1) / kQ32, a.s.heads);
+hipError_t flash32_launch(const FlashArgs &a, int nseg, hipStream_t st) {
+  dim3 grid((a.n + kQ32 - 1) / kQ32, a.s.heads, nseg);
   if (a.kv.half)
     hipLaunchKernelGGL((flash32_kernel<HD, true, BR>), grid, dim3(256), 0, st, a);
   else
@@ -391,8 +406,8 @@ hipError_t flash32_launch(const FlashArgs &a, hipStream_t st) {
 }
 
 template <int HD>
-hipError_t flash32_dispatch(const FlashArgs &a, bool br, hipStream_t st) {
-  return br ? flash32_launch<HD, true>(a, st) : flash32_launch<HD, false>(a, st);
+hipError_t flash32_dispatch(const FlashArgs &a, bool br, int nseg, hipStream_t st) {
+  return br ? flash32_launch<HD, true>(a, nseg, st) : flash32_launch<HD, false>(a, 1, st);
 }
 
 template <int HD>
@@ -429,16 +444,18 @@ hipError_t launch_shared_prefix_attention(const StableDims &s, const KVDev &kv, 
 
 hipError_t launch_flash_prefill(const StableDims &s, const KVDev &kv, const float *q, const int *pos0, int n,
                                 float *out, hipStream_t st, uint16_t *oh, uint16_t *ol, const KVDev *sfx, int prefix,
-                                int sfx_slot0, int64_t ld_o) {
+                                int sfx_slot0, int64_t ld_o, const int *segs, int nseg) {
   if (!oh != !ol || (!out && !oh) || n < 1 || (ld_o && ld_o < (int64_t)s.heads * s.hd)) return hipErrorInvalidValue;
   if (sfx && (sfx->half != kv.half || prefix < 0 || prefix > kv.cap || sfx_slot0 < 0)) return hipErrorInvalidValue;
-  FlashArgs a{s, kv, q, pos0, n, out, oh, ol, sfx ? *sfx : KVDev{}, prefix, sfx_slot0, nullptr, 0, 0, ld_o};
+  if (segs && (!sfx || oh || nseg < 1 || nseg > 65535)) return hipErrorInvalidValue;
+  FlashArgs a{s, kv, q, pos0, n, out, oh, ol, sfx ? *sfx : KVDev{}, prefix, sfx_slot0, nullptr, 0, 0, ld_o, segs};
   const bool br = sfx != nullptr;
+  const int z = segs ? nseg : 1;
   switch (s.hd) {
-    case 64: return flash32_dispatch<64>(a, br, st);
-    case 80: return flash32_dispatch<80>(a, br, st);
-    case 96: return flash32_dispatch<96>(a, br, st);
-    case 128: return flash32_dispatch<128>(a, br, st);
+    case 64: return flash32_dispatch<64>(a, br, z, st);
+    case 80: return flash32_dispatch<80>(a, br, z, st);
+    case 96: return flash32_dispatch<96>(a, br, z, st);
+    case 128: return flash32_dispatch<128>(a, br, z, st);
   }
   return hipErrorInvalidValue;
 }

@@ -147,10 +147,14 @@ bool flash_prefill_supported(int hd);
 // matrix-core GEMM (null: none). With sfx, the queries are one branch's
 // rows: cache positions t >= prefix come from slot sfx_slot0 + (t - prefix)
 // of the branch cache sfx, positions below prefix from kv. The planes' query
-// rows lie ld_o values apart (0: heads * hd).
+// rows lie ld_o values apart (0: heads * hd). With segs (and sfx), nseg
+// runs of branch rows in one launch: segs[3k..3k+2] = (first row, rows,
+// slot of its first position) on the device, n = the longest run, q, pos0
+// (row pairs) and out indexed by row.
 hipError_t launch_flash_prefill(const StableDims &s, const KVDev &kv, const float *q, const int *pos0, int n,
                                 float *out, hipStream_t st, uint16_t *oh = nullptr, uint16_t *ol = nullptr,
-                                const KVDev *sfx = nullptr, int prefix = 0, int sfx_slot0 = 0, int64_t ld_o = 0);
+                                const KVDev *sfx = nullptr, int prefix = 0, int sfx_slot0 = 0, int64_t ld_o = 0,
+                                const int *segs = nullptr, int nseg = 0);
 int attention_steps(int max_pos, int heads);
 // The decode step's attention shape at position pos: attention_steps up to
 // about 1800 positions (fused into the decode_in launch), then wider

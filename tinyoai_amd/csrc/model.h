@@ -239,6 +239,8 @@ struct Branches {
   unsigned *counters = nullptr;  // their arrival counters (zero between launches)
   size_t counter_words = 0;
   float *last = nullptr;         // [count][hidden]: each branch's newest residual row
+  int *segs = nullptr;           // [chunk][3]: the runs of an append's chunk (first row, rows, first slot)
+  std::vector<int> segs_host;    // their host copy (kept until the call has synchronised)
   ~Branches();
   void free_kv();
   // Suffix capacity for `need` positions per branch (existing entries kept).
