@@ -344,7 +344,10 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=3)
-    ap.add_argument("--warmup", type=int, default=1)
+    # Two untimed steps: the first decode loops of a process carry the decode
+    # graphs' capture (about 25 ms in the first) and run about 11% slower
+    # in the second; from the third on the loops repeat to within 0.3%.
+    ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--prompt", type=int, default=512)
     ap.add_argument("--generate", type=int, default=256)
     ap.add_argument("--layers", type=int, default=32)
