@@ -219,14 +219,10 @@ int tinyoai_stablelm_profile(tinyoai_model *m, int32_t enable);
  * ids may then differ from the fp32 engine's where logits nearly tie),
  * zero (the default) keeps two bf16 planes per activation (16 significant
  * bits). Stage 7: grid nonzero (the default) runs the BF16-weight prefill
- * products on hipBLASLt (fp32 accumulation; the sums' order differs from
- * the hand-written matrix-core kernel's, which zero selects). Stage 9:
- * grid nonzero (the default) runs a BF16 layer's two-plane prefill
- * products as one hipBLASLt call each over operand rows [hi | lo] against
- * a prefill copy of the layer's matrices with each weight row held twice
- * (made at the first such prefill: twice those matrices' bytes); zero runs
- * two calls per product, the second accumulating. Returns 0 or
- * TINYOAI_EINVAL. */
+ * products on wide matrix-core tiles (the in-projection with its epilogue
+ * in one launch, the o and down products together as K splits), zero on
+ * 128 x 256 tiles (fp32 accumulation either way; the sums' order
+ * differs). Returns 0 or TINYOAI_EINVAL. */
 int tinyoai_stablelm_set_launch(tinyoai_model *m, int32_t stage, int32_t grid, int32_t threads);
 int tinyoai_stablelm_profile_read(tinyoai_model *m, double *ms, int64_t *counts, int32_t n_stages);
 

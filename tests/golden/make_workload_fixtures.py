@@ -11,6 +11,13 @@ same weights and prompts without storing them.
     python tests/golden/make_workload_fixtures.py q8_0_decode   # 32 layers, 512 + 256
     python tests/golden/make_workload_fixtures.py bf16_long     # 2 layers, 8129 + 16, fp16 KV
     python tests/golden/make_workload_fixtures.py kquant_branches  # 2 layers, 16 ragged branches
+    python tests/golden/make_workload_fixtures.py bf16_long_full   # 32 layers, 8129 + 64, fp16 KV
+    python tests/golden/make_workload_fixtures.py kquant_branches_full  # 32 layers, 16 x 64 steps
+
+The two-layer versions run in minutes; the full-depth ones take hours of CPU
+time (ORACLE_THREADS sets the thread count) and carry the whole trajectory:
+every decode token of the long-context workload and every lockstep token of
+the branch workload.
 
 A logits vector is kept as a summary: its minimum and maximum, its 16
 largest entries (index and value) and its values at LOGIT_SAMPLE, a fixed
@@ -39,6 +46,11 @@ Q8_DECODE = dict(layers=32, max_pos=1024, weights_seed=1234, prompt_seed=1235, p
 BF16_LONG = dict(layers=2, max_pos=8192, weights_seed=41, prompt_seed=43, prompt=8129, generate=16)
 KQ_BRANCHES = dict(layers=2, max_pos=8192, weights_seed=31, prompt_seed=37, prefix=4096, branches=16,
                    min_suffix=1, max_suffix=256, steps=8)
+# Full depth: the same weights seeds and prompts with all 32 layers and the
+# workloads' own token counts. The branch suffixes go through the oracle's
+# batched prefill (prefill.go:33-115), as the forwarder's append submits them.
+BF16_LONG_FULL = dict(BF16_LONG, layers=32, generate=64)
+KQ_BRANCHES_FULL = dict(KQ_BRANCHES, layers=32, steps=64, suffix_prefill=True)
 
 
 def summarize(logits: np.ndarray) -> dict:
@@ -106,8 +118,7 @@ def make_q8_0_decode(path: str) -> None:
                         **{f"logits_{k}": v for k, v in stack(sums).items()})
 
 
-def make_bf16_long(path: str) -> None:
-    p = BF16_LONG
+def make_bf16_long(path: str, p: dict = BF16_LONG) -> None:
     config, tensors, prompt = bf16_inputs(p)
     m = pyoracle.StableLM(config, tensors, half_kv=True, capacity=p["max_pos"])
     m.trace(True)
@@ -121,13 +132,15 @@ def make_bf16_long(path: str) -> None:
         toks.append(int(np.argmax(logits)))
         if n + 1 < p["generate"]:
             logits = m.forward(toks[-1], p["prompt"] + n)
+        if n % 16 == 0:
+            print(f"token {n} ({time.time() - t0:.0f}s)", flush=True)
     trace_last = m.trace_data()
     np.savez_compressed(path, tokens=np.array(toks, np.int32), trace_prompt=trace_prompt.astype(np.float32),
                         trace_last=trace_last.astype(np.float32),
                         **{f"logits_{k}": v for k, v in stack(sums).items()})
 
 
-def make_kquant_branches(path: str) -> None:
+def make_kquant_branches(path: str, p: dict = KQ_BRANCHES) -> None:
     """One oracle prefilled with the shared prefix; each branch is replayed
     on it in turn (forward at position P + s rewrites only positions >= P,
     and attention at position t reads [0, t]), as nativeBranches evaluates a
@@ -142,8 +155,11 @@ def make_kquant_branches(path: str) -> None:
     toks = np.zeros((p["branches"], p["steps"]), np.int32)
     sums = []
     for j, suf in enumerate(suffixes):
-        for i, tok in enumerate(suf):
-            logits = m.forward(int(tok), P + i, i + 1 == len(suf))
+        if p.get("suffix_prefill"):
+            logits = m.prefill(suf, P)
+        else:
+            for i, tok in enumerate(suf):
+                logits = m.forward(int(tok), P + i, i + 1 == len(suf))
         row = []
         for s in range(p["steps"]):
             row.append(summarize(logits))
@@ -158,7 +174,9 @@ def make_kquant_branches(path: str) -> None:
                            for k, v in flat.items()})
 
 
-MAKERS = {"q8_0_decode": make_q8_0_decode, "bf16_long": make_bf16_long, "kquant_branches": make_kquant_branches}
+MAKERS = {"q8_0_decode": make_q8_0_decode, "bf16_long": make_bf16_long, "kquant_branches": make_kquant_branches,
+          "bf16_long_full": lambda path: make_bf16_long(path, BF16_LONG_FULL),
+          "kquant_branches_full": lambda path: make_kquant_branches(path, KQ_BRANCHES_FULL)}
 
 
 def fixture_path(name: str) -> str:

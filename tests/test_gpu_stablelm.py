@@ -271,37 +271,37 @@ def test_fused_decode_attention_matches_separate_launch(hip, dtype, kv_bits):
     ref.close()
 
 
-def test_joined_bf16_products_match_two_calls(hip):
-    """BF16 prefill products as one hipBLASLt call over operand rows
-    [hi | lo] against a copy of the matrices with each weight row held twice
-    (the default) against two calls per product, the second accumulating
-    (launch stage 9 off): the same products summed in another order, so a
-    2100-token prefill (a full 2048-token chunk and a partial one) gives
-    logits, per-layer residuals and (fp32) KV within 1e-5 of their range and the
-    same greedy ids over 8 decode tokens."""
+def test_wide_bf16_prefill_matches_large_tiles(hip):
+    """The BF16 prefill on wide tiles (the default: the in-projection with
+    its epilogue in one launch, the o and down products as one launch of K
+    splits) against the 128 x 256 tiles with a separate down product and
+    epilogue (launch stage 7 off): the same fp32 products summed in another
+    order, so a 2100-token prefill (a full 2048-token chunk and a partial
+    one) gives logits, per-layer residuals and (fp32) KV within 1e-5 of their
+    range, and the same greedy ids over 8 decode tokens."""
     config = W.validate_stablelm_config(dict(W.STABLELM_3B, num_hidden_layers=2, max_position_embeddings=4096))
     tensors = W.synthetic_stablelm(config, W.BF16, seed=21)
     prompt = np.random.default_rng(23).integers(0, 65536, 2100).astype(np.int32)
-    joined = hip.StableLMForwarder(config, tensors)
+    wide = hip.StableLMForwarder(config, tensors)
     ref = hip.StableLMForwarder(config, tensors)
     del tensors
-    ref.set_launch("joined", 0, 0)
-    for f in (joined, ref):
+    ref.set_launch("wide", 0, 0)
+    for f in (wide, ref):
         f.trace(True)
-    lj, lr = joined.forward(0, prompt), ref.forward(0, prompt)
+    lw, lr = wide.forward(0, prompt), ref.forward(0, prompt)
     span = float(np.ptp(lr))
-    assert np.max(np.abs(lj - lr)) <= 1e-5 * span
+    assert np.max(np.abs(lw - lr)) <= 1e-5 * span
     tr = ref.trace_read()
-    assert np.max(np.abs(joined.trace_read() - tr)) <= 1e-5 * float(np.ptp(tr))
+    assert np.max(np.abs(wide.trace_read() - tr)) <= 1e-5 * float(np.ptp(tr))
     for layer in range(2):
         for head in (0, 19):
-            for a, b in zip(joined.read_kv(layer, head, 2100), ref.read_kv(layer, head, 2100)):
+            for a, b in zip(wide.read_kv(layer, head, 2100), ref.read_kv(layer, head, 2100)):
                 assert np.max(np.abs(a - b)) <= 1e-5 * float(np.ptp(b)), (layer, head)
     for step in range(8):
         tok = int(np.argmax(lr))
-        assert int(np.argmax(lj)) == tok, step
-        lj, lr = joined.forward(2100 + step, [tok]), ref.forward(2100 + step, [tok])
-    joined.close()
+        assert int(np.argmax(lw)) == tok, step
+        lw, lr = wide.forward(2100 + step, [tok]), ref.forward(2100 + step, [tok])
+    wide.close()
     ref.close()
 
 

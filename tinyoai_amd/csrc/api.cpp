@@ -307,7 +307,6 @@ void Profiler::clear() {
 // ---------------------------------------------------------------- StableLM
 StableModel::~StableModel() {
   free_kv();
-  blaslt_destroy(blas);
   for (void *p : buffers) hipFree(p);
   if (h_pinned) hipHostFree(h_pinned);
   if (h_io) hipHostFree(h_io);
@@ -508,8 +507,7 @@ int StableModel::init(const tinyoai_stablelm_config &c, const tinyoai_tensor *te
       (rc = alloc((void **)&P, kPrefillSplits * B * d * 4)) || (rc = alloc((void **)&D, kPrefillSplits * B * d * 4)) ||
       (rc = alloc((void **)&XH, 2 * B * wide * 2)) || (rc = alloc((void **)&MH, 2 * B * I * 2)))
     return rc;
-  // One allocation per operand: the hi plane, then the lo plane; joined
-  // products use the whole of it as rows [hi | lo].
+  // One allocation per operand: the hi plane, then the lo plane.
   XL = XH + B * wide;
   ML = MH + B * I;
   // The error word after the logits: set by a decode step whose bounded
@@ -817,28 +815,50 @@ int StableModel::project(const MatDesc &w, const float *x, int ldx, int n, float
 }
 
 
-bool StableModel::blas_ready() {
-  if (!blas_tried) {
-    blas_tried = true;
-    blas = blaslt_create();
-  }
-  return blas != nullptr;
+// The wide-tile shape (rows per block 128 * mf, columns 32 * nf) for an
+// n-row product with N outputs: the fewest rounds of 256 blocks weighted
+// by the tile area, the 64-row-per-wave tiles counted at their measured
+// advantage (2048 x 21504 x 2560 with two planes: 472 us at 256 x 224
+// against 551 at 128 x 256).
+static void wide_shape(int n, int N, int *mf, int *nf) {
+  double best = 1e30;
+  for (int f = 2; f >= 1; f--)
+    for (int c = 7; c <= 8; c++) {
+      const int64_t tiles = (int64_t)((n + 128 * f - 1) / (128 * f)) * ((N + 32 * c - 1) / (32 * c));
+      const double cost = (double)((tiles + 255) / 256) * (128 * f) * (32 * c) / (f == 2 ? 1.0 : 0.85);
+      if (cost < best) {
+        best = cost;
+        *mf = f;
+        *nf = c;
+      }
+    }
 }
 
-bool StableModel::blas_product(const MatDesc &w, const uint16_t *xh, const uint16_t *xl, int n, float *y,
-                               int ldy) {
-  if (!use_blaslt || w.fmt != FMT_BF16 || !blas_ready()) return false;
-  prof.begin(ST_PREFILL_GEMM, stream);
-  hipError_t e = blaslt_bf16_product(blas, w, xh, n, y, ldy, false, stream);
-  if (e == hipSuccess && xl) e = blaslt_bf16_product(blas, w, xl, n, y, ldy, true, stream);
-  prof.end(stream);
-  return e == hipSuccess;
+// K splits of the o and down products of an n-row chunk on 256 x 256
+// tiles, launched together: about one block per CU in all, shared in
+// proportion to the K lengths (2048 rows at the 3B shapes: 1 + 2, 225 us
+// against 258 for 2 + 6 and 326 for 1 + 1), each split at least four K
+// steps.
+static void wide_out_splits(int n, int d, int64_t ko, int64_t kd, int max_splits, int *so, int *sd) {
+  const int tiles = ((n + 255) / 256) * ((d + 255) / 256);
+  const int total = std::max(2, (256 + tiles / 2) / tiles);
+  int o = std::max<int>(1, (int)std::lround((double)total * ko / (ko + kd)));
+  int m = std::max(1, total - o);
+  *so = std::max(1, std::min({o, max_splits, (int)(ko / 32 / 4)}));
+  *sd = std::max(1, std::min({m, max_splits, (int)(kd / 32 / 4)}));
 }
 
 int StableModel::project_planes(const MatDesc &w, const uint16_t *xh, const uint16_t *xl, int n, float *y, int ldy,
                                 int *splits) {
-  if (blas_product(w, xh, xl, n, y, ldy)) {
-    if (splits) *splits = 1;
+  if (use_wide && w.fmt == FMT_BF16) {
+    int mf, nf;
+    wide_shape(n, w.rows, &mf, &nf);
+    const int64_t tiles = (int64_t)((n + 128 * mf - 1) / (128 * mf)) * ((w.rows + 32 * nf - 1) / (32 * nf));
+    int ks = 1;
+    if (splits) ks = (int)std::max<int64_t>(1, std::min<int64_t>({256 / std::max<int64_t>(1, tiles), kPrefillSplits, w.cols / 128}));
+    if (splits) *splits = ks;
+    const WideGemm g{w, xh, xl, w.cols, y, ldy, ks, (int64_t)n * ldy};
+    STAGE(ST_PREFILL_GEMM, launch_gemm_wide(&g, 1, n, mf, nf, stream), "projection");
     return TINYOAI_OK;
   }
   const int ks = splits ? gemm_splits(w, n, kPrefillSplits) : 1;
@@ -847,68 +867,13 @@ int StableModel::project_planes(const MatDesc &w, const uint16_t *xh, const uint
   return TINYOAI_OK;
 }
 
-// The prefill copies of the joined-plane products for every layer whose
-// win and wout are BF16 and fused (rows of each weight row twice).
-int StableModel::ensure_joined() {
-  if (joined_tried) return TINYOAI_OK;
-  joined_tried = true;
-  const int L = cfg.num_hidden_layers;
-  joined_in.assign(L, MatDesc{});
-  joined_out.assign(L, MatDesc{});
-  const int64_t d = dims.d, I = dims.inter;
-  for (int l = 0; l < L; l++) {
-    const LayerDev &w = layers[l];
-    if (w.win.fmt != FMT_BF16 || w.wout.fmt != FMT_BF16 || w.win2.rows || w.wout2.rows) continue;
-    const int64_t down0 = (d + 7) / 8 * 8;
-    if (w.wout.cols < down0 + I) continue;
-    MatDesc a{}, b{};
-    a.fmt = b.fmt = FMT_BF16;
-    a.rows = w.win.rows;
-    a.cols = 2 * w.win.cols;
-    a.vstride = ((int64_t)a.cols * 2 + 15) / 16 * 16;
-    a.chunks = (int32_t)(a.vstride / 16);
-    b.rows = w.wout.rows;
-    b.cols = (int32_t)(2 * d + 2 * I);
-    b.vstride = ((int64_t)b.cols * 2 + 15) / 16 * 16;
-    b.chunks = (int32_t)(b.vstride / 16);
-    void *pa = nullptr, *pb = nullptr;
-    if (int rc = alloc(&pa, (size_t)a.rows * a.vstride)) return rc;
-    if (int rc = alloc(&pb, (size_t)b.rows * b.vstride)) return rc;
-    a.vals = (const uint8_t *)pa;
-    b.vals = (const uint8_t *)pb;
-    const size_t wi = (size_t)w.win.cols * 2;
-    for (int c = 0; c < 2; c++)
-      TRY_HIP(hipMemcpy2DAsync((char *)pa + c * wi, a.vstride, w.win.vals, w.win.vstride, wi, a.rows,
-                               hipMemcpyDeviceToDevice, stream),
-              "joined copy");
-    const size_t wo = (size_t)d * 2, wd = (size_t)I * 2;
-    for (int c = 0; c < 2; c++) {
-      TRY_HIP(hipMemcpy2DAsync((char *)pb + c * wo, b.vstride, w.wout.vals, w.wout.vstride, wo, b.rows,
-                               hipMemcpyDeviceToDevice, stream),
-              "joined copy");
-      TRY_HIP(hipMemcpy2DAsync((char *)pb + 2 * wo + c * wd, b.vstride, w.wout.vals + down0 * 2, w.wout.vstride, wd,
-                               b.rows, hipMemcpyDeviceToDevice, stream),
-              "joined copy");
-    }
-    joined_in[l] = a;
-    joined_out[l] = b;
-  }
-  return TINYOAI_OK;
-}
-
-// Whether layer l's products of an n-row chunk run joined (the copies made
-// and the library holding a plan for each of the three shapes).
-bool StableModel::joined_layer(int l, int n) {
-  if (!use_joined || !use_blaslt || bf16_acts || !blas_ready()) return false;
+// Whether layer l's prefill takes the wide-tile BF16 path: fused BF16
+// win and wout, operands in bf16 planes from their producers.
+bool StableModel::wide_layer(int l) const {
   const LayerDev &w = layers[l];
-  if (w.win.fmt != FMT_BF16 || w.wout.fmt != FMT_BF16 || w.win2.rows || w.wout2.rows ||
-      !flash_prefill_supported(dims.hd) || dims.heads * dims.hd != dims.d)
-    return false;
-  if (ensure_joined() || joined_in[l].rows == 0) return false;
-  const int64_t d = dims.d, I = dims.inter;
-  return blaslt_bf16_ready(blas, joined_in[l], n, win_rows) &&
-         blaslt_bf16_ready(blas, column_view(joined_out[l], 0, 2 * d), n, (int)d) &&
-         blaslt_bf16_ready(blas, column_view(joined_out[l], 2 * d, 2 * I), n, (int)d);
+  return use_wide && w.win.fmt == FMT_BF16 && w.wout.fmt == FMT_BF16 && !w.win2.rows && !w.wout2.rows &&
+         flash_prefill_supported(dims.hd) && dims.heads * dims.hd == dims.d && w.win.cols % 32 == 0 &&
+         dims.inter % 32 == 0;
 }
 
 // n tokens at positions start.. (StableLM.prefill, prefill.go:33-115): per
@@ -935,26 +900,27 @@ int StableModel::prefill_chunk(const int32_t *ids, int n, int start, bool want_l
     // the matrix cores) -> MH, ML -> down; attention -> XH, XL -> o.
     const bool pin = !split_in && gemm_mfma_supported(w.win), pd = gemm_mfma_supported(wd);
     const bool flash = flash_prefill_supported(dims.hd), po = flash && gemm_mfma_supported(wo);
-    if (pin && pd && po && joined_layer(l, n)) {
-      // One product per matrix over operand rows [hi | lo] (K doubled)
-      // against the layer's prefill copies.
-      const MatDesc wj = joined_in[l], woj = column_view(joined_out[l], 0, 2 * d),
-                    wdj = column_view(joined_out[l], 2 * d, 2 * I);
-      STAGE(ST_PREFILL_NORM,
-            launch_layer_norm_rows(X, w.ln_w, w.ln_b, dims.eps, n, d, nullptr, stream, XH, XH + d, 2 * d),
+    if (wide_layer(l)) {
+      // BF16 layers on wide tiles: LayerNorm -> planes; win with its
+      // epilogue in the product's own launch (q, K/V, SiLU-gate planes);
+      // attention -> planes; the o and down products as one launch of K
+      // splits; the parallel residual sums them in order.
+      const uint16_t *lo = lo_plane(w.win);
+      STAGE(ST_PREFILL_NORM, launch_layer_norm_rows(X, w.ln_w, w.ln_b, dims.eps, n, d, nullptr, stream, XH, XL),
             "layer_norm");
-      STAGE(ST_PREFILL_GEMM, blaslt_bf16_product(blas, wj, XH, n, Y, win_rows, false, stream), "projection");
-      STAGE(ST_PREFILL_EPILOGUE,
-            launch_in_epilogue(dims, kv[l], Y, win_rows, rope, d_pos0, n, Q, tracing ? M : nullptr, stream, MH,
-                               MH + I, nullptr, 1, 2 * I),
-            "in_epilogue");
-      STAGE(ST_PREFILL_GEMM, blaslt_bf16_product(blas, wdj, MH, n, D, d, false, stream), "projection");
+      int mf, nf;
+      wide_shape(n, w.win.rows, &mf, &nf);
+      const InEpilogue e{dims, kv[l], rope, d_pos0, Q, tracing ? M : nullptr, MH, ML, 0};
+      STAGE(ST_PREFILL_GEMM, launch_gemm_wide_in_epilogue(w.win, XH, lo, d, n, e, mf, nf, stream),
+            "projection + epilogue");
       STAGE(ST_PREFILL_ATTENTION,
-            launch_flash_prefill(dims, kv[l], Q, d_pos0, n, tracing ? A : nullptr, stream, XH, XH + d, nullptr, 0,
-                                 0, 2 * d),
-            "attention");
-      STAGE(ST_PREFILL_GEMM, blaslt_bf16_product(blas, woj, XH, n, P, d, false, stream), "projection");
-      STAGE(ST_PREFILL_ELEMENTWISE, launch_residual(X, P, 1, D, 1, (int64_t)n * d, stream), "residual");
+            launch_flash_prefill(dims, kv[l], Q, d_pos0, n, tracing ? A : nullptr, stream, XH, XL), "attention");
+      int so, sd;
+      wide_out_splits(n, d, d, I, kPrefillSplits, &so, &sd);
+      const WideGemm prods[2] = {{wd, MH, lo ? ML : nullptr, I, D, d, sd, (int64_t)n * d},
+                                 {wo, XH, lo ? XL : nullptr, d, P, d, so, (int64_t)n * d}};
+      STAGE(ST_PREFILL_GEMM, launch_gemm_wide(prods, 2, n, 2, 8, stream), "projection");
+      STAGE(ST_PREFILL_ELEMENTWISE, launch_residual(X, P, so, D, sd, (int64_t)n * d, stream), "residual");
     } else {
       STAGE(ST_PREFILL_NORM,
             launch_layer_norm_rows(X, w.ln_w, w.ln_b, dims.eps, n, d, pin ? nullptr : H, stream, pin ? XH : nullptr,
@@ -987,13 +953,10 @@ int StableModel::prefill_chunk(const int32_t *ids, int n, int start, bool want_l
         STAGE(ST_PREFILL_EPILOGUE,
               launch_in_epilogue(dims, kv[l], Y, win_rows, rope, d_pos0, n, Q, m32, stream, MH, ML, nullptr, 2),
               "in_epilogue");
-      } else if (pin && pd && !blas_product(w.win, XH, lo_plane(w.win), n, Y, win_rows)) {
-        const InEpilogue e{dims, kv[l], rope, d_pos0, Q, m32, MH, ML};
+      } else if (pin && pd) {
+        const InEpilogue e{dims, kv[l], rope, d_pos0, Q, m32, MH, ML, 0};
         STAGE(ST_PREFILL_GEMM, launch_gemm_in_epilogue(w.win, XH, lo_plane(w.win), n, e, stream),
               "projection + epilogue");
-      } else if (pin && pd) {  // the product is in Y (hipBLASLt)
-        STAGE(ST_PREFILL_EPILOGUE,
-              launch_in_epilogue(dims, kv[l], Y, win_rows, rope, d_pos0, n, Q, m32, stream, MH, ML), "in_epilogue");
       } else {
         if ((rc = pin ? project_planes(w.win, XH, lo_plane(w.win), n, Y, win_rows)
                       : project(w.win, H, d, n, Y, win_rows)))
@@ -1731,12 +1694,8 @@ int tinyoai_stablelm_trace_read_stages(tinyoai_model *m, float *attention, float
 int tinyoai_stablelm_set_launch(tinyoai_model *m, int32_t stage, int32_t grid, int32_t threads) {
   if (!m || !m->stable) return fail(TINYOAI_EINVAL, "not a StableLM handle");
   StableModel &s = *m->stable;
-  if (stage == 9) {  // joined-plane BF16 prefill products (1, the default) or two calls per product (0)
-    s.use_joined = grid != 0;
-    return TINYOAI_OK;
-  }
-  if (stage == 7) {  // BF16-weight prefill products on hipBLASLt (1, the default) or the matrix-core kernel (0)
-    s.use_blaslt = grid != 0;
+  if (stage == 7) {  // BF16-weight prefill products on wide tiles (1, the default) or 128 x 256 tiles (0)
+    s.use_wide = grid != 0;
     return TINYOAI_OK;
   }
   if (stage == 5) {  // BF16-weight prefill products with bf16 activations (1) or two planes (0, the default)

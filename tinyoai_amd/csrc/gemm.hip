@@ -342,6 +342,605 @@ __global__ __launch_bounds__(kLThreads) void gemm_large_kernel(GemmArgs g) {
     }
 }
 
+// ------------------------------------------------------------ wide tiles
+// One wave per SIMD: four waves of a 256-thread block own 32 * MF rows
+// each (block rows BM = 128 * MF) and all BN = 32 * NF columns of the
+// block's tile, as MF x NF tiles of v_mfma_f32_32x32x16_bf16; per k16 a
+// wave reads MF * XS activation and NF weight fragments from LDS for
+// XS * MF * NF products (MF = 2, NF = 7, two planes: 11 fragment reads for
+// 28 products). A K step is 32 values (one Q8_0 block).
+//
+// Both operands reach LDS through registers with coalesced loads (four
+// lanes per 64-byte row segment of a step): loading activations straight
+// into the fragment layout puts 32 rows in every load instruction, and
+// the address unit then stalls on the L1 cache (measured: 41% matrix-core
+// busy, most wave time waiting on loads). Every load and LDS store is
+// issued unconditionally (loads past an operand read zeros; chunks past
+// the tile land in LDS padding), so the count of loads in flight is the
+// same on every path and each wait covers only the loads it needs.
+//
+// Pipeline: three register stages loaded three K steps ahead, the LDS
+// tiles double-buffered. Step kb issues the loads of kb + 3, forms the
+// products of kb, stores the registers of kb + 1 into the other LDS
+// buffer and waits at the block barrier.
+//
+// LDS rows are 64 bytes (32 bf16) as four 16-byte chunks, chunk c of row r
+// at position c ^ ((r >> 2) & 3): the 16 lanes of a fragment read that
+// share a chunk index hit 16 distinct bank groups. Lane l of a fragment
+// holds the 16 consecutive values 16 * (l / 32) .. + 15 of its row's step,
+// the first 8 for the step's first product and the rest for its second;
+// activation and weight fragments use the same k order, so each step is
+// covered exactly once.
+//
+// Q8_0: quants become bf16 (exactly) on their way into LDS, the block's
+// fp16 scale as fp32 beside the tile; each step's products are formed
+// without scale and added as acc += d * t.
+//
+// Blocks map onto the 8 XCDs in runs: XCD x takes tiles [x * per, (x + 1)
+// * per) (M tiles fastest), so the blocks resident on one XCD share their
+// weight tiles through its L2.
+struct WideProduct {
+  MatDesc w;                // N = rows, K = cols (a column view of a larger matrix is fine)
+  const uint16_t *xh, *xl;  // bf16 planes, rows lda values apart
+  int lda;
+  float *y;                 // split s at y + s * split_stride, rows ldy floats apart
+  int ldy;
+  int ksplit;
+  int64_t split_stride;
+};
+struct WideArgs {
+  WideProduct p[2];  // one launch may carry two products of the same tile shape
+  int nprod;
+  int M;
+  InEpilogue e;      // EPI: the fused in-projection epilogue (one product, no split)
+};
+
+constexpr int kWThreads = 256, kWK = 32;
+
+// Weight rows of an LDS stage: the tile's rows rounded up to what the
+// threads' unconditional chunk stores cover (kWThreads chunks of 4 per
+// row for BF16, 2 per row for Q8_0).
+template <int WF, int NF>
+constexpr int kBRows() {
+  constexpr int per = WF == FMT_BF16 ? 4 : 2, chunks = NF * 32 * per;
+  return (chunks + kWThreads - 1) / kWThreads * kWThreads / per;
+}
+// uint16 units of an LDS stage: XS activation planes of BM rows, the
+// weight rows, then (Q8_0) one fp32 scale per thread.
+template <int WF, int XS, int MF, int NF>
+constexpr int wide_stage_u16() {
+  return XS * 128 * MF * kWK + kBRows<WF, NF>() * kWK + (WF == FMT_Q8_0 ? kWThreads * 2 : 0);
+}
+
+template <int WF, int XS, int MF, int NF, bool EPI>
+constexpr size_t gemm_wide_lds() {
+  // two stages; with EPI also 32 output rows per wave
+  const size_t stage = (size_t)2 * wide_stage_u16<WF, XS, MF, NF>() * 2;
+  const size_t rows = (size_t)4 * 32 * (NF * 32 + 4) * 4;
+  return EPI && rows > stage ? rows : stage;
+}
+
+__device__ __forceinline__ int swz(int row, int c) { return row * kWK + ((c ^ ((row >> 2) & 3)) << 3); }
+
+template <int WF, int XS, int MF, int NF, bool EPI>
+__global__ __launch_bounds__(kWThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_wide_kernel(WideArgs g) {
+  constexpr int BM = 4 * 32 * MF, BN = 32 * NF;
+  constexpr int kBChunks = WF == FMT_BF16 ? BN * 4 : BN * 2;  // 16-byte weight chunks a stage loads
+  constexpr int NB = (kBChunks + kWThreads - 1) / kWThreads;
+  constexpr int NA = BM * 4 / kWThreads;                      // activation chunks per plane and thread
+  constexpr int kA = BM * kWK;                                // uint16 units of an activation plane
+  constexpr int kStage = wide_stage_u16<WF, XS, MF, NF>();
+  constexpr int kB0 = XS * kA, kS0 = kB0 + kBRows<WF, NF>() * kWK;
+  extern __shared__ __align__(16) uint16_t lds16[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+
+  // Which product, tile and split this block computes.
+  int b = blockIdx.x, pi = 0;
+  {
+    const WideProduct &p0 = g.p[0];
+    const int tiles0 = ((g.M + BM - 1) / BM) * ((p0.w.rows + BN - 1) / BN);
+    const int nb0 = (tiles0 * p0.ksplit + 7) / 8 * 8;
+    if (g.nprod > 1 && b >= nb0) {
+      b -= nb0;
+      pi = 1;
+    }
+  }
+  const WideProduct &P = g.p[pi];
+  const int K = P.w.cols, N = P.w.rows, nk = K / kWK;
+  const int MT = (g.M + BM - 1) / BM, NT = (N + BN - 1) / BN, tiles = MT * NT;
+  const int total = tiles * P.ksplit, per = (total + 7) / 8;
+  const int t = (b & 7) * per + (b >> 3);
+  if (t >= total) return;
+  const int split = t / tiles, tt = t - split * tiles, nt = tt / MT, mt = tt - nt * MT;
+  const int m0 = mt * BM, n0 = nt * BN;
+  const int k_lo = (int)((int64_t)nk * split / P.ksplit), k_hi = (int)((int64_t)nk * (split + 1) / P.ksplit);
+
+  // Sentinels past every operand (each under 1 GiB, checked at launch): a
+  // row past M or N, and a K step past the split; their sum stays below
+  // 2^32.
+  constexpr uint32_t kNone = 0x80000000u, kPast = 0x40000000u;
+  const __amdgpu_buffer_rsrc_t rxh = plane_rsrc(reinterpret_cast<const uint8_t *>(P.xh), (int64_t)g.M * P.lda * 2);
+  const __amdgpu_buffer_rsrc_t rxl =
+      plane_rsrc(reinterpret_cast<const uint8_t *>(XS == 2 ? P.xl : P.xh), (int64_t)g.M * P.lda * 2);
+  const __amdgpu_buffer_rsrc_t rw = plane_rsrc(P.w.vals, (int64_t)N * P.w.vstride);
+  const __amdgpu_buffer_rsrc_t rs =
+      plane_rsrc(WF == FMT_Q8_0 ? P.w.meta : P.w.vals, WF == FMT_Q8_0 ? (int64_t)N * P.w.mstride : 0);
+  auto ld16 = [](__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+    return make_uint4(v.x, v.y, v.z, v.w);
+  };
+
+  // Chunk q = tid + 256 i of a stage: activations row q / 4, chunk q % 4
+  // (per plane); BF16 weights likewise; Q8_0 weights row q / 2, 16 quants
+  // q % 2 (two bf16 chunks); the scale of row tid.
+  uint32_t aoff[NA], boff[NB];
+  int adst[NA], bdst[NB];
+#pragma unroll
+  for (int i = 0; i < NA; i++) {
+    const int q = tid + kWThreads * i, row = q >> 2, c = q & 3;
+    aoff[i] = m0 + row < g.M ? (uint32_t)(((m0 + row) * P.lda + c * 8) * 2) : kNone;
+    adst[i] = swz(row, c);
+  }
+#pragma unroll
+  for (int i = 0; i < NB; i++) {
+    const int q = tid + kWThreads * i;
+    if constexpr (WF == FMT_BF16) {
+      const int row = q >> 2, c = q & 3;
+      boff[i] = q < kBChunks && n0 + row < N ? (uint32_t)((n0 + row) * P.w.vstride + c * 16) : kNone;
+      bdst[i] = swz(row, c);
+    } else {
+      const int row = q >> 1;
+      boff[i] = q < kBChunks && n0 + row < N ? (uint32_t)((n0 + row) * P.w.vstride + (q & 1) * 16) : kNone;
+      bdst[i] = row;
+    }
+  }
+  const uint32_t soff = WF == FMT_Q8_0 && tid < BN && n0 + tid < N ? (uint32_t)((n0 + tid) * P.w.mstride) : kNone;
+
+  struct Regs {
+    uint4 a[XS][NA], b[NB];
+    uint32_t s;
+  };
+  // Loads of step kb (kb past the split: offsets past every operand).
+  auto load = [&](int kb, Regs &r) {
+    const bool in = kb < k_hi;
+    const uint32_t ka = in ? (uint32_t)(kb * kWK * 2) : kPast;
+    const uint32_t kw = in ? (uint32_t)(WF == FMT_BF16 ? kb * kWK * 2 : kb * kWK) : kPast;
+#pragma unroll
+    for (int i = 0; i < NB; i++) r.b[i] = ld16(rw, boff[i] + kw);
+#pragma unroll
+    for (int p = 0; p < XS; p++)
+#pragma unroll
+      for (int i = 0; i < NA; i++) r.a[p][i] = ld16(p ? rxl : rxh, aoff[i] + ka);
+    if constexpr (WF == FMT_Q8_0)
+      r.s = __builtin_amdgcn_raw_buffer_load_b16(rs, (int)(soff + (in ? (uint32_t)kb * 2 : kPast)), 0, 0);
+  };
+  auto store = [&](int buf, const Regs &r) {
+    uint16_t *st = lds16 + buf * kStage;
+#pragma unroll
+    for (int p = 0; p < XS; p++)
+#pragma unroll
+      for (int i = 0; i < NA; i++) *reinterpret_cast<uint4 *>(st + p * kA + adst[i]) = r.a[p][i];
+#pragma unroll
+    for (int i = 0; i < NB; i++) {
+      if constexpr (WF == FMT_BF16) {
+        *reinterpret_cast<uint4 *>(st + kB0 + bdst[i]) = r.b[i];
+      } else {  // 16 int8 -> 16 bf16 (exact): chunks 2h, 2h + 1 of the row
+        const int h = (tid + kWThreads * i) & 1;
+        const uint32_t ws[4] = {r.b[i].x, r.b[i].y, r.b[i].z, r.b[i].w};
+        uint32_t o[8];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          const uint32_t v = ws[j];
+          o[2 * j] = bf16_bits((float)(int8_t)v) | bf16_bits((float)(int8_t)(v >> 8)) << 16;
+          o[2 * j + 1] = bf16_bits((float)(int8_t)(v >> 16)) | bf16_bits((float)(int8_t)(v >> 24)) << 16;
+        }
+        *reinterpret_cast<uint4 *>(st + kB0 + swz(bdst[i], 2 * h)) = make_uint4(o[0], o[1], o[2], o[3]);
+        *reinterpret_cast<uint4 *>(st + kB0 + swz(bdst[i], 2 * h + 1)) = make_uint4(o[4], o[5], o[6], o[7]);
+      }
+    }
+    if constexpr (WF == FMT_Q8_0) reinterpret_cast<float *>(st + kS0)[tid] = hw_half((uint16_t)r.s);
+  };
+
+  f32x16 acc[MF][NF];
+#pragma unroll
+  for (int f = 0; f < MF; f++)
+#pragma unroll
+    for (int j = 0; j < NF; j++)
+#pragma unroll
+      for (int v = 0; v < 16; v++) acc[f][j][v] = 0.f;
+  // Fragment rows: activations wave * 32 * MF + f * 32 + lane % 32 of each
+  // plane, weights j * 32 + lane % 32; chunk 2 * (lane / 32) + s.
+  const int arow = wave * 32 * MF + (lane & 31), brow = lane & 31;
+  auto frag = [&](const uint16_t *base, int row, int s) {
+    return *reinterpret_cast<const bf16x8 *>(base + swz(row, 2 * (lane >> 5) + s));
+  };
+  auto compute = [&](int buf) {
+    const uint16_t *st = lds16 + buf * kStage;
+    if constexpr (WF == FMT_BF16) {
+#pragma unroll
+      for (int s = 0; s < 2; s++) {
+        bf16x8 af[MF][XS], bf[NF];
+#pragma unroll
+        for (int j = 0; j < NF; j++) bf[j] = frag(st + kB0, j * 32 + brow, s);
+#pragma unroll
+        for (int f = 0; f < MF; f++)
+#pragma unroll
+          for (int p = 0; p < XS; p++) af[f][p] = frag(st + p * kA, arow + f * 32, s);
+#pragma unroll
+        for (int f = 0; f < MF; f++)
+#pragma unroll
+          for (int p = 0; p < XS; p++)
+#pragma unroll
+            for (int j = 0; j < NF; j++)
+              acc[f][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[f][p], bf[j], acc[f][j], 0, 0, 0);
+      }
+    } else {
+      const float *scl = reinterpret_cast<const float *>(st + kS0);
+      bf16x8 af[MF][XS][2];
+#pragma unroll
+      for (int f = 0; f < MF; f++)
+#pragma unroll
+        for (int p = 0; p < XS; p++)
+#pragma unroll
+          for (int s = 0; s < 2; s++) af[f][p][s] = frag(st + p * kA, arow + f * 32, s);
+#pragma unroll
+      for (int j = 0; j < NF; j++) {
+        bf16x8 bf[2];
+#pragma unroll
+        for (int s = 0; s < 2; s++) bf[s] = frag(st + kB0, j * 32 + brow, s);
+        const float sc = scl[j * 32 + brow];
+#pragma unroll
+        for (int f = 0; f < MF; f++) {
+          f32x16 tq;
+#pragma unroll
+          for (int v = 0; v < 16; v++) tq[v] = 0.f;
+#pragma unroll
+          for (int s = 0; s < 2; s++)
+#pragma unroll
+            for (int p = 0; p < XS; p++) tq = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[f][p][s], bf[s], tq, 0, 0, 0);
+#pragma unroll
+          for (int v = 0; v < 16; v++) acc[f][j][v] = fmaf(sc, tq[v], acc[f][j][v]);
+        }
+      }
+    }
+  };
+
+  // Six steps per trip (three register stages, two LDS buffers). Full
+  // trips run without conditions (a guard per step made the compiler's
+  // count of loads in flight conservative at every join, and it then
+  // waited for the next step's loads at the head of each step); the last
+  // trip (fewer than six steps) takes the guarded steps. The scheduling
+  // barriers keep the loads at the head of the step (the scheduler
+  // otherwise sank them below the products).
+  Regs r0, r1, r2;
+  load(k_lo, r0);
+  load(k_lo + 1, r1);
+  load(k_lo + 2, r2);
+  store(0, r0);
+  __syncthreads();
+  auto step = [&](int kb, Regs &rload, const Regs &rstore, int buf) {
+    load(kb + 3, rload);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(buf);
+    __builtin_amdgcn_sched_barrier(0);
+    store(buf ^ 1, rstore);
+    __syncthreads();
+  };
+  int kb = k_lo;
+  for (; kb + 6 <= k_hi; kb += 6) {
+    step(kb, r0, r1, 0);
+    step(kb + 1, r1, r2, 1);
+    step(kb + 2, r2, r0, 0);
+    step(kb + 3, r0, r1, 1);
+    step(kb + 4, r1, r2, 0);
+    step(kb + 5, r2, r0, 1);
+  }
+  if (kb < k_hi) step(kb, r0, r1, 0);
+  if (kb + 1 < k_hi) step(kb + 1, r1, r2, 1);
+  if (kb + 2 < k_hi) step(kb + 2, r2, r0, 0);
+  if (kb + 3 < k_hi) step(kb + 3, r0, r1, 1);
+  if (kb + 4 < k_hi) step(kb + 4, r1, r2, 0);
+
+  // D fragment: lane holds column lane % 32 of rows (v / 4) * 8 + (lane / 32) * 4 + v % 4.
+  if constexpr (EPI) {
+    // Each wave passes its rows through LDS, 32 at a time ([32][BN + 4]
+    // floats per wave), then its lanes take (row, output pair) items in
+    // order through the in-projection epilogue: neighbouring lanes store
+    // neighbouring outputs.
+    constexpr int kPitch = BN + 4;
+    float *tile = reinterpret_cast<float *>(lds16) + wave * 32 * kPitch;
+    const StableDims es = g.e.s;
+    const KVDev ekv = g.e.kv;
+    const float *rope = g.e.rope;
+    float *eq = g.e.q, *em = g.e.m;
+    uint16_t *emh = g.e.mh, *eml = g.e.ml;
+    const int ldm = g.e.ldm ? g.e.ldm : es.inter;
+    const int p0 = *g.e.pos0, mu0 = (es.win_q + 2 * es.win_kv) / 2;
+#pragma unroll
+    for (int f = 0; f < MF; f++) {
+#pragma unroll
+      for (int j = 0; j < NF; j++)
+#pragma unroll
+        for (int v = 0; v < 16; v++)
+          tile[((v >> 2) * 8 + (lane >> 5) * 4 + (v & 3)) * kPitch + j * 32 + (lane & 31)] = acc[f][j][v];
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      const int r0w = m0 + (wave * MF + f) * 32;
+      for (int it = lane; it < 32 * (BN / 2); it += 64) {
+        const int r = it / (BN / 2), c = 2 * (it - r * (BN / 2)), m = r0w + r, n = n0 + c, u = n >> 1;
+        if (m >= g.M || n >= N) continue;
+        const float2 pv = *reinterpret_cast<const float2 *>(tile + r * kPitch + c);
+        if (u >= mu0) {
+          const float gv = es.silu ? silu_gate_llama(pv.x, pv.y) : silu_gate(pv.x, pv.y);
+          if (em) em[(int64_t)m * es.inter + (u - mu0)] = gv;
+          store_bf16_split(emh, eml, (int64_t)m * ldm + (u - mu0), gv);
+        } else {
+          const int pos = p0 + m;
+          in_pair_epilogue(es, ekv, rope + (int64_t)pos * es.rot, pos, u, pv.x, pv.y,
+                           eq + (int64_t)m * es.heads * es.hd, nullptr);
+        }
+      }
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+    return;
+  }
+  float *y = P.y + (int64_t)split * P.split_stride;
+#pragma unroll
+  for (int f = 0; f < MF; f++)
+#pragma unroll
+    for (int j = 0; j < NF; j++) {
+      const int n = n0 + j * 32 + (lane & 31);
+      if (n >= N) continue;
+#pragma unroll
+      for (int v = 0; v < 16; v++) {
+        const int m = m0 + (wave * MF + f) * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
+        if (m < g.M) y[(int64_t)m * P.ldy + n] = acc[f][j][v];
+      }
+    }
+}
+
+// ------------------------------------------------------------ BF16 wide tiles, loads direct to LDS
+// The BF16 product on the same tiles as gemm_wide_kernel, with both
+// operands loaded straight into LDS (buffer_load_dwordx4 ... lds): no
+// staging registers, so each wave holds a step's fragments for both k
+// halves and the compiler keeps the LDS reads ahead of the products. A
+// ring of three LDS stages: step kb waits for its own loads of stage kb
+// (the count of loads in flight is exact: every wave issues the same
+// loads every step, past the operands reading zeros), meets the block
+// barrier (every wave's loads of kb landed, and every wave is done with
+// stage kb - 1), issues the loads of kb + 2 into kb - 1's slot and forms
+// the products of kb. Each wave load writes 1 KB of LDS (16 rows of a
+// step, 64 lane x 16 bytes in lane order); the chunk swizzle of the
+// fragment reads is applied on the global side: lane l fetches logical
+// chunk (l % 4) ^ ((row >> 2) & 3) of row l / 4.
+//
+// The loads are inline assembly: the compiler's own handling of LDS DMA
+// waits for every load in flight before any LDS read, which would leave
+// one step to hide the memory latency. The kernel waits for its loads
+// itself (s_waitcnt vmcnt) and issues no other vector memory load in the
+// loop.
+__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t lds_byte) {
+  asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(r), "{m0}"(lds_byte) : "memory");
+}
+// s_waitcnt with vmcnt(n) only (gfx9 encoding: vmcnt bits 3:0 and 15:14).
+template <int n>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(n >= 0 && n < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | 0x0f70);
+}
+
+template <int XS, int MF, int NF>
+constexpr int dma_slot_bytes() {
+  return XS * 128 * MF * 64 + 256 * 64;  // activation planes, then 256 weight rows (the tile's, then padding)
+}
+template <int XS, int MF, int NF, bool EPI>
+constexpr size_t gemm_dma_lds() {
+  const size_t ring = (size_t)3 * dma_slot_bytes<XS, MF, NF>();
+  const size_t rows = (size_t)4 * 32 * (NF * 32 + 4) * 4;
+  return EPI && rows > ring ? rows : ring;
+}
+
+template <int XS, int MF, int NF, bool EPI>
+__global__ __launch_bounds__(kWThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_dma_kernel(WideArgs g) {
+  constexpr int BM = 4 * 32 * MF, BN = 32 * NF;
+  static_assert(BN <= 256, "weight rows of a slot");
+  constexpr int kSlot = dma_slot_bytes<XS, MF, NF>(), kAPlane = BM * 64, kB0 = XS * kAPlane;
+  constexpr int NA = BM / 64;   // wave loads per activation plane and step
+  constexpr int NBW = 4;        // wave loads of the weight rows per step (256 rows)
+  constexpr int kPerStep = XS * NA + NBW;
+  extern __shared__ __align__(16) uint16_t lds16[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+
+  int b = blockIdx.x, pi = 0;
+  {
+    const WideProduct &p0 = g.p[0];
+    const int tiles0 = ((g.M + BM - 1) / BM) * ((p0.w.rows + BN - 1) / BN);
+    const int nb0 = (tiles0 * p0.ksplit + 7) / 8 * 8;
+    if (g.nprod > 1 && b >= nb0) {
+      b -= nb0;
+      pi = 1;
+    }
+  }
+  const WideProduct &P = g.p[pi];
+  const int K = P.w.cols, N = P.w.rows, nk = K / kWK;
+  const int MT = (g.M + BM - 1) / BM, NT = (N + BN - 1) / BN, tiles = MT * NT;
+  const int total = tiles * P.ksplit, per = (total + 7) / 8;
+  const int t = (b & 7) * per + (b >> 3);
+  if (t >= total) return;
+  const int split = t / tiles, tt = t - split * tiles, nt = tt / MT, mt = tt - nt * MT;
+  const int m0 = mt * BM, n0 = nt * BN;
+  const int k_lo = (int)((int64_t)nk * split / P.ksplit), k_hi = (int)((int64_t)nk * (split + 1) / P.ksplit);
+
+  constexpr uint32_t kNone = 0x80000000u, kPast = 0x40000000u;
+  const __amdgpu_buffer_rsrc_t rxh = plane_rsrc(reinterpret_cast<const uint8_t *>(P.xh), (int64_t)g.M * P.lda * 2);
+  const __amdgpu_buffer_rsrc_t rxl =
+      plane_rsrc(reinterpret_cast<const uint8_t *>(XS == 2 ? P.xl : P.xh), (int64_t)g.M * P.lda * 2);
+  const __amdgpu_buffer_rsrc_t rw = plane_rsrc(P.w.vals, (int64_t)N * P.w.vstride);
+
+  // Lane offsets of this wave's loads at k = 0 (the LDS side is the wave's
+  // 1 KB piece: row (16 j + lane / 4), position lane % 4).
+  const int lrow = lane >> 2, lc = (lane & 3) ^ ((lrow >> 2) & 3);
+  uint32_t aoff[NA], boff[NBW];
+#pragma unroll
+  for (int i = 0; i < NA; i++) {
+    const int row = (wave + 4 * i) * 16 + lrow;
+    aoff[i] = m0 + row < g.M ? (uint32_t)(((m0 + row) * P.lda + lc * 8) * 2) : kNone;
+  }
+#pragma unroll
+  for (int i = 0; i < NBW; i++) {
+    const int row = (wave + 4 * i) * 16 + lrow;
+    boff[i] = row < BN && n0 + row < N ? (uint32_t)((n0 + row) * P.w.vstride + lc * 16) : kNone;
+  }
+  const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)lds16;
+  const uint32_t wave_u = __builtin_amdgcn_readfirstlane(wave);
+  auto issue = [&](int kb, int slot) {
+    const uint32_t k2 = kb < k_hi ? (uint32_t)(kb * kWK * 2) : kPast;
+    const uint32_t sb = lds_base + slot * kSlot + wave_u * 1024;
+#pragma unroll
+    for (int p = 0; p < XS; p++)
+#pragma unroll
+      for (int i = 0; i < NA; i++) lds_dma16(p ? rxl : rxh, aoff[i] + k2, sb + p * kAPlane + i * 4096);
+#pragma unroll
+    for (int i = 0; i < NBW; i++) lds_dma16(rw, boff[i] + k2, sb + kB0 + i * 4096);
+  };
+
+  f32x16 acc[MF][NF];
+#pragma unroll
+  for (int f = 0; f < MF; f++)
+#pragma unroll
+    for (int j = 0; j < NF; j++)
+#pragma unroll
+      for (int v = 0; v < 16; v++) acc[f][j][v] = 0.f;
+  const int arow = wave * 32 * MF + (lane & 31), brow = lane & 31;
+  auto frag = [&](const uint16_t *base, int row, int s) {
+    return *reinterpret_cast<const bf16x8 *>(base + swz(row, 2 * (lane >> 5) + s));
+  };
+  auto compute = [&](int slot) {
+    const uint16_t *st = lds16 + slot * (kSlot / 2);
+    bf16x8 af[2][MF][XS], bf[2][NF];
+#pragma unroll
+    for (int s = 0; s < 2; s++) {
+#pragma unroll
+      for (int j = 0; j < NF; j++) bf[s][j] = frag(st + kB0 / 2, j * 32 + brow, s);
+#pragma unroll
+      for (int f = 0; f < MF; f++)
+#pragma unroll
+        for (int p = 0; p < XS; p++) af[s][f][p] = frag(st + p * (kAPlane / 2), arow + f * 32, s);
+    }
+#pragma unroll
+    for (int s = 0; s < 2; s++)
+#pragma unroll
+      for (int f = 0; f < MF; f++)
+#pragma unroll
+        for (int p = 0; p < XS; p++)
+#pragma unroll
+          for (int j = 0; j < NF; j++)
+            acc[f][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[s][f][p], bf[s][j], acc[f][j], 0, 0, 0);
+  };
+  auto step = [&](int kb, int slot) {
+    wait_vmcnt<kPerStep>();  // this wave's loads of kb (those of kb + 1 may be in flight)
+    __syncthreads();
+    issue(kb + 2, (slot + 2) % 3);
+    compute(slot);
+  };
+  issue(k_lo, 0);
+  issue(k_lo + 1, 1);
+  int kb = k_lo;
+  for (; kb + 3 <= k_hi; kb += 3) {
+    step(kb, 0);
+    step(kb + 1, 1);
+    step(kb + 2, 2);
+  }
+  if (kb < k_hi) step(kb, 0);
+  if (kb + 1 < k_hi) step(kb + 1, 1);
+  wait_vmcnt<0>();  // no load may land in LDS after this point
+  __syncthreads();
+
+  if constexpr (EPI) {
+    constexpr int kPitch = BN + 4;
+    float *tile = reinterpret_cast<float *>(lds16) + wave * 32 * kPitch;
+    const StableDims es = g.e.s;
+    const KVDev ekv = g.e.kv;
+    const float *rope = g.e.rope;
+    float *eq = g.e.q, *em = g.e.m;
+    uint16_t *emh = g.e.mh, *eml = g.e.ml;
+    const int ldm = g.e.ldm ? g.e.ldm : es.inter;
+    const int p0 = *g.e.pos0, mu0 = (es.win_q + 2 * es.win_kv) / 2;
+#pragma unroll
+    for (int f = 0; f < MF; f++) {
+#pragma unroll
+      for (int j = 0; j < NF; j++)
+#pragma unroll
+        for (int v = 0; v < 16; v++)
+          tile[((v >> 2) * 8 + (lane >> 5) * 4 + (v & 3)) * kPitch + j * 32 + (lane & 31)] = acc[f][j][v];
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      const int r0w = m0 + (wave * MF + f) * 32;
+      for (int it = lane; it < 32 * (BN / 2); it += 64) {
+        const int r = it / (BN / 2), c = 2 * (it - r * (BN / 2)), m = r0w + r, n = n0 + c, u = n >> 1;
+        if (m >= g.M || n >= N) continue;
+        const float2 pv = *reinterpret_cast<const float2 *>(tile + r * kPitch + c);
+        if (u >= mu0) {
+          const float gv = es.silu ? silu_gate_llama(pv.x, pv.y) : silu_gate(pv.x, pv.y);
+          if (em) em[(int64_t)m * es.inter + (u - mu0)] = gv;
+          store_bf16_split(emh, eml, (int64_t)m * ldm + (u - mu0), gv);
+        } else {
+          const int pos = p0 + m;
+          in_pair_epilogue(es, ekv, rope + (int64_t)pos * es.rot, pos, u, pv.x, pv.y,
+                           eq + (int64_t)m * es.heads * es.hd, nullptr);
+        }
+      }
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+    return;
+  }
+  float *y = P.y + (int64_t)split * P.split_stride;
+#pragma unroll
+  for (int f = 0; f < MF; f++)
+#pragma unroll
+    for (int j = 0; j < NF; j++) {
+      const int n = n0 + j * 32 + (lane & 31);
+      if (n >= N) continue;
+#pragma unroll
+      for (int v = 0; v < 16; v++) {
+        const int m = m0 + (wave * MF + f) * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
+        if (m < g.M) y[(int64_t)m * P.ldy + n] = acc[f][j][v];
+      }
+    }
+}
+
+template <int WF, int XS, int MF, int NF, bool EPI>
+hipError_t gemm_wide_launch(const WideArgs &g, hipStream_t st) {
+  constexpr int BM = 4 * 32 * MF, BN = 32 * NF;
+  int blocks = 0;
+  for (int i = 0; i < g.nprod; i++) {
+    const int tiles = ((g.M + BM - 1) / BM) * ((g.p[i].w.rows + BN - 1) / BN);
+    blocks += (tiles * g.p[i].ksplit + 7) / 8 * 8;
+  }
+  if constexpr (WF == FMT_BF16) {
+    constexpr size_t lds = gemm_dma_lds<XS, MF, NF, EPI>();
+    static const hipError_t attr =
+        hipFuncSetAttribute(reinterpret_cast<const void *>(&gemm_dma_kernel<XS, MF, NF, EPI>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (attr != hipSuccess) return attr;
+    hipLaunchKernelGGL((gemm_dma_kernel<XS, MF, NF, EPI>), dim3(blocks), dim3(kWThreads), lds, st, g);
+  } else {
+    constexpr size_t lds = gemm_wide_lds<WF, XS, MF, NF, EPI>();
+    static const hipError_t attr =
+        hipFuncSetAttribute(reinterpret_cast<const void *>(&gemm_wide_kernel<WF, XS, MF, NF, EPI>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (attr != hipSuccess) return attr;
+    hipLaunchKernelGGL((gemm_wide_kernel<WF, XS, MF, NF, EPI>), dim3(blocks), dim3(kWThreads), lds, st, g);
+  }
+  return hipGetLastError();
+}
+
 template <int WF, int XS, bool EPI = false>
 hipError_t gemm_large_launch(const GemmArgs &g, hipStream_t st) {
   constexpr size_t lds = gemm_large_lds<WF, XS, EPI>();
@@ -399,4 +998,71 @@ hipError_t launch_gemm_in_epilogue(const MatDesc &w, const uint16_t *xh, const u
   GemmArgs g{w, xh, xl, M, nullptr, 0, 1, e};
   if (w.fmt == FMT_Q8_0) return gemm_large_launch<FMT_Q8_0, 2, true>(g, st);
   return xl ? gemm_large_launch<FMT_BF16, 2, true>(g, st) : gemm_large_launch<FMT_BF16, 1, true>(g, st);
+}
+
+namespace {
+
+template <int WF, int XS, bool EPI>
+hipError_t gemm_wide_dispatch(const WideArgs &g, int mf, int nf, hipStream_t st) {
+  if (mf == 2 && nf == 7) return gemm_wide_launch<WF, XS, 2, 7, EPI>(g, st);
+  if (mf == 2 && nf == 8) return gemm_wide_launch<WF, XS, 2, 8, EPI>(g, st);
+  if (mf == 1 && nf == 8) return gemm_wide_launch<WF, XS, 1, 8, EPI>(g, st);
+  if (mf == 1 && nf == 7) return gemm_wide_launch<WF, XS, 1, 7, EPI>(g, st);
+  return hipErrorInvalidValue;
+}
+
+template <int XS, bool EPI>
+hipError_t gemm_wide_q8(const WideArgs &g, int mf, int nf, hipStream_t st) {
+  if (mf == 1 && nf == 8) return gemm_wide_launch<FMT_Q8_0, XS, 1, 8, EPI>(g, st);
+  if (mf == 1 && nf == 7) return gemm_wide_launch<FMT_Q8_0, XS, 1, 7, EPI>(g, st);
+  return hipErrorInvalidValue;
+}
+
+template <bool EPI>
+hipError_t gemm_wide_fmt(const WideArgs &g, int mf, int nf, bool two, hipStream_t st) {
+  if (g.p[0].w.fmt == FMT_Q8_0)
+    return two ? gemm_wide_q8<2, EPI>(g, mf, nf, st) : gemm_wide_q8<1, EPI>(g, mf, nf, st);
+  return two ? gemm_wide_dispatch<FMT_BF16, 2, EPI>(g, mf, nf, st) : gemm_wide_dispatch<FMT_BF16, 1, EPI>(g, mf, nf, st);
+}
+
+bool wide_operand_ok(const MatDesc &w, const uint16_t *xh, int lda, int M) {
+  constexpr int64_t kGiB = int64_t(1) << 30;  // the kernel's offset sentinels need operands below 1 GiB
+  return gemm_mfma_supported(w) && xh && lda >= w.cols && lda % 8 == 0 && (reinterpret_cast<uintptr_t>(xh) & 15) == 0 &&
+         (int64_t)M * lda * 2 < kGiB && (int64_t)w.rows * w.vstride < kGiB && (int64_t)w.rows * w.mstride < kGiB;
+}
+
+}  // namespace
+
+bool gemm_wide_shape(int fmt, int mf, int nf) {
+  return (nf == 7 || nf == 8) && (mf == 1 || (mf == 2 && fmt == FMT_BF16));
+}
+
+hipError_t launch_gemm_wide(const WideGemm *p, int nprod, int M, int mf, int nf, hipStream_t st) {
+  if (nprod < 1 || nprod > 2 || M < 1 || !gemm_wide_shape(p[0].w.fmt, mf, nf)) return hipErrorInvalidValue;
+  WideArgs g{};
+  g.nprod = nprod;
+  g.M = M;
+  const bool two = p[0].xl != nullptr;
+  for (int i = 0; i < nprod; i++) {
+    const WideGemm &q = p[i];
+    if (!wide_operand_ok(q.w, q.xh, q.lda, M) || (q.xl != nullptr) != two || q.w.fmt != p[0].w.fmt || q.ksplit < 1 ||
+        q.ksplit > q.w.cols / kWK || (q.xl && (reinterpret_cast<uintptr_t>(q.xl) & 15)) || !q.y ||
+        (q.ksplit > 1 && q.split_stride < (int64_t)M * q.ldy))
+      return hipErrorInvalidValue;
+    g.p[i] = WideProduct{q.w, q.xh, q.xl, q.lda, q.y, q.ldy, q.ksplit, q.split_stride};
+  }
+  return gemm_wide_fmt<false>(g, mf, nf, two, st);
+}
+
+hipError_t launch_gemm_wide_in_epilogue(const MatDesc &w, const uint16_t *xh, const uint16_t *xl, int lda, int M,
+                                        const InEpilogue &e, int mf, int nf, hipStream_t st) {
+  if (!wide_operand_ok(w, xh, lda, M) || M < 1 || !gemm_wide_shape(w.fmt, mf, nf) || !e.mh || !e.ml || !e.q || !e.rope ||
+      !e.pos0 || w.rows % 2 || e.s.win_q % 2 || (xl && (reinterpret_cast<uintptr_t>(xl) & 15)))
+    return hipErrorInvalidValue;
+  WideArgs g{};
+  g.nprod = 1;
+  g.M = M;
+  g.p[0] = WideProduct{w, xh, xl, lda, nullptr, 0, 1, 0};
+  g.e = e;
+  return gemm_wide_fmt<true>(g, mf, nf, xl != nullptr, st);
 }

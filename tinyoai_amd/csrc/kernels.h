@@ -201,18 +201,6 @@ hipError_t launch_gemm(const MatDesc &w, const float *x, int n, float *out, hipS
 // most max_splits).
 bool gemm_mfma_supported(const MatDesc &w);
 int gemm_planes(const MatDesc &w, bool bf16_path = false);
-// The same product for BF16 weights on hipBLASLt (one bf16 plane X per
-// call; accumulate: y += X W^T, else y = X W^T). hipErrorNotSupported when
-// the library has no algorithm for the shape (the caller's own kernel then
-// runs it).
-struct BlasLt;
-BlasLt *blaslt_create();
-void blaslt_destroy(BlasLt *b);
-hipError_t blaslt_bf16_product(BlasLt *b, const MatDesc &w, const uint16_t *x, int m, float *y, int ldy,
-                               bool accumulate, hipStream_t st);
-// Whether the library has an algorithm for y = X W^T at this shape (the
-// plan is made and kept).
-bool blaslt_bf16_ready(BlasLt *b, const MatDesc &w, int m, int ldy);
 int gemm_splits(const MatDesc &w, int M, int max_splits);
 hipError_t launch_gemm_mfma(const MatDesc &w, const uint16_t *xh, const uint16_t *xl, int M, float *y, int ldy,
                             hipStream_t st, int ksplit = 1);
@@ -245,9 +233,33 @@ struct InEpilogue {
   float *q;
   float *m;
   uint16_t *mh, *ml;
+  int ldm;  // values between rows of mh / ml (0: inter)
 };
 hipError_t launch_gemm_in_epilogue(const MatDesc &w, const uint16_t *xh, const uint16_t *xl, int M,
                                    const InEpilogue &e, hipStream_t st);
+// Wide-tile matrix-core products (one wave per SIMD, weights through LDS,
+// activations straight into registers): y = X * W^T for Q8_0 and BF16
+// weights with K % 32 == 0, X as bf16 planes xh (and xl, or null for one
+// plane) with rows lda values apart. A launch carries one or two products
+// of M rows each (their blocks side by side, the first product's first);
+// product i cuts its K range in ksplit parts whose results go to
+// y + s * split_stride. Block tiles are (128 * mf) x (32 * nf):
+// gemm_wide_shape names the instances built (Q8_0: mf 1).
+struct WideGemm {
+  MatDesc w;
+  const uint16_t *xh, *xl;
+  int lda;
+  float *y;
+  int ldy;
+  int ksplit;
+  int64_t split_stride;
+};
+bool gemm_wide_shape(int fmt, int mf, int nf);
+hipError_t launch_gemm_wide(const WideGemm *p, int nprod, int M, int mf, int nf, hipStream_t st);
+// The in-projection (win) product with its epilogue fused (no output
+// matrix), on wide tiles.
+hipError_t launch_gemm_wide_in_epilogue(const MatDesc &w, const uint16_t *xh, const uint16_t *xl, int lda, int M,
+                                        const InEpilogue &e, int mf, int nf, hipStream_t st);
 // x fp32 [rows][k] (row stride ldx) -> bf16 hi [rows][k] and lo = x - hi.
 hipError_t launch_split_bf16(const float *x, int ldx, int k, int64_t rows, uint16_t *hi, uint16_t *lo,
                              hipStream_t st);

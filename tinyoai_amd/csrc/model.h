@@ -179,25 +179,11 @@ struct StableModel {
   const uint16_t *lo_plane(const MatDesc &w) const { return gemm_planes(w, bf16_acts) == 2 ? XL : nullptr; }
   int project_planes(const MatDesc &w, const uint16_t *xh, const uint16_t *xl, int n, float *y, int ldy,
                      int *splits = nullptr);
-  // BF16-weight prefill products on hipBLASLt (set_launch stage 7, on by
-  // default; the handle is made on first use): y = xh W^T (+ xl W^T).
-  // False where it does not apply or the library has no algorithm (the
-  // matrix-core kernel then runs the product).
-  bool use_blaslt = true, blas_tried = false;
-  BlasLt *blas = nullptr;
-  bool blas_ready();
-  // Joined-plane products (set_launch stage 9, on by default): with two
-  // activation planes a BF16 product is one hipBLASLt call over rows
-  // [hi | lo] (K doubled) against a prefill copy of the matrix whose rows
-  // hold each weight row twice (win: [w | w]; wout: [o | o | down | down]),
-  // instead of two calls of which the second reads and rewrites y. The
-  // copies (twice the layer matrices' bytes) are made at the first such
-  // prefill; a layer whose sections differ in format has none.
-  bool use_joined = true, joined_tried = false;
-  std::vector<MatDesc> joined_in, joined_out;  // per layer; rows == 0: none
-  int ensure_joined();
-  bool joined_layer(int l, int n);
-  bool blas_product(const MatDesc &w, const uint16_t *xh, const uint16_t *xl, int n, float *y, int ldy);
+  // BF16-weight prefill products on the wide-tile kernel (set_launch
+  // stage 7, on by default), else on the 128 x 256 tiles; wide_layer: the
+  // layer's whole prefill takes the wide-tile path.
+  bool use_wide = true;
+  bool wide_layer(int l) const;
   int prefill_chunk(const int32_t *ids, int n, int start, bool want_logits);
   // Scoring of a forward_logprobs call: while set, prefill_chunk also
   // computes every row's logits and their log probabilities (device
