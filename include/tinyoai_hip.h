@@ -222,7 +222,9 @@ int tinyoai_stablelm_profile(tinyoai_model *m, int32_t enable);
  * products on wide matrix-core tiles (the in-projection with its epilogue
  * in one launch, the o and down products together as K splits), zero on
  * 128 x 256 tiles (fp32 accumulation either way; the sums' order
- * differs). Returns 0 or TINYOAI_EINVAL. */
+ * differs). Stage 8: grid nonzero forms the wide-tile in-projection's
+ * epilogue in the product's own launch, zero (the default) as a kernel of
+ * its own (same arithmetic). Returns 0 or TINYOAI_EINVAL. */
 int tinyoai_stablelm_set_launch(tinyoai_model *m, int32_t stage, int32_t grid, int32_t threads);
 int tinyoai_stablelm_profile_read(tinyoai_model *m, double *ms, int64_t *counts, int32_t n_stages);
 

@@ -901,18 +901,26 @@ int StableModel::prefill_chunk(const int32_t *ids, int n, int start, bool want_l
     const bool pin = !split_in && gemm_mfma_supported(w.win), pd = gemm_mfma_supported(wd);
     const bool flash = flash_prefill_supported(dims.hd), po = flash && gemm_mfma_supported(wo);
     if (wide_layer(l)) {
-      // BF16 layers on wide tiles: LayerNorm -> planes; win with its
-      // epilogue in the product's own launch (q, K/V, SiLU-gate planes);
-      // attention -> planes; the o and down products as one launch of K
-      // splits; the parallel residual sums them in order.
+      // BF16 layers on wide tiles: LayerNorm -> planes; win, then its
+      // epilogue (q, K/V, SiLU-gate planes); attention -> planes; the o and
+      // down products as one launch of K splits; the parallel residual sums
+      // them in order.
       const uint16_t *lo = lo_plane(w.win);
       STAGE(ST_PREFILL_NORM, launch_layer_norm_rows(X, w.ln_w, w.ln_b, dims.eps, n, d, nullptr, stream, XH, XL),
             "layer_norm");
       int mf, nf;
       wide_shape(n, w.win.rows, &mf, &nf);
-      const InEpilogue e{dims, kv[l], rope, d_pos0, Q, tracing ? M : nullptr, MH, ML, 0};
-      STAGE(ST_PREFILL_GEMM, launch_gemm_wide_in_epilogue(w.win, XH, lo, d, n, e, mf, nf, stream),
-            "projection + epilogue");
+      if (wide_epi) {
+        const InEpilogue e{dims, kv[l], rope, d_pos0, Q, tracing ? M : nullptr, MH, ML, 0};
+        STAGE(ST_PREFILL_GEMM, launch_gemm_wide_in_epilogue(w.win, XH, lo, d, n, e, mf, nf, stream),
+              "projection + epilogue");
+      } else {
+        const WideGemm g{w.win, XH, lo, d, Y, win_rows, 1, 0};
+        STAGE(ST_PREFILL_GEMM, launch_gemm_wide(&g, 1, n, mf, nf, stream), "projection");
+        STAGE(ST_PREFILL_EPILOGUE,
+              launch_in_epilogue(dims, kv[l], Y, win_rows, rope, d_pos0, n, Q, tracing ? M : nullptr, stream, MH, ML),
+              "in_epilogue");
+      }
       STAGE(ST_PREFILL_ATTENTION,
             launch_flash_prefill(dims, kv[l], Q, d_pos0, n, tracing ? A : nullptr, stream, XH, XL), "attention");
       int so, sd;
@@ -1696,6 +1704,10 @@ int tinyoai_stablelm_set_launch(tinyoai_model *m, int32_t stage, int32_t grid, i
   StableModel &s = *m->stable;
   if (stage == 7) {  // BF16-weight prefill products on wide tiles (1, the default) or 128 x 256 tiles (0)
     s.use_wide = grid != 0;
+    return TINYOAI_OK;
+  }
+  if (stage == 8) {  // wide-tile in-projection with its epilogue fused (1) or a kernel of its own (0, the default)
+    s.wide_epi = grid != 0;
     return TINYOAI_OK;
   }
   if (stage == 5) {  // BF16-weight prefill products with bf16 activations (1) or two planes (0, the default)

@@ -422,6 +422,49 @@ constexpr size_t gemm_wide_lds() {
 
 __device__ __forceinline__ int swz(int row, int c) { return row * kWK + ((c ^ ((row >> 2) & 3)) << 3); }
 
+// The in-projection epilogue of 32 output rows staged in LDS (row r of
+// the wave's band at tile + r * pitch, bn columns from n0): the wave's
+// lanes take (row, output pair) items in order, four at a time so that
+// their float64 exp chains and stores overlap (one wave per SIMD runs
+// this part).
+__device__ __forceinline__ void wide_epilogue_rows(const WideArgs &g, const float *tile, int pitch, int bn, int r0,
+                                                   int n0, int N, int lane) {
+  const StableDims es = g.e.s;
+  const KVDev ekv = g.e.kv;
+  const float *rope = g.e.rope;
+  float *eq = g.e.q, *em = g.e.m;
+  uint16_t *emh = g.e.mh, *eml = g.e.ml;
+  const int ldm = g.e.ldm ? g.e.ldm : es.inter;
+  const int p0 = *g.e.pos0, mu0 = (es.win_q + 2 * es.win_kv) / 2;
+  const int half = bn / 2, items = 32 * half;
+  for (int it0 = lane; it0 < items; it0 += 4 * 64) {
+    float2 pv[4];
+    int m[4], u[4];
+    bool ok[4];
+#pragma unroll
+    for (int b = 0; b < 4; b++) {
+      const int it = it0 + b * 64, r = it / half, c = 2 * (it - r * half);
+      m[b] = r0 + r;
+      u[b] = (n0 + c) >> 1;
+      ok[b] = it < items && m[b] < g.M && n0 + c < N;
+      pv[b] = ok[b] ? *reinterpret_cast<const float2 *>(tile + r * pitch + c) : make_float2(0.f, 0.f);
+    }
+#pragma unroll
+    for (int b = 0; b < 4; b++) {
+      if (!ok[b]) continue;
+      if (u[b] >= mu0) {
+        const float gv = es.silu ? silu_gate_llama(pv[b].x, pv[b].y) : silu_gate(pv[b].x, pv[b].y);
+        if (em) em[(int64_t)m[b] * es.inter + (u[b] - mu0)] = gv;
+        store_bf16_split(emh, eml, (int64_t)m[b] * ldm + (u[b] - mu0), gv);
+      } else {
+        const int pos = p0 + m[b];
+        in_pair_epilogue(es, ekv, rope + (int64_t)pos * es.rot, pos, u[b], pv[b].x, pv[b].y,
+                         eq + (int64_t)m[b] * es.heads * es.hd, nullptr);
+      }
+    }
+  }
+}
+
 template <int WF, int XS, int MF, int NF, bool EPI>
 __global__ __launch_bounds__(kWThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_wide_kernel(WideArgs g) {
   constexpr int BM = 4 * 32 * MF, BN = 32 * NF;
@@ -649,13 +692,6 @@ __global__ __launch_bounds__(kWThreads) __attribute__((amdgpu_waves_per_eu(1, 1)
     // neighbouring outputs.
     constexpr int kPitch = BN + 4;
     float *tile = reinterpret_cast<float *>(lds16) + wave * 32 * kPitch;
-    const StableDims es = g.e.s;
-    const KVDev ekv = g.e.kv;
-    const float *rope = g.e.rope;
-    float *eq = g.e.q, *em = g.e.m;
-    uint16_t *emh = g.e.mh, *eml = g.e.ml;
-    const int ldm = g.e.ldm ? g.e.ldm : es.inter;
-    const int p0 = *g.e.pos0, mu0 = (es.win_q + 2 * es.win_kv) / 2;
 #pragma unroll
     for (int f = 0; f < MF; f++) {
 #pragma unroll
@@ -667,20 +703,7 @@ __global__ __launch_bounds__(kWThreads) __attribute__((amdgpu_waves_per_eu(1, 1)
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
       const int r0w = m0 + (wave * MF + f) * 32;
-      for (int it = lane; it < 32 * (BN / 2); it += 64) {
-        const int r = it / (BN / 2), c = 2 * (it - r * (BN / 2)), m = r0w + r, n = n0 + c, u = n >> 1;
-        if (m >= g.M || n >= N) continue;
-        const float2 pv = *reinterpret_cast<const float2 *>(tile + r * kPitch + c);
-        if (u >= mu0) {
-          const float gv = es.silu ? silu_gate_llama(pv.x, pv.y) : silu_gate(pv.x, pv.y);
-          if (em) em[(int64_t)m * es.inter + (u - mu0)] = gv;
-          store_bf16_split(emh, eml, (int64_t)m * ldm + (u - mu0), gv);
-        } else {
-          const int pos = p0 + m;
-          in_pair_epilogue(es, ekv, rope + (int64_t)pos * es.rot, pos, u, pv.x, pv.y,
-                           eq + (int64_t)m * es.heads * es.hd, nullptr);
-        }
-      }
+      wide_epilogue_rows(g, tile, kPitch, BN, r0w, n0, N, lane);
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -862,13 +885,6 @@ __global__ __launch_bounds__(kWThreads) __attribute__((amdgpu_waves_per_eu(1, 1)
   if constexpr (EPI) {
     constexpr int kPitch = BN + 4;
     float *tile = reinterpret_cast<float *>(lds16) + wave * 32 * kPitch;
-    const StableDims es = g.e.s;
-    const KVDev ekv = g.e.kv;
-    const float *rope = g.e.rope;
-    float *eq = g.e.q, *em = g.e.m;
-    uint16_t *emh = g.e.mh, *eml = g.e.ml;
-    const int ldm = g.e.ldm ? g.e.ldm : es.inter;
-    const int p0 = *g.e.pos0, mu0 = (es.win_q + 2 * es.win_kv) / 2;
 #pragma unroll
     for (int f = 0; f < MF; f++) {
 #pragma unroll
@@ -880,20 +896,7 @@ __global__ __launch_bounds__(kWThreads) __attribute__((amdgpu_waves_per_eu(1, 1)
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
       const int r0w = m0 + (wave * MF + f) * 32;
-      for (int it = lane; it < 32 * (BN / 2); it += 64) {
-        const int r = it / (BN / 2), c = 2 * (it - r * (BN / 2)), m = r0w + r, n = n0 + c, u = n >> 1;
-        if (m >= g.M || n >= N) continue;
-        const float2 pv = *reinterpret_cast<const float2 *>(tile + r * kPitch + c);
-        if (u >= mu0) {
-          const float gv = es.silu ? silu_gate_llama(pv.x, pv.y) : silu_gate(pv.x, pv.y);
-          if (em) em[(int64_t)m * es.inter + (u - mu0)] = gv;
-          store_bf16_split(emh, eml, (int64_t)m * ldm + (u - mu0), gv);
-        } else {
-          const int pos = p0 + m;
-          in_pair_epilogue(es, ekv, rope + (int64_t)pos * es.rot, pos, u, pv.x, pv.y,
-                           eq + (int64_t)m * es.heads * es.hd, nullptr);
-        }
-      }
+      wide_epilogue_rows(g, tile, kPitch, BN, r0w, n0, N, lane);
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");

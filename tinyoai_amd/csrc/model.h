@@ -184,6 +184,12 @@ struct StableModel {
   // layer's whole prefill takes the wide-tile path.
   bool use_wide = true;
   bool wide_layer(int l) const;
+  // The wide-tile in-projection forms its epilogue as a kernel of its own
+  // from the product's output (the default), or in the product's own
+  // launch (set_launch stage 8 on: one wave per SIMD then runs the float64
+  // exp chains and scattered stores while the matrix cores idle; the 8K
+  // BF16 prefill takes 129 ms against 117.5).
+  bool wide_epi = false;
   int prefill_chunk(const int32_t *ids, int n, int start, bool want_logits);
   // Scoring of a forward_logprobs call: while set, prefill_chunk also
   // computes every row's logits and their log probabilities (device
