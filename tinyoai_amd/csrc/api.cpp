@@ -1527,7 +1527,7 @@ int tinyoai_stablelm_branches_open(tinyoai_model *m, int32_t prefix, int32_t cou
       (int64_t)count * s.cfg.vocab_size > (int64_t)s.chunk * s.win_rows || room < 1)
     return fail(TINYOAI_EINVAL, "invalid branch prefix or batch size (prefix %d, offset %d, count %d)", prefix,
                 s.offset, count);
-  if (hd != 8 && hd != 64 && hd != 80) return fail(TINYOAI_EINVAL, "branch attention: head width %d", hd);
+  if (hd != 8 && hd != 64 && hd != 80 && hd != 128) return fail(TINYOAI_EINVAL, "branch attention: head width %d", hd);
   if (int rc = s.ensure_kv(std::max(prefix, 1))) return rc;
   auto h = std::make_unique<tinyoai_branches>();
   h->b = std::make_unique<Branches>();

@@ -239,6 +239,8 @@ hipError_t launch_branch_attention(const StableDims &s, const KVDev &kv, const K
                             : launch_branch_attention_hd<80, false>(a, nq, splits, steps, st);
     case 8: return kv.half ? launch_branch_attention_hd<8, true>(a, nq, splits, steps, st)
                            : launch_branch_attention_hd<8, false>(a, nq, splits, steps, st);
+    case 128: return kv.half ? launch_branch_attention_hd<128, true>(a, nq, splits, steps, st)
+                             : launch_branch_attention_hd<128, false>(a, nq, splits, steps, st);
   }
   return hipErrorInvalidValue;
 }

@@ -123,7 +123,7 @@ hipError_t launch_attention(const StableDims &s, const KVDev &kv, const float *q
 // from kv (the shared prefix), position t >= prefix from slot rows[2j + 1]
 // - rows[2j] + t of sfx (the branch's suffix, stored contiguously). Every
 // query's position is at most max_pos. partials holds nq * heads *
-// partial_region(max_splits, hd) floats. Head widths 8, 64 and 80.
+// partial_region(max_splits, hd) floats. Head widths 8, 64, 80 and 128.
 // With a prefix, at most 128 queries and a matrix-core head width, the
 // prefix is attended once for all queries (launch_shared_prefix_attention)
 // and the suffix splits continue from its records. max_splits must be at
