@@ -100,15 +100,18 @@ int tinyoai_stablelm_forward(tinyoai_model *m, int32_t prefix, const int32_t *to
  * likely ids top_ids[i][count] with their log probabilities
  * top_logprobs[i][count], descending, ties to the lower id, normalised over
  * the whole vocabulary in float64 (summarizeLogits, logprobs.go:60-95).
- * `logits` receives the last position's row. 1 <= count <= min(vocab,
- * 1024); every target in [0, vocab). */
+ * `logits` receives the last position's row. 1 <= count <= vocab; every
+ * target in [0, vocab). -0 and +0 rank as equal (ties to the lower id). A
+ * row holding NaN is refused (TINYOAI_EINVAL, naming the position): the
+ * reference's float64 max would make every value NaN. */
 int tinyoai_stablelm_forward_logprobs(tinyoai_model *m, int32_t prefix, const int32_t *tokens,
                                       const int32_t *targets, int32_t n, int32_t count, float *logits,
                                       double *chosen, int32_t *top_ids, double *top_logprobs);
 
 /* summarizeLogits (logprobs.go:60-95) on the device for `rows` caller rows
  * of logits [rows][vocab]: chosen[r] = log p(targets[r]) and the `count`
- * best ids and log probabilities per row, as forward_logprobs scores them. */
+ * best ids and log probabilities per row (1 <= count <= vocab), as
+ * forward_logprobs scores them; a row holding NaN is refused. */
 int tinyoai_summarize_logits(const float *logits, int32_t rows, int32_t vocab, const int32_t *targets, int32_t count,
                              double *chosen, int32_t *top_ids, double *top_logprobs);
 
@@ -138,7 +141,7 @@ int tinyoai_stablelm_close(tinyoai_model *m);
  * (0 <= prefix <= offset) read-only. Branch j holds the suffix positions
  * prefix + [0, length(j)); the suffix KV grows with use (in powers of two,
  * at most max_len positions per branch; 0 = up to the context), in the
- * model's KV format at opening. Head widths 8, 64 and 80; count * vocab <=
+ * model's KV format at opening. Head widths 8, 64, 80 and 128; count * vocab <=
  * the prefill chunk's product buffer. While branches are open the model
  * refuses forward, reset, set_kv_bits, limit_cache and close with
  * TINYOAI_EINVAL (the reference's session holds the model gate,
@@ -260,9 +263,14 @@ int tinyoai_weight_mul_device(tinyoai_weight *w, const float *x_dev, int32_t n, 
  * The activations' operand planes (16 MiB) and the product's K-split
  * partials (32 MiB) live in a library array of 48 MiB on each GPU the
  * library runs on (held until the process ends), so n * cols
- * may be at most 4,194,304 (TINYOAI_EINVAL beyond), the current device
- * must be the weight's, and calls that overlap on one GPU race for that
- * array; each call overwrites what the previous one left there. */
+ * may be at most 4,194,304 (TINYOAI_EINVAL beyond) and the current device
+ * must be the weight's. Calls share that array and each overwrites what
+ * the previous one left there, so the library orders them: `stream` NULL
+ * runs the call on one library stream per GPU (not the weight's own
+ * stream), and a caller's stream first waits for the previous call on
+ * that GPU, on whatever stream it ran. Under HIP stream capture no such
+ * wait is recorded: captured calls that overlap on one GPU race for the
+ * array. */
 int tinyoai_weight_mul_device_noalloc(tinyoai_weight *w, const float *x_dev, int32_t n, float *out_dev, void *stream);
 int tinyoai_weight_free(tinyoai_weight *w);
 

@@ -30,11 +30,14 @@ def expected(logits, targets, count):
     return lp[np.arange(v.shape[0]), targets], order, np.take_along_axis(lp, order, axis=1)
 
 
-@pytest.mark.parametrize("vocab,count", [(65536, 20), (342, 342), (5000, 1024), (7, 1)])
+@pytest.mark.parametrize("vocab,count", [(65536, 20), (342, 342), (5000, 1024), (7, 1), (5000, 1025),
+                                         (65536, 2000), (65536, 65536)])
 def test_summarize_random_rows(hip, vocab, count):
     """Random logits (N(0, 4)): chosen and top values within 1e-12 of
     log_softmax (float64 arithmetic on both sides), ids identical; the
-    probabilities of a full-vocabulary top list sum to 1."""
+    probabilities of a full-vocabulary top list sum to 1. Counts above 1024
+    rank their candidates in global scratch (a bitonic sort) instead of
+    LDS, up to the whole 65536-entry vocabulary."""
     rng = np.random.default_rng(vocab + count)
     rows = 6
     x = (rng.standard_normal((rows, vocab)) * 4).astype(np.float32)
@@ -64,6 +67,34 @@ def test_summarize_ties_go_to_the_lower_id(hip):
     assert list(ids[1]) == [0, 1, 2] and list(ids[2]) == [3, 5, 77]
     assert np.max(np.abs(lp - wl)) <= 1e-12
     assert abs(chosen[1] - (-np.log(3000.0))) <= 1e-12
+
+
+@pytest.mark.parametrize("count", [3, 1500])
+def test_summarize_signed_zeros_tie(hip, count):
+    """-0 and +0 compare equal in summarizeLogits (v > x and v == x), so
+    they tie and the lower id goes first even when the +0 entries come
+    later and the count boundary falls among them; in both rankings (LDS
+    up to 1024 candidates, global scratch beyond)."""
+    x = np.full((2, 4000), -3.0, np.float32)
+    x[0, [10, 20, 30]] = np.float32(-0.0)
+    x[0, [5, 15, 25]] = np.float32(0.0)
+    x[1, :2000] = np.float32(-0.0)
+    x[1, 2000:] = np.float32(0.0)
+    _, ids, _ = hip.summarize_logits(x, np.array([0, 0]), count)
+    assert list(ids[0][:3]) == [5, 10, 15]
+    assert list(ids[1][: min(count, 2000)]) == list(range(min(count, 2000)))
+
+
+def test_summarize_refuses_nan_rows(hip):
+    """A row holding NaN: the reference's float64 max turns every value
+    NaN; the library refuses the request with an error that names the row
+    (the other rows' results are not returned either)."""
+    x = np.zeros((3, 100), np.float32)
+    x[2, 40] = np.nan
+    with pytest.raises(hip.TinyoaiError, match="row 2 holds NaN"):
+        hip.summarize_logits(x, np.array([0, 1, 2]), 5)
+    with pytest.raises(hip.TinyoaiError, match="row 2 holds NaN"):
+        hip.summarize_logits(np.tile(x, (1, 30)), np.array([0, 1, 2]), 1100)
 
 
 def test_forward_with_logprobs_reference_model(hip, oracle, tiny_stablelm):

@@ -85,3 +85,36 @@ def test_no_alloc_product_matches_allocating_entry_point(dtype, rows, cols):
     finally:
         w.close()
         buf.close()
+
+
+def test_no_alloc_calls_on_two_weights_are_ordered():
+    """Calls with a null stream on two weights, back to back, each on a
+    weight whose own stream would let them overlap: both results equal the
+    allocating entry point's (the library runs such calls one after
+    another on its own stream, so the second does not overwrite the
+    first's operand planes or partials while that one still reads them)."""
+    from tinyoai_amd import hip
+    rng = np.random.default_rng(77)
+    t1, t2 = W.synthetic_q8_0(2048, 2560, rng), W.synthetic_bf16(1536, 2560, rng)
+    buf = DeviceBuffers()
+    w1, w2 = hip.Weight(t1), hip.Weight(t2)
+    try:
+        n = 128
+        x1 = buf.upload(rng.standard_normal((n, 2560)).astype(np.float32))
+        x2 = buf.upload(rng.standard_normal((n, 2560)).astype(np.float32))
+        r1, r2 = buf.upload(np.zeros((n, 2048), np.float32)), buf.upload(np.zeros((n, 1536), np.float32))
+        w1.mul_device(x1, n, r1)
+        w2.mul_device(x2, n, r2)
+        want1, want2 = buf.download(r1, (n, 2048)), buf.download(r2, (n, 1536))
+        for _ in range(3):
+            y1 = buf.upload(np.full((n, 2048), np.nan, np.float32))
+            y2 = buf.upload(np.full((n, 1536), np.nan, np.float32))
+            w1.mul_device_noalloc(x1, n, y1)
+            w2.mul_device_noalloc(x2, n, y2)
+            assert np.array_equal(buf.download(y1, (n, 2048)), want1)
+            assert np.array_equal(buf.download(y2, (n, 1536)), want2)
+    finally:
+        w1.close()
+        w2.close()
+        buf.close()
+

@@ -1032,7 +1032,7 @@ int StableModel::score_rows(int n) {
     const int row = scoring.row + r0;
     const size_t c = (size_t)scoring.count;
     TRY_HIP(launch_logprobs(Y, V, nr, V, scoring.targets + row, scoring.count, scoring.chosen + row,
-                            scoring.top_ids + row * c, scoring.top_lp + row * c, stream),
+                            scoring.top_ids + row * c, scoring.top_lp + row * c, scoring.scratch, stream),
             "log probabilities");
   }
   scoring.row += n;
@@ -1266,8 +1266,7 @@ int StableModel::forward_logprobs(int prefix, const int32_t *tokens, const int32
                                   float *logits, double *chosen, int32_t *top_ids, double *top_lp) {
   if (int rc = busy_with_branches()) return rc;
   const int V = cfg.vocab_size;
-  if (!tokens || !targets || !logits || !chosen || !top_ids || !top_lp || n <= 0 || count < 1 ||
-      count > std::min(V, logprob_max_count()))
+  if (!tokens || !targets || !logits || !chosen || !top_ids || !top_lp || n <= 0 || count < 1 || count > V)
     return fail(TINYOAI_EINVAL, "invalid probability request");
   for (int i = 0; i < n; i++)
     if (targets[i] < 0 || targets[i] >= V) return fail(TINYOAI_EINVAL, "invalid probability target %d", targets[i]);
@@ -1276,24 +1275,27 @@ int StableModel::forward_logprobs(int prefix, const int32_t *tokens, const int32
                 offset, n);
   for (int i = 0; i < n; i++)
     if (tokens[i] < 0 || tokens[i] >= V) return fail(TINYOAI_EINVAL, "invalid token %d", tokens[i]);
-  // device scratch: targets, chosen, top ids, top log probabilities
+  // device scratch: targets, chosen, top ids, top log probabilities, the
+  // ranking scratch (its first word the NaN error word)
   auto r256 = [](size_t b) { return (b + 255) / 256 * 256; };
   const size_t bt = r256((size_t)n * 4), bc = r256((size_t)n * 8), bi = r256((size_t)n * count * 4),
-               bl = r256((size_t)n * count * 8);
-  if (bt + bc + bi + bl > score_bytes) {
+               bl = r256((size_t)n * count * 8), bs = r256(logprob_scratch_bytes(count));
+  if (bt + bc + bi + bl + bs > score_bytes) {
     hipStreamSynchronize(stream);
     if (score_mem) hipFree(score_mem);
     score_mem = nullptr;
     score_bytes = 0;
-    hipError_t e = hipMalloc(&score_mem, bt + bc + bi + bl);
+    hipError_t e = hipMalloc(&score_mem, bt + bc + bi + bl + bs);
     if (e != hipSuccess) return fail(TINYOAI_ENOMEM, "probability scratch: %s", hipGetErrorString(e));
-    score_bytes = bt + bc + bi + bl;
+    score_bytes = bt + bc + bi + bl + bs;
   }
   char *base = (char *)score_mem;
   int *d_targets = (int *)base;
+  void *rank = base + bt + bc + bi + bl;
   TRY_HIP(hipMemcpyAsync(d_targets, targets, (size_t)n * 4, hipMemcpyHostToDevice, stream), "targets");
+  TRY_HIP(hipMemsetAsync(rank, 0, 4, stream), "probability error word");
   scoring = Scoring{d_targets, count, 0, (double *)(base + bt), (double *)(base + bt + bc + bi),
-                    (int *)(base + bt + bc)};
+                    (int *)(base + bt + bc), rank};
   offset = prefix;
   int rc = ensure_kv(prefix + n);
   for (int done = 0; done < n && !rc;) {
@@ -1308,8 +1310,11 @@ int StableModel::forward_logprobs(int prefix, const int32_t *tokens, const int32
     if (e == hipSuccess) e = hipMemcpyAsync(chosen, sc.chosen, (size_t)n * 8, hipMemcpyDeviceToHost, stream);
     if (e == hipSuccess) e = hipMemcpyAsync(top_ids, sc.top_ids, (size_t)n * count * 4, hipMemcpyDeviceToHost, stream);
     if (e == hipSuccess) e = hipMemcpyAsync(top_lp, sc.top_lp, (size_t)n * count * 8, hipMemcpyDeviceToHost, stream);
+    int bad = 0;
+    if (e == hipSuccess) e = hipMemcpyAsync(&bad, sc.scratch, 4, hipMemcpyDeviceToHost, stream);
     if (e == hipSuccess) e = hipStreamSynchronize(stream);
     if (e != hipSuccess) rc = hip_fail(e, "log probabilities");
+    else if (bad) rc = fail(TINYOAI_EINVAL, "the logits of position %d hold NaN", prefix + bad - 1);
     else memcpy(logits, h_pinned, (size_t)V * 4);
   }
   if (rc) {
@@ -1427,29 +1432,35 @@ int tinyoai_stablelm_forward_logprobs(tinyoai_model *m, int32_t prefix, const in
 int tinyoai_summarize_logits(const float *logits, int32_t rows, int32_t vocab, const int32_t *targets, int32_t count,
                              double *chosen, int32_t *top_ids, double *top_logprobs) {
   if (!logits || !targets || !chosen || !top_ids || !top_logprobs || rows < 1 || vocab < 1 || count < 1 ||
-      count > std::min<int>(vocab, logprob_max_count()))
+      count > vocab)
     return fail(TINYOAI_EINVAL, "invalid probability request");
   for (int i = 0; i < rows; i++)
     if (targets[i] < 0 || targets[i] >= vocab) return fail(TINYOAI_EINVAL, "invalid probability target %d", targets[i]);
   const size_t nl = (size_t)rows * vocab * 4, nt = (size_t)rows * 4, nc = (size_t)rows * 8;
-  const size_t ni = (size_t)rows * count * 4, np = (size_t)rows * count * 8;
+  const size_t ni = (size_t)rows * count * 4, np = (size_t)rows * count * 8, ns = logprob_scratch_bytes(count);
   auto r256 = [](size_t b) { return (b + 255) / 256 * 256; };
   char *mem = nullptr;
-  hipError_t e = hipMalloc(&mem, r256(nl) + r256(nt) + r256(nc) + r256(ni) + r256(np));
+  hipError_t e = hipMalloc(&mem, r256(nl) + r256(nt) + r256(nc) + r256(ni) + r256(np) + r256(ns));
   if (e != hipSuccess) return fail(TINYOAI_ENOMEM, "hipMalloc: %s", hipGetErrorString(e));
   float *dl = (float *)mem;
   int *dt = (int *)(mem + r256(nl));
   double *dc = (double *)((char *)dt + r256(nt));
   int *di = (int *)((char *)dc + r256(nc));
   double *dp = (double *)((char *)di + r256(ni));
+  void *ds = (char *)dp + r256(np);
+  int bad = 0;
   e = hipMemcpy(dl, logits, nl, hipMemcpyHostToDevice);
   if (e == hipSuccess) e = hipMemcpy(dt, targets, nt, hipMemcpyHostToDevice);
-  if (e == hipSuccess) e = launch_logprobs(dl, vocab, rows, vocab, dt, count, dc, di, dp, nullptr);
+  if (e == hipSuccess) e = hipMemset(ds, 0, 4);
+  if (e == hipSuccess) e = launch_logprobs(dl, vocab, rows, vocab, dt, count, dc, di, dp, ds, nullptr);
   if (e == hipSuccess) e = hipMemcpy(chosen, dc, nc, hipMemcpyDeviceToHost);
   if (e == hipSuccess) e = hipMemcpy(top_ids, di, ni, hipMemcpyDeviceToHost);
   if (e == hipSuccess) e = hipMemcpy(top_logprobs, dp, np, hipMemcpyDeviceToHost);
+  if (e == hipSuccess) e = hipMemcpy(&bad, ds, 4, hipMemcpyDeviceToHost);
   hipFree(mem);
-  return e == hipSuccess ? TINYOAI_OK : hip_fail(e, "log probabilities");
+  if (e != hipSuccess) return hip_fail(e, "log probabilities");
+  if (bad) return fail(TINYOAI_EINVAL, "logits row %d holds NaN", bad - 1);
+  return TINYOAI_OK;
 }
 
 int tinyoai_stablelm_set_kv_bits(tinyoai_model *m, int32_t bits, int32_t *cleared) {
@@ -1875,24 +1886,36 @@ static __device__ __align__(256) uint16_t scratch[2 * kScratchValues + kProductP
 
 namespace {
 constexpr int kMaxDevices = 64;
+// Per device: the array's address, the library stream that calls with a
+// null stream share, and an event that orders every call's use of the
+// array after the previous call's (whatever streams they came on).
+struct ScratchDev {
+  void *ptr = nullptr;
+  hipStream_t stream = nullptr;
+  hipEvent_t done = nullptr;
+};
 std::mutex g_scratch_mu;
-void *g_scratch_dev[kMaxDevices];
+ScratchDev g_scratch_dev[kMaxDevices];
 
-// The current device's copy of `scratch`, looked up on the first call on
-// that device.
-int scratch_address(void **out) {
+// The current device's set-up, made on the first call on that device
+// (the caller holds g_scratch_mu).
+int scratch_device(ScratchDev **out) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
   if (dev < 0 || dev >= kMaxDevices) return fail(TINYOAI_EINVAL, "device %d out of range", dev);
-  std::lock_guard<std::mutex> lock(g_scratch_mu);
-  if (!g_scratch_dev[dev]) {
+  ScratchDev &d = g_scratch_dev[dev];
+  if (!d.ptr) {
     void *p = nullptr;
     e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
-    g_scratch_dev[dev] = p;
+    if ((e = hipStreamCreateWithFlags(&d.stream, hipStreamNonBlocking)) != hipSuccess)
+      return hip_fail(e, "no-allocation stream");
+    if ((e = hipEventCreateWithFlags(&d.done, hipEventDisableTiming)) != hipSuccess)
+      return hip_fail(e, "no-allocation event");
+    d.ptr = p;
   }
-  *out = g_scratch_dev[dev];
+  *out = &d;
   return TINYOAI_OK;
 }
 }  // namespace
@@ -1905,19 +1928,27 @@ int tinyoai_weight_mul_device_noalloc(tinyoai_weight *w, const float *x_dev, int
   if ((size_t)n * m.cols > kScratchValues)
     return fail(TINYOAI_EINVAL, "product of %d x %d activation values exceeds the no-allocation limit of %zu", n, m.cols,
                 kScratchValues);
+  if (product_scratch(m, x_dev, n) > sizeof(scratch))
+    return fail(TINYOAI_EINVAL, "product of %d x %d needs more than the no-allocation limit of %zu bytes", n, m.cols,
+                sizeof(scratch));
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
   if (dev != w->device) return fail(TINYOAI_EINVAL, "the weight lives on device %d, not the current %d", w->device, dev);
-  hipStream_t st = stream ? (hipStream_t)stream : w->stream;
-  void *planes = nullptr;
-  if (product_scratch(m, x_dev, n)) {
-    if (product_scratch(m, x_dev, n) > sizeof(scratch))
-      return fail(TINYOAI_EINVAL, "product of %d x %d needs more than the no-allocation limit of %zu bytes", n, m.cols,
-                  sizeof(scratch));
-    if (int rc = scratch_address(&planes)) return rc;
-  }
-  e = product_launch(m, x_dev, n, out_dev, planes, st);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  ScratchDev *d = nullptr;
+  if (int rc = scratch_device(&d)) return rc;
+  // A null stream means the library's own stream for this device, so
+  // such calls run one after another; a caller's stream waits for the
+  // previous call (on any stream) to finish with the array first. Under
+  // stream capture the captured graph orders the calls instead.
+  hipStream_t st = stream ? (hipStream_t)stream : d->stream;
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if ((e = hipStreamIsCapturing(st, &cap)) != hipSuccess) return hip_fail(e, "hipStreamIsCapturing");
+  const bool order = cap == hipStreamCaptureStatusNone;
+  if (order && (e = hipStreamWaitEvent(st, d->done, 0)) != hipSuccess) return hip_fail(e, "no-allocation ordering");
+  e = product_launch(m, x_dev, n, out_dev, product_scratch(m, x_dev, n) ? d->ptr : nullptr, st);
+  if (e == hipSuccess && order) e = hipEventRecord(d->done, st);
   return e == hipSuccess ? TINYOAI_OK : hip_fail(e, "product launch");
 }
 

@@ -288,10 +288,13 @@ hipError_t launch_copy_words(const void *src, void *dst, int n, hipStream_t st);
 // entries each), normalised over the whole row in float64: chosen[r] for
 // targets[r], and the count largest entries of each row as top_ids[r][k] /
 // top_lp[r][k], descending with ties to the lower id (summarizeLogits,
-// logprobs.go:60-95). 1 <= count <= min(vocab, logprob_max_count()).
-int logprob_max_count();
+// logprobs.go:60-95). 1 <= count <= vocab. `scratch` (16-byte aligned
+// device memory of logprob_scratch_bytes(count) bytes) starts with the
+// error word, which the caller zeroes first: a row holding NaN leaves its
+// row + 1 there (the largest such) and no results for that row.
+size_t logprob_scratch_bytes(int count);
 hipError_t launch_logprobs(const float *logits, int64_t ld, int rows, int vocab, const int *targets, int count,
-                           double *chosen, int *top_ids, double *top_lp, hipStream_t st);
+                           double *chosen, int *top_ids, double *top_lp, void *scratch, hipStream_t st);
 
 // ---- weights ----
 // Places raw GGUF-encoded bytes (already in device memory) of a

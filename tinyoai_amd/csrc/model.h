@@ -199,6 +199,7 @@ struct StableModel {
     int count = 0, row = 0;
     double *chosen = nullptr, *top_lp = nullptr;
     int *top_ids = nullptr;
+    void *scratch = nullptr;  // launch_logprobs scratch (the NaN error word first)
   } scoring;
   void *score_mem = nullptr;
   size_t score_bytes = 0;
