@@ -320,39 +320,43 @@ def branches_workload(args):
                          "weight_bytes": int(weight_bytes)}}
 
 
-def cpu_baseline(config, tensors, threads, prompt_len, decode_tokens=6, prefill_tokens=128):
+def cpu_baseline(config, tensors, threads, prompt, decode_tokens=6):
     """The oracle (C restatement of the Go scalar engine) on the host cores,
-    at each thread count of `threads`: a batched prefill of 128 tokens
-    (prefillBatch, timed), then `decode_tokens` greedy decode forwards with
-    logits at the positions that follow (timed). The headline figure is the
-    last thread count's decode rate."""
+    on the workload's own positions: the bench's prompt prefilled in the
+    oracle's 128-token batches (prefillBatch) at the largest thread count
+    (timed), then, at each thread count of `threads`, `decode_tokens`
+    greedy decode forwards with logits at positions len(prompt) onwards
+    (timed; each count rewrites the same positions). The headline figure is
+    the largest thread count's decode rate."""
     import numpy as np
     from oracle import pyoracle
-    rng = np.random.default_rng(5)
-    ids = rng.integers(0, config["vocab_size"], prefill_tokens).astype(np.int32)
+    P = len(prompt)
+    top = max(threads)
+    pyoracle.set_threads(top)
+    m = pyoracle.StableLM(config, tensors, capacity=1024)
+    t0 = time.perf_counter()
+    first = m.prefill(np.asarray(prompt, np.int32), 0)
+    prefill_s = time.perf_counter() - t0
+    print(f"[bench] cpu oracle: {P}-token prefill at {top} threads in {prefill_s:.1f}s", file=sys.stderr, flush=True)
     runs = {}
     for th in threads:
         pyoracle.set_threads(th)
-        m = pyoracle.StableLM(config, tensors, capacity=1024)
-        t0 = time.perf_counter()
-        logits = m.prefill(ids, 0)
-        prefill_tok_s = prefill_tokens / (time.perf_counter() - t0)
+        logits = first
         t0 = time.perf_counter()
         for i in range(decode_tokens):
-            logits = m.forward(int(np.argmax(logits)), prefill_tokens + i)
+            logits = m.forward(int(np.argmax(logits)), P + i)
         decode_tok_s = decode_tokens / (time.perf_counter() - t0)
-        m.close()
-        runs[th] = {"decode_tok_s": round(decode_tok_s, 4), "prefill_tok_s": round(prefill_tok_s, 3),
-                    "prefill_s_extrapolated": round(prompt_len / prefill_tok_s, 2)}
+        runs[th] = {"decode_tok_s": round(decode_tok_s, 4)}
         print(f"[bench] cpu oracle at {th} threads: {runs[th]}", file=sys.stderr, flush=True)
-    top = threads[-1]
+    m.close()
     return {"value": runs[top]["decode_tok_s"], "unit": "tok/s", "cores": top, "kind": "port",
-            "prefill_tok_s": runs[top]["prefill_tok_s"], "prefill_s_extrapolated": runs[top]["prefill_s_extrapolated"],
+            "prefill_s": round(prefill_s, 2), "prefill_tok_s": round(P / prefill_s, 3),
             "by_threads": {str(k): v for k, v in runs.items()},
             "sample": f"oracle (C restatement of tinyoai's Go scalar-float64 engine, -ffp-contract=off, OpenMP "
-                      f"threads {list(threads)}; {top} = the host cores given to one GPU): a {prefill_tokens}-token "
-                      f"batched prefill, then {decode_tokens} greedy decode forwards with logits at positions "
-                      f"{prefill_tokens}-{prefill_tokens + decode_tokens - 1}, same weights"}
+                      f"threads {list(threads)}; {top} = the host cores given to one GPU): the bench's {P}-token "
+                      f"prompt prefilled in 128-token batches at {top} threads (timed), then {decode_tokens} greedy "
+                      f"decode forwards with logits at positions {P}-{P + decode_tokens - 1} at each thread "
+                      f"count, same weights"}
 
 
 def main():
@@ -422,8 +426,9 @@ def main():
         t_c = time.perf_counter()
         return t_b - t_a, t_c - t_b, toks
 
+    warm_decode_s = []
     for _ in range(args.warmup):
-        step()
+        warm_decode_s.append(step()[1])
         print("[bench] warmup step done", file=sys.stderr, flush=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -483,6 +488,8 @@ def main():
                    "weights_seed": args.seed},
         "prefill_s": round(mean_prefill, 4),
         "prefill_tok_s": round(args.prompt / mean_prefill, 1),
+        "decode_tok_s_by_loop": {"warmup": [round((args.generate - 1) / t, 1) for t in warm_decode_s],
+                                 "timed": [round((args.generate - 1) / t, 1) for t in decode_s]},
         "decode_roofline_tok_s": round(roof_tok_s, 1),
         "decode_frac_of_hbm_roofline": round(decode_tok_s / roof_tok_s, 4),
         "greedy_stream_stable": all(s == streams[0] for s in streams),
@@ -501,7 +508,7 @@ def main():
     if not args.no_cpu:
         print("[bench] timing the CPU oracle", file=sys.stderr, flush=True)
         threads = [int(t) for t in args.cpu_threads.split(",") if t]
-        out["cpu_baseline"] = cpu_baseline(config, tensors, threads, args.prompt)
+        out["cpu_baseline"] = cpu_baseline(config, tensors, threads, prompt)
     else:
         out["cpu_baseline"] = None
     del tensors

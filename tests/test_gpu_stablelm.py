@@ -114,7 +114,15 @@ def test_prefix_rewind_and_errors(hip, tiny_stablelm):
     assert f.offset == 6  # validation failures happen before any work
     assert f.set_kv_bits(16) is True and f.offset == 0
     assert f.set_kv_bits(16) is False
-    assert f.limit_cache(32) is False or f.offset == 0
+    # LimitCache (mlx_native.go:231-244): cleared only when the retained
+    # capacity exceeds the limit, which also becomes the capacity reserved
+    # at the next allocation. The precision change released the KV, so
+    # nothing is retained; six tokens then take the reserved 32 positions.
+    assert f.limit_cache(32) is False
+    f.forward(0, ids)
+    assert f.offset == 6
+    assert f.limit_cache(32) is False and f.offset == 6
+    assert f.limit_cache(16) is True and f.offset == 0
 
 
 def test_half_kv_prefix_reuse(hip, tiny_stablelm):
@@ -372,8 +380,8 @@ def test_mixed_format_layers_against_oracle(hip, oracle, mlp, attn):
     keeps its sections as matrices of their own. StableLM-3B layer shapes,
     two layers, fp16 KV, a 300-token prompt (prefill in one chunk) and 8
     decode tokens: logits within 1e-3 of their range of the oracle's (2e-2
-    where BF16 matrices make it a bf16 path: their prefill products take
-    bf16 activations), identical greedy ids."""
+    where a section is BF16: north_star's bound for the bf16 paths, which
+    the two-plane products meet by far), identical greedy ids."""
     config = W.validate_stablelm_config(dict(W.STABLELM_3B, num_hidden_layers=2, max_position_embeddings=512))
     tensors = W.synthetic_stablelm(config, mlp, seed=23, attn_dtype=attn, head_dtype=attn)
     prompt = np.random.default_rng(29).integers(0, 65536, 300).astype(np.int32)
