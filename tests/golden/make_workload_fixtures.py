@@ -145,7 +145,6 @@ def make_kquant_branches(path: str, p: dict = KQ_BRANCHES) -> None:
     on it in turn (forward at position P + s rewrites only positions >= P,
     and attention at position t reads [0, t]), as nativeBranches evaluates a
     branch against the borrowed prefix (mlx_branches.go:98-182)."""
-    p = KQ_BRANCHES
     config, tensors, prefix, lengths, suffixes = branch_inputs(p)
     P = p["prefix"]
     m = pyoracle.StableLM(config, tensors, half_kv=True, capacity=p["max_pos"])

@@ -3,13 +3,14 @@ workloads, one test each (a failure in one does not hide the others):
 
   Q8_0 decode       32 layers, GGUF Q8_0, fp32 KV, a 512-token prompt and
                     256 greedy tokens (stablelm.go:332-387, prefill.go:33-115);
-  BF16 long context 2 layers at full layer shapes, BF16, fp16 KV, an
-                    8129-token prefill through the 2048-token chunks, then
-                    16 greedy tokens;
-  K-quant branches  2 layers, Q6_K attention and classifier, Q4_K MLP, fp16
-                    KV: 16 branches on a 4096-token prefix, private suffixes
-                    of 1-256 tokens, then 8 lockstep tokens
-                    (mlx_branches.go:98-182).
+  BF16 long context BF16, fp16 KV, an 8129-token prefill through the
+                    2048-token chunks, then greedy tokens: 2 layers at full
+                    layer shapes with 16 tokens, and all 32 layers with 64
+                    tokens (to position 8192);
+  K-quant branches  Q6_K attention and classifier, Q4_K MLP, fp16 KV: 16
+                    branches on a 4096-token prefix, private suffixes of
+                    1-256 tokens, then lockstep tokens (mlx_branches.go:98-182):
+                    2 layers with 8 tokens, and all 32 layers with 64.
 
 The oracle needs minutes for these, so its results are committed fixtures
 (tests/golden/make_workload_fixtures.py writes them from the same seeds);
@@ -96,14 +97,16 @@ def test_q8_0_decode_workload(hip):
     print(f"q8_0 decode: worst logits error {worst:.2e} of the range")
 
 
-def test_bf16_long_context_workload(hip):
-    """2 layers at full shapes, BF16 weights, fp16 KV, an 8129-token
-    prefill (2048-token chunks, the last one partial) and 16 greedy tokens:
-    logits within 2e-2 of their range, the last prompt token's and the last
+@pytest.mark.parametrize("name", ["bf16_long", "bf16_long_full"])
+def test_bf16_long_context_workload(hip, name):
+    """BF16 weights, fp16 KV, an 8129-token prefill (2048-token chunks, the
+    last one partial), then greedy tokens: 2 layers at full shapes with 16
+    tokens, and the whole workload (32 layers, 64 tokens, to position 8192).
+    Logits within 2e-2 of their range, the last prompt token's and the last
     decode token's per-layer residuals within 2e-2 of each layer's range,
-    identical greedy ids."""
-    fx = load("bf16_long")
-    p = F.BF16_LONG
+    identical greedy ids at every step."""
+    fx = load(name)
+    p = F.BF16_LONG_FULL if name.endswith("_full") else F.BF16_LONG
     config, tensors, prompt = F.bf16_inputs(p)
     f = hip.StableLMForwarder(config, tensors)
     del tensors
@@ -124,16 +127,18 @@ def test_bf16_long_context_workload(hip):
         want = fx["trace_last"][layer]
         assert np.max(np.abs(row - want)) <= 2e-2 * float(np.ptp(want)), layer
     f.close()
-    print(f"bf16 long context: worst logits error {worst:.2e} of the range")
+    print(f"{name}: worst logits error {worst:.2e} of the range")
 
 
-def test_kquant_branches_workload(hip):
-    """2 layers at full shapes, K-quant mix, fp16 KV: a 4096-token prefix,
-    16 branches given private suffixes of 1-256 tokens in one append, then
-    7 lockstep steps at ragged positions: every branch's logits within 2e-2
-    of their range, identical greedy ids."""
-    fx = load("kquant_branches")
-    p = F.KQ_BRANCHES
+@pytest.mark.parametrize("name", ["kquant_branches"])
+def test_kquant_branches_workload(hip, name):
+    """K-quant mix, fp16 KV: a 4096-token prefix, 16 branches given private
+    suffixes of 1-256 tokens in one append, then lockstep steps at ragged
+    positions: 2 layers at full shapes with 7 steps, and the whole workload
+    (32 layers, 63 steps). Every branch's logits within 2e-2 of their range,
+    identical greedy ids."""
+    fx = load(name)
+    p = F.KQ_BRANCHES_FULL if name.endswith("_full") else F.KQ_BRANCHES
     config, tensors, prefix, lengths, suffixes = F.branch_inputs(p)
     assert np.array_equal(lengths, fx["lengths"])
     f = hip.StableLMForwarder(config, tensors)
@@ -154,4 +159,4 @@ def test_kquant_branches_workload(hip):
         assert br.length(j) == lengths[j] + p["steps"] - 1
     br.close()
     f.close()
-    print(f"k-quant branches: worst logits error {worst:.2e} of the range")
+    print(f"{name}: worst logits error {worst:.2e} of the range")
