@@ -343,26 +343,12 @@ __global__ __launch_bounds__(kLThreads) void gemm_large_kernel(GemmArgs g) {
 }
 
 // ------------------------------------------------------------ wide tiles
-// One wave per SIMD: four waves of a 256-thread block own 32 * MF rows
-// each (block rows BM = 128 * MF) and all BN = 32 * NF columns of the
-// block's tile, as MF x NF tiles of v_mfma_f32_32x32x16_bf16; per k16 a
-// wave reads MF * XS activation and NF weight fragments from LDS for
+// BF16 weights. One wave per SIMD: four waves of a 256-thread block own
+// 32 * MF rows each (block rows BM = 128 * MF) and all BN = 32 * NF columns
+// of the block's tile, as MF x NF tiles of v_mfma_f32_32x32x16_bf16; per
+// k16 a wave reads MF * XS activation and NF weight fragments from LDS for
 // XS * MF * NF products (MF = 2, NF = 7, two planes: 11 fragment reads for
-// 28 products). A K step is 32 values (one Q8_0 block).
-//
-// Both operands reach LDS through registers with coalesced loads (four
-// lanes per 64-byte row segment of a step): loading activations straight
-// into the fragment layout puts 32 rows in every load instruction, and
-// the address unit then stalls on the L1 cache (measured: 41% matrix-core
-// busy, most wave time waiting on loads). Every load and LDS store is
-// issued unconditionally (loads past an operand read zeros; chunks past
-// the tile land in LDS padding), so the count of loads in flight is the
-// same on every path and each wait covers only the loads it needs.
-//
-// Pipeline: three register stages loaded three K steps ahead, the LDS
-// tiles double-buffered. Step kb issues the loads of kb + 3, forms the
-// products of kb, stores the registers of kb + 1 into the other LDS
-// buffer and waits at the block barrier.
+// 28 products). A K step is 32 values.
 //
 // LDS rows are 64 bytes (32 bf16) as four 16-byte chunks, chunk c of row r
 // at position c ^ ((r >> 2) & 3): the 16 lanes of a fragment read that
@@ -371,10 +357,6 @@ __global__ __launch_bounds__(kLThreads) void gemm_large_kernel(GemmArgs g) {
 // the first 8 for the step's first product and the rest for its second;
 // activation and weight fragments use the same k order, so each step is
 // covered exactly once.
-//
-// Q8_0: quants become bf16 (exactly) on their way into LDS, the block's
-// fp16 scale as fp32 beside the tile; each step's products are formed
-// without scale and added as acc += d * t.
 //
 // Blocks map onto the 8 XCDs in runs: XCD x takes tiles [x * per, (x + 1)
 // * per) (M tiles fastest), so the blocks resident on one XCD share their
@@ -396,29 +378,6 @@ struct WideArgs {
 };
 
 constexpr int kWThreads = 256, kWK = 32;
-
-// Weight rows of an LDS stage: the tile's rows rounded up to what the
-// threads' unconditional chunk stores cover (kWThreads chunks of 4 per
-// row for BF16, 2 per row for Q8_0).
-template <int WF, int NF>
-constexpr int kBRows() {
-  constexpr int per = WF == FMT_BF16 ? 4 : 2, chunks = NF * 32 * per;
-  return (chunks + kWThreads - 1) / kWThreads * kWThreads / per;
-}
-// uint16 units of an LDS stage: XS activation planes of BM rows, the
-// weight rows, then (Q8_0) one fp32 scale per thread.
-template <int WF, int XS, int MF, int NF>
-constexpr int wide_stage_u16() {
-  return XS * 128 * MF * kWK + kBRows<WF, NF>() * kWK + (WF == FMT_Q8_0 ? kWThreads * 2 : 0);
-}
-
-template <int WF, int XS, int MF, int NF, bool EPI>
-constexpr size_t gemm_wide_lds() {
-  // two stages; with EPI also 32 output rows per wave
-  const size_t stage = (size_t)2 * wide_stage_u16<WF, XS, MF, NF>() * 2;
-  const size_t rows = (size_t)4 * 32 * (NF * 32 + 4) * 4;
-  return EPI && rows > stage ? rows : stage;
-}
 
 __device__ __forceinline__ int swz(int row, int c) { return row * kWK + ((c ^ ((row >> 2) & 3)) << 3); }
 
@@ -465,271 +424,12 @@ __device__ __forceinline__ void wide_epilogue_rows(const WideArgs &g, const floa
   }
 }
 
-template <int WF, int XS, int MF, int NF, bool EPI>
-__global__ __launch_bounds__(kWThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_wide_kernel(WideArgs g) {
-  constexpr int BM = 4 * 32 * MF, BN = 32 * NF;
-  constexpr int kBChunks = WF == FMT_BF16 ? BN * 4 : BN * 2;  // 16-byte weight chunks a stage loads
-  constexpr int NB = (kBChunks + kWThreads - 1) / kWThreads;
-  constexpr int NA = BM * 4 / kWThreads;                      // activation chunks per plane and thread
-  constexpr int kA = BM * kWK;                                // uint16 units of an activation plane
-  constexpr int kStage = wide_stage_u16<WF, XS, MF, NF>();
-  constexpr int kB0 = XS * kA, kS0 = kB0 + kBRows<WF, NF>() * kWK;
-  extern __shared__ __align__(16) uint16_t lds16[];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-
-  // Which product, tile and split this block computes.
-  int b = blockIdx.x, pi = 0;
-  {
-    const WideProduct &p0 = g.p[0];
-    const int tiles0 = ((g.M + BM - 1) / BM) * ((p0.w.rows + BN - 1) / BN);
-    const int nb0 = (tiles0 * p0.ksplit + 7) / 8 * 8;
-    if (g.nprod > 1 && b >= nb0) {
-      b -= nb0;
-      pi = 1;
-    }
-  }
-  const WideProduct &P = g.p[pi];
-  const int K = P.w.cols, N = P.w.rows, nk = K / kWK;
-  const int MT = (g.M + BM - 1) / BM, NT = (N + BN - 1) / BN, tiles = MT * NT;
-  const int total = tiles * P.ksplit, per = (total + 7) / 8;
-  const int t = (b & 7) * per + (b >> 3);
-  if (t >= total) return;
-  const int split = t / tiles, tt = t - split * tiles, nt = tt / MT, mt = tt - nt * MT;
-  const int m0 = mt * BM, n0 = nt * BN;
-  const int k_lo = (int)((int64_t)nk * split / P.ksplit), k_hi = (int)((int64_t)nk * (split + 1) / P.ksplit);
-
-  // Sentinels past every operand (each under 1 GiB, checked at launch): a
-  // row past M or N, and a K step past the split; their sum stays below
-  // 2^32.
-  constexpr uint32_t kNone = 0x80000000u, kPast = 0x40000000u;
-  const __amdgpu_buffer_rsrc_t rxh = plane_rsrc(reinterpret_cast<const uint8_t *>(P.xh), (int64_t)g.M * P.lda * 2);
-  const __amdgpu_buffer_rsrc_t rxl =
-      plane_rsrc(reinterpret_cast<const uint8_t *>(XS == 2 ? P.xl : P.xh), (int64_t)g.M * P.lda * 2);
-  const __amdgpu_buffer_rsrc_t rw = plane_rsrc(P.w.vals, (int64_t)N * P.w.vstride);
-  const __amdgpu_buffer_rsrc_t rs =
-      plane_rsrc(WF == FMT_Q8_0 ? P.w.meta : P.w.vals, WF == FMT_Q8_0 ? (int64_t)N * P.w.mstride : 0);
-  auto ld16 = [](__amdgpu_buffer_rsrc_t r, uint32_t off) {
-    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
-    return make_uint4(v.x, v.y, v.z, v.w);
-  };
-
-  // Chunk q = tid + 256 i of a stage: activations row q / 4, chunk q % 4
-  // (per plane); BF16 weights likewise; Q8_0 weights row q / 2, 16 quants
-  // q % 2 (two bf16 chunks); the scale of row tid.
-  uint32_t aoff[NA], boff[NB];
-  int adst[NA], bdst[NB];
-#pragma unroll
-  for (int i = 0; i < NA; i++) {
-    const int q = tid + kWThreads * i, row = q >> 2, c = q & 3;
-    aoff[i] = m0 + row < g.M ? (uint32_t)(((m0 + row) * P.lda + c * 8) * 2) : kNone;
-    adst[i] = swz(row, c);
-  }
-#pragma unroll
-  for (int i = 0; i < NB; i++) {
-    const int q = tid + kWThreads * i;
-    if constexpr (WF == FMT_BF16) {
-      const int row = q >> 2, c = q & 3;
-      boff[i] = q < kBChunks && n0 + row < N ? (uint32_t)((n0 + row) * P.w.vstride + c * 16) : kNone;
-      bdst[i] = swz(row, c);
-    } else {
-      const int row = q >> 1;
-      boff[i] = q < kBChunks && n0 + row < N ? (uint32_t)((n0 + row) * P.w.vstride + (q & 1) * 16) : kNone;
-      bdst[i] = row;
-    }
-  }
-  const uint32_t soff = WF == FMT_Q8_0 && tid < BN && n0 + tid < N ? (uint32_t)((n0 + tid) * P.w.mstride) : kNone;
-
-  struct Regs {
-    uint4 a[XS][NA], b[NB];
-    uint32_t s;
-  };
-  // Loads of step kb (kb past the split: offsets past every operand).
-  auto load = [&](int kb, Regs &r) {
-    const bool in = kb < k_hi;
-    const uint32_t ka = in ? (uint32_t)(kb * kWK * 2) : kPast;
-    const uint32_t kw = in ? (uint32_t)(WF == FMT_BF16 ? kb * kWK * 2 : kb * kWK) : kPast;
-#pragma unroll
-    for (int i = 0; i < NB; i++) r.b[i] = ld16(rw, boff[i] + kw);
-#pragma unroll
-    for (int p = 0; p < XS; p++)
-#pragma unroll
-      for (int i = 0; i < NA; i++) r.a[p][i] = ld16(p ? rxl : rxh, aoff[i] + ka);
-    if constexpr (WF == FMT_Q8_0)
-      r.s = __builtin_amdgcn_raw_buffer_load_b16(rs, (int)(soff + (in ? (uint32_t)kb * 2 : kPast)), 0, 0);
-  };
-  auto store = [&](int buf, const Regs &r) {
-    uint16_t *st = lds16 + buf * kStage;
-#pragma unroll
-    for (int p = 0; p < XS; p++)
-#pragma unroll
-      for (int i = 0; i < NA; i++) *reinterpret_cast<uint4 *>(st + p * kA + adst[i]) = r.a[p][i];
-#pragma unroll
-    for (int i = 0; i < NB; i++) {
-      if constexpr (WF == FMT_BF16) {
-        *reinterpret_cast<uint4 *>(st + kB0 + bdst[i]) = r.b[i];
-      } else {  // 16 int8 -> 16 bf16 (exact): chunks 2h, 2h + 1 of the row
-        const int h = (tid + kWThreads * i) & 1;
-        const uint32_t ws[4] = {r.b[i].x, r.b[i].y, r.b[i].z, r.b[i].w};
-        uint32_t o[8];
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-          const uint32_t v = ws[j];
-          o[2 * j] = bf16_bits((float)(int8_t)v) | bf16_bits((float)(int8_t)(v >> 8)) << 16;
-          o[2 * j + 1] = bf16_bits((float)(int8_t)(v >> 16)) | bf16_bits((float)(int8_t)(v >> 24)) << 16;
-        }
-        *reinterpret_cast<uint4 *>(st + kB0 + swz(bdst[i], 2 * h)) = make_uint4(o[0], o[1], o[2], o[3]);
-        *reinterpret_cast<uint4 *>(st + kB0 + swz(bdst[i], 2 * h + 1)) = make_uint4(o[4], o[5], o[6], o[7]);
-      }
-    }
-    if constexpr (WF == FMT_Q8_0) reinterpret_cast<float *>(st + kS0)[tid] = hw_half((uint16_t)r.s);
-  };
-
-  f32x16 acc[MF][NF];
-#pragma unroll
-  for (int f = 0; f < MF; f++)
-#pragma unroll
-    for (int j = 0; j < NF; j++)
-#pragma unroll
-      for (int v = 0; v < 16; v++) acc[f][j][v] = 0.f;
-  // Fragment rows: activations wave * 32 * MF + f * 32 + lane % 32 of each
-  // plane, weights j * 32 + lane % 32; chunk 2 * (lane / 32) + s.
-  const int arow = wave * 32 * MF + (lane & 31), brow = lane & 31;
-  auto frag = [&](const uint16_t *base, int row, int s) {
-    return *reinterpret_cast<const bf16x8 *>(base + swz(row, 2 * (lane >> 5) + s));
-  };
-  auto compute = [&](int buf) {
-    const uint16_t *st = lds16 + buf * kStage;
-    if constexpr (WF == FMT_BF16) {
-#pragma unroll
-      for (int s = 0; s < 2; s++) {
-        bf16x8 af[MF][XS], bf[NF];
-#pragma unroll
-        for (int j = 0; j < NF; j++) bf[j] = frag(st + kB0, j * 32 + brow, s);
-#pragma unroll
-        for (int f = 0; f < MF; f++)
-#pragma unroll
-          for (int p = 0; p < XS; p++) af[f][p] = frag(st + p * kA, arow + f * 32, s);
-#pragma unroll
-        for (int f = 0; f < MF; f++)
-#pragma unroll
-          for (int p = 0; p < XS; p++)
-#pragma unroll
-            for (int j = 0; j < NF; j++)
-              acc[f][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[f][p], bf[j], acc[f][j], 0, 0, 0);
-      }
-    } else {
-      const float *scl = reinterpret_cast<const float *>(st + kS0);
-      bf16x8 af[MF][XS][2];
-#pragma unroll
-      for (int f = 0; f < MF; f++)
-#pragma unroll
-        for (int p = 0; p < XS; p++)
-#pragma unroll
-          for (int s = 0; s < 2; s++) af[f][p][s] = frag(st + p * kA, arow + f * 32, s);
-#pragma unroll
-      for (int j = 0; j < NF; j++) {
-        bf16x8 bf[2];
-#pragma unroll
-        for (int s = 0; s < 2; s++) bf[s] = frag(st + kB0, j * 32 + brow, s);
-        const float sc = scl[j * 32 + brow];
-#pragma unroll
-        for (int f = 0; f < MF; f++) {
-          f32x16 tq;
-#pragma unroll
-          for (int v = 0; v < 16; v++) tq[v] = 0.f;
-#pragma unroll
-          for (int s = 0; s < 2; s++)
-#pragma unroll
-            for (int p = 0; p < XS; p++) tq = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[f][p][s], bf[s], tq, 0, 0, 0);
-#pragma unroll
-          for (int v = 0; v < 16; v++) acc[f][j][v] = fmaf(sc, tq[v], acc[f][j][v]);
-        }
-      }
-    }
-  };
-
-  // Six steps per trip (three register stages, two LDS buffers). Full
-  // trips run without conditions (a guard per step made the compiler's
-  // count of loads in flight conservative at every join, and it then
-  // waited for the next step's loads at the head of each step); the last
-  // trip (fewer than six steps) takes the guarded steps. The scheduling
-  // barriers keep the loads at the head of the step (the scheduler
-  // otherwise sank them below the products).
-  Regs r0, r1, r2;
-  load(k_lo, r0);
-  load(k_lo + 1, r1);
-  load(k_lo + 2, r2);
-  store(0, r0);
-  __syncthreads();
-  auto step = [&](int kb, Regs &rload, const Regs &rstore, int buf) {
-    load(kb + 3, rload);
-    __builtin_amdgcn_sched_barrier(0);
-    compute(buf);
-    __builtin_amdgcn_sched_barrier(0);
-    store(buf ^ 1, rstore);
-    __syncthreads();
-  };
-  int kb = k_lo;
-  for (; kb + 6 <= k_hi; kb += 6) {
-    step(kb, r0, r1, 0);
-    step(kb + 1, r1, r2, 1);
-    step(kb + 2, r2, r0, 0);
-    step(kb + 3, r0, r1, 1);
-    step(kb + 4, r1, r2, 0);
-    step(kb + 5, r2, r0, 1);
-  }
-  if (kb < k_hi) step(kb, r0, r1, 0);
-  if (kb + 1 < k_hi) step(kb + 1, r1, r2, 1);
-  if (kb + 2 < k_hi) step(kb + 2, r2, r0, 0);
-  if (kb + 3 < k_hi) step(kb + 3, r0, r1, 1);
-  if (kb + 4 < k_hi) step(kb + 4, r1, r2, 0);
-
-  // D fragment: lane holds column lane % 32 of rows (v / 4) * 8 + (lane / 32) * 4 + v % 4.
-  if constexpr (EPI) {
-    // Each wave passes its rows through LDS, 32 at a time ([32][BN + 4]
-    // floats per wave), then its lanes take (row, output pair) items in
-    // order through the in-projection epilogue: neighbouring lanes store
-    // neighbouring outputs.
-    constexpr int kPitch = BN + 4;
-    float *tile = reinterpret_cast<float *>(lds16) + wave * 32 * kPitch;
-#pragma unroll
-    for (int f = 0; f < MF; f++) {
-#pragma unroll
-      for (int j = 0; j < NF; j++)
-#pragma unroll
-        for (int v = 0; v < 16; v++)
-          tile[((v >> 2) * 8 + (lane >> 5) * 4 + (v & 3)) * kPitch + j * 32 + (lane & 31)] = acc[f][j][v];
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      const int r0w = m0 + (wave * MF + f) * 32;
-      wide_epilogue_rows(g, tile, kPitch, BN, r0w, n0, N, lane);
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    }
-    return;
-  }
-  float *y = P.y + (int64_t)split * P.split_stride;
-#pragma unroll
-  for (int f = 0; f < MF; f++)
-#pragma unroll
-    for (int j = 0; j < NF; j++) {
-      const int n = n0 + j * 32 + (lane & 31);
-      if (n >= N) continue;
-#pragma unroll
-      for (int v = 0; v < 16; v++) {
-        const int m = m0 + (wave * MF + f) * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
-        if (m < g.M) y[(int64_t)m * P.ldy + n] = acc[f][j][v];
-      }
-    }
-}
-
-// ------------------------------------------------------------ BF16 wide tiles, loads direct to LDS
-// The BF16 product on the same tiles as gemm_wide_kernel, with both
-// operands loaded straight into LDS (buffer_load_dwordx4 ... lds): no
-// staging registers, so each wave holds a step's fragments for both k
-// halves and the compiler keeps the LDS reads ahead of the products. A
+// ------------------------------------------------------------ loads direct to LDS
+// Both operands are loaded straight into LDS (buffer_load_dwordx4 ...
+// lds): no staging registers, so each wave holds a step's fragments for
+// both k halves and the compiler keeps the LDS reads ahead of the
+// products. (Staging through registers with coalesced loads kept the
+// matrix cores 41% busy at best, most wave time waiting on loads.) A
 // ring of three LDS stages: step kb waits for its own loads of stage kb
 // (the count of loads in flight is exact: every wave issues the same
 // loads every step, past the operands reading zeros), meets the block
@@ -918,7 +618,7 @@ __global__ __launch_bounds__(kWThreads) __attribute__((amdgpu_waves_per_eu(1, 1)
     }
 }
 
-template <int WF, int XS, int MF, int NF, bool EPI>
+template <int XS, int MF, int NF, bool EPI>
 hipError_t gemm_wide_launch(const WideArgs &g, hipStream_t st) {
   constexpr int BM = 4 * 32 * MF, BN = 32 * NF;
   int blocks = 0;
@@ -926,21 +626,12 @@ hipError_t gemm_wide_launch(const WideArgs &g, hipStream_t st) {
     const int tiles = ((g.M + BM - 1) / BM) * ((g.p[i].w.rows + BN - 1) / BN);
     blocks += (tiles * g.p[i].ksplit + 7) / 8 * 8;
   }
-  if constexpr (WF == FMT_BF16) {
-    constexpr size_t lds = gemm_dma_lds<XS, MF, NF, EPI>();
-    static const hipError_t attr =
-        hipFuncSetAttribute(reinterpret_cast<const void *>(&gemm_dma_kernel<XS, MF, NF, EPI>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (attr != hipSuccess) return attr;
-    hipLaunchKernelGGL((gemm_dma_kernel<XS, MF, NF, EPI>), dim3(blocks), dim3(kWThreads), lds, st, g);
-  } else {
-    constexpr size_t lds = gemm_wide_lds<WF, XS, MF, NF, EPI>();
-    static const hipError_t attr =
-        hipFuncSetAttribute(reinterpret_cast<const void *>(&gemm_wide_kernel<WF, XS, MF, NF, EPI>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (attr != hipSuccess) return attr;
-    hipLaunchKernelGGL((gemm_wide_kernel<WF, XS, MF, NF, EPI>), dim3(blocks), dim3(kWThreads), lds, st, g);
-  }
+  constexpr size_t lds = gemm_dma_lds<XS, MF, NF, EPI>();
+  static const hipError_t attr =
+      hipFuncSetAttribute(reinterpret_cast<const void *>(&gemm_dma_kernel<XS, MF, NF, EPI>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  if (attr != hipSuccess) return attr;
+  hipLaunchKernelGGL((gemm_dma_kernel<XS, MF, NF, EPI>), dim3(blocks), dim3(kWThreads), lds, st, g);
   return hipGetLastError();
 }
 
@@ -1005,27 +696,18 @@ hipError_t launch_gemm_in_epilogue(const MatDesc &w, const uint16_t *xh, const u
 
 namespace {
 
-template <int WF, int XS, bool EPI>
-hipError_t gemm_wide_dispatch(const WideArgs &g, int mf, int nf, hipStream_t st) {
-  if (mf == 2 && nf == 7) return gemm_wide_launch<WF, XS, 2, 7, EPI>(g, st);
-  if (mf == 2 && nf == 8) return gemm_wide_launch<WF, XS, 2, 8, EPI>(g, st);
-  if (mf == 1 && nf == 8) return gemm_wide_launch<WF, XS, 1, 8, EPI>(g, st);
-  if (mf == 1 && nf == 7) return gemm_wide_launch<WF, XS, 1, 7, EPI>(g, st);
-  return hipErrorInvalidValue;
-}
-
 template <int XS, bool EPI>
-hipError_t gemm_wide_q8(const WideArgs &g, int mf, int nf, hipStream_t st) {
-  if (mf == 1 && nf == 8) return gemm_wide_launch<FMT_Q8_0, XS, 1, 8, EPI>(g, st);
-  if (mf == 1 && nf == 7) return gemm_wide_launch<FMT_Q8_0, XS, 1, 7, EPI>(g, st);
+hipError_t gemm_wide_dispatch(const WideArgs &g, int mf, int nf, hipStream_t st) {
+  if (mf == 2 && nf == 7) return gemm_wide_launch<XS, 2, 7, EPI>(g, st);
+  if (mf == 2 && nf == 8) return gemm_wide_launch<XS, 2, 8, EPI>(g, st);
+  if (mf == 1 && nf == 8) return gemm_wide_launch<XS, 1, 8, EPI>(g, st);
+  if (mf == 1 && nf == 7) return gemm_wide_launch<XS, 1, 7, EPI>(g, st);
   return hipErrorInvalidValue;
 }
 
 template <bool EPI>
 hipError_t gemm_wide_fmt(const WideArgs &g, int mf, int nf, bool two, hipStream_t st) {
-  if (g.p[0].w.fmt == FMT_Q8_0)
-    return two ? gemm_wide_q8<2, EPI>(g, mf, nf, st) : gemm_wide_q8<1, EPI>(g, mf, nf, st);
-  return two ? gemm_wide_dispatch<FMT_BF16, 2, EPI>(g, mf, nf, st) : gemm_wide_dispatch<FMT_BF16, 1, EPI>(g, mf, nf, st);
+  return two ? gemm_wide_dispatch<2, EPI>(g, mf, nf, st) : gemm_wide_dispatch<1, EPI>(g, mf, nf, st);
 }
 
 bool wide_operand_ok(const MatDesc &w, const uint16_t *xh, int lda, int M) {
@@ -1036,9 +718,7 @@ bool wide_operand_ok(const MatDesc &w, const uint16_t *xh, int lda, int M) {
 
 }  // namespace
 
-bool gemm_wide_shape(int fmt, int mf, int nf) {
-  return (nf == 7 || nf == 8) && (mf == 1 || (mf == 2 && fmt == FMT_BF16));
-}
+bool gemm_wide_shape(int fmt, int mf, int nf) { return fmt == FMT_BF16 && (nf == 7 || nf == 8) && (mf == 1 || mf == 2); }
 
 hipError_t launch_gemm_wide(const WideGemm *p, int nprod, int M, int mf, int nf, hipStream_t st) {
   if (nprod < 1 || nprod > 2 || M < 1 || !gemm_wide_shape(p[0].w.fmt, mf, nf)) return hipErrorInvalidValue;

@@ -237,14 +237,14 @@ struct InEpilogue {
 };
 hipError_t launch_gemm_in_epilogue(const MatDesc &w, const uint16_t *xh, const uint16_t *xl, int M,
                                    const InEpilogue &e, hipStream_t st);
-// Wide-tile matrix-core products (one wave per SIMD, weights through LDS,
-// activations straight into registers): y = X * W^T for Q8_0 and BF16
-// weights with K % 32 == 0, X as bf16 planes xh (and xl, or null for one
-// plane) with rows lda values apart. A launch carries one or two products
-// of M rows each (their blocks side by side, the first product's first);
-// product i cuts its K range in ksplit parts whose results go to
-// y + s * split_stride. Block tiles are (128 * mf) x (32 * nf):
-// gemm_wide_shape names the instances built (Q8_0: mf 1).
+// Wide-tile matrix-core products (one wave per SIMD, both operands loaded
+// straight into LDS): y = X * W^T for BF16 weights with K % 32 == 0, X as
+// bf16 planes xh (and xl, or null for one plane) with rows lda values
+// apart. A launch carries one or two products of M rows each (their
+// blocks side by side, the first product's first); product i cuts its K
+// range in ksplit parts whose results go to y + s * split_stride. Block
+// tiles are (128 * mf) x (32 * nf): gemm_wide_shape names the instances
+// built.
 struct WideGemm {
   MatDesc w;
   const uint16_t *xh, *xl;
