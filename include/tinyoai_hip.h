@@ -222,12 +222,16 @@ int tinyoai_stablelm_profile(tinyoai_model *m, int32_t enable);
  * ids may then differ from the fp32 engine's where logits nearly tie),
  * zero (the default) keeps two bf16 planes per activation (16 significant
  * bits). Stage 7: grid nonzero (the default) runs the BF16-weight prefill
- * products on wide matrix-core tiles (the in-projection with its epilogue
- * in one launch, the o and down products together as K splits), zero on
- * 128 x 256 tiles (fp32 accumulation either way; the sums' order
- * differs). Stage 8: grid nonzero forms the wide-tile in-projection's
+ * products on wide matrix-core tiles (the o and down products together
+ * as K splits of one launch), zero on 128 x 256 tiles (fp32 accumulation
+ * either way; the sums' order differs). Stage 8: grid nonzero forms the wide-tile in-projection's
  * epilogue in the product's own launch, zero (the default) as a kernel of
- * its own (same arithmetic). Returns 0 or TINYOAI_EINVAL. */
+ * its own (same arithmetic). Stage 9: grid nonzero (the default) splits a
+ * prefill call's attention over key ranges when its query tiles would
+ * leave CUs idle (a few hundred tokens after a resident prefix of 1024 or
+ * more), the ranges' partial results combined in a fixed order; zero
+ * keeps one block per query tile (the sums' order differs). Returns 0 or
+ * TINYOAI_EINVAL. */
 int tinyoai_stablelm_set_launch(tinyoai_model *m, int32_t stage, int32_t grid, int32_t threads);
 int tinyoai_stablelm_profile_read(tinyoai_model *m, double *ms, int64_t *counts, int32_t n_stages);
 

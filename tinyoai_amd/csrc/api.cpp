@@ -922,7 +922,9 @@ int StableModel::prefill_chunk(const int32_t *ids, int n, int start, bool want_l
               "in_epilogue");
       }
       STAGE(ST_PREFILL_ATTENTION,
-            launch_flash_prefill(dims, kv[l], Q, d_pos0, n, tracing ? A : nullptr, stream, XH, XL), "attention");
+            launch_flash_prefill(dims, kv[l], Q, d_pos0, n, tracing ? A : nullptr, stream, XH, XL, nullptr, 0, 0, 0,
+                                 nullptr, 0, flash_ksplit ? Y : nullptr, (int64_t)chunk * win_rows, start + n - 1),
+            "attention");
       int so, sd;
       wide_out_splits(n, d, d, I, kPrefillSplits, &so, &sd);
       const WideGemm prods[2] = {{wd, MH, lo ? ML : nullptr, I, D, d, sd, (int64_t)n * d},
@@ -980,7 +982,9 @@ int StableModel::prefill_chunk(const int32_t *ids, int n, int start, bool want_l
       if (flash)
         STAGE(ST_PREFILL_ATTENTION,
               launch_flash_prefill(dims, kv[l], Q, d_pos0, n, po && !tracing ? nullptr : A, stream, po ? XH : nullptr,
-                                   po ? XL : nullptr),
+                                   po ? XL : nullptr, nullptr, 0, 0, 0, nullptr, 0, flash_ksplit ? Y : nullptr,
+                                   (int64_t)chunk * win_rows,
+                                   start + n - 1),
               "attention");
       else
         STAGE(ST_PREFILL_ATTENTION,
@@ -1723,6 +1727,10 @@ int tinyoai_stablelm_set_launch(tinyoai_model *m, int32_t stage, int32_t grid, i
   }
   if (stage == 5) {  // BF16-weight prefill products with bf16 activations (1) or two planes (0, the default)
     s.bf16_acts = grid != 0;
+    return TINYOAI_OK;
+  }
+  if (stage == 9) {  // prefill attention split over keys where query tiles leave CUs idle (1, the default) or not (0)
+    s.flash_ksplit = grid != 0;
     return TINYOAI_OK;
   }
   if (stage == 4) {  // decode attention inside the decode_in launch (1, the default) or after it (0)

@@ -39,6 +39,11 @@ struct FlashArgs {
   int64_t region;
   int split_keys;
   int64_t ld_o;  // values between the query rows of oh, ol (0: heads * hd)
+  // Key splits (prefill, ksplit > 1): block z of a query tile attends the
+  // key tiles of split z (key_split_tiles) and writes its record {m, l,
+  // o[hd]} at partials + (j * heads + h) * region + z * (hd + 2), as the
+  // shared-prefix pass does; flash_combine_kernel forms the output.
+  int ksplit;
   // Branch runs in one launch (BR instances): segment blockIdx.z is
   // segs[3z..3z+2] = (first row a0, rows, slot of its first position): its
   // queries are rows a0.. of q / out and its positions and slots rows a0..
@@ -70,6 +75,17 @@ __device__ __forceinline__ void split_half(float x, _Float16 &hi, _Float16 &lo) 
 //   v % 4), so each lane fetches the softmax factors of its 16 rows.
 constexpr int kQ32 = 128;  // queries per block
 constexpr int kSharedKeys = 256;  // cache positions per block of the shared-prefix pass
+
+// Key splits of a query tile whose first query sits at position `first`:
+// the key tiles 0 .. first / kTile (each starts at or before every query of
+// the tile, so every query sees a key of every split) are cut in at most
+// `ks` runs of `per` tiles; the last split also takes the tiles past them
+// (the diagonal). Returns the number of splits.
+__host__ __device__ inline int key_split_tiles(int first, int ks, int &per) {
+  const int d = first / kTile + 1;
+  per = (d + ks - 1) / ks;
+  return (d + per - 1) / per;
+}
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
@@ -154,7 +170,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
   const int64_t head_base = (int64_t)kvh * a.kv.cap * HD;
   // BR: the branch's suffix, position t >= prefix at element sfx_base + (t - prefix) * HD.
   const int64_t sfx_base = BR ? ((int64_t)kvh * a.sfx.cap + a.sfx_slot0) * HD : 0;
-  const int ntiles = last_pos / kTile + 1, tile0 = k_lo / kTile;
+  int ntiles = last_pos / kTile + 1, tile0 = k_lo / kTile;
+  if (!SH && !BR && a.ksplit > 1) {  // block-uniform
+    int per;
+    const int splits = key_split_tiles(p0 + qb, a.ksplit, per), z = blockIdx.z;
+    if (z >= splits) return;
+    tile0 = z * per;
+    if (z + 1 < splits) ntiles = tile0 + per;
+  }
   // fp16 cache: a tile is loaded into registers while the previous one is
   // computed. Buffer loads read zeros past the block's last position.
   constexpr int KC = kTile * (HD / 8), KPT = (KC + 255) / 256;  // 16-byte K pieces
@@ -353,8 +376,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
       }
   }
   // ---- normalise and store: lane holds queries (v / 4) * 8 + g * 4 + v % 4, dim t * 32 + col
-  if constexpr (SH) {
+  if (SH || (!BR && a.ksplit > 1)) {  // the record of this key range
     constexpr float kLn2 = 0.6931471805599453f;
+    const int slot = SH ? blockIdx.x : blockIdx.z;
 #pragma unroll
     for (int v = 0; v < 16; v++) {
       const int src = (v >> 2) * 8 + g * 4 + (v & 3);
@@ -362,7 +386,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
       const float mq = __shfl(ref, src, 64) * kLn2;
       const int qi = qw + src;
       if (qi >= a.n) continue;
-      float *part = a.partials + ((int64_t)qi * s.heads + h) * a.region + (int64_t)blockIdx.x * (HD + 2);
+      float *part = a.partials + ((int64_t)qi * s.heads + h) * a.region + (int64_t)slot * (HD + 2);
       if (col == 0) {
         part[0] = mq;
         part[1] = lq;
@@ -395,6 +419,32 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
   }
 }
 
+// The output of query j, head h (block j * heads + h, thread = dim) from
+// the records of its tile's key splits, in split order: with M the largest
+// m, out = sum o_z e_z / sum l_z e_z, e_z = exp(m_z - M).
+template <int HD>
+__global__ __launch_bounds__(128) void flash_combine_kernel(FlashArgs a) {
+  const StableDims &s = a.s;
+  const int qi = blockIdx.x / s.heads, h = blockIdx.x % s.heads, d = threadIdx.x;
+  if (d >= HD) return;
+  int per;
+  const int splits = key_split_tiles(*a.pos0 + qi / kQ32 * kQ32, a.ksplit, per);
+  const float *rec = a.partials + ((int64_t)qi * s.heads + h) * a.region;
+  float m = rec[0];
+  for (int z = 1; z < splits; z++) m = fmaxf(m, rec[z * (HD + 2)]);
+  float l = 0.f, acc = 0.f;
+  for (int z = 0; z < splits; z++) {
+    const float *r = rec + z * (HD + 2);
+    const float e = expf(r[0] - m);
+    l = fmaf(r[1], e, l);
+    acc = fmaf(r[2 + d], e, acc);
+  }
+  const float v = acc / l;
+  const int64_t ob = ((int64_t)qi * s.heads + h) * HD;
+  if (a.out) a.out[ob + d] = v;
+  if (a.oh) store_bf16_split(a.oh, a.ol, (a.ld_o ? (int64_t)qi * a.ld_o + h * HD : ob) + d, v);
+}
+
 template <int HD, bool BR>
 hipError_t flash32_launch(const FlashArgs &a, int nseg, hipStream_t st) {
   dim3 grid((a.n + kQ32 - 1) / kQ32, a.s.heads, nseg);
@@ -407,7 +457,12 @@ hipError_t flash32_launch(const FlashArgs &a, int nseg, hipStream_t st) {
 
 template <int HD>
 hipError_t flash32_dispatch(const FlashArgs &a, bool br, int nseg, hipStream_t st) {
-  return br ? flash32_launch<HD, true>(a, nseg, st) : flash32_launch<HD, false>(a, 1, st);
+  if (br) return flash32_launch<HD, true>(a, nseg, st);
+  if (a.ksplit <= 1) return flash32_launch<HD, false>(a, 1, st);
+  hipError_t e = flash32_launch<HD, false>(a, a.ksplit, st);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(flash_combine_kernel<HD>, dim3(a.n * a.s.heads), dim3(128), 0, st, a);
+  return hipGetLastError();
 }
 
 template <int HD>
@@ -431,7 +486,8 @@ hipError_t launch_shared_prefix_attention(const StableDims &s, const KVDev &kv, 
   if (nq < 1 || nq > kQ32 || prefix < 1 || prefix > kv.cap || !flash_prefill_supported(s.hd) ||
       region < (int64_t)shared_prefix_splits(prefix) * (s.hd + 2))
     return hipErrorInvalidValue;
-  FlashArgs a{s, kv, q, nullptr, nq, nullptr, nullptr, nullptr, KVDev{}, prefix, 0, partials, region, kSharedKeys};
+  FlashArgs a{s, kv, q, nullptr, nq, nullptr, nullptr, nullptr, KVDev{}, prefix, 0, partials, region, kSharedKeys, 0, 0,
+              nullptr};
   const int splits = shared_prefix_splits(prefix);
   switch (s.hd) {
     case 64: return flash32_shared<64>(a, splits, st);
@@ -444,11 +500,24 @@ hipError_t launch_shared_prefix_attention(const StableDims &s, const KVDev &kv, 
 
 hipError_t launch_flash_prefill(const StableDims &s, const KVDev &kv, const float *q, const int *pos0, int n,
                                 float *out, hipStream_t st, uint16_t *oh, uint16_t *ol, const KVDev *sfx, int prefix,
-                                int sfx_slot0, int64_t ld_o, const int *segs, int nseg) {
+                                int sfx_slot0, int64_t ld_o, const int *segs, int nseg, float *work,
+                                int64_t work_floats, int last_pos) {
   if (!oh != !ol || (!out && !oh) || n < 1 || (ld_o && ld_o < (int64_t)s.heads * s.hd)) return hipErrorInvalidValue;
   if (sfx && (sfx->half != kv.half || prefix < 0 || prefix > kv.cap || sfx_slot0 < 0)) return hipErrorInvalidValue;
   if (segs && (!sfx || oh || nseg < 1 || nseg > 65535)) return hipErrorInvalidValue;
-  FlashArgs a{s, kv, q, pos0, n, out, oh, ol, sfx ? *sfx : KVDev{}, prefix, sfx_slot0, nullptr, 0, 0, ld_o, segs};
+  FlashArgs a{s, kv, q, pos0, n, out, oh, ol, sfx ? *sfx : KVDev{}, prefix, sfx_slot0, nullptr, 0, 0, ld_o, 0, segs};
+  // Key splits where the query tiles alone leave CUs idle (a few hundred
+  // queries against a long cache): about 512 blocks, the records in `work`.
+  const int blocks = (n + kQ32 - 1) / kQ32 * s.heads;
+  if (!sfx && work && blocks < 256 && last_pos >= 1024) {
+    int ks = std::min(8, (512 + blocks - 1) / blocks);
+    while (ks > 1 && (int64_t)n * s.heads * ks * (s.hd + 2) > work_floats) ks--;
+    if (ks > 1) {
+      a.ksplit = ks;
+      a.partials = work;
+      a.region = (int64_t)ks * (s.hd + 2);
+    }
+  }
   const bool br = sfx != nullptr;
   const int z = segs ? nseg : 1;
   switch (s.hd) {

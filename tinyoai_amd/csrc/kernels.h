@@ -151,10 +151,15 @@ bool flash_prefill_supported(int hd);
 // runs of branch rows in one launch: segs[3k..3k+2] = (first row, rows,
 // slot of its first position) on the device, n = the longest run, q, pos0
 // (row pairs) and out indexed by row.
+// Without sfx, when the query tiles leave CUs idle and the last query's
+// position (last_pos, known to the host) reaches 1024, each tile's keys are
+// split over several blocks whose records (in `work`, at most work_floats)
+// a second kernel combines in order (null work: no splits).
 hipError_t launch_flash_prefill(const StableDims &s, const KVDev &kv, const float *q, const int *pos0, int n,
                                 float *out, hipStream_t st, uint16_t *oh = nullptr, uint16_t *ol = nullptr,
                                 const KVDev *sfx = nullptr, int prefix = 0, int sfx_slot0 = 0, int64_t ld_o = 0,
-                                const int *segs = nullptr, int nseg = 0);
+                                const int *segs = nullptr, int nseg = 0, float *work = nullptr,
+                                int64_t work_floats = 0, int last_pos = 0);
 int attention_steps(int max_pos, int heads);
 // The decode step's attention shape at position pos: attention_steps up to
 // about 1800 positions (fused into the decode_in launch), then wider
