@@ -148,3 +148,36 @@ def test_branches_3b_shapes(hip, oracle, mlp, attn, kv_bits):
     suffixes = [list(rng.integers(0, 65536, n)) for n in (1, 70, 13, 64, 65)]
     oracle.set_threads(8)
     branch_case(hip, oracle, config, tensors, prompt, 70, suffixes, 3, kv_bits, True)
+
+
+@pytest.mark.parametrize("mlp,attn,kv_bits", [(W.Q4_K, W.Q6_K, 16), (W.Q8_0, W.Q8_0, 32)])
+def test_branch_steps_from_graphs_match_direct_launches(hip, mlp, attn, kv_bits):
+    """Lockstep branch steps replay a captured graph per attention shape;
+    a second session on the same weights and prefix runs with the profiler
+    on (every kernel launched directly). Ragged suffixes, then 40 lockstep
+    steps (the suffix attention changes shape on the way, so several graphs
+    are captured and each is replayed many times, with the host's own work
+    and a synchronisation between replays): every step's logits are
+    bit-identical, and the caches' growth past 64 positions (which drops
+    the graphs) happens within the run."""
+    config = W.validate_stablelm_config(dict(W.STABLELM_3B, num_hidden_layers=2, max_position_embeddings=512))
+    tensors = W.synthetic_stablelm(config, mlp, seed=71, attn_dtype=attn, head_dtype=attn)
+    rng = np.random.default_rng(73)
+    prompt = list(rng.integers(0, 65536, 96))
+    suffixes = [list(rng.integers(0, 65536, n)) for n in (1, 30, 7, 24, 12, 3)]
+    runs = []
+    for direct in (False, True):
+        f = hip.StableLMForwarder(config, tensors)
+        f.set_kv_bits(kv_bits)
+        f.forward(0, prompt, want_logits=False)
+        if direct:
+            f.profile(True)
+        br = f.new_branches(96, len(suffixes))
+        rows = [br.append(suffixes)]
+        for s in range(40):
+            rows.append(br.forward(np.argmax(rows[-1], axis=1).astype(np.int32)))
+        br.close()
+        f.close()
+        runs.append(rows)
+    for s, (a, b) in enumerate(zip(*runs)):
+        assert np.array_equal(a, b), s

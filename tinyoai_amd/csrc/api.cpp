@@ -1015,6 +1015,11 @@ int StableModel::busy_with_branches() const {
                            : TINYOAI_OK;
 }
 
+void Branches::drop_graphs() {
+  for (auto &g : graphs) hipGraphExecDestroy(g.second);
+  graphs.clear();
+}
+
 void Branches::free_kv() {
   for (auto &l : kv) {
     if (l.k) hipFree(l.k);
@@ -1045,6 +1050,7 @@ int StableModel::score_rows(int n) {
 
 Branches::~Branches() {
   if (m && m->stream) hipStreamSynchronize(m->stream);
+  drop_graphs();
   free_kv();
   if (partials) hipFree(partials);
   if (counters) hipFree(counters);
@@ -1089,6 +1095,7 @@ int Branches::grow(int need) {
       }
   }
   hipError_t e = hipStreamSynchronize(m->stream);
+  drop_graphs();  // they name the old caches
   free_kv();
   kv = grown;
   scap = want;
@@ -1100,6 +1107,7 @@ int Branches::ensure_partials(int nq, int splits) {
   const size_t words = (size_t)nq * m->dims.heads;
   if (need > partial_floats) {
     hipStreamSynchronize(m->stream);
+    drop_graphs();
     if (partials) hipFree(partials);
     partials = nullptr;
     partial_floats = 0;
@@ -1109,6 +1117,7 @@ int Branches::ensure_partials(int nq, int splits) {
   }
   if (words > counter_words) {
     hipStreamSynchronize(m->stream);
+    drop_graphs();
     if (counters) hipFree(counters);
     counters = nullptr;
     counter_words = 0;
@@ -1151,6 +1160,12 @@ int StableModel::branch_rows(Branches &b, const int32_t *ids, const int32_t *br,
     per = (int)std::min<size_t>(per, std::max<size_t>(1, ((size_t)64 << 20) / region));
   }
   const int hq = dims.heads * dims.hd;
+  // Final LayerNorm of every branch's newest row, then the classifier.
+  auto enqueue_head = [&]() -> int {
+    TRY_HIP(launch_layer_norm_rows(b.last, norm_w, norm_b, dims.eps, b.count, d, H, stream), "final norm");
+    return project(head.desc, H, d, b.count, Y, V, nullptr, true);
+  };
+  const bool lockstep = use_graphs && !prof.on && n == b.count && run == 1 && n <= per;
   for (int r0 = 0; r0 < n; r0 += per) {
     const int nc = std::min(per, n - r0);
     const int32_t *cid = ids + r0;
@@ -1191,72 +1206,117 @@ int StableModel::branch_rows(Branches &b, const int32_t *ids, const int32_t *br,
       max_splits = branch_attention_records(dims, pfx, max_pos, nc);
       if (int rc = b.ensure_partials(nc, max_splits)) return rc;
     }
-    TRY_HIP(launch_embed(embed.desc, d_ids, nc, X, stream), "embed");
-    for (int l = 0; l < cfg.num_hidden_layers; l++) {
-      const LayerDev &w = layers[l];
-      const bool split_in = w.win2.rows > 0, split_out = w.wout2.rows > 0;
-      const int64_t vpc = values_per_chunk(w.wout.fmt), down0 = (d + vpc - 1) / vpc * vpc;
-      const MatDesc wo = split_out ? w.wout : column_view(w.wout, 0, d);
-      const MatDesc wd = split_out ? w.wout2 : column_view(w.wout, down0, I);
-      int rc;
-      TRY_HIP(launch_layer_norm_rows(X, w.ln_w, w.ln_b, dims.eps, nc, d, H, stream), "layer_norm");
-      // Y holds chunk * win_rows floats: with few rows, K-split partials of
-      // the in-products fit within it (half each when the two groups are
-      // separate matrices); P and D hold kPrefillSplits * chunk * d.
-      const size_t ycap = (size_t)chunk * win_rows;
-      const bool few = nc <= 32;
-      const int pd_splits = (int)std::min<int64_t>(256, (int64_t)kPrefillSplits * chunk / nc);
-      if (split_in) {
-        StableDims da = dims, dm = dims;
-        da.inter = 0;
-        dm.win_q = dm.win_kv = 0;
-        const int ra = w.win.rows, rm = w.win2.rows;
-        float *Ya = Y, *Ym = few ? Y + ycap / 2 / 4 * 4 : Y + (size_t)nc * ra;
-        int sa = 1, sm = 1;
-        bool staged = false;  // H staged by the first product serves the second
-        if ((rc = project(w.win, H, d, nc, Ya, ra, few ? &sa : nullptr, true, (int)(ycap / 2 / ((size_t)nc * ra)),
-                          &staged)) ||
-            (rc = project(w.win2, H, d, nc, Ym, rm, few ? &sm : nullptr, true, (int)(ycap / 2 / ((size_t)nc * rm)),
-                          &staged)))
-          return rc;
-        TRY_HIP(launch_in_epilogue(da, b.kv[l], Ya, ra, rope, nullptr, nc, Q, M, stream, nullptr, nullptr, d_rows,
-                                   sa),
-                "in_epilogue");
-        TRY_HIP(launch_in_epilogue(dm, b.kv[l], Ym, rm, rope, nullptr, nc, Q, M, stream, nullptr, nullptr, d_rows,
-                                   sm),
-                "in_epilogue");
-      } else {
-        int sy = 1;
-        if ((rc = project(w.win, H, d, nc, Y, win_rows, few ? &sy : nullptr, true,
-                          (int)(ycap / ((size_t)nc * win_rows)))))
-          return rc;
-        TRY_HIP(launch_in_epilogue(dims, b.kv[l], Y, win_rows, rope, nullptr, nc, Q, M, stream, nullptr, nullptr,
-                                   d_rows, sy),
-                "in_epilogue");
+    // The chunk's kernels: embedding, the layers, each branch's newest row.
+    auto enqueue_chunk = [&]() -> int {
+      TRY_HIP(launch_embed(embed.desc, d_ids, nc, X, stream), "embed");
+      for (int l = 0; l < cfg.num_hidden_layers; l++) {
+        const LayerDev &w = layers[l];
+        const bool split_in = w.win2.rows > 0, split_out = w.wout2.rows > 0;
+        const int64_t vpc = values_per_chunk(w.wout.fmt), down0 = (d + vpc - 1) / vpc * vpc;
+        const MatDesc wo = split_out ? w.wout : column_view(w.wout, 0, d);
+        const MatDesc wd = split_out ? w.wout2 : column_view(w.wout, down0, I);
+        int rc;
+        // Y holds chunk * win_rows floats: with few rows, K-split partials of
+        // the in-products fit within it (half each when the two groups are
+        // separate matrices); P and D hold kPrefillSplits * chunk * d.
+        const size_t ycap = (size_t)chunk * win_rows;
+        const bool few = nc <= 32;
+        // When the in-products run on the few-row kernel, the LayerNorm is
+        // formed in their shared staging of X (no LayerNorm launch); the
+        // conditions are those under which project() takes that kernel.
+        const bool norm_in_stage = few && dims.norm == 0 && w.ln_b && d % 256 == 0 && kq_rows_supported(w.win, nc) &&
+                                   (!split_in || kq_rows_supported(w.win2, nc)) &&
+                                   kq_rows_stage_bytes(d, nc) <= (size_t)chunk * std::max(dims.d, dims.inter) * 2;
+        bool staged = false;  // XH holds this layer's staged LayerNorm output
+        if (norm_in_stage) {
+          TRY_HIP(launch_kq_stage_norm(X, d, nc, d, w.ln_w, w.ln_b, dims.eps, XH, stream), "layer_norm + staging");
+          staged = true;
+        } else {
+          TRY_HIP(launch_layer_norm_rows(X, w.ln_w, w.ln_b, dims.eps, nc, d, H, stream), "layer_norm");
+        }
+        const int pd_splits = (int)std::min<int64_t>(256, (int64_t)kPrefillSplits * chunk / nc);
+        if (split_in) {
+          StableDims da = dims, dm = dims;
+          da.inter = 0;
+          dm.win_q = dm.win_kv = 0;
+          const int ra = w.win.rows, rm = w.win2.rows;
+          float *Ya = Y, *Ym = few ? Y + ycap / 2 / 4 * 4 : Y + (size_t)nc * ra;
+          int sa = 1, sm = 1;
+          // H staged by the first product (or with the LayerNorm) serves the second
+          if ((rc = project(w.win, H, d, nc, Ya, ra, few ? &sa : nullptr, true, (int)(ycap / 2 / ((size_t)nc * ra)),
+                            &staged)) ||
+              (rc = project(w.win2, H, d, nc, Ym, rm, few ? &sm : nullptr, true, (int)(ycap / 2 / ((size_t)nc * rm)),
+                            &staged)))
+            return rc;
+          TRY_HIP(launch_in_epilogue(da, b.kv[l], Ya, ra, rope, nullptr, nc, Q, M, stream, nullptr, nullptr, d_rows,
+                                     sa),
+                  "in_epilogue");
+          TRY_HIP(launch_in_epilogue(dm, b.kv[l], Ym, rm, rope, nullptr, nc, Q, M, stream, nullptr, nullptr, d_rows,
+                                     sm),
+                  "in_epilogue");
+        } else {
+          int sy = 1;
+          if ((rc = project(w.win, H, d, nc, Y, win_rows, few ? &sy : nullptr, true,
+                            (int)(ycap / ((size_t)nc * win_rows)), &staged)))
+            return rc;
+          TRY_HIP(launch_in_epilogue(dims, b.kv[l], Y, win_rows, rope, nullptr, nc, Q, M, stream, nullptr, nullptr,
+                                     d_rows, sy),
+                  "in_epilogue");
+        }
+        int sp = 1, sd = 1;
+        if ((rc = project(wd, M, I, nc, D, d, &sd, true, pd_splits))) return rc;
+        if (use_flash) {
+          TRY_HIP(launch_flash_prefill(dims, kv[l], Q, d_rows, longest, A, stream, nullptr, nullptr, &b.kv[l], pfx, 0, 0,
+                                       b.segs, (int)seg.size() - 1),
+                  "branch attention");
+        } else {
+          TRY_HIP(launch_branch_attention(dims, kv[l], b.kv[l], pfx, Q, d_rows, nc, max_pos, b.partials, b.counters,
+                                          A, max_splits, stream),
+                  "branch attention");
+        }
+        if ((rc = project(wo, A, d, nc, P, d, &sp, true, pd_splits))) return rc;
+        TRY_HIP(launch_residual(X, P, sp, D, sd, (int64_t)nc * d, stream), "residual");
       }
-      int sp = 1, sd = 1;
-      if ((rc = project(wd, M, I, nc, D, d, &sd, true, pd_splits))) return rc;
-      if (use_flash) {
-        TRY_HIP(launch_flash_prefill(dims, kv[l], Q, d_rows, longest, A, stream, nullptr, nullptr, &b.kv[l], pfx, 0, 0,
-                                     b.segs, (int)seg.size() - 1),
-                "branch attention");
-      } else {
-        TRY_HIP(launch_branch_attention(dims, kv[l], b.kv[l], pfx, Q, d_rows, nc, max_pos, b.partials, b.counters,
-                                        A, max_splits, stream),
-                "branch attention");
+      // each branch's newest row of this chunk
+      for (size_t k = 0; k + 1 < seg.size(); k++) {
+        const int last_row = seg[k + 1] - 1, j = br[r0 + last_row];
+        TRY_HIP(launch_copy_row(X + (size_t)last_row * d, b.last + (size_t)j * d, d, stream), "branch row");
       }
-      if ((rc = project(wo, A, d, nc, P, d, &sp, true, pd_splits))) return rc;
-      TRY_HIP(launch_residual(X, P, sp, D, sd, (int64_t)nc * d, stream), "residual");
-    }
-    // each branch's newest row of this chunk
-    for (size_t k = 0; k + 1 < seg.size(); k++) {
-      const int last_row = seg[k + 1] - 1, j = br[r0 + last_row];
-      TRY_HIP(launch_copy_row(X + (size_t)last_row * d, b.last + (size_t)j * d, d, stream), "branch row");
+      return TINYOAI_OK;
+    };
+    if (lockstep) {
+      // One row per branch in one chunk: the step's kernels, with the final
+      // LayerNorm and the classifier, replay from a graph keyed by the
+      // attention's launch shape (the model's buffers, the branch caches
+      // and their scratch stay in place while the graph lives; the caches'
+      // growth and larger scratch drop the graphs).
+      const int64_t key = ((int64_t)branch_attention_shape(dims, pfx, max_pos, nc) << 24) ^
+                          ((int64_t)max_splits << 8) ^ (int64_t)launch_gen;
+      auto it = b.graphs.find(key);
+      if (it == b.graphs.end()) {
+        hipGraph_t g = nullptr;
+        TRY_HIP(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal), "graph capture");
+        int rc = enqueue_chunk();
+        if (!rc) rc = enqueue_head();
+        hipError_t e = hipStreamEndCapture(stream, &g);
+        if (rc) {
+          if (g) hipGraphDestroy(g);
+          return rc;
+        }
+        if (e != hipSuccess) return hip_fail(e, "graph capture");
+        hipGraphExec_t exec = nullptr;
+        e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+        hipGraphDestroy(g);
+        if (e != hipSuccess) return hip_fail(e, "graph instantiate");
+        it = b.graphs.emplace(key, exec).first;
+      }
+      TRY_HIP(hipGraphLaunch(it->second, stream), "graph launch");
+    } else if (int rc = enqueue_chunk()) {
+      return rc;
     }
   }
-  // Final LayerNorm of every branch's newest row, then the classifier.
-  TRY_HIP(launch_layer_norm_rows(b.last, norm_w, norm_b, dims.eps, b.count, d, H, stream), "final norm");
-  if (int rc = project(head.desc, H, d, b.count, Y, V, nullptr, true)) return rc;
+  if (!lockstep)
+    if (int rc = enqueue_head()) return rc;
   TRY_HIP(hipMemcpyAsync(logits, Y, (size_t)b.count * V * 4, hipMemcpyDeviceToHost, stream), "logits");
   TRY_HIP(hipStreamSynchronize(stream), "branch step");
   for (int j = 0; j < b.count; j++) b.len[j] += add[j];
@@ -1717,6 +1777,7 @@ int tinyoai_stablelm_trace_read_stages(tinyoai_model *m, float *attention, float
 int tinyoai_stablelm_set_launch(tinyoai_model *m, int32_t stage, int32_t grid, int32_t threads) {
   if (!m || !m->stable) return fail(TINYOAI_EINVAL, "not a StableLM handle");
   StableModel &s = *m->stable;
+  s.launch_gen++;  // an open branch session's step graphs are not replayed after this
   if (stage == 7) {  // BF16-weight prefill products on wide tiles (1, the default) or 128 x 256 tiles (0)
     s.use_wide = grid != 0;
     return TINYOAI_OK;

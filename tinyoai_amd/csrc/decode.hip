@@ -212,6 +212,12 @@ int branch_attention_records(const StableDims &s, int prefix, int max_pos, int n
   return attention_splits(max_pos, std::min(attention_steps(max_pos, s.heads), 4));
 }
 
+int branch_attention_shape(const StableDims &s, int prefix, int max_pos, int nq) {
+  int steps = std::min(attention_steps(max_pos, s.heads), 4), splits = attention_splits(max_pos, steps);
+  if (branch_shared(s, prefix, nq)) suffix_splits(s, prefix, max_pos, steps, splits);
+  return steps * 4096 + splits;
+}
+
 hipError_t launch_branch_attention(const StableDims &s, const KVDev &kv, const KVDev &sfx, int prefix,
                                    const float *q, const int *rows, int nq, int max_pos, float *partials,
                                    unsigned *counters, float *out, int max_splits, hipStream_t st) {

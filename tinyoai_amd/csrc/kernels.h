@@ -132,6 +132,9 @@ hipError_t launch_branch_attention(const StableDims &s, const KVDev &kv, const K
                                    const float *q, const int *rows, int nq, int max_pos, float *partials,
                                    unsigned *counters, float *out, int max_splits, hipStream_t st);
 int branch_attention_records(const StableDims &s, int prefix, int max_pos, int nq);
+// The launch shape launch_branch_attention takes at these arguments (its
+// grid and positions per block), as one integer.
+int branch_attention_shape(const StableDims &s, int prefix, int max_pos, int nq);
 // The shared-prefix pass on the matrix cores: nq <= 128 queries q
 // [nq][heads*hd], every one past `prefix`, against cache positions
 // [0, prefix) of kv, in blocks of 256 positions; block x writes the record
@@ -225,6 +228,10 @@ size_t kq_rows_stage_bytes(int K, int M);
 int kq_rows_splits(const MatDesc &w, int max_splits);
 hipError_t launch_kq_rows(const MatDesc &w, const float *x, int ldx, int M, float *y, int ldy, int ks, void *stage,
                           hipStream_t st, bool staged = false, int64_t split_stride = 0);
+// Stages M <= 32 rows of x (K % 256 == 0) for launch_kq_rows(..., staged)
+// with the LayerNorm (weights lw, bias lb, eps) applied on the way.
+hipError_t launch_kq_stage_norm(const float *x, int ldx, int M, int K, const float *lw, const float *lb, double eps,
+                                void *stage, hipStream_t st);
 // The fused in-projection epilogue of a matrix-core win product for M
 // tokens at positions *pos0 + j: RoPE'd q [M][heads*hd], K/V into the
 // cache, and the SiLU-gate outputs as bf16 planes mh, ml [M][inter] (and

@@ -70,18 +70,78 @@ struct KqArgs {
 // (i / 8) % R and chunk i / (8 R); a chunk's 8 groups are 8 consecutive
 // lanes, which form the sums by fixed-order shuffles. Slice blockIdx.y
 // stages rows [R y, R y + R) at y * nch * chunk_bytes.
+//
+// With lw, the rows are LayerNorm'd on the way (stablelm.go:288-305, the
+// arithmetic of norm_store in device.h: float64 moments about the row's
+// first value in one pass, then t = x - float(mean), t *= float(1 /
+// sqrt(var + eps)), t *= w, t += b, each rounded to float32). Every block
+// forms the moments of its slice's rows itself (256 / R threads per row
+// over contiguous spans of K, then a fixed-order shuffle tree), so no
+// separate LayerNorm launch runs before the staging.
 template <int MT>
-__global__ __launch_bounds__(256) void kq_stage_kernel(const float *x, int ldx, int M, int K, uint8_t *stage) {
-  constexpr int R = 16 * MT;
+__global__ __launch_bounds__(256) void kq_stage_kernel(const float *x, int ldx, int M, int K, uint8_t *stage,
+                                                       const float *lw, const float *lb, double eps) {
+  constexpr int R = 16 * MT, TPR = 256 / R;  // threads per row for the moments
   const int nch = K / 32;
   x += (int64_t)blockIdx.y * R * ldx;
   M -= blockIdx.y * R;
   stage += (size_t)blockIdx.y * nch * chunk_bytes<MT>();
+  __shared__ float s_mean[R], s_inv[R];
+  if (lw) {  // block-uniform
+    const int r = threadIdx.x / TPR, part = threadIdx.x % TPR;
+    const float *xr = x + (int64_t)min(r, M - 1) * ldx;
+    const double shift = (double)xr[0];
+    double s1 = 0.0, s2 = 0.0;
+    const int span = K / TPR;  // a multiple of 4 (K % 256 == 0)
+    constexpr int U = 20;      // float4 loads in flight (a 2560-value row: two rounds)
+    const float *xs = xr + part * span;
+    for (int k0 = 0; k0 < span; k0 += 4 * U) {
+      float4 t[U];
+#pragma unroll
+      for (int u = 0; u < U; u++)
+        t[u] = k0 + 4 * u < span ? *reinterpret_cast<const float4 *>(xs + k0 + 4 * u) : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+      for (int u = 0; u < U; u++) {
+        if (k0 + 4 * u >= span) continue;
+        const float e[4] = {t[u].x, t[u].y, t[u].z, t[u].w};
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          const double dv = (double)e[q] - shift;
+          s1 += dv;
+          s2 += dv * dv;
+        }
+      }
+    }
+#pragma unroll
+    for (int o = 1; o < TPR; o <<= 1) {  // the row's threads are TPR consecutive lanes
+      s1 += __shfl_xor(s1, o, 64);
+      s2 += __shfl_xor(s2, o, 64);
+    }
+    if (part == 0) {
+      const double mean = shift + s1 / (double)K;
+      const double var = fmax((s2 - s1 * s1 / (double)K) / (double)K, 0.0);
+      s_mean[r] = (float)mean;
+      s_inv[r] = (float)(1.0 / sqrt(var + eps));
+    }
+    __syncthreads();
+  }
   const int i = blockIdx.x * 256 + threadIdx.x;
   if (i >= R * nch * 8) return;  // whole groups of 8: R * nch * 8 and the block are multiples of 8
   const int gq = i & 7, row = (i >> 3) % R, c = (i >> 3) / R;
   float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-  if (row < M) v = *reinterpret_cast<const float4 *>(x + (int64_t)row * ldx + c * 32 + 4 * gq);
+  if (row < M) {
+    const int k = c * 32 + 4 * gq;
+    v = *reinterpret_cast<const float4 *>(x + (int64_t)row * ldx + k);
+    if (lw) {
+      const float fm = s_mean[row], inv = s_inv[row];
+      const float4 w4 = *reinterpret_cast<const float4 *>(lw + k), b4 = *reinterpret_cast<const float4 *>(lb + k);
+      auto affine = [&](float xv, float wv, float bv) {
+        return __fadd_rn(__fmul_rn(__fmul_rn(__fsub_rn(xv, fm), inv), wv), bv);
+      };
+      v = make_float4(affine(v.x, w4.x, b4.x), affine(v.y, w4.y, b4.y), affine(v.z, w4.z, b4.z),
+                      affine(v.w, w4.w, b4.w));
+    }
+  }
   const float vv[4] = {v.x, v.y, v.z, v.w};
   uint32_t pl[kPlanes][2];
   float s = 0.f;
@@ -465,10 +525,11 @@ hipError_t kq_dispatch(const KqArgs &g, hipStream_t st) {
 }
 
 template <int MT>
-hipError_t kq_stage(const float *x, int ldx, int M, int K, uint8_t *stage, hipStream_t st) {
+hipError_t kq_stage(const float *x, int ldx, int M, int K, uint8_t *stage, hipStream_t st, const float *lw = nullptr,
+                    const float *lb = nullptr, double eps = 0.0) {
   const int items = 16 * MT * (K / 32) * 8;
   hipLaunchKernelGGL((kq_stage_kernel<MT>), dim3((items + 255) / 256, (M + 16 * MT - 1) / (16 * MT)), dim3(256), 0,
-                     st, x, ldx, M, K, stage);
+                     st, x, ldx, M, K, stage, lw, lb, eps);
   return hipGetLastError();
 }
 
@@ -488,6 +549,16 @@ int kq_rows_splits(const MatDesc &w, int max_splits) {
   // about 320 blocks (measured best at M = 16 for 2560-13824 rows: more
   // splits only add partial sums), at least one batch per split
   return std::max(1, std::min({(320 + NB - 1) / NB, batches, max_splits}));
+}
+
+hipError_t launch_kq_stage_norm(const float *x, int ldx, int M, int K, const float *lw, const float *lb, double eps,
+                                void *stage, hipStream_t st) {
+  if (M < 1 || M > 32 || K < 256 || K % 256 || ldx < K || (ldx & 3) || (reinterpret_cast<uintptr_t>(x) & 15) || !lw ||
+      !lb || (reinterpret_cast<uintptr_t>(lw) & 15) || (reinterpret_cast<uintptr_t>(lb) & 15) || !stage ||
+      (reinterpret_cast<uintptr_t>(stage) & 15))
+    return hipErrorInvalidValue;
+  uint8_t *sb = static_cast<uint8_t *>(stage);
+  return M <= 16 ? kq_stage<1>(x, ldx, M, K, sb, st, lw, lb, eps) : kq_stage<2>(x, ldx, M, K, sb, st, lw, lb, eps);
 }
 
 hipError_t launch_kq_rows(const MatDesc &w, const float *x, int ldx, int M, float *y, int ldy, int ks, void *stage,

@@ -145,6 +145,7 @@ struct StableModel {
   // Decode graphs by attention launch shape (valid for the current KV).
   std::map<int64_t, hipGraphExec_t> graphs;
   bool use_graphs = true;
+  int launch_gen = 0;  // changed by every set_launch call (part of the branch step graphs' keys)
 
   ~StableModel();
   int init(const tinyoai_stablelm_config &c, const tinyoai_tensor *tensors, int n);
@@ -235,8 +236,10 @@ struct Branches {
   float *last = nullptr;         // [count][hidden]: each branch's newest residual row
   int *segs = nullptr;           // [chunk][3]: the runs of an append's chunk (first row, rows, first slot)
   std::vector<int> segs_host;    // their host copy (kept until the call has synchronised)
+  std::map<int64_t, hipGraphExec_t> graphs;  // lockstep steps by attention shape
   ~Branches();
   void free_kv();
+  void drop_graphs();
   // Suffix capacity for `need` positions per branch (existing entries kept).
   int grow(int need);
   // Attention scratch for nq queries with up to `splits` splits.

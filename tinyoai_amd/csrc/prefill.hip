@@ -145,11 +145,25 @@ __global__ void in_epilogue_kernel(StableDims s, KVDev kv, const float *y, int l
   }
 }
 
+// sum = ((v[0] + v[1]) + v[2]) + ... over s partials n apart, eight
+// loads in flight before their adds (the same order as one at a time).
+__device__ __forceinline__ float sum_partials(const float *v, int s, int64_t n, int64_t i) {
+  constexpr int B = 8;
+  float acc = v[i];
+  for (int s0 = 1; s0 < s; s0 += B) {
+    float t[B];
+#pragma unroll
+    for (int k = 0; k < B; k++) t[k] = s0 + k < s ? v[(s0 + k) * n + i] : 0.f;
+#pragma unroll
+    for (int k = 0; k < B; k++)
+      if (s0 + k < s) acc = __fadd_rn(acc, t[k]);
+  }
+  return acc;
+}
+
 __global__ void residual_kernel(float *x, const float *p, int sp, const float *d, int sd, int64_t n) {
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
-    float o = p[i], m = d[i];
-    for (int s = 1; s < sp; s++) o = __fadd_rn(o, p[s * n + i]);
-    for (int s = 1; s < sd; s++) m = __fadd_rn(m, d[s * n + i]);
+    const float o = sum_partials(p, sp, n, i), m = sum_partials(d, sd, n, i);
     x[i] = __fadd_rn(__fadd_rn(x[i], o), m);
   }
 }
@@ -157,9 +171,7 @@ __global__ void residual_kernel(float *x, const float *p, int sp, const float *d
 // out[i] = ((p[0][i] + p[1][i]) + p[2][i]) + ... over sp partials n apart.
 __global__ void sum_splits_kernel(float *out, const float *p, int sp, int64_t n) {
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
-    float v = p[i];
-    for (int s = 1; s < sp; s++) v = __fadd_rn(v, p[s * n + i]);
-    out[i] = v;
+    out[i] = sum_partials(p, sp, n, i);
   }
 }
 
