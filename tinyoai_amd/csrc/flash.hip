@@ -3,9 +3,11 @@
 // queries at positions pos0 .. pos0 + n - 1 against cache positions
 // 0 .. pos0 + n - 1, online softmax in fp32.
 //
-// fp32 operands are carried as fp16 hi + lo (x = hi + lo to ~22 bits):
-// queries and softmax weights always, K and V when the cache is fp32. With
-// an fp16 cache K and V are exact as stored. Products accumulate in fp32.
+// With an fp32 cache the fp32 operands are carried as fp16 hi + lo (x =
+// hi + lo to ~22 bits): queries, softmax weights, K and V. With an fp16
+// cache K and V are exact as stored, and the queries and weights are
+// rounded to fp16 (to nearest), the precision the cache keeps K and V in:
+// one product per operand pair instead of two. Products accumulate in fp32.
 #include "kernels.h"
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
@@ -145,7 +147,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
 #pragma unroll
       for (int i = 0; i < 8; i++) {
         _Float16 hi, lo;
-        split_half(qp[k * 16 + g * 8 + i] * qscale, hi, lo);
+        if constexpr (HALF) {
+          hi = (_Float16)(qp[k * 16 + g * 8 + i] * qscale);
+          lo = (_Float16)0.f;
+        } else {
+          split_half(qp[k * 16 + g * 8 + i] * qscale, hi, lo);
+        }
         qh[k][i] = hi;
         ql[k][i] = lo;
       }
@@ -300,7 +307,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
         const int r = (kh * 32 + col) * KP + k * 16 + g * 8;
         const f16x8 ka = *reinterpret_cast<const f16x8 *>(&ks[0][r]);
         sc[kh] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qh[k], sc[kh], 0, 0, 0);
-        sc[kh] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, ql[k], sc[kh], 0, 0, 0);
+        if constexpr (!HALF) sc[kh] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, ql[k], sc[kh], 0, 0, 0);
         if constexpr (!HALF) {
           const f16x8 kl = *reinterpret_cast<const f16x8 *>(&ks[NPL - 1][r]);
           sc[kh] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kl, qh[k], sc[kh], 0, 0, 0);
@@ -339,7 +346,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
       }
     }
     // Weights 2^(score - ref) in [0, 2^8] (masked: 2^-inf = 0) as fp16 hi + lo
-    // (both truncated: the residual p - hi is exact in fp32).
+    // (both truncated: the residual p - hi is exact in fp32); with an fp16
+    // cache one fp16 part, rounded to nearest (the ones row of V^T then
+    // sums the same rounded weights).
     f16x8 ph[4], pl[4];  // A operands of the four 16-key steps
     float psum = 0.f;
 #pragma unroll
@@ -347,13 +356,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
 #pragma unroll
       for (int v = 0; v < 16; v += 2) {
         const float p0v = __builtin_amdgcn_exp2f(sc[kh][v]), p1v = __builtin_amdgcn_exp2f(sc[kh][v + 1]);
-        if constexpr (!ONES) psum += p0v + p1v;
-        const auto hi = __builtin_amdgcn_cvt_pkrtz(p0v, p1v);
-        const auto lo = __builtin_amdgcn_cvt_pkrtz(p0v - (float)hi[0], p1v - (float)hi[1]);
-        ph[kh * 2 + (v >> 3)][v & 7] = hi[0];
-        ph[kh * 2 + (v >> 3)][(v & 7) + 1] = hi[1];
-        pl[kh * 2 + (v >> 3)][v & 7] = lo[0];
-        pl[kh * 2 + (v >> 3)][(v & 7) + 1] = lo[1];
+        if constexpr (HALF) {
+          const _Float16 h0 = (_Float16)p0v, h1 = (_Float16)p1v;
+          if constexpr (!ONES) psum += (float)h0 + (float)h1;
+          ph[kh * 2 + (v >> 3)][v & 7] = h0;
+          ph[kh * 2 + (v >> 3)][(v & 7) + 1] = h1;
+        } else {
+          if constexpr (!ONES) psum += p0v + p1v;
+          const auto hi = __builtin_amdgcn_cvt_pkrtz(p0v, p1v);
+          const auto lo = __builtin_amdgcn_cvt_pkrtz(p0v - (float)hi[0], p1v - (float)hi[1]);
+          ph[kh * 2 + (v >> 3)][v & 7] = hi[0];
+          ph[kh * 2 + (v >> 3)][(v & 7) + 1] = hi[1];
+          pl[kh * 2 + (v >> 3)][v & 7] = lo[0];
+          pl[kh * 2 + (v >> 3)][(v & 7) + 1] = lo[1];
+        }
       }
     if constexpr (!ONES) l_run += psum + __shfl_xor(psum, 32, 64);
     // ---- O += P V
@@ -366,7 +382,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
         const uint2 a4 = *reinterpret_cast<const uint2 *>(v0), b4 = *reinterpret_cast<const uint2 *>(v0 + 8);
         const f16x8 vb = __builtin_bit_cast(f16x8, make_uint4(a4.x, a4.y, b4.x, b4.y));
         o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ph[kk], vb, o[t], 0, 0, 0);
-        o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pl[kk], vb, o[t], 0, 0, 0);
+        if constexpr (!HALF) o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pl[kk], vb, o[t], 0, 0, 0);
         if constexpr (!HALF) {
           const _Float16 *v1 = &vt[NPL - 1][(t * 32 + col) * VP + base];
           const uint2 c4 = *reinterpret_cast<const uint2 *>(v1), d4 = *reinterpret_cast<const uint2 *>(v1 + 8);
