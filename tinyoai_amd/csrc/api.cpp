@@ -886,11 +886,37 @@ int StableModel::prefill_chunk(const int32_t *ids, int n, int start, bool want_l
   const int *d_pos0 = params, *d_ids = params + 16;
   const int d = dims.d, I = dims.inter;
   STAGE(ST_EMBED, launch_embed(embed.desc, d_ids, n, X, stream), "embed");
+  // Where layer l's LayerNorm output goes: bf16 planes XH, XL for a
+  // matrix-core in-projection, else fp32 H.
+  auto ln_out = [&](int l, float *&out, uint16_t *&oh, uint16_t *&ol) {
+    const LayerDev &w = layers[l];
+    const bool planes = wide_layer(l) || (!w.win2.rows && gemm_mfma_supported(w.win));
+    out = planes ? nullptr : H;
+    oh = planes ? XH : nullptr;
+    ol = planes ? XL : nullptr;
+  };
+  // The residual of layer l and the LayerNorm of layer l + 1 in one launch
+  // (LayerNorm models); normed: layer l's LayerNorm is already formed.
+  auto residual = [&](int l, int sp, int sd) -> int {
+    if (l + 1 < cfg.num_hidden_layers && dims.norm == 0) {
+      float *out;
+      uint16_t *oh, *ol;
+      ln_out(l + 1, out, oh, ol);
+      const LayerDev &nw = layers[l + 1];
+      STAGE(ST_PREFILL_ELEMENTWISE,
+            launch_residual_norm_rows(X, P, sp, D, sd, n, d, nw.ln_w, nw.ln_b, dims.eps, out, oh, ol, stream),
+            "residual + layer_norm");
+      return TINYOAI_OK;
+    }
+    STAGE(ST_PREFILL_ELEMENTWISE, launch_residual(X, P, sp, D, sd, (int64_t)n * d, stream), "residual");
+    return TINYOAI_OK;
+  };
   for (int l = 0; l < cfg.num_hidden_layers; l++) {
     const LayerDev &w = layers[l];
     const bool split_in = w.win2.rows > 0, split_out = w.wout2.rows > 0;
     const int64_t vpc = values_per_chunk(w.wout.fmt), down0 = (d + vpc - 1) / vpc * vpc;
     const MatDesc wo = split_out ? w.wout : column_view(w.wout, 0, d);
+    const bool normed = l > 0 && dims.norm == 0;  // formed with the previous layer's residual
     const MatDesc wd = split_out ? w.wout2 : column_view(w.wout, down0, I);
     int rc;
     // Inputs of matrix-core projections leave their producers as bf16
@@ -906,8 +932,9 @@ int StableModel::prefill_chunk(const int32_t *ids, int n, int start, bool want_l
       // down products as one launch of K splits; the parallel residual sums
       // them in order.
       const uint16_t *lo = lo_plane(w.win);
-      STAGE(ST_PREFILL_NORM, launch_layer_norm_rows(X, w.ln_w, w.ln_b, dims.eps, n, d, nullptr, stream, XH, XL),
-            "layer_norm");
+      if (!normed)
+        STAGE(ST_PREFILL_NORM, launch_layer_norm_rows(X, w.ln_w, w.ln_b, dims.eps, n, d, nullptr, stream, XH, XL),
+              "layer_norm");
       int mf, nf;
       wide_shape(n, w.win.rows, &mf, &nf);
       if (wide_epi) {
@@ -930,12 +957,13 @@ int StableModel::prefill_chunk(const int32_t *ids, int n, int start, bool want_l
       const WideGemm prods[2] = {{wd, MH, lo ? ML : nullptr, I, D, d, sd, (int64_t)n * d},
                                  {wo, XH, lo ? XL : nullptr, d, P, d, so, (int64_t)n * d}};
       STAGE(ST_PREFILL_GEMM, launch_gemm_wide(prods, 2, n, 2, 8, stream), "projection");
-      STAGE(ST_PREFILL_ELEMENTWISE, launch_residual(X, P, so, D, sd, (int64_t)n * d, stream), "residual");
+      if ((rc = residual(l, so, sd))) return rc;
     } else {
-      STAGE(ST_PREFILL_NORM,
-            launch_layer_norm_rows(X, w.ln_w, w.ln_b, dims.eps, n, d, pin ? nullptr : H, stream, pin ? XH : nullptr,
-                                   pin ? XL : nullptr),
-            "layer_norm");
+      if (!normed)
+        STAGE(ST_PREFILL_NORM,
+              launch_layer_norm_rows(X, w.ln_w, w.ln_b, dims.eps, n, d, pin ? nullptr : H, stream, pin ? XH : nullptr,
+                                     pin ? XL : nullptr),
+              "layer_norm");
       float *m32 = pd && !tracing ? nullptr : M;
       if (split_in) {
         // [q | k | v] and the gate/up pairs in formats of their own: two
@@ -991,7 +1019,7 @@ int StableModel::prefill_chunk(const int32_t *ids, int n, int start, bool want_l
               launch_attention(dims, kv[l], Q, d_pos0, n, start + n - 1, partials, counters, A, stream), "attention");
       if ((rc = po ? project_planes(wo, XH, lo_plane(wo), n, P, d, &sp) : project(wo, A, d, n, P, d, &sp)))
         return rc;
-      STAGE(ST_PREFILL_ELEMENTWISE, launch_residual(X, P, sp, D, sd, (int64_t)n * d, stream), "residual");
+      if ((rc = residual(l, sp, sd))) return rc;
     }
     if (tracing) {
       TRY_HIP(launch_copy_row(X + (size_t)(n - 1) * d, trace_dev + (size_t)l * d, d, stream), "trace");

@@ -289,6 +289,13 @@ hipError_t launch_in_epilogue(const StableDims &s, const KVDev &kv, const float 
 // x = (x + sum_s p[s]) + sum_s d[s] over sp and sd partial products n
 // floats apart (K-split GEMM outputs), summed in order.
 hipError_t launch_residual(float *x, const float *p, int sp, const float *d, int sd, int64_t n, hipStream_t st);
+// launch_residual over n rows of d values, then the LayerNorm of the new
+// rows (launch_layer_norm_rows' arithmetic, weights w, bias b) into out
+// and / or the bf16 planes oh, ol, in one pass over x: the same bits as
+// the two launches.
+hipError_t launch_residual_norm_rows(float *x, const float *p, int sp, const float *dd, int sd, int n, int d,
+                                     const float *w, const float *b, double eps, float *out, uint16_t *oh,
+                                     uint16_t *ol, hipStream_t st);
 // out[i] = sum over s < sp of p[s * n + i], in order of s.
 hipError_t launch_sum_splits(float *out, const float *p, int sp, int64_t n, hipStream_t st);
 hipError_t launch_copy_row(const float *src, float *dst, int n, hipStream_t st);

@@ -161,6 +161,46 @@ __device__ __forceinline__ float sum_partials(const float *v, int s, int64_t n, 
   return acc;
 }
 
+// The residual of a chunk's row (residual_kernel's arithmetic) and the
+// next layer's LayerNorm of it (layer_norm_rows_kernel's): one block per
+// row stages the new row in LDS while it stores it, so the row is read
+// once for both. Two elements per thread at a time, their loads issued
+// before their stores.
+__global__ __launch_bounds__(256) void residual_norm_rows_kernel(float *x, const float *p, int sp, const float *dd,
+                                                                 int sd, int64_t n, int d, const float *w,
+                                                                 const float *b, double eps, float *out, uint16_t *oh,
+                                                                 uint16_t *ol, int ldo) {
+  extern __shared__ __align__(16) float lds[];
+  double *red = reinterpret_cast<double *>(lds + ((d + 3) & ~3));
+  const int64_t row = blockIdx.x;
+  constexpr int E = 2;
+  for (int i0 = threadIdx.x; i0 < d; i0 += E * blockDim.x) {
+    float v[E];
+#pragma unroll
+    for (int e = 0; e < E; e++) {
+      const int i = i0 + e * blockDim.x;
+      if (i < d) {
+        const int64_t k = row * d + i;
+        v[e] = __fadd_rn(__fadd_rn(x[k], sum_partials(p, sp, n, k)), sum_partials(dd, sd, n, k));
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < E; e++) {
+      const int i = i0 + e * blockDim.x;
+      if (i < d) {
+        x[row * d + i] = v[e];
+        lds[i] = v[e];
+      }
+    }
+  }
+  __syncthreads();
+  layer_norm_lds(lds, d, w, b, eps, red);
+  for (int i = threadIdx.x; i < d; i += blockDim.x) {
+    if (out) out[row * d + i] = lds[i];
+    if (oh) store_bf16_split(oh, ol, row * ldo + i, lds[i]);
+  }
+}
+
 __global__ void residual_kernel(float *x, const float *p, int sp, const float *d, int sd, int64_t n) {
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
     const float o = sum_partials(p, sp, n, i), m = sum_partials(d, sd, n, i);
@@ -192,6 +232,16 @@ __global__ void copy_words_kernel(const uint32_t *src, uint32_t *dst, int n) {
 int elementwise_grid(int64_t n) { return (int)std::min<int64_t>((n + 255) / 256, 4096); }
 
 }  // namespace
+
+hipError_t launch_residual_norm_rows(float *x, const float *p, int sp, const float *dd, int sd, int n, int d,
+                                     const float *w, const float *b, double eps, float *out, uint16_t *oh,
+                                     uint16_t *ol, hipStream_t st) {
+  if (sp < 1 || sd < 1 || !oh != !ol || (!out && !oh)) return hipErrorInvalidValue;
+  const size_t lds = (size_t)((d + 3) & ~3) * 4 + 8 * sizeof(double);
+  hipLaunchKernelGGL(residual_norm_rows_kernel, dim3(n), dim3(256), lds, st, x, p, sp, dd, sd, (int64_t)n * d, d, w, b,
+                     eps, out, oh, ol, d);
+  return hipGetLastError();
+}
 
 hipError_t launch_layer_norm_rows(const float *x, const float *w, const float *b, double eps, int n, int d,
                                   float *out, hipStream_t st, uint16_t *oh, uint16_t *ol, int ldo) {
