@@ -228,8 +228,8 @@ int tinyoai_stablelm_profile(tinyoai_model *m, int32_t enable);
  * epilogue in the product's own launch, zero (the default) as a kernel of
  * its own (same arithmetic). Stage 9: grid nonzero (the default) splits a
  * prefill call's attention over key ranges when its query tiles would
- * leave CUs idle (a few hundred tokens after a resident prefix of 1024 or
- * more), the ranges' partial results combined in a fixed order; zero
+ * leave CUs idle (calls of fewer than about 900 tokens whose last position
+ * reaches 256), the ranges' partial results combined in a fixed order; zero
  * keeps one block per query tile (the sums' order differs). Returns 0 or
  * TINYOAI_EINVAL. */
 int tinyoai_stablelm_set_launch(tinyoai_model *m, int32_t stage, int32_t grid, int32_t threads);

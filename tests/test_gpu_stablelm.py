@@ -282,14 +282,15 @@ def test_fused_decode_attention_matches_separate_launch(hip, dtype, kv_bits):
 @pytest.mark.parametrize("fmt,kv_bits", [(W.Q8_0, 32), (W.BF16, 16)])
 def test_key_split_prefill_matches_one_block_per_tile(hip, fmt, kv_bits):
     """A 1600-token prompt submitted in 512-token calls and a 64-token tail
-    (as MLX.generate chunks a prompt, mlx.go:346-354): the calls after
-    1024 resident positions split their attention over key ranges (the
-    default) and combine the ranges' records; against one block per query
+    (as MLX.generate chunks a prompt, mlx.go:346-354): every call, its last
+    position past 256, splits its attention over key ranges (the default)
+    and combines the ranges' records; against one block per query
     tile (launch stage 9 off) the logits of every call, the last token's
     per-layer residuals and the fp32 KV agree within 1e-5 of their range
-    (the same products summed in another order; an fp16 KV entry within one
-    fp16 step of its largest value, as a rounding of those sums may flip),
-    with the same greedy ids."""
+    (the same products summed in another order), with the same greedy ids.
+    With an fp16 cache a last-bit difference in one layer's attention may
+    flip the fp16 rounding of the next layer's K/V: an entry within one
+    fp16 step of its largest value, logits and residuals within 1e-4."""
     config = W.validate_stablelm_config(dict(W.STABLELM_3B, num_hidden_layers=2, max_position_embeddings=2048))
     tensors = W.synthetic_stablelm(config, fmt, seed=61)
     prompt = np.random.default_rng(67).integers(0, 65536, 1600).astype(np.int32)
@@ -298,13 +299,14 @@ def test_key_split_prefill_matches_one_block_per_tile(hip, fmt, kv_bits):
     for f in (split, whole):
         f.set_kv_bits(kv_bits)
         f.trace(True)
+    tol = 1e-5 if kv_bits == 32 else 1e-4
     for a, b in ((0, 512), (512, 1024), (1024, 1536), (1536, 1600)):
         ls, lw = split.forward(a, prompt[a:b]), whole.forward(a, prompt[a:b])
-        assert np.max(np.abs(ls - lw)) <= 1e-5 * float(np.ptp(lw)), a
+        assert np.max(np.abs(ls - lw)) <= tol * float(np.ptp(lw)), a
         assert int(np.argmax(ls)) == int(np.argmax(lw)), a
     ts, tw = split.trace_read(), whole.trace_read()
     for layer in range(2):
-        assert np.max(np.abs(ts[layer] - tw[layer])) <= 1e-5 * float(np.ptp(tw[layer])), layer
+        assert np.max(np.abs(ts[layer] - tw[layer])) <= tol * float(np.ptp(tw[layer])), layer
         k1, v1 = split.read_kv(layer, 0, 1600)
         k2, v2 = whole.read_kv(layer, 0, 1600)
         for got, want in ((k1, k2), (v1, v2)):

@@ -525,7 +525,7 @@ hipError_t launch_flash_prefill(const StableDims &s, const KVDev &kv, const floa
   // Key splits where the query tiles alone leave CUs idle (a few hundred
   // queries against a long cache): about 512 blocks, the records in `work`.
   const int blocks = (n + kQ32 - 1) / kQ32 * s.heads;
-  if (!sfx && work && blocks < 256 && last_pos >= 1024) {
+  if (!sfx && work && blocks < 256 && last_pos >= 256) {
     int ks = std::min(8, (512 + blocks - 1) / blocks);
     while (ks > 1 && (int64_t)n * s.heads * ks * (s.hd + 2) > work_floats) ks--;
     if (ks > 1) {

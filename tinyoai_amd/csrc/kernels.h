@@ -155,7 +155,7 @@ bool flash_prefill_supported(int hd);
 // slot of its first position) on the device, n = the longest run, q, pos0
 // (row pairs) and out indexed by row.
 // Without sfx, when the query tiles leave CUs idle and the last query's
-// position (last_pos, known to the host) reaches 1024, each tile's keys are
+// position (last_pos, known to the host) reaches 256, each tile's keys are
 // split over several blocks whose records (in `work`, at most work_floats)
 // a second kernel combines in order (null work: no splits).
 hipError_t launch_flash_prefill(const StableDims &s, const KVDev &kv, const float *q, const int *pos0, int n,
