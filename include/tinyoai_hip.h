@@ -248,6 +248,15 @@ int tinyoai_llama_forward(tinyoai_model *m, int32_t prefix, const int32_t *token
                           int32_t all_logits, float *logits);
 int tinyoai_llama_reset(tinyoai_model *m);  /* Reset (mlx_llama.go:32-33) */
 int tinyoai_llama_close(tinyoai_model *m);  /* Close (mlx_llama.go:34) */
+/* Launch choice (no counterpart in the reference: a tuning and test
+ * switch, like tinyoai_stablelm_set_launch). Stage 0: value nonzero (the
+ * default where the model fits: dim 64, 8 query / 4 kv heads, MLP 172, at
+ * most 8 layers, 512 positions and a 512-token vocabulary, the stories260K
+ * shape) runs every token of a forward call in one launch of one
+ * workgroup; zero runs five kernels per layer and token. The sums' order
+ * differs between the two. Returns 0, or TINYOAI_EINVAL for another stage,
+ * or for value nonzero on a model of another shape. */
+int tinyoai_llama_set_launch(tinyoai_model *m, int32_t stage, int32_t value);
 
 /* ---------------- single weight matrices (weightTensor, safetensors.go:193-280) ---------------- */
 

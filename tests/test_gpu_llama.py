@@ -38,12 +38,14 @@ def _check(want, got):
     assert _kl(want, got) <= 1e-6
 
 
+@pytest.mark.parametrize("single", [1, 0], ids=["one_launch", "per_layer"])
 @pytest.mark.parametrize("prompt,generated", [(128, 256), (480, 32)])
-def test_forward_parity(oracle, stories, prompt, generated):
+def test_forward_parity(oracle, stories, prompt, generated, single):
     from tinyoai_amd import hip
     c, w = stories
     ref = oracle.Llama(c, w)
     f = hip.LlamaForwarder(c, w)
+    f.set_launch("single_launch", single)
     rng = np.random.default_rng(prompt)
     ids = np.concatenate([[1], rng.integers(3, 512, prompt - 1)]).astype(np.int32)
     want = None
@@ -63,6 +65,55 @@ def test_forward_parity(oracle, stories, prompt, generated):
     ref.close()
 
 
+def test_one_launch_long_call(oracle, stories):
+    """One forward of 300 tokens (two launches of the one-launch kernel:
+    256 tokens, then 44) with every row, then greedy tokens: the same bar
+    as above against the CPU engine."""
+    from tinyoai_amd import hip
+    c, w = stories
+    ref = oracle.Llama(c, w)
+    f = hip.LlamaForwarder(c, w)
+    rng = np.random.default_rng(300)
+    ids = np.concatenate([[1], rng.integers(3, 512, 299)]).astype(np.int32)
+    got = f.forward(0, ids, all_logits=True)
+    assert got.shape == (300, c["vocab_size"])
+    want = None
+    for i in range(300):
+        want = ref.transformer(int(ids[i]), i)
+        _check(want, got[i])
+    for i in range(8):
+        tok = int(np.argmax(want))
+        got = f.forward(300 + i, [tok])
+        want = ref.transformer(tok, 300 + i)
+        _check(want, got)
+    f.close()
+    ref.close()
+
+
+def test_one_launch_matches_per_layer_kernels(stories):
+    """The one-launch kernel and the per-layer kernels on the same calls:
+    logits within 1e-4 of their range (the sums' order differs) and the
+    same argmax, for a 64-token prompt and 64 greedy steps."""
+    from tinyoai_amd import hip
+    c, w = stories
+    fs = [hip.LlamaForwarder(c, w) for _ in range(2)]
+    fs[1].set_launch("single_launch", 0)
+    rng = np.random.default_rng(64)
+    ids = np.concatenate([[1], rng.integers(3, 512, 63)]).astype(np.int32)
+    a, b = (f.forward(0, ids, all_logits=True) for f in fs)
+    for i in range(64):
+        assert np.max(np.abs(a[i] - b[i])) <= 1e-4 * float(np.ptp(b[i])), i
+        assert int(np.argmax(a[i])) == int(np.argmax(b[i])), i
+    tok = int(np.argmax(a[-1]))
+    for i in range(64):
+        a, b = (f.forward(64 + i, [tok]) for f in fs)
+        assert np.max(np.abs(a - b)) <= 1e-4 * float(np.ptp(b)), i
+        assert int(np.argmax(a)) == int(np.argmax(b)), i
+        tok = int(np.argmax(b))
+    for f in fs:
+        f.close()
+
+
 def test_grouped_query_shapes(oracle):
     """A seeded llama2.c model with wider heads and 4:1 grouped KV: per-step
     logits within 1e-3 of their range (fp32 path) and the same greedy ids."""
@@ -71,6 +122,8 @@ def test_grouped_query_shapes(oracle):
     w = W.synthetic_llama(c, seed=9)
     ref = oracle.Llama(c, w)
     f = hip.LlamaForwarder(c, w)
+    with pytest.raises(hip.TinyoaiError):
+        f.set_launch("single_launch", 1)  # not the stories260K shape
     tok = 1
     for pos in range(100):
         got = f.forward(pos, [tok])

@@ -23,7 +23,7 @@ ARCH = os.environ.get("TINYOAI_OFFLOAD_ARCH", "gfx950")
 # (matvec_<format>.hip), so they compile in parallel.
 MATVEC_FORMATS = ["q8_0", "bf16", "f32", "f16", "q5_1", "q4_k", "q5_k", "q6_k"]
 SOURCES = ["decode.hip", "api.cpp", "llama.cpp", "prefill.hip", "weights.hip", "gemm.hip",
-           "flash.hip", "logprobs.hip", "kq_rows.hip"] + [f"matvec_{f}.hip" for f in MATVEC_FORMATS]
+           "flash.hip", "logprobs.hip", "kq_rows.hip", "llama_tiny.hip"] + [f"matvec_{f}.hip" for f in MATVEC_FORMATS]
 FLAGS = ["-O3", "-std=c++17", "-fPIC", "-x", "hip", f"--offload-arch={ARCH}", "-ffp-contract=off",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
          "-Wall", "-Wno-unused-function", "-Wno-unused-variable", "-Wno-unused-value", "-Wno-unused-result",

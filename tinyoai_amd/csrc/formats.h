@@ -391,6 +391,20 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t plane_rsrc(const uint8_t *p, i
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(p), (short)0, (int)(uint32_t)bytes, 0x00020000);
 }
 
+// 16 bytes per lane from a buffer straight into LDS (buffer_load_dwordx4
+// ... lds): the wave's 64 lanes fill 1 KB at LDS byte address lds_byte in
+// lane order. Inline assembly, so the compiler neither tracks nor waits for
+// it: the caller waits (wait_vmcnt) before any wave reads the bytes.
+__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t lds_byte) {
+  asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(r), "{m0}"(lds_byte) : "memory");
+}
+// s_waitcnt with vmcnt(n) only (gfx9 encoding: vmcnt bits 3:0 and 15:14).
+template <int n>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(n >= 0 && n < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | 0x0f70);
+}
+
 __device__ __forceinline__ Planes make_planes(const MatDesc &M) {
   Planes P;
   P.v = plane_rsrc(M.vals, (int64_t)M.rows * M.vstride);

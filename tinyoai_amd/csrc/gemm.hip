@@ -445,15 +445,6 @@ __device__ __forceinline__ void wide_epilogue_rows(const WideArgs &g, const floa
 // one step to hide the memory latency. The kernel waits for its loads
 // itself (s_waitcnt vmcnt) and issues no other vector memory load in the
 // loop.
-__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t lds_byte) {
-  asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(r), "{m0}"(lds_byte) : "memory");
-}
-// s_waitcnt with vmcnt(n) only (gfx9 encoding: vmcnt bits 3:0 and 15:14).
-template <int n>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(n >= 0 && n < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | 0x0f70);
-}
 
 template <int XS, int MF, int NF>
 constexpr int dma_slot_bytes() {

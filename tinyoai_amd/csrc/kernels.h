@@ -315,6 +315,24 @@ size_t logprob_scratch_bytes(int count);
 hipError_t launch_logprobs(const float *logits, int64_t ld, int rows, int vocab, const int *targets, int count,
                            double *chosen, int *top_ids, double *top_lp, void *scratch, hipStream_t st);
 
+// ---- the stories260K-shaped Llama, every token of a call in one launch ----
+constexpr int kTinyDim = 64, kTinyHidden = 172, kTinyMaxLayers = 8, kTinyMaxSeq = 512, kTinyMaxVocab = 512,
+              kTinyMaxTokens = 256;
+struct TinyLlamaArgs {
+  const uint8_t *w[kTinyMaxLayers][4];  // fp32 rows: [wq | wk | wv], wo, w1/w3 interleaved, w2 (unpadded)
+  const uint8_t *emb;                   // [vocab][dim], also the classifier
+  float *k[kTinyMaxLayers], *v[kTinyMaxLayers];  // [kv_heads][cap][8]
+  const float *rms_att, *rms_ffn, *rms_final;    // [layers][dim], [layers][dim], [dim]
+  const float *rope;                    // [cap][8]: (cos, sin) of pairs 0..3
+  float att_scale;                      // float32(sqrt(8))
+  int layers, vocab, cap, prefix, n;
+  int all, last;                        // rows written: every token's (all) or the last token's (last)
+  float *out;                           // [n or 1][vocab]
+  int tokens[kTinyMaxTokens];
+};
+bool tiny_llama_supported(int dim, int hidden, int heads, int kv_heads, int layers, int vocab, int seq);
+hipError_t launch_tiny_llama(const TinyLlamaArgs &a, hipStream_t st);
+
 // ---- weights ----
 // Places raw GGUF-encoded bytes (already in device memory) of a
 // [rows][cols] tensor into `dst` under `map`, starting at column col0.

@@ -30,6 +30,7 @@ LlamaModel::~LlamaModel() {
   }
   for (void *p : buffers) hipFree(p);
   if (h_pinned) hipHostFree(h_pinned);
+  if (out_host) hipHostFree(out_host);
   if (params_copied) hipEventDestroy(params_copied);
   if (stream) hipStreamDestroy(stream);
 }
@@ -155,6 +156,16 @@ int LlamaModel::init(const tinyoai_llama_config &c, const float *w, uint64_t n_f
   grid_mlp = grid_for(hidden, 256);
   grid_out = grid_for(dim, 256);
   grid_head = grid_for((vocab + 1) / 2, 256);
+  // The one-launch kernel reads unpadded fp32 rows and a cache of seq_len
+  // positions per kv head.
+  tiny_ok = tiny_llama_supported(c.dim, c.hidden_dim, c.n_heads, c.n_kv_heads, c.n_layers, c.vocab_size, c.seq_len) &&
+            embed.desc.vstride == dim * 4;
+  for (int64_t l = 0; l < L && tiny_ok; l++) {
+    const DevMatrix *m = &mats[l * 4];
+    tiny_ok = m[0].desc.vstride == dim * 4 && m[1].desc.vstride == dim * 4 && m[2].desc.vstride == dim * 4 &&
+              m[3].desc.vstride == hidden * 4 && kv[l].cap == seq;
+  }
+  tiny = tiny_ok;
   return TINYOAI_OK;
 }
 
@@ -242,6 +253,16 @@ int LlamaModel::forward(int prefix, const int32_t *tokens, int n, bool all_logit
   for (int i = 0; i < n; i++)
     if (tokens[i] < 0 || tokens[i] >= cfg.vocab_size) return fail(TINYOAI_EINVAL, "invalid token %d", tokens[i]);
   offset = prefix;
+  if (tiny) {
+    const int rc = forward_tiny(prefix, tokens, n, all_logits, logits);
+    if (rc) {
+      hipStreamSynchronize(stream);
+      offset = 0;  // native errors reset KV (mlx_llama_native.go:170-172)
+      return rc;
+    }
+    offset = prefix + n;
+    return TINYOAI_OK;
+  }
   const int rows = all_logits ? n : 1;
   int rc = ensure_logits(rows);
   for (int j = 0; j < n && !rc; j++) {
@@ -265,6 +286,56 @@ int LlamaModel::forward(int prefix, const int32_t *tokens, int n, bool all_logit
     return rc;
   }
   offset = prefix + n;
+  return TINYOAI_OK;
+}
+
+// forward for the stories260K shape: one launch per kTinyMaxTokens tokens
+// (every token of the call in one workgroup, in order), the logits rows
+// written by the kernel into mapped pinned host memory.
+int LlamaModel::forward_tiny(int prefix, const int32_t *tokens, int n, bool all_logits, float *logits) {
+  const int rows = all_logits ? n : 1, vocab = cfg.vocab_size;
+  if (rows > out_rows) {
+    if (out_host) {
+      TRY_HIP(hipStreamSynchronize(stream), "logits rows");
+      hipHostFree(out_host);
+      out_host = out_dev = nullptr;
+      out_rows = 0;
+    }
+    void *h = nullptr;
+    hipError_t e = hipHostMalloc(&h, (size_t)rows * vocab * 4, hipHostMallocMapped);
+    if (e != hipSuccess) return fail(TINYOAI_ENOMEM, "hipHostMalloc: %s", hipGetErrorString(e));
+    out_host = (float *)h;
+    e = hipHostGetDevicePointer((void **)&out_dev, h, 0);
+    if (e != hipSuccess) return hip_fail(e, "mapped logits rows");
+    out_rows = rows;
+  }
+  TinyLlamaArgs a{};
+  for (int l = 0; l < cfg.n_layers; l++) {
+    for (int k = 0; k < 4; k++) a.w[l][k] = mats[l * 4 + k].desc.vals;
+    a.k[l] = (float *)kv[l].k;
+    a.v[l] = (float *)kv[l].v;
+  }
+  a.emb = embed.desc.vals;
+  a.rms_att = att_layers[0].ln_w;
+  a.rms_ffn = mlp_layers[0].ln_w;
+  a.rms_final = rms_final;
+  a.rope = rope;
+  a.att_scale = att.att_scale;
+  a.layers = cfg.n_layers;
+  a.vocab = vocab;
+  a.cap = cfg.seq_len;
+  for (int c0 = 0; c0 < n; c0 += kTinyMaxTokens) {
+    const int cnt = std::min(kTinyMaxTokens, n - c0);
+    a.prefix = prefix + c0;
+    a.n = cnt;
+    a.all = all_logits;
+    a.last = !all_logits && c0 + cnt == n;
+    a.out = out_dev + (all_logits ? (size_t)c0 * vocab : 0);
+    std::memcpy(a.tokens, tokens + c0, (size_t)cnt * 4);
+    TRY_HIP(launch_tiny_llama(a, stream), "token launch");
+  }
+  TRY_HIP(hipStreamSynchronize(stream), "logits");
+  std::memcpy(logits, out_host, (size_t)rows * vocab * 4);
   return TINYOAI_OK;
 }
 
@@ -296,6 +367,16 @@ int tinyoai_llama_reset(tinyoai_model *m) {
   if (!m || !m->llama) return fail(TINYOAI_EINVAL, "not a Llama handle");
   hipStreamSynchronize(m->llama->stream);
   m->llama->offset = 0;
+  return TINYOAI_OK;
+}
+
+int tinyoai_llama_set_launch(tinyoai_model *m, int32_t stage, int32_t value) {
+  if (!m || !m->llama) return fail(TINYOAI_EINVAL, "not a Llama handle");
+  LlamaModel &l = *m->llama;
+  if (stage != 0) return fail(TINYOAI_EINVAL, "unknown Llama launch stage %d", stage);
+  if (value && !l.tiny_ok) return fail(TINYOAI_EINVAL, "the one-launch kernel does not fit this model's shape");
+  hipStreamSynchronize(l.stream);
+  l.tiny = value != 0;
   return TINYOAI_OK;
 }
 

@@ -272,6 +272,11 @@ struct LlamaModel {
   int grid_in = 1, grid_mlp = 1, grid_out = 1, grid_head = 1;
   std::map<int64_t, hipGraphExec_t> graphs;
   std::vector<void *> buffers;
+  // One launch per call (launch_tiny_llama) where the shape allows: the
+  // logits rows land in pinned host memory (out_host, out_rows rows).
+  bool tiny_ok = false, tiny = false;
+  float *out_host = nullptr, *out_dev = nullptr;
+  int out_rows = 0;
 
   ~LlamaModel();
   int init(const tinyoai_llama_config &c, const float *weights, uint64_t n_floats);
@@ -280,6 +285,7 @@ struct LlamaModel {
   int enqueue_step(int steps, int splits, float *logits);
   int step(int token, int pos, float *logits);
   int forward(int prefix, const int32_t *tokens, int n, bool all_logits, float *logits);
+  int forward_tiny(int prefix, const int32_t *tokens, int n, bool all_logits, float *logits);
 };
 
 }  // namespace tinyoai

@@ -25,7 +25,8 @@ EXPORTS = [
     "tinyoai_stablelm_set_launch", "tinyoai_stablelm_branches_open", "tinyoai_stablelm_branches_forward",
     "tinyoai_stablelm_branches_append", "tinyoai_stablelm_branches_length", "tinyoai_stablelm_branches_close",
     "tinyoai_stablelm_profile", "tinyoai_stablelm_profile_read", "tinyoai_llama_load",
-    "tinyoai_llama_forward", "tinyoai_llama_reset", "tinyoai_llama_close", "tinyoai_weight_upload",
+    "tinyoai_llama_forward", "tinyoai_llama_reset", "tinyoai_llama_close", "tinyoai_llama_set_launch",
+    "tinyoai_weight_upload",
     "tinyoai_weight_read_values", "tinyoai_weight_mul", "tinyoai_weight_mul_device",
     "tinyoai_weight_mul_device_noalloc", "tinyoai_weight_free",
 ]
@@ -93,6 +94,7 @@ def lib():
         L.tinyoai_llama_forward.argtypes = [P, C.c_int32, ip, C.c_int32, C.c_int32, fp]
         L.tinyoai_llama_reset.argtypes = [P]
         L.tinyoai_llama_close.argtypes = [P]
+        L.tinyoai_llama_set_launch.argtypes = [P, C.c_int32, C.c_int32]
         L.tinyoai_weight_upload.argtypes = [C.c_int32, C.c_int64, C.c_int64, P, C.c_uint64, C.POINTER(P)]
         L.tinyoai_weight_read_values.argtypes = [P, C.c_int64, C.c_int64, fp]
         L.tinyoai_weight_mul.argtypes = [P, fp, C.c_int32, fp]
@@ -405,6 +407,14 @@ class LlamaForwarder:
 
     def reset(self) -> None:
         check(lib().tinyoai_llama_reset(self.h))
+
+    LAUNCH_STAGES = {"single_launch": 0}
+
+    def set_launch(self, stage: str, value: int) -> None:
+        """Stage "single_launch": nonzero (the default for stories260K-shaped
+        models) runs every token of a forward in one launch, zero five
+        kernels per layer and token."""
+        check(lib().tinyoai_llama_set_launch(self.h, self.LAUNCH_STAGES[stage], int(value)))
 
     def close(self) -> None:
         if self.h:
