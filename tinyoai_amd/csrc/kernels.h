@@ -318,16 +318,26 @@ hipError_t launch_logprobs(const float *logits, int64_t ld, int rows, int vocab,
 // ---- the stories260K-shaped Llama, every token of a call in one launch ----
 constexpr int kTinyDim = 64, kTinyHidden = 172, kTinyMaxLayers = 8, kTinyMaxSeq = 512, kTinyMaxVocab = 512,
               kTinyMaxTokens = 256;
+// Packed fp32 weights, per layer: [wq | wk | wv] (128 x 64), wo (64 x 64),
+// w1/w3 interleaved (344 x 64), w2 (64 x 172), rows unpadded; the buffer
+// ends with kTinyPad spare bytes (reads of a row's last chunks may run past
+// a matrix, never past the buffer). The K/V cache is one buffer too: per
+// layer K [kv_heads][cap][8], then V the same, then kTinyPad bytes.
+constexpr int64_t kTinyQkvOff = 0, kTinyWoOff = 128 * 64 * 4, kTinyW13Off = kTinyWoOff + 64 * 64 * 4,
+                  kTinyW2Off = kTinyW13Off + 344 * 64 * 4, kTinyLayerBytes = kTinyW2Off + 64 * 172 * 4,
+                  kTinyPad = 1024;
 struct TinyLlamaArgs {
-  const uint8_t *w[kTinyMaxLayers][4];  // fp32 rows: [wq | wk | wv], wo, w1/w3 interleaved, w2 (unpadded)
-  const uint8_t *emb;                   // [vocab][dim], also the classifier
-  float *k[kTinyMaxLayers], *v[kTinyMaxLayers];  // [kv_heads][cap][8]
-  const float *rms_att, *rms_ffn, *rms_final;    // [layers][dim], [layers][dim], [dim]
-  const float *rope;                    // [cap][8]: (cos, sin) of pairs 0..3
-  float att_scale;                      // float32(sqrt(8))
+  const uint8_t *w;                  // packed weights, layers * kTinyLayerBytes + kTinyPad bytes
+  const uint8_t *emb;                // [vocab][dim] fp32, also the classifier
+  float *kv;                         // the K/V buffer
+  const float *rms_att, *rms_ffn, *rms_final;  // [layers][dim], [layers][dim], [dim]
+  const float *rope;                 // [cap][8]: (cos, sin) of pairs 0..3
+  float att_scale;                   // float32(sqrt(8))
   int layers, vocab, cap, prefix, n;
-  int all, last;                        // rows written: every token's (all) or the last token's (last)
-  float *out;                           // [n or 1][vocab]
+  int all, last;                     // rows written: every token's (all) or the last token's (last)
+  float *out;                        // [n or 1][vocab]
+  unsigned *done;                    // set to `seq` (system scope) after the rows, when non-null
+  unsigned seq;
   int tokens[kTinyMaxTokens];
 };
 bool tiny_llama_supported(int dim, int hidden, int heads, int kv_heads, int layers, int vocab, int seq);

@@ -8,6 +8,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <chrono>
 #include <cmath>
 #include <cstring>
 
@@ -24,13 +25,11 @@ namespace tinyoai {
 
 LlamaModel::~LlamaModel() {
   for (auto &g : graphs) hipGraphExecDestroy(g.second);
-  for (auto &l : kv) {
-    if (l.k) hipFree(l.k);
-    if (l.v) hipFree(l.v);
-  }
+  if (kv_base) hipFree(kv_base);
   for (void *p : buffers) hipFree(p);
   if (h_pinned) hipHostFree(h_pinned);
   if (out_host) hipHostFree(out_host);
+  if (done_host) hipHostFree(done_host);
   if (params_copied) hipEventDestroy(params_copied);
   if (stream) hipStreamDestroy(stream);
 }
@@ -132,13 +131,18 @@ int LlamaModel::init(const tinyoai_llama_config &c, const float *w, uint64_t n_f
   if ((rc = alloc((void **)&rope, rt.size() * 4))) return rc;
   TRY_HIP(hipMemcpyAsync(rope, rt.data(), rt.size() * 4, hipMemcpyHostToDevice, stream), "rope upload");
   // KV: the whole context, as runState's caches (model.go:379-398).
+  // One buffer: per layer K, then V, then spare bytes for the one-launch
+  // kernel's whole-chunk reads.
   kv.resize(L);
-  for (auto &l : kv) {
-    const size_t bytes = (size_t)kv_dim * seq * 4;
-    if (hipMalloc(&l.k, bytes) != hipSuccess || hipMalloc(&l.v, bytes) != hipSuccess)
-      return fail(TINYOAI_ENOMEM, "KV allocation");
-    l.cap = (int)seq;
-    l.half = 0;
+  {
+    const size_t per = (size_t)kv_dim * seq * 4;
+    if (hipMalloc(&kv_base, 2 * L * per + kTinyPad) != hipSuccess) return fail(TINYOAI_ENOMEM, "KV allocation");
+    for (int64_t l = 0; l < L; l++) {
+      kv[l].k = (uint8_t *)kv_base + 2 * l * per;
+      kv[l].v = (uint8_t *)kv_base + (2 * l + 1) * per;
+      kv[l].cap = (int)seq;
+      kv[l].half = 0;
+    }
   }
   max_splits = (int)(seq / 64 + 1);
   if ((rc = alloc((void **)&x, dim * 4)) || (rc = alloc((void **)&qbuf, dim * 4)) ||
@@ -164,6 +168,19 @@ int LlamaModel::init(const tinyoai_llama_config &c, const float *w, uint64_t n_f
     const DevMatrix *m = &mats[l * 4];
     tiny_ok = m[0].desc.vstride == dim * 4 && m[1].desc.vstride == dim * 4 && m[2].desc.vstride == dim * 4 &&
               m[3].desc.vstride == hidden * 4 && kv[l].cap == seq;
+  }
+  if (tiny_ok) {  // the packed copy of every layer's matrices
+    if ((rc = alloc((void **)&tiny_w, (size_t)L * kTinyLayerBytes + kTinyPad))) return rc;
+    TRY_HIP(hipMemsetAsync(tiny_w + L * kTinyLayerBytes, 0, kTinyPad, stream), "packed weights");
+    const int64_t off[4] = {kTinyQkvOff, kTinyWoOff, kTinyW13Off, kTinyW2Off};
+    for (int64_t l = 0; l < L; l++)
+      for (int k = 0; k < 4; k++) {
+        const MatDesc &d = mats[l * 4 + k].desc;
+        TRY_HIP(hipMemcpyAsync(tiny_w + l * kTinyLayerBytes + off[k], d.vals, (size_t)d.rows * d.vstride,
+                               hipMemcpyDeviceToDevice, stream),
+                "packed weights");
+      }
+    TRY_HIP(hipStreamSynchronize(stream), "packed weights");
   }
   tiny = tiny_ok;
   return TINYOAI_OK;
@@ -289,11 +306,22 @@ int LlamaModel::forward(int prefix, const int32_t *tokens, int n, bool all_logit
   return TINYOAI_OK;
 }
 
+constexpr int kTinySpinMs = 200;  // host wait for the completion word before waiting on the stream
+
 // forward for the stories260K shape: one launch per kTinyMaxTokens tokens
 // (every token of the call in one workgroup, in order), the logits rows
 // written by the kernel into mapped pinned host memory.
 int LlamaModel::forward_tiny(int prefix, const int32_t *tokens, int n, bool all_logits, float *logits) {
   const int rows = all_logits ? n : 1, vocab = cfg.vocab_size;
+  if (!done_host) {
+    void *h = nullptr;
+    hipError_t e = hipHostMalloc(&h, 64, hipHostMallocMapped | hipHostMallocCoherent);
+    if (e != hipSuccess) return fail(TINYOAI_ENOMEM, "hipHostMalloc: %s", hipGetErrorString(e));
+    done_host = (unsigned *)h;
+    *done_host = 0;
+    e = hipHostGetDevicePointer((void **)&done_dev, h, 0);
+    if (e != hipSuccess) return hip_fail(e, "mapped completion word");
+  }
   if (rows > out_rows) {
     if (out_host) {
       TRY_HIP(hipStreamSynchronize(stream), "logits rows");
@@ -302,7 +330,7 @@ int LlamaModel::forward_tiny(int prefix, const int32_t *tokens, int n, bool all_
       out_rows = 0;
     }
     void *h = nullptr;
-    hipError_t e = hipHostMalloc(&h, (size_t)rows * vocab * 4, hipHostMallocMapped);
+    hipError_t e = hipHostMalloc(&h, (size_t)rows * vocab * 4, hipHostMallocMapped | hipHostMallocCoherent);
     if (e != hipSuccess) return fail(TINYOAI_ENOMEM, "hipHostMalloc: %s", hipGetErrorString(e));
     out_host = (float *)h;
     e = hipHostGetDevicePointer((void **)&out_dev, h, 0);
@@ -310,11 +338,8 @@ int LlamaModel::forward_tiny(int prefix, const int32_t *tokens, int n, bool all_
     out_rows = rows;
   }
   TinyLlamaArgs a{};
-  for (int l = 0; l < cfg.n_layers; l++) {
-    for (int k = 0; k < 4; k++) a.w[l][k] = mats[l * 4 + k].desc.vals;
-    a.k[l] = (float *)kv[l].k;
-    a.v[l] = (float *)kv[l].v;
-  }
+  a.w = tiny_w;
+  a.kv = (float *)kv_base;
   a.emb = embed.desc.vals;
   a.rms_att = att_layers[0].ln_w;
   a.rms_ffn = mlp_layers[0].ln_w;
@@ -331,10 +356,27 @@ int LlamaModel::forward_tiny(int prefix, const int32_t *tokens, int n, bool all_
     a.all = all_logits;
     a.last = !all_logits && c0 + cnt == n;
     a.out = out_dev + (all_logits ? (size_t)c0 * vocab : 0);
+    const bool final = c0 + cnt == n;
+    a.done = final ? done_dev : nullptr;
+    a.seq = ++done_seq;
     std::memcpy(a.tokens, tokens + c0, (size_t)cnt * 4);
     TRY_HIP(launch_tiny_llama(a, stream), "token launch");
   }
-  TRY_HIP(hipStreamSynchronize(stream), "logits");
+  // The last launch sets the completion word after its rows: the rows are
+  // read as soon as it appears (the stream's own completion comes later).
+  // Past the time limit, or if the word never comes, the stream is waited
+  // for, which also reports a failed launch.
+  const auto t0 = std::chrono::steady_clock::now();
+  bool seen = false;
+  for (int spin = 0; !seen; spin++) {
+    seen = __atomic_load_n(done_host, __ATOMIC_ACQUIRE) == done_seq;
+    if (!seen && (spin & 1023) == 1023 &&
+        std::chrono::steady_clock::now() - t0 > std::chrono::milliseconds(kTinySpinMs))
+      break;
+  }
+  if (!seen) TRY_HIP(hipStreamSynchronize(stream), "logits");
+  if (!seen && __atomic_load_n(done_host, __ATOMIC_ACQUIRE) != done_seq)
+    return fail(TINYOAI_EDEVICE, "the token launch ended without its completion word");
   std::memcpy(logits, out_host, (size_t)rows * vocab * 4);
   return TINYOAI_OK;
 }

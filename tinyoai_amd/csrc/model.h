@@ -275,8 +275,12 @@ struct LlamaModel {
   // One launch per call (launch_tiny_llama) where the shape allows: the
   // logits rows land in pinned host memory (out_host, out_rows rows).
   bool tiny_ok = false, tiny = false;
+  uint8_t *tiny_w = nullptr;  // packed weights (layout in kernels.h)
+  void *kv_base = nullptr;    // every layer's K and V (kv[l] points into it)
   float *out_host = nullptr, *out_dev = nullptr;
   int out_rows = 0;
+  unsigned *done_host = nullptr, *done_dev = nullptr;  // completion word (mapped, coherent)
+  unsigned done_seq = 0;
 
   ~LlamaModel();
   int init(const tinyoai_llama_config &c, const float *weights, uint64_t n_floats);
