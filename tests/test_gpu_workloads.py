@@ -130,7 +130,7 @@ def test_bf16_long_context_workload(hip, name):
     print(f"{name}: worst logits error {worst:.2e} of the range")
 
 
-@pytest.mark.parametrize("name", ["kquant_branches"])
+@pytest.mark.parametrize("name", ["kquant_branches", "kquant_branches_full"])
 def test_kquant_branches_workload(hip, name):
     """K-quant mix, fp16 KV: a 4096-token prefix, 16 branches given private
     suffixes of 1-256 tokens in one append, then lockstep steps at ragged
@@ -152,6 +152,7 @@ def test_kquant_branches_workload(hip, name):
     for s in range(p["steps"]):
         for j in range(p["branches"]):
             sub = {k: v[j] for k, v in fx.items() if k.startswith("logits_")}
+            assert int(np.argmax(rows[j])) == int(toks[j, s]), (j, s)
             worst = max(worst, check_logits(rows[j], sub, s, 2e-2, f"branch {j} step {s}"))
         if s + 1 < p["steps"]:
             rows = br.forward(toks[:, s])
