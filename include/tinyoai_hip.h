@@ -230,8 +230,12 @@ int tinyoai_stablelm_profile(tinyoai_model *m, int32_t enable);
  * prefill call's attention over key ranges when its query tiles would
  * leave CUs idle (calls of fewer than about 900 tokens whose last position
  * reaches 256), the ranges' partial results combined in a fixed order; zero
- * keeps one block per query tile (the sums' order differs). Returns 0 or
- * TINYOAI_EINVAL. */
+ * keeps one block per query tile (the sums' order differs). Stage 10:
+ * grid nonzero (the default) runs the Q8_0-weight prefill of fused layers
+ * on wide tiles (the o and down products together as K splits of one
+ * launch; chunks over 1024 rows also their in-projection), zero on
+ * 128 x 256 tiles throughout (the quants exact either way; the sums' order
+ * differs). Returns 0 or TINYOAI_EINVAL. */
 int tinyoai_stablelm_set_launch(tinyoai_model *m, int32_t stage, int32_t grid, int32_t threads);
 int tinyoai_stablelm_profile_read(tinyoai_model *m, double *ms, int64_t *counts, int32_t n_stages);
 

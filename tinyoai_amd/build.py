@@ -22,7 +22,7 @@ ARCH = os.environ.get("TINYOAI_OFFLOAD_ARCH", "gfx950")
 # The streaming matrix-vector kernels come one weight format per file
 # (matvec_<format>.hip), so they compile in parallel.
 MATVEC_FORMATS = ["q8_0", "bf16", "f32", "f16", "q5_1", "q4_k", "q5_k", "q6_k"]
-SOURCES = ["decode.hip", "api.cpp", "llama.cpp", "prefill.hip", "weights.hip", "gemm.hip",
+SOURCES = ["decode.hip", "api.cpp", "llama.cpp", "prefill.hip", "weights.hip", "gemm.hip", "gemm_q8.hip",
            "flash.hip", "logprobs.hip", "kq_rows.hip", "llama_tiny.hip"] + [f"matvec_{f}.hip" for f in MATVEC_FORMATS]
 FLAGS = ["-O3", "-std=c++17", "-fPIC", "-x", "hip", f"--offload-arch={ARCH}", "-ffp-contract=off",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
@@ -37,9 +37,16 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found")
 
 
+# Per-source additions: the Q8_0 wide-tile kernel keeps its matrix-core
+# results in ordinary vector registers (each quant block's products are
+# rescaled on the vector unit, which cannot read the accumulation
+# registers); the BF16 kernels keep theirs in the accumulation registers.
+EXTRA = {"gemm_q8.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
+
+
 def _compile(src: str) -> str:
     obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
-    cmd = [hipcc(), *FLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
+    cmd = [hipcc(), *FLAGS, *EXTRA.get(src, []), "-c", os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode:
         raise RuntimeError(f"hipcc failed for {src}:\n{r.stdout}\n{r.stderr}")

@@ -820,6 +820,12 @@ int StableModel::project(const MatDesc &w, const float *x, int ldx, int n, float
 // by the tile area, the 64-row-per-wave tiles counted at their measured
 // advantage (2048 x 21504 x 2560 with two planes: 472 us at 256 x 224
 // against 551 at 128 x 256).
+// Q8_0 wide tiles are 128 rows x 32 * nf columns, nf 8 or 6: the one
+// that pads N less (8 on a tie).
+static int wide_q8_nf(int N) {
+  const int p8 = (N + 255) / 256 * 256 - N, p6 = (N + 191) / 192 * 192 - N;
+  return p6 < p8 ? 6 : 8;
+}
 static void wide_shape(int n, int N, int *mf, int *nf) {
   double best = 1e30;
   for (int f = 2; f >= 1; f--)
@@ -839,8 +845,8 @@ static void wide_shape(int n, int N, int *mf, int *nf) {
 // proportion to the K lengths (2048 rows at the 3B shapes: 1 + 2, 225 us
 // against 258 for 2 + 6 and 326 for 1 + 1), each split at least four K
 // steps.
-static void wide_out_splits(int n, int d, int64_t ko, int64_t kd, int max_splits, int *so, int *sd) {
-  const int tiles = ((n + 255) / 256) * ((d + 255) / 256);
+static void wide_out_splits(int n, int d, int64_t ko, int64_t kd, int max_splits, int *so, int *sd, int bm = 256) {
+  const int tiles = ((n + bm - 1) / bm) * ((d + 255) / 256);
   const int total = std::max(2, (256 + tiles / 2) / tiles);
   int o = std::max<int>(1, (int)std::lround((double)total * ko / (ko + kd)));
   int m = std::max(1, total - o);
@@ -871,7 +877,11 @@ int StableModel::project_planes(const MatDesc &w, const uint16_t *xh, const uint
 // win and wout, operands in bf16 planes from their producers.
 bool StableModel::wide_layer(int l) const {
   const LayerDev &w = layers[l];
-  return use_wide && w.win.fmt == FMT_BF16 && w.wout.fmt == FMT_BF16 && !w.win2.rows && !w.wout2.rows &&
+  const bool bf16 = w.win.fmt == FMT_BF16 && w.wout.fmt == FMT_BF16;
+  // Q8_0: the down section of wout starts on an even quant block (d % 64)
+  const bool q8 = q8_wide && w.win.fmt == FMT_Q8_0 && w.wout.fmt == FMT_Q8_0 && wide_q8_ok(w.win) &&
+                  wide_q8_ok(w.wout) && dims.d % 64 == 0;
+  return use_wide && (bf16 || q8) && !w.win2.rows && !w.wout2.rows &&
          flash_prefill_supported(dims.hd) && dims.heads * dims.hd == dims.d && w.win.cols % 32 == 0 &&
          dims.inter % 32 == 0;
 }
@@ -935,9 +945,20 @@ int StableModel::prefill_chunk(const int32_t *ids, int n, int start, bool want_l
       if (!normed)
         STAGE(ST_PREFILL_NORM, launch_layer_norm_rows(X, w.ln_w, w.ln_b, dims.eps, n, d, nullptr, stream, XH, XL),
               "layer_norm");
-      int mf, nf;
-      wide_shape(n, w.win.rows, &mf, &nf);
-      if (wide_epi) {
+      const bool q8 = w.win.fmt == FMT_Q8_0;  // Q8_0: 128-row tiles
+      int mf = 1, nf = wide_q8_nf(w.win.rows);
+      if (!q8) wide_shape(n, w.win.rows, &mf, &nf);
+      if (q8 && n <= 1024 && 2 * n <= chunk) {
+        // Up to 1024 rows the Q8_0 in-projection runs on the 128 x 256 tiles
+        // as two K halves that the epilogue sums (704 blocks at 512 rows:
+        // 157 us, where the 336 wide tiles take two rounds of one block per
+        // CU, 207 us).
+        STAGE(ST_PREFILL_GEMM, launch_gemm_mfma(w.win, XH, lo, n, Y, win_rows, stream, 2), "projection");
+        STAGE(ST_PREFILL_EPILOGUE,
+              launch_in_epilogue(dims, kv[l], Y, win_rows, rope, d_pos0, n, Q, tracing ? M : nullptr, stream, MH, ML,
+                                 nullptr, 2),
+              "in_epilogue");
+      } else if (wide_epi) {
         const InEpilogue e{dims, kv[l], rope, d_pos0, Q, tracing ? M : nullptr, MH, ML, 0};
         STAGE(ST_PREFILL_GEMM, launch_gemm_wide_in_epilogue(w.win, XH, lo, d, n, e, mf, nf, stream),
               "projection + epilogue");
@@ -953,10 +974,10 @@ int StableModel::prefill_chunk(const int32_t *ids, int n, int start, bool want_l
                                  nullptr, 0, flash_ksplit ? Y : nullptr, (int64_t)chunk * win_rows, start + n - 1),
             "attention");
       int so, sd;
-      wide_out_splits(n, d, d, I, kPrefillSplits, &so, &sd);
+      wide_out_splits(n, d, d, I, kPrefillSplits, &so, &sd, q8 ? 128 : 256);
       const WideGemm prods[2] = {{wd, MH, lo ? ML : nullptr, I, D, d, sd, (int64_t)n * d},
                                  {wo, XH, lo ? XL : nullptr, d, P, d, so, (int64_t)n * d}};
-      STAGE(ST_PREFILL_GEMM, launch_gemm_wide(prods, 2, n, 2, 8, stream), "projection");
+      STAGE(ST_PREFILL_GEMM, launch_gemm_wide(prods, 2, n, q8 ? 1 : 2, 8, stream), "projection");
       if ((rc = residual(l, so, sd))) return rc;
     } else {
       if (!normed)
@@ -1808,6 +1829,10 @@ int tinyoai_stablelm_set_launch(tinyoai_model *m, int32_t stage, int32_t grid, i
   s.launch_gen++;  // an open branch session's step graphs are not replayed after this
   if (stage == 7) {  // BF16-weight prefill products on wide tiles (1, the default) or 128 x 256 tiles (0)
     s.use_wide = grid != 0;
+    return TINYOAI_OK;
+  }
+  if (stage == 10) {  // Q8_0 prefill products on wide tiles (1, the default) or 128 x 256 tiles (0)
+    s.q8_wide = grid != 0;
     return TINYOAI_OK;
   }
   if (stage == 8) {  // wide-tile in-projection with its epilogue fused (1) or a kernel of its own (0, the default)

@@ -398,6 +398,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t plane_rsrc(const uint8_t *p, i
 __device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t lds_byte) {
   asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(r), "{m0}"(lds_byte) : "memory");
 }
+// The same with 4 bytes per lane (buffer_load_dword ... lds): 256 bytes.
+__device__ __forceinline__ void lds_dma4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t lds_byte) {
+  asm volatile("buffer_load_dword %0, %1, 0 offen lds" ::"v"(voff), "s"(r), "{m0}"(lds_byte) : "memory");
+}
 // s_waitcnt with vmcnt(n) only (gfx9 encoding: vmcnt bits 3:0 and 15:14).
 template <int n>
 __device__ __forceinline__ void wait_vmcnt() {

@@ -250,9 +250,9 @@ struct InEpilogue {
 hipError_t launch_gemm_in_epilogue(const MatDesc &w, const uint16_t *xh, const uint16_t *xl, int M,
                                    const InEpilogue &e, hipStream_t st);
 // Wide-tile matrix-core products (one wave per SIMD, both operands loaded
-// straight into LDS): y = X * W^T for BF16 weights with K % 32 == 0, X as
-// bf16 planes xh (and xl, or null for one plane) with rows lda values
-// apart. A launch carries one or two products of M rows each (their
+// straight into LDS): y = X * W^T for BF16 weights with K % 32 == 0 (X as
+// bf16 planes xh and xl, or xh alone for one plane), or Q8_0 weights that
+// wide_q8_ok accepts (two planes, mf 1), with rows lda values apart. A launch carries one or two products of M rows each (their
 // blocks side by side, the first product's first); product i cuts its K
 // range in ksplit parts whose results go to y + s * split_stride. Block
 // tiles are (128 * mf) x (32 * nf): gemm_wide_shape names the instances
@@ -267,6 +267,13 @@ struct WideGemm {
   int64_t split_stride;
 };
 bool gemm_wide_shape(int fmt, int mf, int nf);
+// A Q8_0 matrix (or column view) the wide tiles take: K a multiple of 32,
+// each row's fp16 block scales starting on a dword (the kernel loads them
+// two blocks at a time) and its quants on 16 bytes.
+inline bool wide_q8_ok(const MatDesc &w) {
+  return w.fmt == FMT_Q8_0 && w.cols % 32 == 0 && w.vstride % 16 == 0 && w.mstride % 4 == 0 &&
+         (reinterpret_cast<uintptr_t>(w.meta) & 3) == 0 && (reinterpret_cast<uintptr_t>(w.vals) & 15) == 0;
+}
 hipError_t launch_gemm_wide(const WideGemm *p, int nprod, int M, int mf, int nf, hipStream_t st);
 // The in-projection (win) product with its epilogue fused (no output
 // matrix), on wide tiles.
