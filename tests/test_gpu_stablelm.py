@@ -360,19 +360,20 @@ def test_wide_bf16_prefill_matches_large_tiles(hip):
 
 
 def test_wide_q8_0_prefill_matches_large_tiles(hip):
-    """The Q8_0 prefill on wide tiles (the default: the o and down products
-    as one launch of K splits on the Q8_0 ring kernel; chunks over 1024 rows
-    also take their in-projection there, smaller ones the 128 x 256 tiles in
-    two K halves) against the 128 x 256 tiles throughout (launch stage 10
-    off): the same exact quants and fp32 products summed in another order,
-    so a 2100-token prefill (a 2048-token chunk and a 52-token one) gives
-    logits, per-layer residuals and (fp32) KV within 1e-5 of their range,
-    and the same greedy ids over 8 decode tokens. The wide in-projection
-    with its epilogue in the product's launch (stage 8 on) gives
-    bit-identical results to the default."""
+    """The Q8_0 prefill on wide tiles (the default: the in-projection of a
+    chunk of 256 rows or more and the o and down products, as one launch of
+    K splits, on the Q8_0 ring kernel; shorter chunks take their
+    in-projection on the 128 x 256 tiles in two K halves) against the
+    128 x 256 tiles throughout (launch stage 10 off): the same exact quants
+    and fp32 products summed in another order. A 2400-token call (chunks of
+    2048 rows on 256 x 256 tiles and 352 rows on 256 x 192) and a 52-token
+    continuation give logits, per-layer residuals and (fp32) KV within 1e-5
+    of their range, and the same greedy ids over 8 decode tokens. The wide
+    in-projection with its epilogue in the product's launch (stage 8 on)
+    gives bit-identical results to the default."""
     config = W.validate_stablelm_config(dict(W.STABLELM_3B, num_hidden_layers=2, max_position_embeddings=4096))
     tensors = W.synthetic_stablelm(config, W.Q8_0, seed=31)
-    prompt = np.random.default_rng(33).integers(0, 65536, 2100).astype(np.int32)
+    prompt = np.random.default_rng(33).integers(0, 65536, 2452).astype(np.int32)
     wide = hip.StableLMForwarder(config, tensors)
     fused = hip.StableLMForwarder(config, tensors)
     ref = hip.StableLMForwarder(config, tensors)
@@ -381,24 +382,25 @@ def test_wide_q8_0_prefill_matches_large_tiles(hip):
     fused.set_launch("wide_epilogue", 1, 0)
     for f in (wide, fused, ref):
         f.trace(True)
-    lw, lf, lr = wide.forward(0, prompt), fused.forward(0, prompt), ref.forward(0, prompt)
-    assert np.array_equal(lw, lf)
-    span = float(np.ptp(lr))
-    assert np.max(np.abs(lw - lr)) <= 1e-5 * span
-    tr = ref.trace_read()
-    assert np.max(np.abs(wide.trace_read() - tr)) <= 1e-5 * float(np.ptp(tr))
-    assert np.array_equal(wide.trace_read(), fused.trace_read())
+    for start, end in ((0, 2400), (2400, 2452)):
+        part = prompt[start:end]
+        lw, lf, lr = wide.forward(start, part), fused.forward(start, part), ref.forward(start, part)
+        assert np.array_equal(lw, lf), start
+        assert np.max(np.abs(lw - lr)) <= 1e-5 * float(np.ptp(lr)), start
+        tr = ref.trace_read()
+        assert np.max(np.abs(wide.trace_read() - tr)) <= 1e-5 * float(np.ptp(tr)), start
+        assert np.array_equal(wide.trace_read(), fused.trace_read()), start
     for layer in range(2):
         for head in (0, 19):
-            kw, kr = wide.read_kv(layer, head, 2100), ref.read_kv(layer, head, 2100)
+            kw, kr = wide.read_kv(layer, head, 2452), ref.read_kv(layer, head, 2452)
             for a, b in zip(kw, kr):
                 assert np.max(np.abs(a - b)) <= 1e-5 * float(np.ptp(b)), (layer, head)
-            for a, b in zip(kw, fused.read_kv(layer, head, 2100)):
+            for a, b in zip(kw, fused.read_kv(layer, head, 2452)):
                 assert np.array_equal(a, b), (layer, head)
     for step in range(8):
         tok = int(np.argmax(lr))
         assert int(np.argmax(lw)) == tok, step
-        lw, lr = wide.forward(2100 + step, [tok]), ref.forward(2100 + step, [tok])
+        lw, lr = wide.forward(2452 + step, [tok]), ref.forward(2452 + step, [tok])
     for f in (wide, fused, ref):
         f.close()
 

@@ -820,18 +820,30 @@ int StableModel::project(const MatDesc &w, const float *x, int ldx, int n, float
 // by the tile area, the 64-row-per-wave tiles counted at their measured
 // advantage (2048 x 21504 x 2560 with two planes: 472 us at 256 x 224
 // against 551 at 128 x 256).
-// Q8_0 wide tiles are 128 rows x 32 * nf columns, nf 8 or 6: the one
-// that pads N less (8 on a tie).
-static int wide_q8_nf(int N) {
-  const int p8 = (N + 255) / 256 * 256 - N, p6 = (N + 191) / 192 * 192 - N;
-  return p6 < p8 ? 6 : 8;
-}
 static void wide_shape(int n, int N, int *mf, int *nf) {
   double best = 1e30;
   for (int f = 2; f >= 1; f--)
     for (int c = 7; c <= 8; c++) {
       const int64_t tiles = (int64_t)((n + 128 * f - 1) / (128 * f)) * ((N + 32 * c - 1) / (32 * c));
       const double cost = (double)((tiles + 255) / 256) * (128 * f) * (32 * c) / (f == 2 ? 1.0 : 0.85);
+      if (cost < best) {
+        best = cost;
+        *mf = f;
+        *nf = c;
+      }
+    }
+}
+
+// The same for a Q8_0 product on the wide tiles, 128 * mf rows x 32 * nf
+// columns (nf 8 or 6), the 256-row tiles counted at their measured
+// advantage (about 1.25x the work per K step of the 128-row ones): the 3B
+// 512-row in-projection takes 256 x 192 tiles (224 blocks, one round).
+static void wide_q8_shape(int n, int N, int *mf, int *nf) {
+  double best = 1e30;
+  for (int f = 2; f >= 1; f--)
+    for (int c = 8; c >= 6; c -= 2) {
+      const int64_t tiles = (int64_t)((n + 128 * f - 1) / (128 * f)) * ((N + 32 * c - 1) / (32 * c));
+      const double cost = (double)((tiles + 255) / 256) * (128 * f) * (32 * c) / (f == 2 ? 1.0 : 0.8);
       if (cost < best) {
         best = cost;
         *mf = f;
@@ -945,14 +957,14 @@ int StableModel::prefill_chunk(const int32_t *ids, int n, int start, bool want_l
       if (!normed)
         STAGE(ST_PREFILL_NORM, launch_layer_norm_rows(X, w.ln_w, w.ln_b, dims.eps, n, d, nullptr, stream, XH, XL),
               "layer_norm");
-      const bool q8 = w.win.fmt == FMT_Q8_0;  // Q8_0: 128-row tiles
-      int mf = 1, nf = wide_q8_nf(w.win.rows);
-      if (!q8) wide_shape(n, w.win.rows, &mf, &nf);
-      if (q8 && n <= 1024 && 2 * n <= chunk) {
-        // Up to 1024 rows the Q8_0 in-projection runs on the 128 x 256 tiles
-        // as two K halves that the epilogue sums (704 blocks at 512 rows:
-        // 157 us, where the 336 wide tiles take two rounds of one block per
-        // CU, 207 us).
+      const bool q8 = w.win.fmt == FMT_Q8_0;
+      int mf, nf;
+      if (q8) wide_q8_shape(n, w.win.rows, &mf, &nf);
+      else wide_shape(n, w.win.rows, &mf, &nf);
+      if (q8 && n < 256 && 2 * n <= chunk) {
+        // Below 256 rows the Q8_0 in-projection runs on the 128 x 256 tiles
+        // as two K halves that the epilogue sums (more blocks than the wide
+        // tiles give a short chunk).
         STAGE(ST_PREFILL_GEMM, launch_gemm_mfma(w.win, XH, lo, n, Y, win_rows, stream, 2), "projection");
         STAGE(ST_PREFILL_EPILOGUE,
               launch_in_epilogue(dims, kv[l], Y, win_rows, rope, d_pos0, n, Q, tracing ? M : nullptr, stream, MH, ML,
@@ -974,10 +986,11 @@ int StableModel::prefill_chunk(const int32_t *ids, int n, int start, bool want_l
                                  nullptr, 0, flash_ksplit ? Y : nullptr, (int64_t)chunk * win_rows, start + n - 1),
             "attention");
       int so, sd;
-      wide_out_splits(n, d, d, I, kPrefillSplits, &so, &sd, q8 ? 128 : 256);
+      const int omf = q8 && n < 256 ? 1 : 2;  // Q8_0 below 256 rows: 128-row tiles
+      wide_out_splits(n, d, d, I, kPrefillSplits, &so, &sd, 128 * omf);
       const WideGemm prods[2] = {{wd, MH, lo ? ML : nullptr, I, D, d, sd, (int64_t)n * d},
                                  {wo, XH, lo ? XL : nullptr, d, P, d, so, (int64_t)n * d}};
-      STAGE(ST_PREFILL_GEMM, launch_gemm_wide(prods, 2, n, q8 ? 1 : 2, 8, stream), "projection");
+      STAGE(ST_PREFILL_GEMM, launch_gemm_wide(prods, 2, n, omf, 8, stream), "projection");
       if ((rc = residual(l, so, sd))) return rc;
     } else {
       if (!normed)

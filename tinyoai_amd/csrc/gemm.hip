@@ -582,9 +582,9 @@ hipError_t gemm_wide_dispatch(const WideArgs &g, int mf, int nf, hipStream_t st)
 
 template <bool EPI>
 hipError_t gemm_wide_fmt(const WideArgs &g, int mf, int nf, bool two, hipStream_t st) {
-  if (g.p[0].w.fmt == FMT_Q8_0) {  // two planes, 128-row tiles
-    if (!two || mf != 1) return hipErrorInvalidValue;
-    return launch_gemm_wideq(g, nf, EPI, st);
+  if (g.p[0].w.fmt == FMT_Q8_0) {  // two planes
+    if (!two) return hipErrorInvalidValue;
+    return launch_gemm_wideq(g, mf, nf, EPI, st);
   }
   return two ? gemm_wide_dispatch<2, EPI>(g, mf, nf, st) : gemm_wide_dispatch<1, EPI>(g, mf, nf, st);
 }
@@ -599,7 +599,7 @@ bool wide_operand_ok(const MatDesc &w, const uint16_t *xh, int lda, int M) {
 }  // namespace
 
 bool gemm_wide_shape(int fmt, int mf, int nf) {
-  if (fmt == FMT_Q8_0) return mf == 1 && (nf == 6 || nf == 8);
+  if (fmt == FMT_Q8_0) return (mf == 1 || mf == 2) && (nf == 6 || nf == 8);
   return fmt == FMT_BF16 && (nf == 7 || nf == 8) && (mf == 1 || mf == 2);
 }
 

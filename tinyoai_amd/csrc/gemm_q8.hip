@@ -9,14 +9,13 @@
 namespace tinyoai_gemm {
 namespace {
 
-constexpr int kQSlots = 4;    // ring stages
 constexpr int kQThreads = 512;  // eight waves: 4 (rows) x 2 (column halves)
 
 // ------------------------------------------------------------ Q8_0 on the ring
-// Q8_0 weights on wide tiles: 128 rows x 32 * NF columns, two activation
-// planes, eight waves of 32 rows x 16 * NF columns, two per SIMD (one
-// wave's vector work, the scales and the conversion below, runs beside the
-// other's matrix products). A K step is 32 values, one quant block: the
+// Q8_0 weights on wide tiles: 128 * WM rows x 32 * NF columns, two
+// activation planes, eight waves of 32 * WM rows x 16 * NF columns, two
+// per SIMD (one wave's vector work, the scales and the conversion below,
+// runs beside the other's matrix products). A K step is 32 values, one quant block: the
 // step's activation planes, quants (32 bytes a row) and the dword of fp16
 // block scales holding its scale (blocks 2i and 2i + 1 of a row share
 // one) land in an LDS ring of SLOTS stages by buffer_load ... lds, with
@@ -36,27 +35,35 @@ constexpr int kQThreads = 512;  // eight waves: 4 (rows) x 2 (column halves)
 // cycle hit distinct banks; the swizzle is applied on the global side
 // (lane l of a wave load fetches logical half (l % 2) ^ ((row >> 3) & 1) of
 // row l / 2). The bf16 buffers use the activation rows' layout (swz).
+template <int WM>
 constexpr int dmaq_slot_bytes() {
-  return 2 * 128 * 64 + 256 * 32 + 512 * 4;  // activation planes, quant rows, scale dwords (64 rows a wave)
+  return 2 * 128 * WM * 64 + 256 * 32 + 512 * 4;  // activation planes, quant rows, scale dwords (64 rows a wave)
+}
+// Ring stages: four for 128-row tiles, three (all the LDS) for 256 rows.
+template <int WM>
+constexpr int dmaq_slots() {
+  return WM == 1 ? 4 : 3;
 }
 template <int NF>
 constexpr int dmaq_bf_bytes() {
   return 32 * NF * 64;  // one bf16 weight buffer
 }
-template <int NF, int SLOTS, bool EPI>
+template <int WM, int NF, bool EPI>
 constexpr size_t gemm_dmaq_lds() {
-  const size_t ring = (size_t)SLOTS * dmaq_slot_bytes() + 2 * (size_t)dmaq_bf_bytes<NF>() + 2 * 256 * 4;
+  const size_t ring = (size_t)dmaq_slots<WM>() * dmaq_slot_bytes<WM>() + 2 * (size_t)dmaq_bf_bytes<NF>() + 2 * 256 * 4;
   const size_t rows = (size_t)8 * 32 * (NF * 16 + 4) * 4;
   return EPI && rows > ring ? rows : ring;
 }
 
-template <int NF, int SLOTS, bool EPI>
+template <int WM, int NF, bool EPI>
 __global__ __launch_bounds__(kQThreads) void gemm_dmaq_kernel(WideArgs g) {
-  constexpr int XS = 2, BM = 128, BN = 32 * NF, NW = NF / 2;  // NW weight tiles a wave
-  static_assert(NF % 2 == 0 && BN <= 256 && SLOTS >= 3 && SLOTS <= 8, "column halves; quant rows of a slot; ring");
-  constexpr int kSlot = dmaq_slot_bytes(), kAPlane = BM * 64, kB0 = XS * kAPlane, kS0 = kB0 + 256 * 32;
+  constexpr int XS = 2, BM = 128 * WM, BN = 32 * NF, NW = NF / 2;  // NW weight tiles a wave
+  constexpr int SLOTS = dmaq_slots<WM>();
+  static_assert(NF % 2 == 0 && BN <= 256 && (WM == 1 || WM == 2), "column halves; quant rows of a slot");
+  constexpr int kSlot = dmaq_slot_bytes<WM>(), kAPlane = BM * 64, kB0 = XS * kAPlane, kS0 = kB0 + 256 * 32;
   constexpr int kBF = SLOTS * kSlot, kBFBytes = dmaq_bf_bytes<NF>(), kSC = kBF + 2 * kBFBytes;
-  constexpr int kPerStep = XS + 2;  // a wave's loads per step: 16 rows of each plane, 32 quant rows, 64 scale dwords
+  // a wave's loads per step: 16 * WM rows of each plane, 32 quant rows, 64 scale dwords
+  constexpr int kPerStep = XS * WM + 2;
   static_assert((SLOTS - 2) * kPerStep < 64, "vmcnt range");
   extern __shared__ __align__(16) uint16_t lds16[];
   uint8_t *lds8 = reinterpret_cast<uint8_t *>(lds16);
@@ -88,11 +95,15 @@ __global__ __launch_bounds__(kQThreads) void gemm_dmaq_kernel(WideArgs g) {
   const __amdgpu_buffer_rsrc_t rw = plane_rsrc(P.w.vals, (int64_t)N * P.w.vstride);
   const __amdgpu_buffer_rsrc_t rs = plane_rsrc(P.w.meta, (int64_t)N * P.w.mstride);
 
-  // Lane offsets at k = 0. Wave w loads activation rows w * 16 .. + 15 of
-  // each plane (lane l: row l / 4, chunk as swz), quant rows w * 32 .. + 31
-  // (lane l: row l / 2) and the scale dwords of rows w * 64 .. + 63.
-  const int arow0 = wave * 16 + (lane >> 2), alc = (lane & 3) ^ ((arow0 >> 2) & 3);
-  const uint32_t aoff = m0 + arow0 < g.M ? (uint32_t)(((m0 + arow0) * P.lda + alc * 8) * 2) : kNone;
+  // Lane offsets at k = 0. Wave w loads activation rows (w + 8 i) * 16 ..
+  // + 15 of each plane (lane l: row l / 4, chunk as swz), quant rows w * 32
+  // .. + 31 (lane l: row l / 2) and the scale dwords of rows w * 64 .. + 63.
+  uint32_t aoff[WM];
+#pragma unroll
+  for (int i = 0; i < WM; i++) {
+    const int row = (wave + 8 * i) * 16 + (lane >> 2), lc = (lane & 3) ^ ((row >> 2) & 3);
+    aoff[i] = m0 + row < g.M ? (uint32_t)(((m0 + row) * P.lda + lc * 8) * 2) : kNone;
+  }
   const int brow0 = wave * 32 + (lane >> 1), bh = (lane & 1) ^ ((brow0 >> 3) & 1);
   const uint32_t boff = brow0 < BN && n0 + brow0 < N ? (uint32_t)((n0 + brow0) * P.w.vstride + bh * 16) : kNone;
   const int srow = wave * 64 + lane;
@@ -107,8 +118,11 @@ __global__ __launch_bounds__(kQThreads) void gemm_dmaq_kernel(WideArgs g) {
     const uint32_t ka = in ? (uint32_t)(kb * kWK * 2) : kPast, kq = in ? (uint32_t)(kb * kWK) : kPast;
     const uint32_t ks = in ? (uint32_t)((kb >> 1) * 4) : kPast;
     const uint32_t sb = lds_base + slot * kSlot + wave_u * 1024;
-    lds_dma16(rxh, aoff + ka, sb);
-    lds_dma16(rxl, aoff + ka, sb + kAPlane);
+#pragma unroll
+    for (int i = 0; i < WM; i++) {
+      lds_dma16(rxh, aoff[i] + ka, sb + i * 8192);
+      lds_dma16(rxl, aoff[i] + ka, sb + kAPlane + i * 8192);
+    }
     lds_dma16(rw, boff + kq, sb + kB0);
     lds_dma4(rs, soff + ks, lds_base + slot * kSlot + kS0 + wave_u * 256);
   };
@@ -138,12 +152,14 @@ __global__ __launch_bounds__(kQThreads) void gemm_dmaq_kernel(WideArgs g) {
     }
   };
 
-  f32x16 acc[NW];
+  f32x16 acc[WM][NW];
 #pragma unroll
-  for (int j = 0; j < NW; j++)
+  for (int f = 0; f < WM; f++)
 #pragma unroll
-    for (int v = 0; v < 16; v++) acc[j][v] = 0.f;
-  const int arow = wm * 32 + (lane & 31), brow = lane & 31;
+    for (int j = 0; j < NW; j++)
+#pragma unroll
+      for (int v = 0; v < 16; v++) acc[f][j][v] = 0.f;
+  const int arow = wm * 32 * WM + (lane & 31), brow = lane & 31;
   auto frag = [&](const uint16_t *base, int row, int s) {
     return *reinterpret_cast<const bf16x8 *>(base + swz(row, 2 * (lane >> 5) + s));
   };
@@ -153,33 +169,41 @@ __global__ __launch_bounds__(kQThreads) void gemm_dmaq_kernel(WideArgs g) {
     const uint16_t *st = lds16 + slot * (kSlot / 2);
     const uint16_t *wb = lds16 + (kBF + bb * kBFBytes) / 2;
     const float *sc = reinterpret_cast<const float *>(lds8 + kSC) + bb * 256;
-    bf16x8 af[2][XS];
+    bf16x8 af[2][WM][XS];
 #pragma unroll
     for (int s = 0; s < 2; s++)
 #pragma unroll
-      for (int p = 0; p < XS; p++) af[s][p] = frag(st + p * (kAPlane / 2), arow, s);
-    // two weight tiles at a time: consecutive products write different
-    // accumulators
+      for (int f = 0; f < WM; f++)
 #pragma unroll
-    for (int j0 = 0; j0 < NW; j0 += 2) {
-      f32x16 tb[2];
-      float d[2];
+        for (int p = 0; p < XS; p++) af[s][f][p] = frag(st + p * (kAPlane / 2), arow + f * 32, s);
+    // two products at a time (two weight tiles, or one tile's two row
+    // tiles): consecutive matrix-core ops write different accumulators
+    constexpr int JU = WM == 1 ? 2 : 1;
 #pragma unroll
-      for (int u = 0; u < 2; u++) {
+    for (int j0 = 0; j0 < NW; j0 += JU) {
+      f32x16 tb[JU][WM];
+      float d[JU];
+#pragma unroll
+      for (int u = 0; u < JU; u++) {
         if (j0 + u >= NW) continue;
         const int col = (wn * NW + j0 + u) * 32 + brow;
         const bf16x8 b0 = frag(wb, col, 0), b1 = frag(wb, col, 1);
         d[u] = sc[col];
-        tb[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[0][0], b0, zero, 0, 0, 0);
-        tb[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[0][1], b0, tb[u], 0, 0, 0);
-        tb[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[1][0], b1, tb[u], 0, 0, 0);
-        tb[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[1][1], b1, tb[u], 0, 0, 0);
+#pragma unroll
+        for (int f = 0; f < WM; f++) {
+          tb[u][f] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[0][f][0], b0, zero, 0, 0, 0);
+          tb[u][f] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[0][f][1], b0, tb[u][f], 0, 0, 0);
+          tb[u][f] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[1][f][0], b1, tb[u][f], 0, 0, 0);
+          tb[u][f] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[1][f][1], b1, tb[u][f], 0, 0, 0);
+        }
       }
 #pragma unroll
-      for (int u = 0; u < 2; u++) {
+      for (int u = 0; u < JU; u++) {
         if (j0 + u >= NW) continue;
 #pragma unroll
-        for (int v = 0; v < 16; v++) acc[j0 + u][v] = fmaf(d[u], tb[u][v], acc[j0 + u][v]);
+        for (int f = 0; f < WM; f++)
+#pragma unroll
+          for (int v = 0; v < 16; v++) acc[f][j0 + u][v] = fmaf(d[u], tb[u][f][v], acc[f][j0 + u][v]);
       }
     }
   };
@@ -209,57 +233,67 @@ __global__ __launch_bounds__(kQThreads) void gemm_dmaq_kernel(WideArgs g) {
   __syncthreads();
 
   // D fragment: lane holds column lane % 32 of rows (v / 4) * 8 + (lane / 32) * 4 + v % 4.
-  const int r0 = m0 + wm * 32, c0 = n0 + wn * (BN / 2);
+  const int r0 = m0 + wm * 32 * WM, c0 = n0 + wn * (BN / 2);
   if constexpr (EPI) {
     constexpr int kPitch = BN / 2 + 4;
     float *tile = reinterpret_cast<float *>(lds16) + wave * 32 * kPitch;
 #pragma unroll
-    for (int j = 0; j < NW; j++)
+    for (int f = 0; f < WM; f++) {
 #pragma unroll
-      for (int v = 0; v < 16; v++)
-        tile[((v >> 2) * 8 + (lane >> 5) * 4 + (v & 3)) * kPitch + j * 32 + (lane & 31)] = acc[j][v];
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    wide_epilogue_rows(g, tile, kPitch, BN / 2, r0, c0, N, lane);
+      for (int j = 0; j < NW; j++)
+#pragma unroll
+        for (int v = 0; v < 16; v++)
+          tile[((v >> 2) * 8 + (lane >> 5) * 4 + (v & 3)) * kPitch + j * 32 + (lane & 31)] = acc[f][j][v];
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      wide_epilogue_rows(g, tile, kPitch, BN / 2, r0 + f * 32, c0, N, lane);
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
     return;
   }
   float *y = P.y + (int64_t)split * P.split_stride;
 #pragma unroll
-  for (int j = 0; j < NW; j++) {
-    const int n = c0 + j * 32 + (lane & 31);
-    if (n >= N) continue;
+  for (int f = 0; f < WM; f++)
 #pragma unroll
-    for (int v = 0; v < 16; v++) {
-      const int m = r0 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
-      if (m < g.M) y[(int64_t)m * P.ldy + n] = acc[j][v];
+    for (int j = 0; j < NW; j++) {
+      const int n = c0 + j * 32 + (lane & 31);
+      if (n >= N) continue;
+#pragma unroll
+      for (int v = 0; v < 16; v++) {
+        const int m = r0 + f * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
+        if (m < g.M) y[(int64_t)m * P.ldy + n] = acc[f][j][v];
+      }
     }
-  }
 }
 
-template <int NF, int SLOTS, bool EPI>
+template <int WM, int NF, bool EPI>
 hipError_t gemm_wideq_launch(const WideArgs &g, hipStream_t st) {
-  constexpr int BM = 128, BN = 32 * NF;
+  constexpr int BM = 128 * WM, BN = 32 * NF;
   int blocks = 0;
   for (int i = 0; i < g.nprod; i++) {
     const int tiles = ((g.M + BM - 1) / BM) * ((g.p[i].w.rows + BN - 1) / BN);
     blocks += (tiles * g.p[i].ksplit + 7) / 8 * 8;
   }
-  constexpr size_t lds = gemm_dmaq_lds<NF, SLOTS, EPI>();
+  constexpr size_t lds = gemm_dmaq_lds<WM, NF, EPI>();
   static_assert(lds <= 160 * 1024, "LDS of a CU");
   static const hipError_t attr =
-      hipFuncSetAttribute(reinterpret_cast<const void *>(&gemm_dmaq_kernel<NF, SLOTS, EPI>),
+      hipFuncSetAttribute(reinterpret_cast<const void *>(&gemm_dmaq_kernel<WM, NF, EPI>),
                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (attr != hipSuccess) return attr;
-  hipLaunchKernelGGL((gemm_dmaq_kernel<NF, SLOTS, EPI>), dim3(blocks), dim3(kQThreads), lds, st, g);
+  hipLaunchKernelGGL((gemm_dmaq_kernel<WM, NF, EPI>), dim3(blocks), dim3(kQThreads), lds, st, g);
   return hipGetLastError();
 }
 
 }  // namespace
 
-hipError_t launch_gemm_wideq(const WideArgs &g, int nf, bool epi, hipStream_t st) {
-  if (nf == 8) return epi ? gemm_wideq_launch<8, kQSlots, true>(g, st) : gemm_wideq_launch<8, kQSlots, false>(g, st);
-  if (nf == 6) return epi ? gemm_wideq_launch<6, kQSlots, true>(g, st) : gemm_wideq_launch<6, kQSlots, false>(g, st);
+hipError_t launch_gemm_wideq(const WideArgs &g, int mf, int nf, bool epi, hipStream_t st) {
+  if (mf == 1 && nf == 8) return epi ? gemm_wideq_launch<1, 8, true>(g, st) : gemm_wideq_launch<1, 8, false>(g, st);
+  if (mf == 1 && nf == 6) return epi ? gemm_wideq_launch<1, 6, true>(g, st) : gemm_wideq_launch<1, 6, false>(g, st);
+  if (mf == 2 && nf == 8) return epi ? gemm_wideq_launch<2, 8, true>(g, st) : gemm_wideq_launch<2, 8, false>(g, st);
+  if (mf == 2 && nf == 6) return epi ? gemm_wideq_launch<2, 6, true>(g, st) : gemm_wideq_launch<2, 6, false>(g, st);
   return hipErrorInvalidValue;
 }
 

@@ -137,7 +137,7 @@ __device__ __forceinline__ void wide_finish(const WideArgs &g, const WideProduct
     }
 }
 
-// The Q8_0 products on wide tiles (128 x 32 * nf, two activation planes).
-hipError_t launch_gemm_wideq(const WideArgs &g, int nf, bool epi, hipStream_t st);
+// The Q8_0 products on wide tiles (128 * mf x 32 * nf, two activation planes).
+hipError_t launch_gemm_wideq(const WideArgs &g, int mf, int nf, bool epi, hipStream_t st);
 
 }  // namespace tinyoai_gemm
