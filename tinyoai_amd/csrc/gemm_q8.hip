@@ -127,29 +127,33 @@ __global__ __launch_bounds__(kQThreads) void gemm_dmaq_kernel(WideArgs g) {
     lds_dma4(rs, soff + ks, lds_base + slot * kSlot + kS0 + wave_u * 256);
   };
   // The quants of step kb (ring slot `slot`) -> bf16 buffer bb, and each
-  // row's scale -> fp32. Thread item: (row, half) of 16 values.
+  // row's scale -> fp32. Thread item: (row, half) of 16 values; threads
+  // past the items (NF = 6) repeat the last row's (the same bytes to the
+  // same places), so the conversion has no branch and schedules among the
+  // products. A quant's fp32 value has zero low 16 bits (|q| <= 128), so
+  // its bf16 is the high half, and two go to a dword with one permute.
   auto convert = [&](int kb, int slot, int bb) {
-    if (tid >= 2 * BN) return;
-    const int row = tid >> 1, h = tid & 1;
+    const int row = min(tid >> 1, BN - 1), h = tid & 1;
     const uint8_t *q = lds8 + slot * kSlot + kB0;
     const uint32_t *sd = reinterpret_cast<const uint32_t *>(lds8 + slot * kSlot + kS0);
     uint16_t *wb = lds16 + (kBF + bb * kBFBytes) / 2;
     float *sc = reinterpret_cast<float *>(lds8 + kSC) + bb * 256;
     const uint4 w = *reinterpret_cast<const uint4 *>(q + row * 32 + ((h ^ ((row >> 3) & 1)) << 4));
     const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+    auto pair = [](uint32_t v, int sh) {
+      const uint32_t lo = __float_as_uint((float)(int8_t)(v >> sh)), hi = __float_as_uint((float)(int8_t)(v >> (sh + 8)));
+      return __builtin_amdgcn_perm(hi, lo, 0x07060302u);  // hi[31:16] : lo[31:16]
+    };
     uint32_t o[8];
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-      const uint32_t v = ws[j];
-      o[2 * j] = bf16_bits((float)(int8_t)v) | bf16_bits((float)(int8_t)(v >> 8)) << 16;
-      o[2 * j + 1] = bf16_bits((float)(int8_t)(v >> 16)) | bf16_bits((float)(int8_t)(v >> 24)) << 16;
+      o[2 * j] = pair(ws[j], 0);
+      o[2 * j + 1] = pair(ws[j], 16);
     }
     *reinterpret_cast<uint4 *>(wb + swz(row, 2 * h)) = make_uint4(o[0], o[1], o[2], o[3]);
     *reinterpret_cast<uint4 *>(wb + swz(row, 2 * h + 1)) = make_uint4(o[4], o[5], o[6], o[7]);
-    if (h == 0) {
-      const uint32_t dw = sd[row];
-      sc[row] = hw_half((uint16_t)((kb & 1) ? dw >> 16 : dw));
-    }
+    const uint32_t dw = sd[row];
+    sc[row] = hw_half((uint16_t)((kb & 1) ? dw >> 16 : dw));
   };
 
   f32x16 acc[WM][NW];
@@ -225,7 +229,7 @@ __global__ __launch_bounds__(kQThreads) void gemm_dmaq_kernel(WideArgs g) {
     __syncthreads();
     issue(kb + SLOTS - 1, slot == 0 ? SLOTS - 1 : slot - 1);
     const int next = slot + 1 == SLOTS ? 0 : slot + 1, r = kb - k_lo;
-    if (kb + 1 < k_hi) convert(kb + 1, next, (r + 1) & 1);
+    convert(kb + 1, next, (r + 1) & 1);  // past k_hi: zeros (kPast loads), never read
     compute(slot, r & 1);
     slot = next;
   }
