@@ -159,7 +159,8 @@ def test_branch_steps_from_graphs_match_direct_launches(hip, mlp, attn, kv_bits)
     are captured and each is replayed many times, with the host's own work
     and a synchronisation between replays): every step's logits are
     bit-identical, and the caches' growth past 64 positions (which drops
-    the graphs) happens within the run."""
+    the graphs) happens within the run. The graph run takes its logits into
+    a caller's array (forward's `out`), which must have the rows' shape."""
     config = W.validate_stablelm_config(dict(W.STABLELM_3B, num_hidden_layers=2, max_position_embeddings=512))
     tensors = W.synthetic_stablelm(config, mlp, seed=71, attn_dtype=attn, head_dtype=attn)
     rng = np.random.default_rng(73)
@@ -174,8 +175,16 @@ def test_branch_steps_from_graphs_match_direct_launches(hip, mlp, attn, kv_bits)
             f.profile(True)
         br = f.new_branches(96, len(suffixes))
         rows = [br.append(suffixes)]
+        out = np.empty_like(rows[0])  # the graph run also takes the logits into a caller's array
         for s in range(40):
-            rows.append(br.forward(np.argmax(rows[-1], axis=1).astype(np.int32)))
+            toks = np.argmax(rows[-1], axis=1).astype(np.int32)
+            if direct:
+                rows.append(br.forward(toks))
+            else:
+                assert br.forward(toks, out=out) is out
+                rows.append(out.copy())
+        with pytest.raises(ValueError):
+            br.forward(toks, out=np.empty((2, 3), np.float32))
         br.close()
         f.close()
         runs.append(rows)

@@ -1118,6 +1118,7 @@ Branches::~Branches() {
   if (counters) hipFree(counters);
   if (last) hipFree(last);
   if (segs) hipFree(segs);
+  if (logits_host) hipHostFree(logits_host);
   if (m) m->open_branches--;
 }
 
@@ -1379,8 +1380,22 @@ int StableModel::branch_rows(Branches &b, const int32_t *ids, const int32_t *br,
   }
   if (!lockstep)
     if (int rc = enqueue_head()) return rc;
-  TRY_HIP(hipMemcpyAsync(logits, Y, (size_t)b.count * V * 4, hipMemcpyDeviceToHost, stream), "logits");
+  // The logits reach the caller through the session's pinned buffer: one
+  // DMA and one host copy (a copy straight into pageable memory goes
+  // through the runtime's staging buffer in pieces, each waited for).
+  const size_t lbytes = (size_t)b.count * V * 4;
+  if (b.logits_bytes < lbytes) {
+    TRY_HIP(hipStreamSynchronize(stream), "branch step");
+    if (b.logits_host) hipHostFree(b.logits_host);
+    b.logits_host = nullptr;
+    b.logits_bytes = 0;
+    if (hipHostMalloc((void **)&b.logits_host, lbytes, hipHostMallocDefault) != hipSuccess)
+      return fail(TINYOAI_ENOMEM, "pinned logits buffer");
+    b.logits_bytes = lbytes;
+  }
+  TRY_HIP(hipMemcpyAsync(b.logits_host, Y, lbytes, hipMemcpyDeviceToHost, stream), "logits");
   TRY_HIP(hipStreamSynchronize(stream), "branch step");
+  memcpy(logits, b.logits_host, lbytes);
   for (int j = 0; j < b.count; j++) b.len[j] += add[j];
   return TINYOAI_OK;
 }

@@ -239,6 +239,8 @@ struct Branches {
   float *last = nullptr;         // [count][hidden]: each branch's newest residual row
   int *segs = nullptr;           // [chunk][3]: the runs of an append's chunk (first row, rows, first slot)
   std::vector<int> segs_host;    // their host copy (kept until the call has synchronised)
+  float *logits_host = nullptr;  // [count][vocab] pinned: a step's logits on their way to the caller
+  size_t logits_bytes = 0;
   std::map<int64_t, hipGraphExec_t> graphs;  // lockstep steps by attention shape
   ~Branches();
   void free_kv();

@@ -199,19 +199,33 @@ class Branches:
         check(lib().tinyoai_stablelm_branches_open(fwd.h, prefix, count, max_len, C.byref(self.h)))
         self._logits = np.empty((count, self.vocab), np.float32)
 
-    def forward(self, tokens) -> np.ndarray:
-        toks = np.ascontiguousarray(tokens, np.int32)
-        check(lib().tinyoai_stablelm_branches_forward(self.h, _ip(toks), toks.size, _fp(self._logits)))
-        return self._logits.copy()
+    def _out(self, out):
+        """The caller's float32 [count][vocab] C-contiguous array, or None."""
+        if out is None:
+            return None
+        if out.dtype != np.float32 or out.shape != (self.count, self.vocab) or not out.flags.c_contiguous:
+            raise ValueError(f"out must be a C-contiguous float32 array of shape {(self.count, self.vocab)}")
+        return out
 
-    def append(self, suffixes) -> np.ndarray:
+    def forward(self, tokens, out=None) -> np.ndarray:
+        """One token per branch; returns the logits rows [count][vocab], in a
+        new array or, with `out`, written into it (no copy)."""
+        toks = np.ascontiguousarray(tokens, np.int32)
+        dst = self._out(out)
+        buf = self._logits if dst is None else dst
+        check(lib().tinyoai_stablelm_branches_forward(self.h, _ip(toks), toks.size, _fp(buf)))
+        return buf.copy() if dst is None else dst
+
+    def append(self, suffixes, out=None) -> np.ndarray:
         """Appends suffixes[j] (a nonempty id sequence) to branch j; returns
-        each branch's last-row logits [count][vocab]."""
+        each branch's last-row logits [count][vocab] (into `out` as forward
+        does)."""
         lengths = np.array([len(x) for x in suffixes], np.int32)
         toks = np.ascontiguousarray(np.concatenate([np.asarray(x, np.int32) for x in suffixes]), np.int32)
-        check(lib().tinyoai_stablelm_branches_append(self.h, _ip(toks), _ip(lengths), lengths.size,
-                                                     _fp(self._logits)))
-        return self._logits.copy()
+        dst = self._out(out)
+        buf = self._logits if dst is None else dst
+        check(lib().tinyoai_stablelm_branches_append(self.h, _ip(toks), _ip(lengths), lengths.size, _fp(buf)))
+        return buf.copy() if dst is None else dst
 
     def length(self, branch: int) -> int:
         return check(lib().tinyoai_stablelm_branches_length(self.h, branch))
