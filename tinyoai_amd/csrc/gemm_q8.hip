@@ -15,11 +15,11 @@ constexpr int kQThreads = 512;  // eight waves: 4 (rows) x 2 (column halves)
 // Q8_0 weights on wide tiles: 128 * WM rows x 32 * NF columns, two
 // activation planes, eight waves of 32 * WM rows x 16 * NF columns, two
 // per SIMD (one wave's vector work, the scales and the conversion below,
-// runs beside the other's matrix products). A K step is 32 values, one quant block: the
-// step's activation planes, quants (32 bytes a row) and the dword of fp16
-// block scales holding its scale (blocks 2i and 2i + 1 of a row share
-// one) land in an LDS ring of SLOTS stages by buffer_load ... lds, with
-// no staging registers. The quants are converted to bf16 once per block,
+// runs beside the other's matrix products). A K step is 32 values, one
+// quant block: the step's activation planes, quants (32 bytes a row) and
+// the dword of fp16 block scales holding its scale (blocks 2i and 2i + 1
+// of a row share one) land in an LDS ring of SLOTS stages by
+// buffer_load ... lds, with no staging registers. The quants are converted to bf16 once per block,
 // not once per wave: while the products of step kb run, each thread
 // converts 16 quants of step kb + 1 (exact: |q| <= 128) into one of two
 // bf16 weight buffers, and the scale of each row to fp32. Step kb's
