@@ -190,3 +190,34 @@ def test_branch_steps_from_graphs_match_direct_launches(hip, mlp, attn, kv_bits)
         runs.append(rows)
     for s, (a, b) in enumerate(zip(*runs)):
         assert np.array_equal(a, b), s
+
+
+@pytest.mark.parametrize("mlp,attn,count", [(W.Q4_K, W.Q6_K, 6), (W.Q6_K, W.Q4_K, 6), (W.Q4_K, W.Q6_K, 18)])
+def test_paired_in_products_match_separate_launches(hip, mlp, attn, count):
+    """A branch step's two few-row in-products (q/k/v and gate/up, each in
+    its own K-quant format) run as one launch by default (launch stage
+    "kq_pair"); with the switch off they run as two launches. Both orders
+    of the two formats, 6 branches (one 16-row tile) and 18 (two): the
+    ragged appends' and 12 lockstep steps' logits are bit-identical."""
+    config = W.validate_stablelm_config(dict(W.STABLELM_3B, num_hidden_layers=2, max_position_embeddings=512))
+    tensors = W.synthetic_stablelm(config, mlp, seed=83, attn_dtype=attn, head_dtype=attn)
+    rng = np.random.default_rng(89)
+    prompt = list(rng.integers(0, 65536, 40))
+    suffixes = [list(rng.integers(0, 65536, 1 + (7 * i) % 11)) for i in range(count)]
+    runs = []
+    for paired in (True, False):
+        f = hip.StableLMForwarder(config, tensors)
+        f.set_kv_bits(16)
+        if not paired:
+            f.set_launch("kq_pair", 0, 0)
+        f.forward(0, prompt, want_logits=False)
+        br = f.new_branches(40, count)
+        rows = [br.append(suffixes)]
+        for s in range(12):
+            rows.append(br.forward(np.argmax(rows[-1], axis=1).astype(np.int32)))
+        br.close()
+        f.close()
+        runs.append(rows)
+    for s, (a, b) in enumerate(zip(*runs)):
+        assert np.all(np.isfinite(a)), s
+        assert np.array_equal(a, b), s

@@ -1305,12 +1305,20 @@ int StableModel::branch_rows(Branches &b, const int32_t *ids, const int32_t *br,
           const int ra = w.win.rows, rm = w.win2.rows;
           float *Ya = Y, *Ym = few ? Y + ycap / 2 / 4 * 4 : Y + (size_t)nc * ra;
           int sa = 1, sm = 1;
-          // H staged by the first product (or with the LayerNorm) serves the second
-          if ((rc = project(w.win, H, d, nc, Ya, ra, few ? &sa : nullptr, true, (int)(ycap / 2 / ((size_t)nc * ra)),
-                            &staged)) ||
-              (rc = project(w.win2, H, d, nc, Ym, rm, few ? &sm : nullptr, true, (int)(ycap / 2 / ((size_t)nc * rm)),
-                            &staged)))
+          if (kq_pair && norm_in_stage && staged && kq_rows_pair_supported(w.win.fmt, w.win2.fmt)) {
+            // both few-row in-products from the LayerNorm's staging of X in
+            // one launch, with the split counts project() gives each
+            sa = kq_rows_splits(w.win, (int)(ycap / 2 / ((size_t)nc * ra)));
+            sm = kq_rows_splits(w.win2, (int)(ycap / 2 / ((size_t)nc * rm)));
+            const KqProduct pa{w.win, XH, Ya, ra, sa, 0}, pm{w.win2, XH, Ym, rm, sm, 0};
+            STAGE(ST_PREFILL_GEMM, launch_kq_rows_pair(pa, pm, nc, stream), "projection");
+          } else if ((rc = project(w.win, H, d, nc, Ya, ra, few ? &sa : nullptr, true,
+                                   (int)(ycap / 2 / ((size_t)nc * ra)), &staged)) ||
+                     (rc = project(w.win2, H, d, nc, Ym, rm, few ? &sm : nullptr, true,
+                                   (int)(ycap / 2 / ((size_t)nc * rm)), &staged))) {
+            // H staged by the first product (or with the LayerNorm) serves the second
             return rc;
+          }
           TRY_HIP(launch_in_epilogue(da, b.kv[l], Ya, ra, rope, nullptr, nc, Q, M, stream, nullptr, nullptr, d_rows,
                                      sa),
                   "in_epilogue");
@@ -1861,6 +1869,10 @@ int tinyoai_stablelm_set_launch(tinyoai_model *m, int32_t stage, int32_t grid, i
   }
   if (stage == 10) {  // Q8_0 prefill products on wide tiles (1, the default) or 128 x 256 tiles (0)
     s.q8_wide = grid != 0;
+    return TINYOAI_OK;
+  }
+  if (stage == 11) {  // few-row K-quant in-products of a branch step in one launch (1, the default) or two (0)
+    s.kq_pair = grid != 0;
     return TINYOAI_OK;
   }
   if (stage == 8) {  // wide-tile in-projection with its epilogue fused (1) or a kernel of its own (0, the default)

@@ -228,6 +228,19 @@ size_t kq_rows_stage_bytes(int K, int M);
 int kq_rows_splits(const MatDesc &w, int max_splits);
 hipError_t launch_kq_rows(const MatDesc &w, const float *x, int ldx, int M, float *y, int ldy, int ks, void *stage,
                           hipStream_t st, bool staged = false, int64_t split_stride = 0);
+// Two few-row products of the same M rows (each from its own staged X, as
+// launch_kq_rows(..., staged) reads it) in one launch, each block running
+// its own product's format, with the results of two launch_kq_rows calls
+// with the same split counts. Formats: Q4_K and Q6_K, in either order.
+struct KqProduct {
+  MatDesc w;
+  const void *stage;     // staged X of this product
+  float *y;
+  int ldy, ks;
+  int64_t split_stride;  // 0: M * ldy
+};
+bool kq_rows_pair_supported(int fmt1, int fmt2);
+hipError_t launch_kq_rows_pair(const KqProduct &a, const KqProduct &b, int M, hipStream_t st);
 // Stages M <= 32 rows of x (K % 256 == 0) for launch_kq_rows(..., staged)
 // with the LayerNorm (weights lw, bias lb, eps) applied on the way.
 hipError_t launch_kq_stage_norm(const float *x, int ldx, int M, int K, const float *lw, const float *lb, double eps,

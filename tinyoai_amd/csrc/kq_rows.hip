@@ -210,9 +210,9 @@ struct Quants {
   uint32_t d6[2];
 };
 
+// One block's work: block bx of the product (bx = split * NB + row block).
 template <int F, int MT>
-__global__ __launch_bounds__(kThreads) void kq_rows_kernel(KqArgs g) {
-  extern __shared__ __align__(16) uint8_t lds[];
+__device__ __forceinline__ void kq_rows_body(const KqArgs &g, int bx, uint8_t *lds) {
   constexpr int R = 16 * MT;
   constexpr int CB = chunk_bytes<MT>();
   constexpr int kCopy = (kWindow * CB / 16 + kThreads - 1) / kThreads;  // 16-byte pieces per thread
@@ -220,7 +220,7 @@ __global__ __launch_bounds__(kThreads) void kq_rows_kernel(KqArgs g) {
   const MatDesc w = g.w;
   const int N = w.rows, K = w.cols, nch = (K + 31) / 32;
   const int NB = (N + kBlockRows - 1) / kBlockRows;
-  const int nb = blockIdx.x % NB, split = blockIdx.x / NB;
+  const int nb = bx % NB, split = bx / NB;
   // K range of the split, in whole batches of 8 chunks
   const int batches = (nch + 7) / 8;
   const int b_lo = (int)((int64_t)batches * split / g.ks), b_hi = (int)((int64_t)batches * (split + 1) / g.ks);
@@ -502,6 +502,46 @@ __global__ __launch_bounds__(kThreads) void kq_rows_kernel(KqArgs g) {
 }
 
 template <int F, int MT>
+__global__ __launch_bounds__(kThreads) void kq_rows_kernel(KqArgs g) {
+  extern __shared__ __align__(16) uint8_t lds[];
+  kq_rows_body<F, MT>(g, blockIdx.x, lds);
+}
+
+// Two products of the same rows in one launch, the second's blocks after
+// the first's, each block running its own product's format: their blocks
+// share the device instead of running as two launches one after the other
+// (each block's work and results are those of its own launch).
+template <int F1, int F2, int MT>
+__global__ __launch_bounds__(kThreads) void kq_rows_pair_kernel(KqArgs g1, KqArgs g2, int blocks1) {
+  extern __shared__ __align__(16) uint8_t lds[];
+  if ((int)blockIdx.x < blocks1)
+    kq_rows_body<F1, MT>(g1, blockIdx.x, lds);
+  else
+    kq_rows_body<F2, MT>(g2, (int)blockIdx.x - blocks1, lds);
+}
+
+template <int F1, int F2, int MT>
+hipError_t kq_pair_launch(const KqArgs &a, const KqArgs &b, hipStream_t st) {
+  constexpr size_t lds = lds_bytes<MT>();
+  static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&kq_rows_pair_kernel<F1, F2, MT>),
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  if (attr != hipSuccess) return attr;
+  const int n1 = (a.w.rows + kBlockRows - 1) / kBlockRows * a.ks, n2 = (b.w.rows + kBlockRows - 1) / kBlockRows * b.ks;
+  hipLaunchKernelGGL((kq_rows_pair_kernel<F1, F2, MT>), dim3(n1 + n2), dim3(kThreads), lds, st, a, b, n1);
+  return hipGetLastError();
+}
+
+template <int MT>
+hipError_t kq_pair_dispatch(const KqArgs &a, const KqArgs &b, hipStream_t st) {
+  const int fa = a.w.fmt, fb = b.w.fmt;
+  if (fa == FMT_Q6_K && fb == FMT_Q4_K) return kq_pair_launch<FMT_Q6_K, FMT_Q4_K, MT>(a, b, st);
+  if (fa == FMT_Q4_K && fb == FMT_Q6_K) return kq_pair_launch<FMT_Q4_K, FMT_Q6_K, MT>(a, b, st);
+  if (fa == FMT_Q4_K && fb == FMT_Q4_K) return kq_pair_launch<FMT_Q4_K, FMT_Q4_K, MT>(a, b, st);
+  if (fa == FMT_Q6_K && fb == FMT_Q6_K) return kq_pair_launch<FMT_Q6_K, FMT_Q6_K, MT>(a, b, st);
+  return hipErrorNotSupported;
+}
+
+template <int F, int MT>
 hipError_t kq_launch(const KqArgs &g, hipStream_t st) {
   constexpr size_t lds = lds_bytes<MT>();
   static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&kq_rows_kernel<F, MT>),
@@ -577,4 +617,24 @@ hipError_t launch_kq_rows(const MatDesc &w, const float *x, int ldx, int M, floa
   }
   const hipError_t e = staged ? hipSuccess : kq_stage<2>(x, ldx, M, w.cols, sb, st);
   return e != hipSuccess ? e : kq_dispatch<2>(g, st);
+}
+
+bool kq_rows_pair_supported(int fmt1, int fmt2) {
+  return (fmt1 == FMT_Q4_K || fmt1 == FMT_Q6_K) && (fmt2 == FMT_Q4_K || fmt2 == FMT_Q6_K);
+}
+
+hipError_t launch_kq_rows_pair(const KqProduct &a, const KqProduct &b, int M, hipStream_t st) {
+  const KqProduct *p[2] = {&a, &b};
+  KqArgs g[2];
+  if (M < 1 || M > 32 || !kq_rows_pair_supported(a.w.fmt, b.w.fmt)) return hipErrorInvalidValue;
+  for (int i = 0; i < 2; i++) {
+    const KqProduct &q = *p[i];
+    if (!kq_rows_supported(q.w, M) || q.ks < 1 || q.ks > (q.w.cols / 32 + 7) / 8 || q.ldy < q.w.rows || !q.y ||
+        !q.stage || (reinterpret_cast<uintptr_t>(q.stage) & 15))
+      return hipErrorInvalidValue;
+    const int64_t ss = q.split_stride ? q.split_stride : (int64_t)M * q.ldy;
+    if (q.ks > 1 && ss < (int64_t)M * q.ldy) return hipErrorInvalidValue;
+    g[i] = KqArgs{q.w, static_cast<const uint8_t *>(q.stage), M, q.y, q.ldy, q.ks, ss};
+  }
+  return M <= 16 ? kq_pair_dispatch<1>(g[0], g[1], st) : kq_pair_dispatch<2>(g[0], g[1], st);
 }

@@ -365,13 +365,14 @@ class StableLMForwarder:
               "prefill_projections", "prefill_epilogue", "prefill_attention", "prefill_elementwise")
 
     LAUNCH_STAGES = {"decode_in": 0, "decode_out": 1, "lm_head": 2, "attention": 3, "fused_attention": 4,
-                     "bf16_activations": 5, "wide": 7, "wide_epilogue": 8, "flash_key_split": 9, "q8_wide": 10}
+                     "bf16_activations": 5, "wide": 7, "wide_epilogue": 8, "flash_key_split": 9, "q8_wide": 10,
+                     "kq_pair": 11}
 
     def set_launch(self, stage: str, grid: int, threads: int) -> None:
         """Launch shape (blocks, threads per block) of a decode matrix
         kernel (results do not depend on it), or a switch (stages
         "fused_attention", "bf16_activations", "wide", "wide_epilogue",
-        "flash_key_split" and "q8_wide": grid nonzero = on)."""
+        "flash_key_split", "q8_wide" and "kq_pair": grid nonzero = on)."""
         check(lib().tinyoai_stablelm_set_launch(self.h, self.LAUNCH_STAGES[stage], int(grid), int(threads)))
 
     def profile(self, enable: bool = True) -> None:
