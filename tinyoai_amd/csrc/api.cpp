@@ -1335,7 +1335,18 @@ int StableModel::branch_rows(Branches &b, const int32_t *ids, const int32_t *br,
                   "in_epilogue");
         }
         int sp = 1, sd = 1;
-        if ((rc = project(wd, M, I, nc, D, d, &sd, true, pd_splits))) return rc;
+        // Few rows with two K-quant output-side matrices: the attention
+        // output and m staged together after the attention, and the o and
+        // down products as one launch (the conditions under which project()
+        // takes the few-row kernel for each; the two staged inputs side by
+        // side in XH).
+        const size_t cap = (size_t)chunk * std::max(dims.d, dims.inter) * 2;
+        const size_t st_a = (kq_rows_stage_bytes(d, nc) + 255) / 256 * 256;
+        const bool out_pair = kq_pair && few && kq_rows_pair_supported(wo.fmt, wd.fmt) && kq_rows_supported(wo, nc) &&
+                              kq_rows_supported(wd, nc) && (reinterpret_cast<uintptr_t>(A) & 15) == 0 &&
+                              (reinterpret_cast<uintptr_t>(M) & 15) == 0 && d % 4 == 0 && I % 4 == 0 &&
+                              st_a + kq_rows_stage_bytes(I, nc) <= cap;
+        if (!out_pair && (rc = project(wd, M, I, nc, D, d, &sd, true, pd_splits))) return rc;
         if (use_flash) {
           TRY_HIP(launch_flash_prefill(dims, kv[l], Q, d_rows, longest, A, stream, nullptr, nullptr, &b.kv[l], pfx, 0, 0,
                                        b.segs, (int)seg.size() - 1),
@@ -1345,7 +1356,16 @@ int StableModel::branch_rows(Branches &b, const int32_t *ids, const int32_t *br,
                                           A, max_splits, stream),
                   "branch attention");
         }
-        if ((rc = project(wo, A, d, nc, P, d, &sp, true, pd_splits))) return rc;
+        if (out_pair) {
+          uint8_t *sa = reinterpret_cast<uint8_t *>(XH), *sm = sa + st_a;
+          sp = kq_rows_splits(wo, pd_splits);
+          sd = kq_rows_splits(wd, pd_splits);
+          STAGE(ST_PREFILL_GEMM, launch_kq_stage_pair(A, d, d, sa, M, I, I, sm, nc, stream), "staging");
+          const KqProduct po{wo, sa, P, d, sp, 0}, pm{wd, sm, D, d, sd, 0};
+          STAGE(ST_PREFILL_GEMM, launch_kq_rows_pair(po, pm, nc, stream), "projection");
+        } else if ((rc = project(wo, A, d, nc, P, d, &sp, true, pd_splits))) {
+          return rc;
+        }
         TRY_HIP(launch_residual(X, P, sp, D, sd, (int64_t)nc * d, stream), "residual");
       }
       // each branch's newest row of this chunk

@@ -240,6 +240,11 @@ struct KqProduct {
   int64_t split_stride;  // 0: M * ldy
 };
 bool kq_rows_pair_supported(int fmt1, int fmt2);
+// Stages two inputs of the same M <= 32 rows (K1, K2 % 32 == 0, rows ldx
+// apart, 16-byte aligned) for launch_kq_rows(..., staged) in one launch,
+// as two unstaged launch_kq_rows calls would (no LayerNorm).
+hipError_t launch_kq_stage_pair(const float *x1, int ldx1, int K1, void *stage1, const float *x2, int ldx2, int K2,
+                                void *stage2, int M, hipStream_t st);
 hipError_t launch_kq_rows_pair(const KqProduct &a, const KqProduct &b, int M, hipStream_t st);
 // Stages M <= 32 rows of x (K % 256 == 0) for launch_kq_rows(..., staged)
 // with the LayerNorm (weights lw, bias lb, eps) applied on the way.

@@ -79,8 +79,8 @@ struct KqArgs {
 // over contiguous spans of K, then a fixed-order shuffle tree), so no
 // separate LayerNorm launch runs before the staging.
 template <int MT>
-__global__ __launch_bounds__(256) void kq_stage_kernel(const float *x, int ldx, int M, int K, uint8_t *stage,
-                                                       const float *lw, const float *lb, double eps) {
+__device__ __forceinline__ void kq_stage_body(const float *x, int ldx, int M, int K, uint8_t *stage, const float *lw,
+                                              const float *lb, double eps, int bx) {
   constexpr int R = 16 * MT, TPR = 256 / R;  // threads per row for the moments
   const int nch = K / 32;
   x += (int64_t)blockIdx.y * R * ldx;
@@ -125,7 +125,7 @@ __global__ __launch_bounds__(256) void kq_stage_kernel(const float *x, int ldx, 
     }
     __syncthreads();
   }
-  const int i = blockIdx.x * 256 + threadIdx.x;
+  const int i = bx * 256 + threadIdx.x;
   if (i >= R * nch * 8) return;  // whole groups of 8: R * nch * 8 and the block are multiples of 8
   const int gq = i & 7, row = (i >> 3) % R, c = (i >> 3) / R;
   float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -209,6 +209,24 @@ struct Quants {
   uint4 mt[2];
   uint32_t d6[2];
 };
+
+template <int MT>
+__global__ __launch_bounds__(256) void kq_stage_kernel(const float *x, int ldx, int M, int K, uint8_t *stage,
+                                                       const float *lw, const float *lb, double eps) {
+  kq_stage_body<MT>(x, ldx, M, K, stage, lw, lb, eps, blockIdx.x);
+}
+
+// Two inputs of the same rows staged in one launch (no LayerNorm; one
+// slice of rows), the second's blocks after the first's.
+template <int MT>
+__global__ __launch_bounds__(256) void kq_stage_pair_kernel(const float *x1, int ldx1, int K1, uint8_t *s1,
+                                                            const float *x2, int ldx2, int K2, uint8_t *s2, int M,
+                                                            int blocks1) {
+  if ((int)blockIdx.x < blocks1)
+    kq_stage_body<MT>(x1, ldx1, M, K1, s1, nullptr, nullptr, 0.0, blockIdx.x);
+  else
+    kq_stage_body<MT>(x2, ldx2, M, K2, s2, nullptr, nullptr, 0.0, (int)blockIdx.x - blocks1);
+}
 
 // One block's work: block bx of the product (bx = split * NB + row block).
 template <int F, int MT>
@@ -617,6 +635,28 @@ hipError_t launch_kq_rows(const MatDesc &w, const float *x, int ldx, int M, floa
   }
   const hipError_t e = staged ? hipSuccess : kq_stage<2>(x, ldx, M, w.cols, sb, st);
   return e != hipSuccess ? e : kq_dispatch<2>(g, st);
+}
+
+hipError_t launch_kq_stage_pair(const float *x1, int ldx1, int K1, void *stage1, const float *x2, int ldx2, int K2,
+                                void *stage2, int M, hipStream_t st) {
+  const float *xs[2] = {x1, x2};
+  const int ld[2] = {ldx1, ldx2}, ks[2] = {K1, K2};
+  void *ss[2] = {stage1, stage2};
+  if (M < 1 || M > 32) return hipErrorInvalidValue;
+  for (int i = 0; i < 2; i++)
+    if (!xs[i] || ks[i] < 32 || ks[i] % 32 || ld[i] < ks[i] || (ld[i] & 3) || (reinterpret_cast<uintptr_t>(xs[i]) & 15) ||
+        !ss[i] || (reinterpret_cast<uintptr_t>(ss[i]) & 15))
+      return hipErrorInvalidValue;
+  const int MT = M <= 16 ? 1 : 2, R = 16 * MT;
+  const int b1 = (R * (K1 / 32) * 8 + 255) / 256, b2 = (R * (K2 / 32) * 8 + 255) / 256;
+  uint8_t *p1 = static_cast<uint8_t *>(stage1), *p2 = static_cast<uint8_t *>(stage2);
+  if (MT == 1)
+    hipLaunchKernelGGL(kq_stage_pair_kernel<1>, dim3(b1 + b2), dim3(256), 0, st, x1, ldx1, K1, p1, x2, ldx2, K2, p2, M,
+                       b1);
+  else
+    hipLaunchKernelGGL(kq_stage_pair_kernel<2>, dim3(b1 + b2), dim3(256), 0, st, x1, ldx1, K1, p1, x2, ldx2, K2, p2, M,
+                       b1);
+  return hipGetLastError();
 }
 
 bool kq_rows_pair_supported(int fmt1, int fmt2) {
