@@ -235,9 +235,12 @@ int tinyoai_stablelm_profile(tinyoai_model *m, int32_t enable);
  * on wide tiles (the o and down products together as K splits of one
  * launch; chunks over 1024 rows also their in-projection), zero on
  * 128 x 256 tiles throughout (the quants exact either way; the sums' order
- * differs). Stage 11: grid nonzero (the default) runs a branch step's two
- * few-row K-quant in-products (Q4_K / Q6_K q/k/v and gate/up) as one
- * launch, zero as two (identical results). Returns 0 or TINYOAI_EINVAL. */
+ * differs). Stage 11: grid nonzero (the default) pairs a branch step's
+ * launches: the two few-row K-quant in-products (Q4_K / Q6_K q/k/v and
+ * gate/up) as one launch, their two epilogues as one, and the o and down
+ * products (their inputs staged together after the attention) as one;
+ * zero runs each as a launch of its own (identical results). Returns 0 or
+ * TINYOAI_EINVAL. */
 int tinyoai_stablelm_set_launch(tinyoai_model *m, int32_t stage, int32_t grid, int32_t threads);
 int tinyoai_stablelm_profile_read(tinyoai_model *m, double *ms, int64_t *counts, int32_t n_stages);
 

@@ -1319,12 +1319,17 @@ int StableModel::branch_rows(Branches &b, const int32_t *ids, const int32_t *br,
             // H staged by the first product (or with the LayerNorm) serves the second
             return rc;
           }
-          TRY_HIP(launch_in_epilogue(da, b.kv[l], Ya, ra, rope, nullptr, nc, Q, M, stream, nullptr, nullptr, d_rows,
-                                     sa),
-                  "in_epilogue");
-          TRY_HIP(launch_in_epilogue(dm, b.kv[l], Ym, rm, rope, nullptr, nc, Q, M, stream, nullptr, nullptr, d_rows,
-                                     sm),
-                  "in_epilogue");
+          if (kq_pair) {  // both epilogues in one launch
+            TRY_HIP(launch_in_epilogue_pair(da, Ya, ra, sa, dm, Ym, rm, sm, b.kv[l], rope, d_rows, nc, Q, M, stream),
+                    "in_epilogue");
+          } else {
+            TRY_HIP(launch_in_epilogue(da, b.kv[l], Ya, ra, rope, nullptr, nc, Q, M, stream, nullptr, nullptr, d_rows,
+                                       sa),
+                    "in_epilogue");
+            TRY_HIP(launch_in_epilogue(dm, b.kv[l], Ym, rm, rope, nullptr, nc, Q, M, stream, nullptr, nullptr, d_rows,
+                                       sm),
+                    "in_epilogue");
+          }
         } else {
           int sy = 1;
           if ((rc = project(w.win, H, d, nc, Y, win_rows, few ? &sy : nullptr, true,
@@ -1891,7 +1896,7 @@ int tinyoai_stablelm_set_launch(tinyoai_model *m, int32_t stage, int32_t grid, i
     s.q8_wide = grid != 0;
     return TINYOAI_OK;
   }
-  if (stage == 11) {  // few-row K-quant in-products of a branch step in one launch (1, the default) or two (0)
+  if (stage == 11) {  // a branch step's launch pairs (1, the default) or each launch of its own (0)
     s.kq_pair = grid != 0;
     return TINYOAI_OK;
   }

@@ -310,6 +310,13 @@ hipError_t launch_split_bf16(const float *x, int ldx, int k, int64_t rows, uint1
 hipError_t launch_in_epilogue(const StableDims &s, const KVDev &kv, const float *y, int ldy, const float *rope,
                               const int *pos0, int n, float *q, float *m, hipStream_t st, uint16_t *mh = nullptr,
                               uint16_t *ml = nullptr, const int *rows = nullptr, int ys = 1, int ldm = 0);
+// Two such epilogues of the same n branch rows (rows as above) in one
+// launch, each with its own dims (sa: q/k/v, sb: gate/up), products y
+// (ys partials n * ldy floats apart) and fp32 m, with the results of two
+// launch_in_epilogue calls.
+hipError_t launch_in_epilogue_pair(const StableDims &sa, const float *ya, int ldya, int ysa, const StableDims &sb,
+                                   const float *yb, int ldyb, int ysb, const KVDev &kv, const float *rope,
+                                   const int *rows, int n, float *q, float *m, hipStream_t st);
 // x = (x + p) + d elementwise (stablelm.go:375-377).
 // x = (x + sum_s p[s]) + sum_s d[s] over sp and sd partial products n
 // floats apart (K-split GEMM outputs), summed in order.

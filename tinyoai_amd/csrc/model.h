@@ -194,7 +194,7 @@ struct StableModel {
   // Q8_0 prefill products on wide tiles (the Q8_0 ring kernel) or on the
   // 128 x 256 tiles (launch stage 10).
   bool q8_wide = true;
-  bool kq_pair = true;     // few-row K-quant in-products (q/k/v and gate/up) as one launch
+  bool kq_pair = true;     // a branch step's paired launches (products, stagings, epilogues)
   bool flash_ksplit = true;  // prefill attention split over keys where its query tiles leave CUs idle (stage 9)
   int prefill_chunk(const int32_t *ids, int n, int start, bool want_logits);
   // Scoring of a forward_logprobs call: while set, prefill_chunk also

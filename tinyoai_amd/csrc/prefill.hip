@@ -91,9 +91,12 @@ __global__ __launch_bounds__(256) void gemm_simt_kernel(MatDesc w, const float *
 // With rows, token j sits at position rows[2j] and its K and V go to slot
 // rows[2j + 1] of the cache kv (a branch cache: the slot of the branch's
 // suffix entry).
-__global__ void in_epilogue_kernel(StableDims s, KVDev kv, const float *y, int ldy, const float *rope,
-                                   const int *pos0, int units, float *q, float *m, uint16_t *mh, uint16_t *ml,
-                                   const int *rows, int ys, int ldm) {
+// One epilogue's block (token blockIdx.x, block by of its gy on the grid's
+// second dimension).
+__device__ __forceinline__ void in_epilogue_body(const StableDims &s, const KVDev &kv, const float *y, int ldy,
+                                                 const float *rope, const int *pos0, int units, float *q, float *m,
+                                                 uint16_t *mh, uint16_t *ml, const int *rows, int ys, int ldm, int by,
+                                                 int gy) {
   const int j = blockIdx.x;
   const int pos = rows ? rows[2 * j] : *pos0 + j;
   const int slot = rows ? rows[2 * j + 1] : pos;
@@ -102,13 +105,13 @@ __global__ void in_epilogue_kernel(StableDims s, KVDev kv, const float *y, int l
   const int mu0 = (s.win_q + 2 * s.win_kv) / 2;
   float *qj = q + (int64_t)j * s.heads * s.hd, *mj = m ? m + (int64_t)j * s.inter : nullptr;
   const int64_t split = (int64_t)gridDim.x * ldy;
-  // blockIdx.y takes every gridDim.y-th group of blockDim.x units; a thread
+  // block by takes every gy-th group of blockDim.x units; a thread
   // loads kBatch of its units before it stores any, and the next kBatch
   // before it stores those (the stores could alias y as far as the
   // compiler knows, so loads placed after them would each wait a memory
   // round trip).
   constexpr int kBatch = 4;
-  const int stride = gridDim.y * blockDim.x;
+  const int stride = gy * blockDim.x;
   auto load = [&](int u0, float2 (&v)[kBatch]) {
 #pragma unroll
     for (int b = 0; b < kBatch; b++) {
@@ -123,7 +126,7 @@ __global__ void in_epilogue_kernel(StableDims s, KVDev kv, const float *y, int l
     }
   };
   float2 v[kBatch], nv[kBatch];
-  int u0 = blockIdx.y * blockDim.x + threadIdx.x;
+  int u0 = by * blockDim.x + threadIdx.x;
   if (u0 < units) load(u0, v);
   for (; u0 < units; u0 += kBatch * stride) {
     const int un = u0 + kBatch * stride;
@@ -143,6 +146,31 @@ __global__ void in_epilogue_kernel(StableDims s, KVDev kv, const float *y, int l
 #pragma unroll
     for (int b = 0; b < kBatch; b++) v[b] = nv[b];
   }
+}
+
+__global__ void in_epilogue_kernel(StableDims s, KVDev kv, const float *y, int ldy, const float *rope,
+                                   const int *pos0, int units, float *q, float *m, uint16_t *mh, uint16_t *ml,
+                                   const int *rows, int ys, int ldm) {
+  in_epilogue_body(s, kv, y, ldy, rope, pos0, units, q, m, mh, ml, rows, ys, ldm, blockIdx.y, gridDim.y);
+}
+
+struct InEpiArgs {
+  StableDims s;
+  const float *y;
+  int ldy, units, ys, gy;
+  float *m;
+};
+// Two epilogues of the same tokens in one launch (the second's blocks after
+// the first's on the grid's second dimension): the branch step's q/k/v and
+// gate/up products, each with its own dims, partials and split count.
+__global__ void in_epilogue_pair_kernel(InEpiArgs a, InEpiArgs b, KVDev kv, const float *rope, float *q,
+                                        const int *rows) {
+  if ((int)blockIdx.y < a.gy)
+    in_epilogue_body(a.s, kv, a.y, a.ldy, rope, nullptr, a.units, q, a.m, nullptr, nullptr, rows, a.ys, a.s.inter,
+                     blockIdx.y, a.gy);
+  else
+    in_epilogue_body(b.s, kv, b.y, b.ldy, rope, nullptr, b.units, q, b.m, nullptr, nullptr, rows, b.ys, b.s.inter,
+                     (int)blockIdx.y - a.gy, b.gy);
 }
 
 // sum = ((v[0] + v[1]) + v[2]) + ... over s partials n apart, eight
@@ -268,6 +296,25 @@ hipError_t launch_in_epilogue(const StableDims &s, const KVDev &kv, const float 
   const int per_token = std::max(1, std::min((units + 255) / 256, 8192 / std::max(1, n)));
   hipLaunchKernelGGL(in_epilogue_kernel, dim3(n, per_token), dim3(256), 0, st, s, kv, y, ldy, rope, pos0, units, q,
                      m, mh, ml, rows, ys, ldm ? ldm : s.inter);
+  return hipGetLastError();
+}
+
+hipError_t launch_in_epilogue_pair(const StableDims &sa, const float *ya, int ldya, int ysa, const StableDims &sb,
+                                   const float *yb, int ldyb, int ysb, const KVDev &kv, const float *rope,
+                                   const int *rows, int n, float *q, float *m, hipStream_t st) {
+  const StableDims *ss[2] = {&sa, &sb};
+  const int ld[2] = {ldya, ldyb}, ys[2] = {ysa, ysb};
+  InEpiArgs g[2];
+  if (!rows || n < 1 || !ya || !yb) return hipErrorInvalidValue;
+  for (int i = 0; i < 2; i++) {
+    const StableDims &s = *ss[i];
+    if (ld[i] % 2 || s.win_q % 2 || ys[i] < 1 || (s.inter && !m)) return hipErrorInvalidValue;
+    const int units = (s.win_q + 2 * s.win_kv + 2 * s.inter) / 2;
+    const int gy = std::max(1, std::min((units + 255) / 256, 8192 / n));
+    g[i] = InEpiArgs{s, i ? yb : ya, ld[i], units, ys[i], gy, m};
+  }
+  hipLaunchKernelGGL(in_epilogue_pair_kernel, dim3(n, g[0].gy + g[1].gy), dim3(256), 0, st, g[0], g[1], kv, rope, q,
+                     rows);
   return hipGetLastError();
 }
 
