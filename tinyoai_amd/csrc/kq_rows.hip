@@ -78,7 +78,7 @@ struct KqArgs {
 // forms the moments of its slice's rows itself (256 / R threads per row
 // over contiguous spans of K, then a fixed-order shuffle tree), so no
 // separate LayerNorm launch runs before the staging.
-template <int MT>
+template <int MT, bool NORM>
 __device__ __forceinline__ void kq_stage_body(const float *x, int ldx, int M, int K, uint8_t *stage, const float *lw,
                                               const float *lb, double eps, int bx) {
   constexpr int R = 16 * MT, TPR = 256 / R;  // threads per row for the moments
@@ -87,13 +87,26 @@ __device__ __forceinline__ void kq_stage_body(const float *x, int ldx, int M, in
   M -= blockIdx.y * R;
   stage += (size_t)blockIdx.y * nch * chunk_bytes<MT>();
   __shared__ float s_mean[R], s_inv[R];
-  if (lw) {  // block-uniform
+  // This thread's group of 4 values (and with lw its LayerNorm weight and
+  // bias), loaded before the moments' loads so that they arrive with them.
+  const int i = bx * 256 + threadIdx.x;
+  const bool item = i < R * nch * 8;  // whole groups of 8: R * nch * 8 and the block are multiples of 8
+  const int gq = i & 7, row = (i >> 3) % R, c = (i >> 3) / R, k = c * 32 + 4 * gq;
+  float4 v = make_float4(0.f, 0.f, 0.f, 0.f), w4 = v, b4 = v;
+  if (item && row < M) {
+    v = *reinterpret_cast<const float4 *>(x + (int64_t)row * ldx + k);
+    if constexpr (NORM) {
+      w4 = *reinterpret_cast<const float4 *>(lw + k);
+      b4 = *reinterpret_cast<const float4 *>(lb + k);
+    }
+  }
+  if constexpr (NORM) {
     const int r = threadIdx.x / TPR, part = threadIdx.x % TPR;
     const float *xr = x + (int64_t)min(r, M - 1) * ldx;
     const double shift = (double)xr[0];
     double s1 = 0.0, s2 = 0.0;
     const int span = K / TPR;  // a multiple of 4 (K % 256 == 0)
-    constexpr int U = 20;      // float4 loads in flight (a 2560-value row: two rounds)
+    constexpr int U = 40;      // float4 loads in flight (a 2560-value row of 16: one round)
     const float *xs = xr + part * span;
     for (int k0 = 0; k0 < span; k0 += 4 * U) {
       float4 t[U];
@@ -125,16 +138,10 @@ __device__ __forceinline__ void kq_stage_body(const float *x, int ldx, int M, in
     }
     __syncthreads();
   }
-  const int i = bx * 256 + threadIdx.x;
-  if (i >= R * nch * 8) return;  // whole groups of 8: R * nch * 8 and the block are multiples of 8
-  const int gq = i & 7, row = (i >> 3) % R, c = (i >> 3) / R;
-  float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (!item) return;
   if (row < M) {
-    const int k = c * 32 + 4 * gq;
-    v = *reinterpret_cast<const float4 *>(x + (int64_t)row * ldx + k);
-    if (lw) {
+    if constexpr (NORM) {
       const float fm = s_mean[row], inv = s_inv[row];
-      const float4 w4 = *reinterpret_cast<const float4 *>(lw + k), b4 = *reinterpret_cast<const float4 *>(lb + k);
       auto affine = [&](float xv, float wv, float bv) {
         return __fadd_rn(__fmul_rn(__fmul_rn(__fsub_rn(xv, fm), inv), wv), bv);
       };
@@ -210,10 +217,10 @@ struct Quants {
   uint32_t d6[2];
 };
 
-template <int MT>
+template <int MT, bool NORM>
 __global__ __launch_bounds__(256) void kq_stage_kernel(const float *x, int ldx, int M, int K, uint8_t *stage,
                                                        const float *lw, const float *lb, double eps) {
-  kq_stage_body<MT>(x, ldx, M, K, stage, lw, lb, eps, blockIdx.x);
+  kq_stage_body<MT, NORM>(x, ldx, M, K, stage, lw, lb, eps, blockIdx.x);
 }
 
 // Two inputs of the same rows staged in one launch (no LayerNorm; one
@@ -223,9 +230,9 @@ __global__ __launch_bounds__(256) void kq_stage_pair_kernel(const float *x1, int
                                                             const float *x2, int ldx2, int K2, uint8_t *s2, int M,
                                                             int blocks1) {
   if ((int)blockIdx.x < blocks1)
-    kq_stage_body<MT>(x1, ldx1, M, K1, s1, nullptr, nullptr, 0.0, blockIdx.x);
+    kq_stage_body<MT, false>(x1, ldx1, M, K1, s1, nullptr, nullptr, 0.0, blockIdx.x);
   else
-    kq_stage_body<MT>(x2, ldx2, M, K2, s2, nullptr, nullptr, 0.0, (int)blockIdx.x - blocks1);
+    kq_stage_body<MT, false>(x2, ldx2, M, K2, s2, nullptr, nullptr, 0.0, (int)blockIdx.x - blocks1);
 }
 
 // One block's work: block bx of the product (bx = split * NB + row block).
@@ -586,8 +593,11 @@ template <int MT>
 hipError_t kq_stage(const float *x, int ldx, int M, int K, uint8_t *stage, hipStream_t st, const float *lw = nullptr,
                     const float *lb = nullptr, double eps = 0.0) {
   const int items = 16 * MT * (K / 32) * 8;
-  hipLaunchKernelGGL((kq_stage_kernel<MT>), dim3((items + 255) / 256, (M + 16 * MT - 1) / (16 * MT)), dim3(256), 0,
-                     st, x, ldx, M, K, stage, lw, lb, eps);
+  const dim3 grid((items + 255) / 256, (M + 16 * MT - 1) / (16 * MT));
+  if (lw)
+    hipLaunchKernelGGL((kq_stage_kernel<MT, true>), grid, dim3(256), 0, st, x, ldx, M, K, stage, lw, lb, eps);
+  else
+    hipLaunchKernelGGL((kq_stage_kernel<MT, false>), grid, dim3(256), 0, st, x, ldx, M, K, stage, lw, lb, eps);
   return hipGetLastError();
 }
 
