@@ -102,24 +102,32 @@ __device__ __forceinline__ void kq_stage_body(const float *x, int ldx, int M, in
   }
   if constexpr (NORM) {
     const int r = threadIdx.x / TPR, part = threadIdx.x % TPR;
-    const float *xr = x + (int64_t)min(r, M - 1) * ldx;
-    const double shift = (double)xr[0];
-    double s1 = 0.0, s2 = 0.0;
+    double shift = 0.0, s1 = 0.0, s2 = 0.0;
     const int span = K / TPR;  // a multiple of 4 (K % 256 == 0)
     constexpr int U = 40;      // float4 loads in flight (a 2560-value row of 16: one round)
-    const float *xs = xr + part * span;
+    // Buffer loads: a load past the span gets an offset past the rows and
+    // reads zeros (never added), so every load issues before any wait (a
+    // conditional plain load became a branch and a wait per load).
+    const __amdgpu_buffer_rsrc_t rx = plane_rsrc(reinterpret_cast<const uint8_t *>(x), (int64_t)M * ldx * 4);
+    const uint32_t xs = (uint32_t)(((int64_t)min(r, M - 1) * ldx + part * span) * 4);
     for (int k0 = 0; k0 < span; k0 += 4 * U) {
       float4 t[U];
 #pragma unroll
-      for (int u = 0; u < U; u++)
-        t[u] = k0 + 4 * u < span ? *reinterpret_cast<const float4 *>(xs + k0 + 4 * u) : make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int u = 0; u < U; u++) {
+        const uint32_t off = k0 + 4 * u < span ? xs + (uint32_t)(k0 + 4 * u) * 4 : kNone;
+        const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(rx, (int)off, 0, 0);
+        t[u] = make_float4(__uint_as_float(w.x), __uint_as_float(w.y), __uint_as_float(w.z), __uint_as_float(w.w));
+      }
+      // the moments are taken about the row's first value, which the row's
+      // first thread (lanes TPR-aligned) holds first
+      if (k0 == 0) shift = (double)__shfl(t[0].x, (int)(threadIdx.x & 63) & ~(TPR - 1), 64);
 #pragma unroll
       for (int u = 0; u < U; u++) {
-        if (k0 + 4 * u >= span) continue;
+        const bool in = k0 + 4 * u < span;  // past the span: +0.0 added (a select, no branch)
         const float e[4] = {t[u].x, t[u].y, t[u].z, t[u].w};
 #pragma unroll
         for (int q = 0; q < 4; q++) {
-          const double dv = (double)e[q] - shift;
+          const double dv = in ? (double)e[q] - shift : 0.0;
           s1 += dv;
           s2 += dv * dv;
         }
