@@ -142,16 +142,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
   f16x8 qh[KS], ql[KS];
   {
     const float *qp = a.q + ((int64_t)min(myq, a.n - 1) * s.heads + h) * HD;
+    // every value loaded before the first conversion (split_half's empty
+    // asm keeps later loads behind it: one memory round trip per value)
+    float qv[KS][8];
+#pragma unroll
+    for (int k = 0; k < KS; k++) {
+      const float4 a0 = *reinterpret_cast<const float4 *>(qp + k * 16 + g * 8);
+      const float4 a1 = *reinterpret_cast<const float4 *>(qp + k * 16 + g * 8 + 4);
+      qv[k][0] = a0.x, qv[k][1] = a0.y, qv[k][2] = a0.z, qv[k][3] = a0.w;
+      qv[k][4] = a1.x, qv[k][5] = a1.y, qv[k][6] = a1.z, qv[k][7] = a1.w;
+    }
 #pragma unroll
     for (int k = 0; k < KS; k++)
 #pragma unroll
       for (int i = 0; i < 8; i++) {
         _Float16 hi, lo;
         if constexpr (HALF) {
-          hi = (_Float16)(qp[k * 16 + g * 8 + i] * qscale);
+          hi = (_Float16)(qv[k][i] * qscale);
           lo = (_Float16)0.f;
         } else {
-          split_half(qp[k * 16 + g * 8 + i] * qscale, hi, lo);
+          split_half(qv[k][i] * qscale, hi, lo);
         }
         qh[k][i] = hi;
         ql[k][i] = lo;
@@ -254,6 +264,27 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
       }
     }
   };
+  // fp32 cache: 16-byte pieces of 4 values of key t at dims [d0, d0 + 4),
+  // read by buffer loads (zeros past the block's last position) as pieces of
+  // the fp16 cache are, so a tile's loads all issue before any is used.
+  const __amdgpu_buffer_rsrc_t rk4 = plane_rsrc(
+      reinterpret_cast<const uint8_t *>(a.kv.k) + head_base * 4, HALF ? 0 : (int64_t)n_model * HD * 4);
+  const __amdgpu_buffer_rsrc_t rv4 = plane_rsrc(
+      reinterpret_cast<const uint8_t *>(a.kv.v) + head_base * 4, HALF ? 0 : (int64_t)n_model * HD * 4);
+  const __amdgpu_buffer_rsrc_t rk4s = plane_rsrc(
+      reinterpret_cast<const uint8_t *>(BR ? a.sfx.k : a.kv.k) + sfx_base * 4, HALF ? 0 : (int64_t)n_sfx * HD * 4);
+  const __amdgpu_buffer_rsrc_t rv4s = plane_rsrc(
+      reinterpret_cast<const uint8_t *>(BR ? a.sfx.v : a.kv.v) + sfx_base * 4, HALF ? 0 : (int64_t)n_sfx * HD * 4);
+  auto piece4 = [&](__amdgpu_buffer_rsrc_t r, __amdgpu_buffer_rsrc_t r2, bool ok, int t, int d0) {
+    if constexpr (BR) {
+      const uint32_t o1 = ok && t < a.prefix ? (uint32_t)((t * HD + d0) * 4) : kNone;
+      const uint32_t o2 = ok && t >= a.prefix ? (uint32_t)(((t - a.prefix) * HD + d0) * 4) : kNone;
+      const uint4 x = ld16(r, o1), y = ld16(r2, o2);
+      return make_uint4(x.x | y.x, x.y | y.y, x.z | y.z, x.w | y.w);
+    } else {
+      return ld16(r, ok ? (uint32_t)((t * HD + d0) * 4) : kNone);
+    }
+  };
   if constexpr (HALF) hload(tile0 * kTile);
   for (int tile = tile0; tile < ntiles; tile++) {
     const int t0 = tile * kTile;
@@ -262,23 +293,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
       hstore();
       if (tile + 1 < ntiles) hload(t0 + kTile);
     } else {
-      // fp32 cache: hi and lo planes, 4 values per 16-byte load
-      for (int e = tid; e < kTile * (HD / 4); e += 256) {
-        const int key = e / (HD / 4), d0 = (e % (HD / 4)) * 4, t = t0 + key;
-        const bool in_sfx = BR && t >= a.prefix;
-        const int64_t idx = (in_sfx ? sfx_base + (int64_t)(t - a.prefix) * HD : head_base + (int64_t)t * HD) + d0;
-        // the cache base as address arithmetic, not a select between two fields
-        const uintptr_t kb = reinterpret_cast<uintptr_t>(a.kv.k), vb = reinterpret_cast<uintptr_t>(a.kv.v);
-        const float *kp = reinterpret_cast<const float *>(
-            kb + (in_sfx ? reinterpret_cast<uintptr_t>(a.sfx.k) - kb : uintptr_t(0)));
-        const float *vp = reinterpret_cast<const float *>(
-            vb + (in_sfx ? reinterpret_cast<uintptr_t>(a.sfx.v) - vb : uintptr_t(0)));
-        float4 kw = make_float4(0.f, 0.f, 0.f, 0.f), vw = kw;
-        if (t <= last_pos) {
-          kw = *reinterpret_cast<const float4 *>(kp + idx);
-          vw = *reinterpret_cast<const float4 *>(vp + idx);
-        }
-        const float kx[4] = {kw.x, kw.y, kw.z, kw.w}, vx[4] = {vw.x, vw.y, vw.z, vw.w};
+      // fp32 cache: hi and lo planes, 4 values per 16-byte load, every load
+      // of the tile issued before the first is used
+      constexpr int KE4 = kTile * (HD / 4), KI = (KE4 + 255) / 256;
+      uint4 kw4[KI], vw4[KI];
+#pragma unroll
+      for (int i = 0; i < KI; i++) {
+        const int e = tid + 256 * i, key = e / (HD / 4), d0 = (e % (HD / 4)) * 4;
+        const bool ok = e < KE4 && t0 + key <= last_pos;
+        kw4[i] = piece4(rk4, rk4s, ok, t0 + key, d0);
+        vw4[i] = piece4(rv4, rv4s, ok, t0 + key, d0);
+      }
+#pragma unroll
+      for (int i = 0; i < KI; i++) {
+        const int e = tid + 256 * i, key = e / (HD / 4), d0 = (e % (HD / 4)) * 4;
+        if (KE4 % 256 != 0 && e >= KE4) continue;
+        const float kx[4] = {__uint_as_float(kw4[i].x), __uint_as_float(kw4[i].y), __uint_as_float(kw4[i].z),
+                             __uint_as_float(kw4[i].w)};
+        const float vx[4] = {__uint_as_float(vw4[i].x), __uint_as_float(vw4[i].y), __uint_as_float(vw4[i].z),
+                             __uint_as_float(vw4[i].w)};
 #pragma unroll
         for (int j = 0; j < 4; j++) {
           _Float16 kh, kl, vh, vl;
