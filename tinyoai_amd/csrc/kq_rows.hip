@@ -622,9 +622,12 @@ size_t kq_rows_stage_bytes(int K, int M) {
 
 int kq_rows_splits(const MatDesc &w, int max_splits) {
   const int NB = (w.rows + kBlockRows - 1) / kBlockRows, batches = (w.cols / 32 + 7) / 8;
-  // about 320 blocks (measured best at M = 16 for 2560-13824 rows: more
-  // splits only add partial sums), at least one batch per split
-  return std::max(1, std::min({(320 + NB - 1) / NB, batches, max_splits}));
+  // about 200 blocks a matrix, at least one batch per split: a branch
+  // step's paired in-products (q/k/v and gate/up, 2560 + 13824 rows) then
+  // fit one round of blocks at two per CU (456 blocks; the 3B K-quant
+  // step 3.65-3.67 ms against 3.74-3.75 with 320 blocks a matrix and
+  // 3.77-3.80 with 240, whose 564 blocks take a second round)
+  return std::max(1, std::min({(200 + NB - 1) / NB, batches, max_splits}));
 }
 
 hipError_t launch_kq_stage_norm(const float *x, int ldx, int M, int K, const float *lw, const float *lb, double eps,
